@@ -1,0 +1,240 @@
+"""Benchmark of the fused disentangled-attention forward + backward on one
+MI355X, in the shape the headline metric is quoted on (BASELINE.json
+configs[1], all-ones mask): B=32, L=512, H=12, D=64, bf16, position buckets
+256, max relative positions 512, c2p|p2c.
+
+A step is one forward and one backward of the op on leaf tensors already
+resident in HBM (q, k, v [B, L, H, D]; projected relative tables kr, qr
+[H, 512, D]; upstream gradient dO).  Projections are outside the op and
+outside the timed region.  The algorithmic count is
+  F_fwd = 4 B H D L^2 + 4 B H D L R,   F_step = 3 F_fwd,   R = 2A = 512.
+
+Prints one JSON line (rank 0) with the throughput, the roofline of the
+dominant kernel (per-kernel times from HIP events on the launch stream),
+and the CPU baseline: the fp32 eager oracle timed on this host's cores on a
+bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "disentangled-attn fwd+bwd TFLOP/s & % bf16 MFMA peak, L=512 H=12 d=64"
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA (published 2.5 PFLOP/s)
+B, L, H, D, BUCKETS, MAX_POS = 32, 512, 12, 64, 256, 512
+A = BUCKETS
+R = 2 * A
+
+
+def flops_fwd(b: int, l: int, h: int, d: int, r: int) -> float:
+    return 4.0 * b * h * d * l * l + 4.0 * b * h * d * l * r
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(budget_s: float = 15.0) -> dict:
+    """fp32 eager oracle fwd+bwd (the reference's op chain restated) on the
+    host's cores, on B=1 of the same shape; repeats until ~budget_s."""
+    import torch
+
+    from oracle import eager
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(0)
+    b = 1
+    q, k, v = (torch.randn(b, H, L, D, generator=g, requires_grad=True) for _ in range(3))
+    kr, qr = (torch.randn(H, R, D, generator=g, requires_grad=True) for _ in range(2))
+    dout = torch.randn(b, H, L, D, generator=g)
+    rel = eager.relative_positions(L, L, BUCKETS, MAX_POS)
+
+    def step():
+        ctx, _ = eager.attend(q, k, v, kr, qr, rel, None, types=["c2p", "p2c"], att_span=A)
+        torch.autograd.grad(ctx, (q, k, v, kr, qr), dout)
+
+    step()  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 50:
+            break
+    times.sort()
+    med = times[len(times) // 2]
+    tflops = 3 * flops_fwd(b, L, H, D, R) / med / 1e12
+    return {
+        "value": round(tflops, 4),
+        "unit": "TFLOP/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"fp32 eager oracle fwd+bwd, B=1 of B={B} L={L} H={H} D={D} R={R} (no mask), "
+        f"median of {len(times)} runs = {med * 1e3:.1f} ms; CPU: {cpu_model()}",
+    }
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(
+            f"bench.py measures one GPU: the op has no cross-GPU exchange and this build runs on a "
+            f"single MI355X (asked for --gpus {args.gpus}).",
+            file=sys.stderr,
+        )
+        sys.exit(2)
+
+    import torch
+
+    import deberta_amd  # noqa: F401
+    from deberta_amd import _lib, ops
+    from deberta_amd.relpos import relative_offset_table
+
+    lib = _lib.load()
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device="cpu").manual_seed(0)
+    mk = lambda *s: torch.randn(*s, generator=g).to(device=dev, dtype=torch.bfloat16)
+    q, k, v = mk(B, L, H, D), mk(B, L, H, D), mk(B, L, H, D)
+    kr, qr = mk(H, R, D), mk(H, R, D)
+    dout = mk(B, L, H, D)
+    for t in (q, k, v, kr, qr):
+        t.requires_grad_(True)
+    table = relative_offset_table(L, L, bucket_size=BUCKETS, max_position=MAX_POS, device=dev)
+    scale = 1.0 / math.sqrt(D * 3)
+    leaves = (q, k, v, kr, qr)
+
+    def step():
+        out, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, A, scale)
+        return torch.autograd.grad(out, leaves, dout)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = e0.elapsed_time(e1) / args.steps
+    f_fwd = flops_fwd(B, L, H, D, R)
+    f_step = 3 * f_fwd
+    tflops = f_step / (ms_step * 1e-3) / 1e12
+
+    # ---- per-kernel times: each launch timed on the stream it runs on ------------
+    stream = torch.cuda.current_stream(dev)
+    out, lse = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, A, scale)
+    f32 = dict(dtype=torch.float32, device=dev)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    dkr, dqr = torch.zeros((H, R, D), **f32), torch.zeros((H, R, D), **f32)
+    bargs = ops.fill_bwd_args(dout, q, k, v, kr, qr, table, None, None, out, lse, A, scale, dq, dk, dv, dkr, dqr)
+    ws = torch.empty((ops.bwd_workspace_bytes(bargs),), dtype=torch.uint8, device=dev)
+    bargs.workspace, bargs.workspace_bytes = ws.data_ptr(), ws.numel()
+    fargs = bargs.fwd
+    sptr = ctypes.c_void_p(stream.cuda_stream)
+
+    def run_fwd():
+        _lib.check(lib.dsa_fwd(ctypes.byref(fargs), sptr), "dsa_fwd")
+
+    def run_stage(st):
+        def f():
+            bargs.stages = st
+            _lib.check(lib.dsa_bwd(ctypes.byref(bargs), sptr), "dsa_bwd")
+
+        return f
+
+    run_stage(_lib.DSA_STAGE_PREP)()  # delta + transposed tables for the stage timings
+    kernels = {
+        "dsa_fwd_kernel": (run_fwd, f_fwd),
+        "dsa_bwd_dq_kernel": (run_stage(_lib.DSA_STAGE_DQ), f_fwd),
+        "dsa_bwd_dkdv_kernel": (run_stage(_lib.DSA_STAGE_DKDV), f_fwd),
+        "bwd_prep": (run_stage(_lib.DSA_STAGE_PREP), 0.0),
+    }
+    per_kernel = {}
+    n_k = max(10, args.steps)
+    for name, (fn, fl) in kernels.items():
+        for _ in range(3):
+            fn()
+        a_, b_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a_.record(stream)
+        for _ in range(n_k):
+            fn()
+        b_.record(stream)
+        torch.cuda.synchronize()
+        ms = a_.elapsed_time(b_) / n_k
+        per_kernel[name] = {"ms": round(ms, 5), "tflops": round(fl / (ms * 1e-3) / 1e12, 2) if fl else None}
+    dom = max((n for n in per_kernel if kernels[n][1] > 0), key=lambda n: per_kernel[n]["ms"])
+    dom_ms = per_kernel[dom]["ms"]
+    achieved = kernels[dom][1] / (dom_ms * 1e-3) / 1e12
+
+    res = {
+        "metric": METRIC,
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "fused disentangled attention fwd+bwd (c2p|p2c), BASELINE configs[1] shape, all-ones mask",
+            "batch": B,
+            "seq_len": L,
+            "heads": H,
+            "head_dim": D,
+            "position_buckets": BUCKETS,
+            "max_relative_positions": MAX_POS,
+            "rel_rows": R,
+            "flop_per_step": f_step,
+        },
+        "pct_bf16_peak": round(100.0 * tflops / PEAK_BF16_TFLOPS, 2),
+        "per_kernel": per_kernel,
+        "roofline": {
+            "kernel": dom,
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": None,
+        },
+        "wall_s_timed": round(wall, 3),
+    }
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,130 @@
+"""ctypes binding of ``libdsa.so``: the C ABI declared in ``include/dsa.h``.
+
+The structures below mirror ``dsa_fwd_args`` / ``dsa_bwd_args`` field for
+field.  ``tests/test_boundary.py`` checks their sizes and offsets against the
+C header compiled with gcc.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+from deberta_amd._build import LIB_PATH
+
+DSA_F32 = 0
+DSA_BF16 = 1
+DSA_C2P = 1
+DSA_P2C = 2
+DSA_STAGE_PREP = 1
+DSA_STAGE_DQ = 2
+DSA_STAGE_DKDV = 4
+
+EXPECTED_VERSION = 1
+
+_i64x3 = ctypes.c_int64 * 3
+_i64x2 = ctypes.c_int64 * 2
+
+
+class DsaFwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("kr", ctypes.c_void_p),
+        ("qr", ctypes.c_void_p),
+        ("rel_table", ctypes.c_void_p),
+        ("key_keep", ctypes.c_void_p),
+        ("pair_keep", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("lse", ctypes.c_void_p),
+        ("q_strides", _i64x3),
+        ("k_strides", _i64x3),
+        ("v_strides", _i64x3),
+        ("o_strides", _i64x3),
+        ("kr_strides", _i64x2),
+        ("qr_strides", _i64x2),
+        ("key_keep_stride_b", ctypes.c_int64),
+        ("pair_keep_strides", _i64x2),
+        ("B", ctypes.c_int32),
+        ("H", ctypes.c_int32),
+        ("Lq", ctypes.c_int32),
+        ("Lk", ctypes.c_int32),
+        ("D", ctypes.c_int32),
+        ("att_span", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("flags", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+    ]
+
+
+class DsaBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("fwd", DsaFwdArgs),
+        ("dout", ctypes.c_void_p),
+        ("do_strides", _i64x3),
+        ("dq", ctypes.c_void_p),
+        ("dk", ctypes.c_void_p),
+        ("dv", ctypes.c_void_p),
+        ("dq_strides", _i64x3),
+        ("dk_strides", _i64x3),
+        ("dv_strides", _i64x3),
+        ("dkr", ctypes.c_void_p),
+        ("dqr", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+        ("stages", ctypes.c_int32),
+    ]
+
+
+# Every entry point include/dsa.h declares.
+EXPORTS = ("dsa_fwd", "dsa_bwd", "dsa_bwd_workspace_bytes", "dsa_last_error", "dsa_version")
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def lib_path() -> Path:
+    return LIB_PATH
+
+
+def load() -> ctypes.CDLL:
+    """Load ``libdsa.so`` (once).  Raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: the fused disentangled-attention kernels are not built. "
+                "Run `python -m deberta_amd._build` (hipcc, gfx950) first."
+            )
+        lib = ctypes.CDLL(str(LIB_PATH))
+        lib.dsa_fwd.argtypes = [ctypes.POINTER(DsaFwdArgs), ctypes.c_void_p]
+        lib.dsa_fwd.restype = ctypes.c_int
+        lib.dsa_bwd.argtypes = [ctypes.POINTER(DsaBwdArgs), ctypes.c_void_p]
+        lib.dsa_bwd.restype = ctypes.c_int
+        lib.dsa_bwd_workspace_bytes.argtypes = [ctypes.POINTER(DsaBwdArgs)]
+        lib.dsa_bwd_workspace_bytes.restype = ctypes.c_size_t
+        lib.dsa_last_error.argtypes = []
+        lib.dsa_last_error.restype = ctypes.c_char_p
+        lib.dsa_version.argtypes = []
+        lib.dsa_version.restype = ctypes.c_int
+        ver = lib.dsa_version()
+        if ver != EXPECTED_VERSION:
+            raise RuntimeError(f"{LIB_PATH} has ABI version {ver}, expected {EXPECTED_VERSION}; rebuild it")
+        _lib = lib
+        return lib
+
+
+def last_error() -> str:
+    msg = load().dsa_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{what} failed: {last_error()}")

@@ -1,0 +1,313 @@
+"""Disentangled self-attention on the fused HIP kernels.
+
+``DisentangledSelfAttention`` keeps the reference module's parameters
+(``query_proj``, ``key_proj``, ``value_proj``, ``pos_key_proj``,
+``pos_query_proj``), attributes and forward signature
+(deberta_v2_native.py:168-222, 564-652), so a reference state dict loads
+into it and an encoder calls it unchanged.  The score/softmax/PV chain and
+its backward run in ``deberta_amd::dsa_fwd`` / ``dsa_bwd``.
+
+``disentangled_attention`` is the functional form: it takes the projected
+layers and relative tables directly.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Any, Optional
+
+import torch
+import torch.nn as nn
+
+from deberta_amd import ops  # noqa: F401  (registers the custom ops)
+from deberta_amd.config import normalize_attention_kernel, normalize_pos_att_type
+from deberta_amd.masks import kernel_masks, normalize_keep_mask
+from deberta_amd.relpos import (
+    is_toeplitz,
+    normalize_relative_pos,
+    relative_offset_table,
+    table_from_matrix,
+)
+
+_TABLE_CACHE: dict[tuple, torch.Tensor] = {}
+_TOEPLITZ_OK: dict[tuple, bool] = {}
+
+
+def _compiling() -> bool:
+    return bool(torch.compiler.is_compiling())
+
+
+def canonical_table(query_len: int, key_len: int, buckets: int, max_position: int, device) -> torch.Tensor:
+    """Cached int32 offset table of ``build_relative_position``."""
+    if _compiling():
+        return relative_offset_table(query_len, key_len, bucket_size=buckets, max_position=max_position, device=device)
+    key = (int(query_len), int(key_len), int(buckets), int(max_position), str(torch.device(device)))
+    t = _TABLE_CACHE.get(key)
+    if t is None:
+        t = relative_offset_table(query_len, key_len, bucket_size=buckets, max_position=max_position, device=device)
+        _TABLE_CACHE[key] = t
+    return t
+
+
+def table_for(
+    relative_pos: Optional[torch.Tensor],
+    query_len: int,
+    key_len: int,
+    buckets: int,
+    max_position: int,
+    device,
+) -> torch.Tensor:
+    """Offset table for the kernels from ``relative_pos`` (or the canonical
+    one when it is None).  A given matrix must depend on ``i - j`` only; this
+    is verified once per tensor version in eager mode."""
+    if relative_pos is None:
+        return canonical_table(query_len, key_len, buckets, max_position, device)
+    rp = normalize_relative_pos(relative_pos.to(device), query_len, key_len)
+    table = table_from_matrix(rp)
+    if not _compiling():
+        key = (rp.data_ptr(), rp._version, tuple(rp.shape), tuple(rp.stride()), str(rp.device))
+        ok = _TOEPLITZ_OK.get(key)
+        if ok is None:
+            ok = is_toeplitz(rp, table)
+            if len(_TOEPLITZ_OK) > 256:
+                _TOEPLITZ_OK.clear()
+            _TOEPLITZ_OK[key] = ok
+        if not ok:
+            raise ValueError(
+                "relative_pos must depend on i - j only (as build_relative_position produces) "
+                "for the fused disentangled-attention kernels"
+            )
+    return table
+
+
+def _require_gpu(t: torch.Tensor) -> None:
+    if t.device.type != "cuda":
+        raise RuntimeError(
+            f"fused disentangled attention runs on the GPU (HIP) only; got a tensor on {t.device}"
+        )
+
+
+def fused_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    kr: Optional[torch.Tensor],
+    qr: Optional[torch.Tensor],
+    table: Optional[torch.Tensor],
+    attention_mask: Optional[torch.Tensor],
+    att_span: int,
+    scale: float,
+) -> torch.Tensor:
+    """Core call on ``[B, L, H, D]`` layers; returns ``[B, Lq, H, D]``."""
+    _require_gpu(q)
+    B, Lq = q.shape[0], q.shape[1]
+    Lk = k.shape[1]
+    key_keep, pair_keep = kernel_masks(attention_mask, B, Lq, Lk)
+    if kr is not None:
+        kr = kr.to(q.dtype)
+    if qr is not None:
+        qr = qr.to(q.dtype)
+    if kr is None and qr is None:
+        table = None
+    out, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, key_keep, pair_keep, int(att_span), float(scale))
+    return out
+
+
+def disentangled_attention(
+    query_layer: torch.Tensor,
+    key_layer: torch.Tensor,
+    value_layer: torch.Tensor,
+    pos_key_layer: Optional[torch.Tensor],
+    pos_query_layer: Optional[torch.Tensor],
+    relative_pos: Optional[torch.Tensor],
+    attention_mask: Optional[torch.Tensor],
+    *,
+    position_buckets: int,
+    max_relative_positions: int,
+    att_type: Any = "c2p|p2c",
+    scale_factor: Optional[int] = None,
+    layout: str = "bhld",
+) -> torch.Tensor:
+    """Fused disentangled attention on already-projected layers.
+
+    ``query/key/value_layer`` are ``(B, H, L, D)`` (``layout="bhld"``, the
+    reference's ``_shape`` output) or ``(B, L, H, D)`` (``layout="blhd"``, the
+    Linear output viewed per head, read in place).  ``pos_key_layer`` /
+    ``pos_query_layer`` are the projected relative tables ``(H, 2A, D)``
+    (``_project_rel``); the c2p / p2c terms are used when ``att_type`` names
+    them.  ``relative_pos`` and ``attention_mask`` follow the module's
+    contract.  ``scale_factor`` defaults to ``1 + #att_type terms``.  The
+    result has the layout of ``query_layer``.
+    """
+    types = normalize_pos_att_type(att_type)
+    if "p2p" in types:
+        raise NotImplementedError("p2p is not supported by the fused disentangled-attention kernels")
+    if layout not in ("bhld", "blhd"):
+        raise ValueError(f"layout must be 'bhld' or 'blhd', got {layout!r}")
+    if layout == "bhld":
+        q, k, v = (t.transpose(1, 2) for t in (query_layer, key_layer, value_layer))
+    else:
+        q, k, v = query_layer, key_layer, value_layer
+    if scale_factor is None:
+        scale_factor = 1 + sum(t in types for t in ("c2p", "p2c", "p2p"))
+    D = q.shape[-1]
+    scale = 1.0 / math.sqrt(float(D * scale_factor))
+    kr = pos_key_layer if "c2p" in types else None
+    qr = pos_query_layer if "p2c" in types else None
+    if "c2p" in types and kr is None:
+        raise RuntimeError("p2p/c2p path requires pos_key projection.")
+    if "p2c" in types and qr is None:
+        raise RuntimeError("p2p/p2c path requires pos_query projection.")
+    if kr is not None or qr is not None:
+        rows = (kr if kr is not None else qr).shape[1]
+        att_span = rows // 2
+        table = table_for(relative_pos, q.shape[1], k.shape[1], position_buckets, max_relative_positions, q.device)
+    else:
+        att_span, table = 1, None
+    if attention_mask is not None:
+        attention_mask = normalize_keep_mask(attention_mask)
+        if attention_mask.ndim != 4:
+            raise ValueError(
+                f"attention_mask must be rank-4 [B,1,Q,K]; got shape={tuple(attention_mask.shape)}"
+            )
+    out = fused_attention(q, k, v, kr, qr, table, attention_mask, att_span, scale)
+    return out.transpose(1, 2) if layout == "bhld" else out
+
+
+class DisentangledSelfAttention(nn.Module):
+    """DeBERTa-v2 disentangled self-attention on the fused HIP kernels.
+
+    Construction mirrors deberta_v2_native.py:171-222 (same parameter names
+    and shapes, same config attributes read with the same defaults).
+    """
+
+    def __init__(self, config: Any) -> None:
+        super().__init__()
+        hidden_size = int(config.hidden_size)
+        num_heads = int(config.num_attention_heads)
+        if hidden_size % num_heads != 0:
+            raise ValueError(
+                f"hidden_size ({hidden_size}) must be divisible by num_attention_heads ({num_heads})."
+            )
+        self.num_attention_heads = num_heads
+        self.attention_head_size = int(getattr(config, "attention_head_size", hidden_size // num_heads))
+        self.all_head_size = self.num_attention_heads * self.attention_head_size
+
+        self.query_proj = nn.Linear(hidden_size, self.all_head_size, bias=True)
+        self.key_proj = nn.Linear(hidden_size, self.all_head_size, bias=True)
+        self.value_proj = nn.Linear(hidden_size, self.all_head_size, bias=True)
+
+        self.share_att_key = bool(getattr(config, "share_att_key", False))
+        self.pos_att_type = normalize_pos_att_type(getattr(config, "pos_att_type", None))
+        self.relative_attention = bool(getattr(config, "relative_attention", False))
+
+        self.position_buckets = int(getattr(config, "position_buckets", -1))
+        self.max_relative_positions = int(getattr(config, "max_relative_positions", -1))
+        if self.max_relative_positions < 1:
+            self.max_relative_positions = int(config.max_position_embeddings)
+
+        self.pos_ebd_size = self.max_relative_positions
+        if self.position_buckets > 0:
+            self.pos_ebd_size = self.position_buckets
+
+        self.pos_dropout = nn.Dropout(float(getattr(config, "hidden_dropout_prob", 0.0)))
+        self.attn_kernel = normalize_attention_kernel(getattr(config, "hf_attention_kernel", "dynamic"))
+
+        if self.relative_attention and (not self.share_att_key):
+            if ("c2p" in self.pos_att_type) or ("p2p" in self.pos_att_type):
+                self.pos_key_proj = nn.Linear(hidden_size, self.all_head_size, bias=True)
+            else:
+                self.pos_key_proj = None
+            if ("p2c" in self.pos_att_type) or ("p2p" in self.pos_att_type):
+                self.pos_query_proj = nn.Linear(hidden_size, self.all_head_size, bias=True)
+            else:
+                self.pos_query_proj = None
+        else:
+            self.pos_key_proj = None
+            self.pos_query_proj = None
+
+        self.dropout = nn.Dropout(float(getattr(config, "attention_probs_dropout_prob", 0.0)))
+
+    def _heads(self, x: torch.Tensor) -> torch.Tensor:
+        """``(B, L, H*D)`` Linear output -> ``(B, L, H, D)`` view (no copy)."""
+        bsz, seq_len, _ = x.shape
+        return x.view(bsz, seq_len, self.num_attention_heads, self.attention_head_size)
+
+    def _project_rel(self, rel_embeddings: torch.Tensor, *, use_query: bool) -> torch.Tensor:
+        """Projected relative table ``(H, 2A, D)`` as a view of the Linear
+        output (deberta_v2_native.py:273-296 without the permute copy)."""
+        att_span = int(self.pos_ebd_size)
+        rel = rel_embeddings[: 2 * att_span, :]
+        if use_query:
+            proj_layer = self.query_proj if self.share_att_key else self.pos_query_proj
+        else:
+            proj_layer = self.key_proj if self.share_att_key else self.pos_key_proj
+        if proj_layer is None:
+            raise RuntimeError("Requested relative projection is not configured for this attention module.")
+        projected = proj_layer(rel)
+        projected = projected.view(2 * att_span, self.num_attention_heads, self.attention_head_size)
+        return projected.permute(1, 0, 2)
+
+    def forward(
+        self,
+        hidden_states: torch.Tensor,
+        attention_mask: Optional[torch.Tensor],
+        output_attentions: bool = False,
+        query_states: Optional[torch.Tensor] = None,
+        relative_pos: Optional[torch.Tensor] = None,
+        rel_embeddings: Optional[torch.Tensor] = None,
+    ) -> tuple[torch.Tensor, Optional[torch.Tensor]]:
+        """Same contract as the reference forward (deberta_v2_native.py:564-652).
+
+        Not provided by the fused kernels (raise ``NotImplementedError``):
+        ``output_attentions=True`` (probabilities are never materialised),
+        ``p2p`` terms, and attention dropout ``p > 0`` in training mode.
+        """
+        if output_attentions:
+            raise NotImplementedError("output_attentions=True: the fused kernels never materialise probabilities")
+        if self.training and self.dropout.p > 0.0:
+            raise NotImplementedError("attention dropout p > 0 is not supported by the fused kernels")
+        if query_states is None:
+            query_states = hidden_states
+        _require_gpu(hidden_states)
+
+        q = self._heads(self.query_proj(query_states))
+        k = self._heads(self.key_proj(hidden_states))
+        v = self._heads(self.value_proj(hidden_states))
+        model_dtype = hidden_states.dtype
+
+        scale_factor = 1 + sum(t in self.pos_att_type for t in ("c2p", "p2c", "p2p"))
+        scale = 1.0 / math.sqrt(float(self.attention_head_size * scale_factor))
+
+        kr = qr = table = None
+        att_span = 1
+        if self.relative_attention and rel_embeddings is not None:
+            if "p2p" in self.pos_att_type:
+                raise NotImplementedError("p2p is not supported by the fused disentangled-attention kernels")
+            rel_embeddings = self.pos_dropout(rel_embeddings)
+            att_span = int(self.pos_ebd_size)
+            if "c2p" in self.pos_att_type:
+                kr = self._project_rel(rel_embeddings, use_query=False)
+            if "p2c" in self.pos_att_type:
+                qr = self._project_rel(rel_embeddings, use_query=True)
+            if kr is not None or qr is not None:
+                table = table_for(
+                    relative_pos,
+                    q.shape[1],
+                    k.shape[1],
+                    self.position_buckets,
+                    self.max_relative_positions,
+                    q.device,
+                )
+
+        if attention_mask is not None:
+            attention_mask = normalize_keep_mask(attention_mask)
+            if attention_mask.ndim != 4:
+                raise ValueError(
+                    f"attention_mask must be rank-4 [B,1,Q,K]; got shape={tuple(attention_mask.shape)}"
+                )
+
+        ctx = fused_attention(q, k, v, kr, qr, table, attention_mask, att_span, scale)
+        bsz, seq_len = ctx.shape[0], ctx.shape[1]
+        context_layer = ctx.reshape(bsz, seq_len, self.all_head_size).to(dtype=model_dtype)
+        return context_layer, None

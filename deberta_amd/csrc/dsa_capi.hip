@@ -1,0 +1,279 @@
+// dsa_capi.hip — C ABI of libdsa.so (declared in include/dsa.h): argument
+// validation, kernel selection and launches for the fused disentangled
+// attention.  Every launch goes on the caller's stream.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/dsa.h"
+#include "dsa_bwd.h"
+#include "dsa_fwd.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+int fail(const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return 1;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+int elem_bytes(int dtype) { return dtype == DSA_BF16 ? 2 : 4; }
+
+// Checks shared by forward and backward.  Shapes are validated on the host
+// so every access the kernels make stays inside the caller's buffers.
+int check_fwd(const dsa_fwd_args* a) {
+  if (!a) return fail("dsa: null arguments");
+  if (a->dtype != DSA_BF16 && a->dtype != DSA_F32) return fail("dsa: unsupported dtype %d", a->dtype);
+  if (a->D != 32 && a->D != 64) return fail("dsa: head dim must be 32 or 64, got %d", a->D);
+  if (a->B < 1 || a->H < 1 || a->Lq < 1 || a->Lk < 1)
+    return fail("dsa: empty shape B=%d H=%d Lq=%d Lk=%d", a->B, a->H, a->Lq, a->Lk);
+  if (a->B > 65535 || a->H > 65535) return fail("dsa: B and H must be <= 65535");
+  if (!a->q || !a->k || !a->v || !a->out || !a->lse) return fail("dsa: q, k, v, out and lse are required");
+  if ((a->flags & ~(DSA_C2P | DSA_P2C)) != 0) return fail("dsa: unknown flags 0x%x", a->flags);
+  if (a->flags) {
+    if (a->att_span < 1 || a->att_span > 16383) return fail("dsa: att_span must be in [1, 16383], got %d", a->att_span);
+    if (!a->rel_table) return fail("dsa: rel_table is required when c2p/p2c is enabled");
+  }
+  if ((a->flags & DSA_C2P) && !a->kr) return fail("dsa: c2p needs the pos-key table kr");
+  if ((a->flags & DSA_P2C) && !a->qr) return fail("dsa: p2c needs the pos-query table qr");
+  if (a->key_keep && a->pair_keep) return fail("dsa: give at most one of key_keep and pair_keep");
+  if ((a->key_keep || a->pair_keep) && a->Lq != a->Lk)
+    return fail("dsa: masks need Lq == Lk (query liveness is read from the key mask)");
+  const int vec = 16 / elem_bytes(a->dtype);
+  const void* ptrs[] = {a->q, a->k, a->v, a->out};
+  const int64_t* strides[] = {a->q_strides, a->k_strides, a->v_strides, a->o_strides};
+  for (int t = 0; t < 4; ++t) {
+    if (!aligned16(ptrs[t])) return fail("dsa: q/k/v/out must be 16-byte aligned");
+    for (int s = 0; s < 3; ++s)
+      if (strides[t][s] % vec != 0) return fail("dsa: q/k/v/out strides must be multiples of %d elements", vec);
+  }
+  if ((a->flags & DSA_C2P) && (!aligned16(a->kr) || a->kr_strides[0] % vec || a->kr_strides[1] % vec))
+    return fail("dsa: kr must be 16-byte aligned with strides that are multiples of %d", vec);
+  if ((a->flags & DSA_P2C) && (!aligned16(a->qr) || a->qr_strides[0] % vec || a->qr_strides[1] % vec))
+    return fail("dsa: qr must be 16-byte aligned with strides that are multiples of %d", vec);
+  return 0;
+}
+
+dsa::FwdParams to_params(const dsa_fwd_args* a) {
+  dsa::FwdParams p;
+  p.q = a->q;
+  p.k = a->k;
+  p.v = a->v;
+  p.kr = a->kr;
+  p.qr = a->qr;
+  p.rel = a->rel_table;
+  p.kk = a->key_keep;
+  p.pk = a->pair_keep;
+  p.out = a->out;
+  p.lse = a->lse;
+  for (int s = 0; s < 3; ++s) {
+    p.qs[s] = a->q_strides[s];
+    p.ks[s] = a->k_strides[s];
+    p.vs[s] = a->v_strides[s];
+    p.os[s] = a->o_strides[s];
+  }
+  for (int s = 0; s < 2; ++s) {
+    p.krs[s] = a->kr_strides[s];
+    p.qrs[s] = a->qr_strides[s];
+  }
+  p.kkb = a->key_keep_stride_b;
+  p.pkb = a->pair_keep_strides[0];
+  p.pkq = a->pair_keep_strides[1];
+  p.B = a->B;
+  p.H = a->H;
+  p.Lq = a->Lq;
+  p.Lk = a->Lk;
+  p.A = a->flags ? a->att_span : 1;
+  p.flags = a->flags;
+  p.scale = a->scale;
+  return p;
+}
+
+int mask_mode(const dsa_fwd_args* a) {
+  return a->pair_keep ? dsa::MASK_PAIR : (a->key_keep ? dsa::MASK_KEY : dsa::MASK_NONE);
+}
+
+int launch_check(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail("dsa: %s launch failed: %s", what, hipGetErrorString(e));
+  return 0;
+}
+
+template <typename T, int D, int MASK>
+int launch_fwd(const dsa::FwdParams& p, hipStream_t st) {
+  dim3 grid((p.Lq + dsa::fwdcfg::BQ - 1) / dsa::fwdcfg::BQ, p.H, p.B);
+  hipLaunchKernelGGL((dsa::dsa_fwd_kernel<T, D, MASK>), grid, dim3(256), 0, st, p);
+  return launch_check("dsa_fwd_kernel");
+}
+
+template <typename T, int D>
+int fwd_mask(const dsa::FwdParams& p, int mode, hipStream_t st) {
+  switch (mode) {
+    case dsa::MASK_KEY: return launch_fwd<T, D, dsa::MASK_KEY>(p, st);
+    case dsa::MASK_PAIR: return launch_fwd<T, D, dsa::MASK_PAIR>(p, st);
+    default: return launch_fwd<T, D, dsa::MASK_NONE>(p, st);
+  }
+}
+
+struct WsLayout {
+  size_t krT, qrT, delta, total;
+  int Rpad;
+};
+
+WsLayout ws_layout(const dsa_bwd_args* a) {
+  const dsa_fwd_args& f = a->fwd;
+  WsLayout w;
+  const int R = f.flags ? 2 * f.att_span : 0;
+  w.Rpad = (int)align_up((size_t)R, 32);
+  const size_t tab = (size_t)f.H * f.D * w.Rpad * elem_bytes(f.dtype);
+  size_t off = 0;
+  w.krT = off;
+  off = align_up(off + ((f.flags & DSA_C2P) ? tab : 0), 256);
+  w.qrT = off;
+  off = align_up(off + ((f.flags & DSA_P2C) ? tab : 0), 256);
+  w.delta = off;
+  off = align_up(off + (size_t)f.B * f.H * f.Lq * sizeof(float), 256);
+  w.total = off;
+  return w;
+}
+
+template <typename T, int D>
+int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t st) {
+  const dsa_fwd_args& f = a->fwd;
+  dsa::BwdParams bp;
+  bp.f = to_params(&f);
+  bp.dout = a->dout;
+  for (int s = 0; s < 3; ++s) {
+    bp.dos[s] = a->do_strides[s];
+    bp.dqs[s] = a->dq_strides[s];
+    bp.dks[s] = a->dk_strides[s];
+    bp.dvs[s] = a->dv_strides[s];
+  }
+  bp.dq = a->dq;
+  bp.dk = a->dk;
+  bp.dv = a->dv;
+  bp.dkr = a->dkr;
+  bp.dqr = a->dqr;
+  char* base = static_cast<char*>(a->workspace);
+  bp.krT = base + ws.krT;
+  bp.qrT = base + ws.qrT;
+  bp.delta = reinterpret_cast<float*>(base + ws.delta);
+  bp.Rpad = ws.Rpad;
+  const int stages = a->stages ? a->stages : (DSA_STAGE_PREP | DSA_STAGE_DQ | DSA_STAGE_DKDV);
+  const int R = 2 * f.att_span;
+
+  if (stages & DSA_STAGE_PREP) {
+    const int64_t n = (int64_t)f.B * f.H * f.Lq;
+    hipLaunchKernelGGL((dsa::dsa_bwd_delta_kernel<T, D>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, bp);
+    if (launch_check("dsa_bwd_delta_kernel")) return 1;
+    const int64_t nt = (int64_t)f.H * D * ws.Rpad;
+    if (f.flags & DSA_C2P) {
+      hipLaunchKernelGGL((dsa::dsa_transpose_table_kernel<T, D>), dim3((unsigned)((nt + 255) / 256)), dim3(256), 0, st,
+                         (const T*)f.kr, f.kr_strides[0], f.kr_strides[1], (T*)(base + ws.krT), f.H, R, ws.Rpad);
+      if (launch_check("dsa_transpose_table_kernel")) return 1;
+    }
+    if (f.flags & DSA_P2C) {
+      hipLaunchKernelGGL((dsa::dsa_transpose_table_kernel<T, D>), dim3((unsigned)((nt + 255) / 256)), dim3(256), 0, st,
+                         (const T*)f.qr, f.qr_strides[0], f.qr_strides[1], (T*)(base + ws.qrT), f.H, R, ws.Rpad);
+      if (launch_check("dsa_transpose_table_kernel")) return 1;
+    }
+  }
+  if (stages & DSA_STAGE_DQ) {
+    dim3 grid((f.Lq + dsa::bwdcfg::TILE_OWN - 1) / dsa::bwdcfg::TILE_OWN, f.H, f.B);
+    switch (mode) {
+      case dsa::MASK_KEY:
+        hipLaunchKernelGGL((dsa::dsa_bwd_dq_kernel<T, D, dsa::MASK_KEY>), grid, dim3(256), 0, st, bp);
+        break;
+      case dsa::MASK_PAIR:
+        hipLaunchKernelGGL((dsa::dsa_bwd_dq_kernel<T, D, dsa::MASK_PAIR>), grid, dim3(256), 0, st, bp);
+        break;
+      default:
+        hipLaunchKernelGGL((dsa::dsa_bwd_dq_kernel<T, D, dsa::MASK_NONE>), grid, dim3(256), 0, st, bp);
+    }
+    if (launch_check("dsa_bwd_dq_kernel")) return 1;
+  }
+  if (stages & DSA_STAGE_DKDV) {
+    dim3 grid((f.Lk + dsa::bwdcfg::TILE_OWN - 1) / dsa::bwdcfg::TILE_OWN, f.H, f.B);
+    switch (mode) {
+      case dsa::MASK_KEY:
+        hipLaunchKernelGGL((dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_KEY>), grid, dim3(256), 0, st, bp);
+        break;
+      case dsa::MASK_PAIR:
+        hipLaunchKernelGGL((dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_PAIR>), grid, dim3(256), 0, st, bp);
+        break;
+      default:
+        hipLaunchKernelGGL((dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_NONE>), grid, dim3(256), 0, st, bp);
+    }
+    if (launch_check("dsa_bwd_dkdv_kernel")) return 1;
+  }
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int dsa_version(void) { return 1; }
+
+const char* dsa_last_error(void) { return g_err.c_str(); }
+
+int dsa_fwd(const dsa_fwd_args* a, void* stream) {
+  g_err.clear();
+  if (check_fwd(a)) return 1;
+  const dsa::FwdParams p = to_params(a);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int mode = mask_mode(a);
+  if (a->dtype == DSA_BF16) {
+    return a->D == 64 ? fwd_mask<dsa::bf16, 64>(p, mode, st) : fwd_mask<dsa::bf16, 32>(p, mode, st);
+  }
+  return a->D == 64 ? fwd_mask<float, 64>(p, mode, st) : fwd_mask<float, 32>(p, mode, st);
+}
+
+size_t dsa_bwd_workspace_bytes(const dsa_bwd_args* a) {
+  if (!a) return 0;
+  return ws_layout(a).total;
+}
+
+int dsa_bwd(const dsa_bwd_args* a, void* stream) {
+  g_err.clear();
+  if (!a) return fail("dsa: null arguments");
+  if (check_fwd(&a->fwd)) return 1;
+  const dsa_fwd_args& f = a->fwd;
+  if (!a->dout || !a->dq || !a->dk || !a->dv) return fail("dsa: dout, dq, dk and dv are required");
+  if ((f.flags & DSA_C2P) && !a->dkr) return fail("dsa: c2p backward needs dkr");
+  if ((f.flags & DSA_P2C) && !a->dqr) return fail("dsa: p2c backward needs dqr");
+  const int vec = 16 / elem_bytes(f.dtype);
+  const void* ptrs[] = {a->dout, a->dq, a->dk, a->dv};
+  const int64_t* strides[] = {a->do_strides, a->dq_strides, a->dk_strides, a->dv_strides};
+  for (int t = 0; t < 4; ++t) {
+    if (!aligned16(ptrs[t])) return fail("dsa: dout/dq/dk/dv must be 16-byte aligned");
+    for (int s = 0; s < 3; ++s)
+      if (strides[t][s] % vec != 0) return fail("dsa: dout/dq/dk/dv strides must be multiples of %d elements", vec);
+  }
+  const WsLayout ws = ws_layout(a);
+  if (!a->workspace || a->workspace_bytes < ws.total)
+    return fail("dsa: workspace of %zu bytes required, got %zu", ws.total, a->workspace_bytes);
+  if (!aligned16(a->workspace)) return fail("dsa: workspace must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int mode = mask_mode(&f);
+  if (f.dtype == DSA_BF16) {
+    return f.D == 64 ? launch_bwd<dsa::bf16, 64>(a, ws, mode, st) : launch_bwd<dsa::bf16, 32>(a, ws, mode, st);
+  }
+  return f.D == 64 ? launch_bwd<float, 64>(a, ws, mode, st) : launch_bwd<float, 32>(a, ws, mode, st);
+}
+
+}  // extern "C"

@@ -1,0 +1,164 @@
+// dsa_common.h — shared device helpers for the fused disentangled-attention
+// kernels (gfx950 / CDNA4).
+//
+// Matrix products use the 16x16 MFMA shapes:
+//   bf16: v_mfma_f32_16x16x32_bf16  (A,B: 8 bf16 per lane, C: 4 fp32 per lane)
+//   fp32: v_mfma_f32_16x16x4_f32    (A,B: 1 fp32 per lane, C: 4 fp32 per lane)
+//
+// Lane l of a wave is addressed as (c16 = l % 16, g = l / 16).  For a
+// 16(M) x 16(N) x K product:
+//   A fragment: row m = c16, a set of K indices chosen by g
+//   B fragment: col n = c16, the same set of K indices chosen by g
+//   C/D:        col n = c16, rows m = 4*g + e for e = 0..3
+// Only the pairing of A and B k-indices matters for the result, so every
+// product here picks a "k-set" per (step s, group g) and loads both operands
+// with it:
+//   CONTIG (bf16): k = 32*s + 8*g + [0..7]          -> one 16-byte load
+//   ACC    (bf16): k = 32*s + 4*g + [0..3]  and  32*s + 16 + 4*g + [0..3]
+//   (fp32)       : k = 16*s + 4*g + [0..3], four K=4 MFMAs per step
+// The ACC set is exactly what a lane holds of two vertically adjacent C
+// tiles, so a C tile (e.g. probabilities P) can be fed straight back into the
+// next product as a B operand without a trip through LDS.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dsa {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+#define DSA_DEV __device__ __forceinline__
+
+template <typename T>
+struct Mfma;
+
+template <>
+struct Mfma<bf16> {
+  static constexpr int KSTEP = 32;  // k indices consumed per step
+  static constexpr int ACC_TILES_PER_STEP = 2;
+  typedef bf16x8 frag;
+  static DSA_DEV f32x4 mma(const frag& a, const frag& b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  static DSA_DEV frag zero() {
+    frag z;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) z[e] = (bf16)0.0f;
+    return z;
+  }
+  // CONTIG k-set from a contiguous row (row points at k = 0).
+  static DSA_DEV frag load_contig(const bf16* row, int s, int g) {
+    return *reinterpret_cast<const bf16x8*>(row + 32 * s + 8 * g);
+  }
+  // ACC k-set from a contiguous row.
+  static DSA_DEV frag load_acc(const bf16* row, int s, int g) {
+    bf16x4 lo = *reinterpret_cast<const bf16x4*>(row + 32 * s + 4 * g);
+    bf16x4 hi = *reinterpret_cast<const bf16x4*>(row + 32 * s + 16 + 4 * g);
+    frag f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      f[e] = lo[e];
+      f[4 + e] = hi[e];
+    }
+    return f;
+  }
+  // ACC k-set from C tiles: tiles[2s] and tiles[2s+1] hold rows 4g+e.
+  static DSA_DEV frag from_acc(const f32x4* tiles, int s) {
+    frag f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      f[e] = (bf16)tiles[2 * s][e];
+      f[4 + e] = (bf16)tiles[2 * s + 1][e];
+    }
+    return f;
+  }
+  // ACC k-set from 8 fp32 values gathered in k order (lo 4, hi 4).
+  static DSA_DEV frag from_f32(const float* v) {
+    frag f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = (bf16)v[e];
+    return f;
+  }
+  // element index within the ACC k-set -> k offset inside the step
+  static DSA_DEV int acc_k(int g, int e) { return (e < 4) ? (4 * g + e) : (16 + 4 * g + (e - 4)); }
+  static constexpr int FRAG_ELEMS = 8;
+};
+
+template <>
+struct Mfma<float> {
+  static constexpr int KSTEP = 16;
+  static constexpr int ACC_TILES_PER_STEP = 1;
+  typedef f32x4 frag;
+  static DSA_DEV f32x4 mma(const frag& a, const frag& b, f32x4 c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[0], b[0], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[1], b[1], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[2], b[2], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[3], b[3], c, 0, 0, 0);
+    return c;
+  }
+  static DSA_DEV frag zero() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+  static DSA_DEV frag load_contig(const float* row, int s, int g) {
+    return *reinterpret_cast<const f32x4*>(row + 16 * s + 4 * g);
+  }
+  static DSA_DEV frag load_acc(const float* row, int s, int g) { return load_contig(row, s, g); }
+  static DSA_DEV frag from_acc(const f32x4* tiles, int s) { return tiles[s]; }
+  static DSA_DEV frag from_f32(const float* v) { return f32x4{v[0], v[1], v[2], v[3]}; }
+  static DSA_DEV int acc_k(int g, int e) { return 4 * g + e; }
+  static constexpr int FRAG_ELEMS = 4;
+};
+
+DSA_DEV f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+template <typename T>
+DSA_DEV float to_f32(T x) { return (float)x; }
+
+template <typename T>
+DSA_DEV T from_f32(float x) { return (T)x; }
+
+// Cross-lane reductions over the 4 lanes that share c16 (lanes l, l^16,
+// l^32, l^48): these hold the 4 row-groups of one C-tile column.
+DSA_DEV float col_max(float x) {
+  x = fmaxf(x, __shfl_xor(x, 16));
+  x = fmaxf(x, __shfl_xor(x, 32));
+  return x;
+}
+DSA_DEV float col_sum(float x) {
+  x += __shfl_xor(x, 16);
+  x += __shfl_xor(x, 32);
+  return x;
+}
+DSA_DEV int wave_min(int x) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) x = min(x, __shfl_xor(x, o));
+  return x;
+}
+DSA_DEV int wave_max(int x) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) x = max(x, __shfl_xor(x, o));
+  return x;
+}
+
+// Orders LDS traffic between lanes of one wave (write by one lane, read by
+// another).  DS instructions of a wave complete in order; this keeps the
+// compiler from moving loads across the point.
+DSA_DEV void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// c2p / p2c rows from a clamped relative position tc in [-A, A]
+// (deberta_v2_native.py:395 / :407 and :488 / :503).
+DSA_DEV int c2p_row(int tc, int A) { return min(max(tc + A, 0), 2 * A - 1); }
+DSA_DEV int p2c_row(int tc, int A) { return min(max(-tc + A, 0), 2 * A - 1); }
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+enum MaskMode { MASK_NONE = 0, MASK_KEY = 1, MASK_PAIR = 2 };
+
+}  // namespace dsa

@@ -1,0 +1,236 @@
+// dsa_fwd.h — fused disentangled-attention forward kernel (gfx950).
+//
+// One workgroup = 4 waves = one (batch b, head h, 128-query tile).  Wave w
+// owns queries [i0 + 32w, i0 + 32w + 32) and streams 64-key tiles:
+//
+//   S^T = K Q^T                      MFMA, K tile from LDS, Q^T in registers
+//   S^T += c2p gather                band MFMA  Kr[cmin..cmax] Q^T  -> LDS -> gather
+//   S^T += p2c gather                band MFMA  K Qr[pmin..pmax]^T  -> LDS -> gather
+//   mask, online softmax (exp2)      fp32, per query column
+//   O^T += V^T P^T                   MFMA, P fed from registers (ACC k-set)
+//
+// The score tile is kept transposed (keys down, queries across) so that the
+// probabilities a lane holds are already the B operand of the PV product.
+//
+// Relative bands: the c2p row of (i, j) is c(i - j), a non-decreasing function
+// of i - j with unit steps for the reference's log buckets, so the rows a tile
+// touches form the contiguous range [c(min), c(max)] of the Kr table.  The
+// band product computes exactly those rows (about one 32x64 tile's worth of
+// MFMA work on average at L=512, buckets 256) and the gather reads the
+// result back from LDS at row c(i - j) - cmin.  The range is found by a
+// min/max scan, so any Toeplitz relative-position table is handled; bands
+// wider than BAND rows are processed in chunks.
+#pragma once
+
+#include "dsa_tiles.h"
+
+namespace dsa {
+
+namespace fwdcfg {
+constexpr int NW = 4;        // waves per workgroup
+constexpr int WQ = 32;       // queries per wave
+constexpr int BQ = NW * WQ;  // queries per workgroup
+constexpr int BK = 64;       // keys per tile
+constexpr int SCR = 64 * (tilecfg::BAND + 1);  // per-wave band scratch (floats)
+constexpr int TBL = BQ + BK;      // relative-position window per tile
+}  // namespace fwdcfg
+
+template <typename T, int D, int MASK>
+__global__ __launch_bounds__(256, 1) void dsa_fwd_kernel(FwdParams p) {
+  using namespace fwdcfg;
+  using M = Mfma<T>;
+  typedef typename M::frag frag;
+  constexpr int NS = D / M::KSTEP;        // k steps over the head dim
+  constexpr int KSTR = D + Pad<T>::v;      // Ks row stride
+  constexpr int VSTR = BK + Pad<T>::v;     // Vt row stride
+  constexpr int ND = D / 16;               // 16-wide tiles over the head dim
+  constexpr int PV_STEPS = BK / M::KSTEP;  // k steps over the key tile
+
+  __shared__ __align__(16) T Ks[BK * KSTR];
+  __shared__ __align__(16) T Vt[D * VSTR];
+  __shared__ short tbl[TBL];
+  __shared__ float scr_all[NW * SCR];
+
+  const int tid = threadIdx.x;
+  const int w = tid >> 6, l = tid & 63, g = l >> 4, c16 = l & 15;
+  const int qt = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int Lq = p.Lq, Lk = p.Lk, A = p.A;
+  const int i0 = qt * BQ;
+  const int iw = i0 + w * WQ;
+  float* scr = scr_all + w * SCR;
+
+  const T* qbase = (const T*)p.q + (int64_t)b * p.qs[0] + (int64_t)h * p.qs[2];
+  const T* kbase = (const T*)p.k + (int64_t)b * p.ks[0] + (int64_t)h * p.ks[2];
+  const T* vbase = (const T*)p.v + (int64_t)b * p.vs[0] + (int64_t)h * p.vs[2];
+  const T* krh = (p.flags & 1) ? (const T*)p.kr + (int64_t)h * p.krs[0] : nullptr;
+  const T* qrh = (p.flags & 2) ? (const T*)p.qr + (int64_t)h * p.qrs[0] : nullptr;
+  const uint8_t* kkb = (MASK == MASK_KEY) ? p.kk + (int64_t)b * p.kkb : nullptr;
+  const uint8_t* pkb = (MASK == MASK_PAIR) ? p.pk + (int64_t)b * p.pkb : nullptr;
+
+  // Per-lane query columns (two 16-wide tiles per wave).
+  int irow[2];
+  bool ilive[2];
+#pragma unroll
+  for (int ib = 0; ib < 2; ++ib) {
+    irow[ib] = iw + 16 * ib + c16;
+    bool valid = irow[ib] < Lq;
+    bool live = valid;
+    if (MASK == MASK_KEY && valid) live = kkb[irow[ib]] != 0;
+    if (MASK == MASK_PAIR && valid) live = pkb[(int64_t)irow[ib] * p.pkq + irow[ib]] != 0;
+    ilive[ib] = live;
+  }
+
+  // Q^T fragments stay in registers for the whole key loop.
+  frag qf[2][NS];
+#pragma unroll
+  for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+      qf[ib][s] = (irow[ib] < Lq) ? M::load_contig(qbase + (int64_t)irow[ib] * p.qs[1], s, g) : M::zero();
+
+  float mrow[2] = {-INFINITY, -INFINITY};
+  float lrow[2] = {0.f, 0.f};
+  f32x4 o[ND][2];
+#pragma unroll
+  for (int db = 0; db < ND; ++db) o[db][0] = o[db][1] = zero4();
+
+  const float sl2 = p.scale * kLog2e;
+  const int nkt = (Lk + BK - 1) / BK;
+
+  // Is any query row of this workgroup live?  If not, nothing to compute.
+  int wg_live = 0;
+  if (tid < BQ) {
+    int i = i0 + tid;
+    if (i < Lq) {
+      if (MASK == MASK_NONE) wg_live = 1;
+      else if (MASK == MASK_KEY) wg_live = kkb[i] != 0;
+      else wg_live = pkb[(int64_t)i * p.pkq + i] != 0;
+    }
+  }
+  const bool any_live = __syncthreads_or(wg_live);
+
+  for (int kt = 0; any_live && kt < nkt; ++kt) {
+    const int j0 = kt * BK;
+    // Skip key tiles that every query row of the workgroup masks out: their
+    // probabilities are exactly zero.
+    if (MASK == MASK_KEY) {
+      int keep = 0;
+      if (tid < BK) keep = (j0 + tid < Lk) && kkb[j0 + tid];
+      if (!__syncthreads_or(keep)) continue;
+    } else if (MASK == MASK_PAIR) {
+      int keep = 0;
+      const int r = tid >> 1, half = tid & 1;
+      const int i = i0 + r;
+      if (i < Lq) {
+        const uint8_t* row = pkb + (int64_t)i * p.pkq;
+        const int jb0 = j0 + half * (BK / 2);
+        const int jend = min(jb0 + BK / 2, Lk);
+        for (int j = jb0; j < jend; ++j) keep |= row[j];
+      }
+      if (!__syncthreads_or(keep)) continue;
+    }
+    __syncthreads();  // previous tile's LDS reads are done
+    load_rows<T, D, BK, 256>(Ks, KSTR, nullptr, 0, kbase, p.ks[1], j0, Lk, tid);
+    load_rows<T, D, BK, 256>(nullptr, 0, Vt, VSTR, vbase, p.vs[1], j0, Lk, tid);
+    if (p.flags) load_rel_window(tbl, p.rel, i0 - j0 - (BK - 1), BQ + BK - 1, Lq, Lk, A, tid, 256);
+    __syncthreads();
+
+    // ---- S^T = K Q^T + c2p + p2c ------------------------------------------
+    frag kf[4][NS];
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+      for (int s = 0; s < NS; ++s) kf[jb][s] = M::load_contig(&Ks[(16 * jb + c16) * KSTR], s, g);
+    f32x4 st[2][4];
+    score_tile_T<T, D>(st, kf, qf, scr, tbl, w * WQ, l, g, c16, krh, p.krs[1], qrh, p.qrs[1], A, p.flags);
+
+    // ---- mask + online softmax (log2 domain) --------------------------------
+#pragma unroll
+    for (int ib = 0; ib < 2; ++ib) {
+      const int i = irow[ib];
+      float mt = -INFINITY;
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb) {
+        uint32_t pk4 = 0;
+        if (MASK == MASK_PAIR && ilive[ib]) {
+          const uint8_t* row = pkb + (int64_t)i * p.pkq;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int j = j0 + 16 * jb + 4 * g + e;
+            pk4 |= (j < Lk && row[j]) ? (1u << e) : 0u;
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int j = j0 + 16 * jb + 4 * g + e;
+          bool keep = ilive[ib] && j < Lk;
+          if (MASK == MASK_KEY) keep = keep && kkb[j] != 0;
+          if (MASK == MASK_PAIR) keep = keep && ((pk4 >> e) & 1u);
+          const float y = keep ? st[ib][jb][e] * sl2 : -INFINITY;
+          st[ib][jb][e] = y;
+          mt = fmaxf(mt, y);
+        }
+      }
+      mt = col_max(mt);
+      const float mnew = fmaxf(mrow[ib], mt);
+      float alpha = 1.f;
+      if (mnew != -INFINITY) {
+        alpha = exp2f(mrow[ib] - mnew);  // 0 when mrow was -inf
+        float ls = 0.f;
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float pe = exp2f(st[ib][jb][e] - mnew);
+            st[ib][jb][e] = pe;
+            ls += pe;
+          }
+        lrow[ib] = lrow[ib] * alpha + ls;
+        mrow[ib] = mnew;
+      } else {
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) st[ib][jb] = zero4();
+      }
+#pragma unroll
+      for (int db = 0; db < ND; ++db) o[db][ib] *= alpha;
+    }
+
+    // ---- O^T += V^T P^T -------------------------------------------------------
+#pragma unroll
+    for (int s = 0; s < PV_STEPS; ++s) {
+      frag pf[2];
+#pragma unroll
+      for (int ib = 0; ib < 2; ++ib) pf[ib] = M::from_acc(st[ib], s);
+#pragma unroll
+      for (int db = 0; db < ND; ++db) {
+        const frag vf = M::load_acc(&Vt[(16 * db + c16) * VSTR], s, g);
+#pragma unroll
+        for (int ib = 0; ib < 2; ++ib) o[db][ib] = M::mma(vf, pf[ib], o[db][ib]);
+      }
+    }
+  }
+
+  // ---- epilogue -----------------------------------------------------------
+  T* obase = (T*)p.out + (int64_t)b * p.os[0] + (int64_t)h * p.os[2];
+#pragma unroll
+  for (int ib = 0; ib < 2; ++ib) {
+    const int i = irow[ib];
+    const float lsum = col_sum(lrow[ib]);
+    const bool ok = ilive[ib] && lsum > 0.f;
+    const float inv = ok ? 1.f / lsum : 0.f;
+    if (i < Lq) {
+      T* orow = obase + (int64_t)i * p.os[1];
+#pragma unroll
+      for (int db = 0; db < ND; ++db) {
+        typedef T vec4 __attribute__((ext_vector_type(4)));
+        vec4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (T)(o[db][ib][e] * inv);
+        *reinterpret_cast<vec4*>(orow + 16 * db + 4 * g) = v;
+      }
+      if (g == 0) p.lse[((int64_t)b * p.H + h) * Lq + i] = ok ? (mrow[ib] * kLn2 + logf(lsum)) : INFINITY;
+    }
+  }
+}
+
+}  // namespace dsa

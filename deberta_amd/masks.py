@@ -1,0 +1,97 @@
+"""Keep-mask contract of the attention (bool/int keep masks, float rejected),
+and its translation into the byte masks the kernels read.
+
+Mirrors ``normalize_keep_mask`` (mask_utils.py:8-32), the encoder's
+``get_attention_mask`` (deberta_v2_native.py:1049-1068) and the packed
+document mask ``_build_doc_block_mask`` (training/compile.py:310-349).
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+
+def normalize_keep_mask(mask: torch.Tensor, *, name: str = "attention_mask") -> torch.Tensor:
+    """Bool keep mask: bool passes through, integers become ``!= 0``, floating
+    masks raise ``ValueError`` and non-tensors ``TypeError`` (same messages as
+    the reference)."""
+    if not isinstance(mask, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor, got {type(mask)!r}.")
+    if mask.dtype == torch.bool:
+        return mask
+    if torch.is_floating_point(mask):
+        raise ValueError(
+            f"{name} must be a bool/integer keep-mask tensor. "
+            "Floating-point masks are ambiguous (0/1 keep vs 0/-inf additive)."
+        )
+    return mask.ne(0)
+
+
+def get_attention_mask(attention_mask: torch.Tensor) -> torch.Tensor:
+    """Encoder-side canonical 4-D keep mask: ``(B,S) -> (B,1,1,S)``,
+    ``(B,S,S) -> (B,1,S,S)``, ``(B,H,..) -> any over heads``."""
+    mask = normalize_keep_mask(attention_mask)
+    if mask.ndim <= 2:
+        return mask[:, None, None, :]
+    if mask.ndim == 3:
+        return mask.unsqueeze(1)
+    if mask.ndim == 4:
+        if mask.shape[1] == 1:
+            return mask
+        return mask.any(dim=1, keepdim=True)
+    raise ValueError(f"attention_mask must be rank-2/3/4; got rank={mask.ndim}")
+
+
+def build_doc_block_mask(doc_ids: torch.Tensor) -> torch.Tensor:
+    """Pairwise ``(B, S, S)`` keep mask for packed documents: active tokens
+    (``doc_id != 0``) attend within their document, the diagonal marks query
+    activity, and pad queries keep one edge to key 0 (CLS)."""
+    if doc_ids.ndim != 2:
+        raise ValueError(f"doc_ids must be rank-2 (B,S); got shape={tuple(doc_ids.shape)}")
+    seq_len = int(doc_ids.shape[1])
+    device = doc_ids.device
+    eye = torch.eye(seq_len, dtype=torch.bool, device=device)
+    cls_key = torch.zeros(seq_len, dtype=torch.bool, device=device)
+    cls_key[0] = True
+    active = doc_ids.ne(0)
+    same_doc = doc_ids[:, :, None].eq(doc_ids[:, None, :])
+    keep = same_doc & active[:, :, None] & active[:, None, :]
+    keep = keep | ((~active)[:, :, None] & cls_key[None, None, :])
+    keep = (keep & ~eye[None, :, :]) | (eye[None, :, :] & active[:, :, None])
+    return keep
+
+
+def kernel_masks(
+    attention_mask: Optional[torch.Tensor], batch: int, query_len: int, key_len: int
+) -> tuple[Optional[torch.Tensor], Optional[torch.Tensor]]:
+    """Split a rank-4 keep mask into the kernels' ``(key_keep, pair_keep)``.
+
+    ``(B|1, 1, 1, K)`` becomes a ``[B, K]`` byte view (``key_keep``),
+    ``(B|1, 1, Q, K)`` a ``[B, Q, K]`` byte view (``pair_keep``).  A batch
+    dimension of 1 is broadcast with stride 0.  ``None`` means no mask.
+    """
+    if attention_mask is None:
+        return None, None
+    keep = normalize_keep_mask(attention_mask)
+    if keep.ndim != 4:
+        raise ValueError(f"attention_mask must be rank-4 [B,1,Q,K]; got shape={tuple(keep.shape)}")
+    if keep.shape[1] != 1:
+        raise ValueError(f"attention_mask must have a singleton head dim [B,1,Q,K]; got shape={tuple(keep.shape)}")
+    if keep.shape[0] not in (1, batch) or keep.shape[-1] != key_len or keep.shape[-2] not in (1, query_len):
+        raise ValueError(
+            f"attention_mask shape {tuple(keep.shape)} does not broadcast to (B={batch},1,Q={query_len},K={key_len})"
+        )
+    if query_len != key_len:
+        raise ValueError("masked attention needs query_len == key_len (query liveness is read from the mask)")
+    bytes_ = keep.view(torch.uint8) if keep.dtype == torch.bool else keep.to(torch.uint8)
+    if keep.shape[-2] == 1:
+        kk = bytes_[:, 0, 0, :]
+        if kk.stride(-1) != 1:
+            kk = kk.contiguous()
+        return kk.expand(batch, key_len), None
+    pk = bytes_[:, 0, :, :]
+    if pk.stride(-1) != 1:
+        pk = pk.contiguous()
+    return None, pk.expand(batch, query_len, key_len)

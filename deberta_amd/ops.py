@@ -1,0 +1,284 @@
+"""torch.library custom ops over the HIP kernels of ``libdsa.so``.
+
+``deberta_amd::dsa_fwd`` and ``deberta_amd::dsa_bwd`` are functional (they
+allocate their outputs and mutate nothing), carry fake-tensor
+implementations for ``torch.compile``, and are linked by
+``register_autograd``.  They have a CUDA/HIP implementation only: called on
+CPU tensors they raise, there is no fallback.
+
+Tensor layouts (see include/dsa.h):
+  q, k, v           [B, L, H, D] views, head dim contiguous
+  kr, qr            [H, 2A, D] views (projected relative tables) or None
+  rel_table         int32 [Lq + Lk - 1]: relative position of offset i - j at
+                    index (i - j) + (Lk - 1)
+  key_keep          uint8 [B, Lk] or None  (broadcast keep mask)
+  pair_keep         uint8 [B, Lq, Lk] or None (pairwise keep mask)
+  out               [B, Lq, H, D] contiguous, dtype of q
+  lse               float32 [B, H, Lq]
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+from torch import Tensor
+
+from deberta_amd import _lib
+
+_DTYPES = {torch.float32: _lib.DSA_F32, torch.bfloat16: _lib.DSA_BF16}
+
+
+def _ptr(t: Optional[Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _strides3(t: Tensor) -> tuple[int, int, int]:
+    s = t.stride()
+    return (s[0], s[1], s[2])
+
+
+def _vec(dtype: torch.dtype) -> int:
+    return 16 // (2 if dtype == torch.bfloat16 else 4)
+
+
+def _kernel_ready(t: Tensor) -> Tensor:
+    """Return ``t`` if the kernels can read it in place (head dim contiguous,
+    16-byte aligned rows), else a contiguous copy."""
+    vec = _vec(t.dtype)
+    ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all(s % vec == 0 for s in t.stride()[:-1])
+    return t if ok else t.contiguous()
+
+
+def _flags(kr: Optional[Tensor], qr: Optional[Tensor]) -> int:
+    return (_lib.DSA_C2P if kr is not None else 0) | (_lib.DSA_P2C if qr is not None else 0)
+
+
+def _fill_fwd_args(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    kr: Optional[Tensor],
+    qr: Optional[Tensor],
+    rel_table: Optional[Tensor],
+    key_keep: Optional[Tensor],
+    pair_keep: Optional[Tensor],
+    out: Tensor,
+    lse: Tensor,
+    att_span: int,
+    scale: float,
+) -> _lib.DsaFwdArgs:
+    B, Lq, H, D = q.shape
+    Lk = k.shape[1]
+    a = _lib.DsaFwdArgs()
+    a.q, a.k, a.v = q.data_ptr(), k.data_ptr(), v.data_ptr()
+    a.kr, a.qr = _ptr(kr), _ptr(qr)
+    a.rel_table = _ptr(rel_table)
+    a.key_keep, a.pair_keep = _ptr(key_keep), _ptr(pair_keep)
+    a.out, a.lse = out.data_ptr(), lse.data_ptr()
+    a.q_strides[:] = _strides3(q)
+    a.k_strides[:] = _strides3(k)
+    a.v_strides[:] = _strides3(v)
+    a.o_strides[:] = _strides3(out)
+    if kr is not None:
+        a.kr_strides[:] = (kr.stride(0), kr.stride(1))
+    if qr is not None:
+        a.qr_strides[:] = (qr.stride(0), qr.stride(1))
+    if key_keep is not None:
+        a.key_keep_stride_b = key_keep.stride(0)
+    if pair_keep is not None:
+        a.pair_keep_strides[:] = (pair_keep.stride(0), pair_keep.stride(1))
+    a.B, a.H, a.Lq, a.Lk, a.D = B, H, Lq, Lk, D
+    a.att_span = int(att_span)
+    a.dtype = _DTYPES[q.dtype]
+    a.flags = _flags(kr, qr)
+    a.scale = float(scale)
+    return a
+
+
+def _validate(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    kr: Optional[Tensor],
+    qr: Optional[Tensor],
+    rel_table: Optional[Tensor],
+    key_keep: Optional[Tensor],
+    pair_keep: Optional[Tensor],
+    att_span: int,
+) -> None:
+    if q.dtype not in _DTYPES:
+        raise TypeError(f"dsa: q dtype must be float32 or bfloat16, got {q.dtype}")
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("dsa: q, k, v must be [B, L, H, D]")
+    B, Lq, H, D = q.shape
+    if k.shape[0] != B or k.shape[2:] != (H, D) or v.shape != k.shape:
+        raise ValueError(f"dsa: shape mismatch q={tuple(q.shape)} k={tuple(k.shape)} v={tuple(v.shape)}")
+    if D not in (32, 64):
+        raise ValueError(f"dsa: head dim must be 32 or 64, got {D}")
+    for name, t in (("k", k), ("v", v), ("kr", kr), ("qr", qr)):
+        if t is not None and t.dtype != q.dtype:
+            raise TypeError(f"dsa: {name} dtype {t.dtype} differs from q dtype {q.dtype}")
+    R = 2 * int(att_span)
+    for name, t in (("kr", kr), ("qr", qr)):
+        if t is not None and (t.dim() != 3 or t.shape[0] != H or t.shape[1] != R or t.shape[2] != D):
+            raise ValueError(f"dsa: {name} must be [H={H}, 2A={R}, D={D}], got {tuple(t.shape)}")
+    if (kr is not None or qr is not None) and (rel_table is None or rel_table.numel() != Lq + k.shape[1] - 1):
+        raise ValueError("dsa: rel_table of Lq + Lk - 1 entries is required with relative tables")
+    if key_keep is not None and pair_keep is not None:
+        raise ValueError("dsa: give at most one of key_keep and pair_keep")
+
+
+@torch.library.custom_op("deberta_amd::dsa_fwd", mutates_args=(), device_types="cuda")
+def dsa_fwd(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    kr: Optional[Tensor],
+    qr: Optional[Tensor],
+    rel_table: Optional[Tensor],
+    key_keep: Optional[Tensor],
+    pair_keep: Optional[Tensor],
+    att_span: int,
+    scale: float,
+) -> tuple[Tensor, Tensor]:
+    _validate(q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span)
+    q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
+    kr = None if kr is None else _kernel_ready(kr)
+    qr = None if qr is None else _kernel_ready(qr)
+    B, Lq, H, D = q.shape
+    out = torch.empty((B, Lq, H, D), dtype=q.dtype, device=q.device)
+    lse = torch.empty((B, H, Lq), dtype=torch.float32, device=q.device)
+    args = _fill_fwd_args(q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, att_span, scale)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(q.device).cuda_stream
+    _lib.check(lib.dsa_fwd(ctypes.byref(args), ctypes.c_void_p(stream)), "dsa_fwd")
+    return out, lse
+
+
+@dsa_fwd.register_fake
+def _dsa_fwd_fake(q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, scale):
+    B, Lq, H, D = q.shape
+    out = q.new_empty((B, Lq, H, D))
+    lse = q.new_empty((B, H, Lq), dtype=torch.float32)
+    return out, lse
+
+
+def bwd_workspace_bytes(args: _lib.DsaBwdArgs) -> int:
+    return int(_lib.load().dsa_bwd_workspace_bytes(ctypes.byref(args)))
+
+
+def fill_bwd_args(
+    dout: Tensor,
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    kr: Optional[Tensor],
+    qr: Optional[Tensor],
+    rel_table: Optional[Tensor],
+    key_keep: Optional[Tensor],
+    pair_keep: Optional[Tensor],
+    out: Tensor,
+    lse: Tensor,
+    att_span: int,
+    scale: float,
+    dq: Tensor,
+    dk: Tensor,
+    dv: Tensor,
+    dkr: Optional[Tensor],
+    dqr: Optional[Tensor],
+) -> _lib.DsaBwdArgs:
+    a = _lib.DsaBwdArgs()
+    a.fwd = _fill_fwd_args(q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, att_span, scale)
+    a.dout = dout.data_ptr()
+    a.do_strides[:] = _strides3(dout)
+    a.dq, a.dk, a.dv = dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
+    a.dq_strides[:] = _strides3(dq)
+    a.dk_strides[:] = _strides3(dk)
+    a.dv_strides[:] = _strides3(dv)
+    a.dkr, a.dqr = _ptr(dkr), _ptr(dqr)
+    a.stages = 0
+    return a
+
+
+@torch.library.custom_op("deberta_amd::dsa_bwd", mutates_args=(), device_types="cuda")
+def dsa_bwd(
+    dout: Tensor,
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    kr: Optional[Tensor],
+    qr: Optional[Tensor],
+    rel_table: Optional[Tensor],
+    key_keep: Optional[Tensor],
+    pair_keep: Optional[Tensor],
+    out: Tensor,
+    lse: Tensor,
+    att_span: int,
+    scale: float,
+) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Gradients (dq, dk, dv, dkr, dqr).  dkr/dqr are float32 [H, 2A, D]
+    (empty when the matching table is None)."""
+    q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
+    kr = None if kr is None else _kernel_ready(kr)
+    qr = None if qr is None else _kernel_ready(qr)
+    dout = _kernel_ready(dout.to(q.dtype))
+    out = _kernel_ready(out)
+    B, Lq, H, D = q.shape
+    R = 2 * int(att_span)
+    dq = torch.empty_like(q, memory_format=torch.contiguous_format)
+    dk = torch.empty_like(k, memory_format=torch.contiguous_format)
+    dv = torch.empty_like(v, memory_format=torch.contiguous_format)
+    f32 = dict(dtype=torch.float32, device=q.device)
+    dkr = torch.zeros((H, R, D), **f32) if kr is not None else torch.empty((0,), **f32)
+    dqr = torch.zeros((H, R, D), **f32) if qr is not None else torch.empty((0,), **f32)
+    args = fill_bwd_args(
+        dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, att_span, scale,
+        dq, dk, dv, dkr if kr is not None else None, dqr if qr is not None else None,
+    )
+    ws = torch.empty((max(bwd_workspace_bytes(args), 16),), dtype=torch.uint8, device=q.device)
+    args.workspace = ws.data_ptr()
+    args.workspace_bytes = ws.numel()
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(q.device).cuda_stream
+    _lib.check(lib.dsa_bwd(ctypes.byref(args), ctypes.c_void_p(stream)), "dsa_bwd")
+    return dq, dk, dv, dkr, dqr
+
+
+@dsa_bwd.register_fake
+def _dsa_bwd_fake(dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, att_span, scale):
+    H, D = q.shape[2], q.shape[3]
+    R = 2 * int(att_span)
+    f32 = dict(dtype=torch.float32)
+    dkr = q.new_empty((H, R, D), **f32) if kr is not None else q.new_empty((0,), **f32)
+    dqr = q.new_empty((H, R, D), **f32) if qr is not None else q.new_empty((0,), **f32)
+    return (
+        q.new_empty(q.shape),
+        k.new_empty(k.shape),
+        v.new_empty(v.shape),
+        dkr,
+        dqr,
+    )
+
+
+def _setup_context(ctx, inputs, output):
+    q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, scale = inputs
+    out, lse = output
+    ctx.mark_non_differentiable(lse)
+    ctx.save_for_backward(q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse)
+    ctx.att_span = att_span
+    ctx.scale = scale
+
+
+def _backward(ctx, dout, dlse):
+    q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse = ctx.saved_tensors
+    dq, dk, dv, dkr, dqr = dsa_bwd(
+        dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, ctx.att_span, ctx.scale
+    )
+    gkr = dkr.to(kr.dtype) if kr is not None else None
+    gqr = dqr.to(qr.dtype) if qr is not None else None
+    return dq, dk, dv, gkr, gqr, None, None, None, None, None
+
+
+torch.library.register_autograd("deberta_amd::dsa_fwd", _backward, setup_context=_setup_context)

@@ -1,0 +1,133 @@
+/*
+ * dsa.h — C ABI of the fused disentangled self-attention library (libdsa.so).
+ *
+ * The library replaces the eager ATen op chain of the reference's
+ * DisentangledSelfAttention (pszemraj/deberta):
+ *   forward   src/deberta/modeling/deberta_v2_native.py:564-652
+ *   bias      src/deberta/modeling/deberta_v2_native.py:349-562 (c2p/p2c terms)
+ *   rel ids   src/deberta/modeling/deberta_v2_native.py:51-112, 235-271
+ *   mask      src/deberta/modeling/mask_utils.py:8-32
+ * and the autograd graph ATen records for it (the reference has no custom
+ * backward).  The reference is pure Python, so there is no FFI in it to bind
+ * to: the caller of these entry points is the torch.library custom op in
+ * deberta_amd/ops.py (via ctypes), which keeps the reference's Python call
+ * surface.
+ *
+ * Conventions
+ *   - Ownership: the caller allocates and owns every buffer.  The library
+ *     never allocates or frees device memory and keeps no tensor state.
+ *   - Streams: all work is enqueued on `stream` (hipStream_t passed as void*),
+ *     with no implicit device synchronisation.  Calls are re-entrant.
+ *   - Errors: a nonzero return code means nothing was launched (argument
+ *     error) or the launch failed; dsa_last_error() returns a thread-local
+ *     message describing it.
+ *   - Layouts: q/k/v/out/dq/dk/dv are [B, L, H, D] with element strides
+ *     (b, l, h) given explicitly and the D axis contiguous (stride 1).  This is
+ *     the natural view of a Linear output [B, L, H*D], so no permute copies
+ *     are needed.  kr/qr (projected relative tables) are [H, R, D] with
+ *     strides (h, r) and D contiguous; R = 2*att_span.
+ *   - Relative positions: `rel_table` holds the (already bucketed) relative
+ *     position of every query/key offset, rel_table[(i - j) + (Lk - 1)] for
+ *     i - j in [-(Lk-1), Lq-1]: the reference's relative_pos matrix is a
+ *     Toeplitz matrix (it depends on i - j only), and this is its first
+ *     column and row.  The kernels derive the c2p row clamp(clamp(t,-A,A)+A,
+ *     0, 2A-1) and the p2c row clamp(-clamp(t,-A,A)+A, 0, 2A-1) in registers
+ *     (deberta_v2_native.py:377, 395, 407).
+ *   - Masks: key_keep is a [B, Lk] byte mask (nonzero = keep) for the
+ *     reference's broadcast (B,1,1,S) keep mask; pair_keep is a [B, Lq, Lk]
+ *     byte mask for the pairwise (B,1,S,S) form.  At most one may be given.
+ *     A zero batch stride broadcasts one mask over the batch.  Query liveness
+ *     follows the reference (deberta_v2_native.py:625-639): key_keep[b,i]
+ *     for the broadcast form, pair_keep[b,i,i] for the pairwise form; dead
+ *     query rows produce exactly zero output and zero gradient.
+ */
+#ifndef DSA_H_
+#define DSA_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element types */
+enum { DSA_F32 = 0, DSA_BF16 = 1 };
+
+/* score terms (deberta_v2_native.py:592-598, pos_att_type) */
+enum { DSA_C2P = 1, DSA_P2C = 2 };
+
+/* backward stages, for dsa_bwd_args.stages (0 means all) */
+enum { DSA_STAGE_PREP = 1, DSA_STAGE_DQ = 2, DSA_STAGE_DKDV = 4 };
+
+typedef struct dsa_fwd_args {
+  const void* q;          /* [B, Lq, H, D] */
+  const void* k;          /* [B, Lk, H, D] */
+  const void* v;          /* [B, Lk, H, D] */
+  const void* kr;         /* [H, R, D] pos-key table (c2p), NULL if !C2P */
+  const void* qr;         /* [H, R, D] pos-query table (p2c), NULL if !P2C */
+  const int32_t* rel_table; /* [Lq + Lk - 1], required when flags != 0 */
+  const uint8_t* key_keep;  /* [B, Lk] or NULL */
+  const uint8_t* pair_keep; /* [B, Lq, Lk] or NULL */
+  void* out;              /* [B, Lq, H, D], same dtype as q */
+  float* lse;             /* [B, H, Lq] contiguous, natural-log logsumexp */
+  int64_t q_strides[3];   /* element strides of b, l, h */
+  int64_t k_strides[3];
+  int64_t v_strides[3];
+  int64_t o_strides[3];
+  int64_t kr_strides[2];  /* element strides of h, r */
+  int64_t qr_strides[2];
+  int64_t key_keep_stride_b;
+  int64_t pair_keep_strides[2]; /* b, q (k contiguous) */
+  int32_t B, H, Lq, Lk, D;
+  int32_t att_span;       /* A; R = 2A rows in kr/qr */
+  int32_t dtype;          /* DSA_F32 or DSA_BF16 */
+  int32_t flags;          /* DSA_C2P | DSA_P2C */
+  float scale;            /* 1/sqrt(D * scale_factor) */
+} dsa_fwd_args;
+
+typedef struct dsa_bwd_args {
+  /* forward inputs, exactly as passed to dsa_fwd */
+  dsa_fwd_args fwd;
+  const void* dout;       /* [B, Lq, H, D] upstream gradient */
+  int64_t do_strides[3];
+  /* outputs; gradient strides follow the [B, L, H, D] convention */
+  void* dq;               /* [B, Lq, H, D], dtype of q */
+  void* dk;               /* [B, Lk, H, D] */
+  void* dv;               /* [B, Lk, H, D] */
+  int64_t dq_strides[3];
+  int64_t dk_strides[3];
+  int64_t dv_strides[3];
+  float* dkr;             /* [H, R, D] fp32 contiguous, accumulated (+=); NULL if !C2P */
+  float* dqr;             /* [H, R, D] fp32 contiguous, accumulated (+=); NULL if !P2C */
+  /* workspace: dsa_bwd_workspace_bytes() bytes, caller-allocated */
+  void* workspace;
+  size_t workspace_bytes;
+  int32_t stages;         /* DSA_STAGE_* mask; 0 = all */
+} dsa_bwd_args;
+
+/* Forward: out = softmax(mask((QK^T + c2p + p2c) * scale)) V and its
+ * logsumexp.  Replaces DisentangledSelfAttention.forward's score/softmax/PV
+ * chain (deberta_v2_native.py:592-652). */
+int dsa_fwd(const dsa_fwd_args* args, void* stream);
+
+/* Backward of dsa_fwd: dq, dk, dv and the gradients of the projected
+ * relative tables (dkr, dqr, accumulated into fp32 buffers the caller has
+ * zeroed).  Replaces ATen autograd through deberta_v2_native.py:592-652 and
+ * the einsum/bmm + gather bias path (:349-528). */
+int dsa_bwd(const dsa_bwd_args* args, void* stream);
+
+/* Workspace bytes dsa_bwd needs for these arguments. */
+size_t dsa_bwd_workspace_bytes(const dsa_bwd_args* args);
+
+/* Thread-local description of the last error (empty string if none). */
+const char* dsa_last_error(void);
+
+/* Library version, for the loader's compatibility check. */
+int dsa_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSA_H_ */
