@@ -100,6 +100,17 @@ def main() -> None:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument(
+        "--kernels-only",
+        action="store_true",
+        help="only run each kernel --steps times (for rocprofv3 counter passes); prints per-kernel times",
+    )
+    ap.add_argument(
+        "--copy-probe-mib",
+        type=int,
+        default=0,
+        help="also run a plain device copy of this many MiB (calibrates FETCH_SIZE / WRITE_SIZE)",
+    )
     args = ap.parse_args()
     if args.gpus != 1:
         print(
@@ -132,18 +143,29 @@ def main() -> None:
         out, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, A, scale)
         return torch.autograd.grad(out, leaves, dout)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(args.steps):
-        step()
-    e1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_step = e0.elapsed_time(e1) / args.steps
+    if args.copy_probe_mib:
+        n = args.copy_probe_mib * (1 << 20) // 4
+        src_t = torch.ones(n, dtype=torch.float32, device=dev)
+        dst_t = torch.empty_like(src_t)
+        for _ in range(3):
+            dst_t.copy_(src_t)
+        torch.cuda.synchronize()
+        del src_t, dst_t
+
+    ms_step = wall = float("nan")
+    if not args.kernels_only:
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        ms_step = e0.elapsed_time(e1) / args.steps
     f_fwd = flops_fwd(B, L, H, D, R)
     f_step = 3 * f_fwd
     tflops = f_step / (ms_step * 1e-3) / 1e12
@@ -178,7 +200,7 @@ def main() -> None:
         "bwd_prep": (run_stage(_lib.DSA_STAGE_PREP), 0.0),
     }
     per_kernel = {}
-    n_k = max(10, args.steps)
+    n_k = args.steps if args.kernels_only else max(10, args.steps)
     for name, (fn, fl) in kernels.items():
         for _ in range(3):
             fn()
@@ -193,6 +215,9 @@ def main() -> None:
     dom = max((n for n in per_kernel if kernels[n][1] > 0), key=lambda n: per_kernel[n]["ms"])
     dom_ms = per_kernel[dom]["ms"]
     achieved = kernels[dom][1] / (dom_ms * 1e-3) / 1e12
+    if args.kernels_only:
+        print(json.dumps({"per_kernel": per_kernel}), flush=True)
+        return
 
     res = {
         "metric": METRIC,

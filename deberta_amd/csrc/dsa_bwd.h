@@ -144,12 +144,16 @@ __global__ __launch_bounds__(256, 1) void dsa_bwd_dq_kernel(BwdParams bp) {
   constexpr int QTSTR = BQ + Pad<T>::v;   // Qt: [D][BQ]
   const FwdParams& p = bp.f;
 
+  typedef typename BandType<T>::type BT;
+  constexpr int DBAND = (dcfg::NW * dcfg::CB_ELEMS + dcfg::PB_ELEMS) * (int)sizeof(BT);
+  constexpr int UNI_BYTES = (DBAND > WB * WB_STR * 4) ? DBAND : WB * WB_STR * 4;
   __shared__ __align__(16) T Ks[BK * KSTR];
   __shared__ __align__(16) T Vs[BK * KSTR];
   __shared__ __align__(16) T Kt[BF ? D * KTSTR : 1];
   __shared__ __align__(16) T Qt[BF ? D * QTSTR : 1];
   __shared__ short tbl[TBL];
-  __shared__ __align__(16) float uni[UNION];
+  __shared__ short crow[dcfg::XG], prow[dcfg::XG];
+  __shared__ __align__(16) float uni[UNI_BYTES / 4];
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, g = l >> 4, c16 = l & 15;
@@ -157,7 +161,8 @@ __global__ __launch_bounds__(256, 1) void dsa_bwd_dq_kernel(BwdParams bp) {
   const int Lq = p.Lq, Lk = p.Lk, A = p.A, R = 2 * A;
   const int i0 = qt * BQ;
   const int iw = i0 + w * WQ;
-  float* scr = uni + w * SCR;
+  BT* cbw = reinterpret_cast<BT*>(uni) + w * dcfg::CB_ELEMS;
+  BT* pbs = reinterpret_cast<BT*>(uni) + dcfg::NW * dcfg::CB_ELEMS;
   float* band = uni;
 
   const T* qbase = (const T*)p.q + (int64_t)b * p.qs[0] + (int64_t)h * p.qs[2];
@@ -242,17 +247,31 @@ __global__ __launch_bounds__(256, 1) void dsa_bwd_dq_kernel(BwdParams bp) {
     __syncthreads();
     load_rows<T, D, BK, 256>(Ks, KSTR, BF ? Kt : nullptr, KTSTR, kbase, p.ks[1], j0, Lk, tid);
     load_rows<T, D, BK, 256>(Vs, KSTR, nullptr, 0, vbase, p.vs[1], j0, Lk, tid);
-    if (p.flags) load_rel_window(tbl, p.rel, i0 - j0 - (BK - 1), BQ + BK - 1, Lq, Lk, A, tid, 256);
+    if (p.flags) {
+      load_rel_window(tbl, p.rel, i0 - j0 - (BK - 1), BQ + BK - 1, Lq, Lk, A, tid, 256);
+      load_row_tables(crow, prow, p.rel, i0, j0, Lq, Lk, A, tid);
+    }
     __syncthreads();
 
-    // ---- recompute scores ----------------------------------------------------
+    // ---- recompute scores (log2 domain, as the forward) ------------------------
     frag kf[4][NS];
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
       for (int s = 0; s < NS; ++s) kf[jb][s] = M::load_contig(&Ks[(16 * jb + c16) * KSTR], s, g);
     f32x4 st[2][4];
-    score_tile_T<T, D>(st, kf, qf, scr, tbl, w * WQ, l, g, c16, krh, p.krs[1], qrh, p.qrs[1], A, p.flags);
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+      for (int ib = 0; ib < 2; ++ib) {
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int s = 0; s < NS; ++s) acc = M::mma(kf[jb][s], qf[ib][s], acc);
+        st[ib][jb] = acc * sl2;
+      }
+    if (p.flags)
+      add_delta_bands_T<T, D>(st, kf, qf, cbw, pbs, crow, prow, w, g, c16, krh, p.krs[1], qrh, p.qrs[1], p.flags,
+                              sl2);
 
     // ---- P^T, dP^T, dS^T -----------------------------------------------------
     f32x4 ds[2][4];
@@ -273,7 +292,7 @@ __global__ __launch_bounds__(256, 1) void dsa_bwd_dq_kernel(BwdParams bp) {
           bool keep = ilive[ib] && j < Lk;
           if (MASK == MASK_KEY) keep = keep && kkb[j] != 0;
           if (MASK == MASK_PAIR) keep = keep && pkb[(int64_t)i * p.pkq + j] != 0;
-          const float pe = keep ? exp2f(st[ib][jb][e] * sl2 - lse2[ib]) : 0.f;
+          const float pe = keep ? exp2f(st[ib][jb][e] - lse2[ib]) : 0.f;
           ds[ib][jb][e] = pe * (dp[e] - dlt[ib]);
         }
       }
@@ -739,19 +758,29 @@ __global__ __launch_bounds__(256, 1) void dsa_bwd_dkdv_kernel(BwdParams bp) {
 // ===========================================================================
 template <typename T, int D>
 __global__ __launch_bounds__(256) void dsa_bwd_delta_kernel(BwdParams bp) {
+  // D / VEC lanes per row, one 16-byte load each, then a butterfly sum.
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr int LPR = D / VEC;
+  typedef T vecT __attribute__((ext_vector_type(VEC)));
   const FwdParams& p = bp.f;
   const int64_t n = (int64_t)p.B * p.H * p.Lq;
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= n) return;
-  const int i = (int)(idx % p.Lq);
-  const int h = (int)((idx / p.Lq) % p.H);
-  const int b = (int)(idx / ((int64_t)p.Lq * p.H));
-  const T* o = (const T*)p.out + (int64_t)b * p.os[0] + (int64_t)i * p.os[1] + (int64_t)h * p.os[2];
-  const T* d = (const T*)bp.dout + (int64_t)b * bp.dos[0] + (int64_t)i * bp.dos[1] + (int64_t)h * bp.dos[2];
+  const int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) / LPR;
+  const int part = threadIdx.x % LPR;
   float acc = 0.f;
-#pragma unroll 8
-  for (int e = 0; e < D; ++e) acc += (float)o[e] * (float)d[e];
-  bp.delta[idx] = acc;
+  if (row < n) {
+    const int i = (int)(row % p.Lq);
+    const int h = (int)((row / p.Lq) % p.H);
+    const int b = (int)(row / ((int64_t)p.Lq * p.H));
+    const T* o = (const T*)p.out + (int64_t)b * p.os[0] + (int64_t)i * p.os[1] + (int64_t)h * p.os[2];
+    const T* d = (const T*)bp.dout + (int64_t)b * bp.dos[0] + (int64_t)i * bp.dos[1] + (int64_t)h * bp.dos[2];
+    const vecT ov = *reinterpret_cast<const vecT*>(o + part * VEC);
+    const vecT dv = *reinterpret_cast<const vecT*>(d + part * VEC);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc += (float)ov[e] * (float)dv[e];
+  }
+#pragma unroll
+  for (int m = LPR / 2; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);
+  if (row < n && part == 0) bp.delta[row] = acc;
 }
 
 // dst[h, d, r] = src[h, r, d] for r < R, 0 for R <= r < Rpad

@@ -115,7 +115,7 @@ int launch_check(const char* what) {
 
 template <typename T, int D, int MASK>
 int launch_fwd(const dsa::FwdParams& p, hipStream_t st) {
-  dim3 grid((p.Lq + dsa::fwdcfg::BQ - 1) / dsa::fwdcfg::BQ, p.H, p.B);
+  dim3 grid((p.Lq + dsa::dcfg::BQ - 1) / dsa::dcfg::BQ, p.H, p.B);
   hipLaunchKernelGGL((dsa::dsa_fwd_kernel<T, D, MASK>), grid, dim3(256), 0, st, p);
   return launch_check("dsa_fwd_kernel");
 }
@@ -177,7 +177,7 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
   const int R = 2 * f.att_span;
 
   if (stages & DSA_STAGE_PREP) {
-    const int64_t n = (int64_t)f.B * f.H * f.Lq;
+    const int64_t n = (int64_t)f.B * f.H * f.Lq * (D / (16 / (int)sizeof(T)));
     hipLaunchKernelGGL((dsa::dsa_bwd_delta_kernel<T, D>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, bp);
     if (launch_check("dsa_bwd_delta_kernel")) return 1;
     const int64_t nt = (int64_t)f.H * D * ws.Rpad;

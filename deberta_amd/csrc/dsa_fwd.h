@@ -4,42 +4,28 @@
 // owns queries [i0 + 32w, i0 + 32w + 32) and streams 64-key tiles:
 //
 //   S^T = K Q^T                      MFMA, K tile from LDS, Q^T in registers
-//   S^T += c2p gather                band MFMA  Kr[cmin..cmax] Q^T  -> LDS -> gather
-//   S^T += p2c gather                band MFMA  K Qr[pmin..pmax]^T  -> LDS -> gather
+//   + c2p band (per wave)            MFMA  Kr[c(x)] Q^T  -> LDS (fp16) -> gather
+//   + p2c band (per workgroup)       MFMA  K Qr[p(x)]^T  -> LDS (fp16) -> gather
 //   mask, online softmax (exp2)      fp32, per query column
 //   O^T += V^T P^T                   MFMA, P fed from registers (ACC k-set)
 //
 // The score tile is kept transposed (keys down, queries across) so that the
 // probabilities a lane holds are already the B operand of the PV product.
-//
-// Relative bands: the c2p row of (i, j) is c(i - j), a non-decreasing function
-// of i - j with unit steps for the reference's log buckets, so the rows a tile
-// touches form the contiguous range [c(min), c(max)] of the Kr table.  The
-// band product computes exactly those rows (about one 32x64 tile's worth of
-// MFMA work on average at L=512, buckets 256) and the gather reads the
-// result back from LDS at row c(i - j) - cmin.  The range is found by a
-// min/max scan, so any Toeplitz relative-position table is handled; bands
-// wider than BAND rows are processed in chunks.
+// The relative terms are computed per query/key offset x = i - j (see
+// add_delta_bands_T): every score element reads its band value at a
+// compile-time offset from a per-lane base.
 #pragma once
 
 #include "dsa_tiles.h"
 
 namespace dsa {
 
-namespace fwdcfg {
-constexpr int NW = 4;        // waves per workgroup
-constexpr int WQ = 32;       // queries per wave
-constexpr int BQ = NW * WQ;  // queries per workgroup
-constexpr int BK = 64;       // keys per tile
-constexpr int SCR = 64 * (tilecfg::BAND + 1);  // per-wave band scratch (floats)
-constexpr int TBL = BQ + BK;      // relative-position window per tile
-}  // namespace fwdcfg
-
 template <typename T, int D, int MASK>
-__global__ __launch_bounds__(256, 1) void dsa_fwd_kernel(FwdParams p) {
-  using namespace fwdcfg;
+__global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
+  using namespace dcfg;
   using M = Mfma<T>;
   typedef typename M::frag frag;
+  typedef typename BandType<T>::type BT;
   constexpr int NS = D / M::KSTEP;        // k steps over the head dim
   constexpr int KSTR = D + Pad<T>::v;      // Ks row stride
   constexpr int VSTR = BK + Pad<T>::v;     // Vt row stride
@@ -48,16 +34,17 @@ __global__ __launch_bounds__(256, 1) void dsa_fwd_kernel(FwdParams p) {
 
   __shared__ __align__(16) T Ks[BK * KSTR];
   __shared__ __align__(16) T Vt[D * VSTR];
-  __shared__ short tbl[TBL];
-  __shared__ float scr_all[NW * SCR];
+  __shared__ short crow[XG], prow[XG];
+  __shared__ __align__(16) BT cb_all[NW * CB_ELEMS];
+  __shared__ __align__(16) BT pb[PB_ELEMS];
 
   const int tid = threadIdx.x;
-  const int w = tid >> 6, l = tid & 63, g = l >> 4, c16 = l & 15;
+  const int w = tid >> 6, g = (tid & 63) >> 4, c16 = tid & 15;
   const int qt = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int Lq = p.Lq, Lk = p.Lk, A = p.A;
   const int i0 = qt * BQ;
   const int iw = i0 + w * WQ;
-  float* scr = scr_all + w * SCR;
+  BT* cb = cb_all + w * CB_ELEMS;
 
   const T* qbase = (const T*)p.q + (int64_t)b * p.qs[0] + (int64_t)h * p.qs[2];
   const T* kbase = (const T*)p.k + (int64_t)b * p.ks[0] + (int64_t)h * p.ks[2];
@@ -132,17 +119,28 @@ __global__ __launch_bounds__(256, 1) void dsa_fwd_kernel(FwdParams p) {
     __syncthreads();  // previous tile's LDS reads are done
     load_rows<T, D, BK, 256>(Ks, KSTR, nullptr, 0, kbase, p.ks[1], j0, Lk, tid);
     load_rows<T, D, BK, 256>(nullptr, 0, Vt, VSTR, vbase, p.vs[1], j0, Lk, tid);
-    if (p.flags) load_rel_window(tbl, p.rel, i0 - j0 - (BK - 1), BQ + BK - 1, Lq, Lk, A, tid, 256);
+    if (p.flags) load_row_tables(crow, prow, p.rel, i0, j0, Lq, Lk, A, tid);
     __syncthreads();
 
-    // ---- S^T = K Q^T + c2p + p2c ------------------------------------------
+    // ---- y = (K Q^T) * scale*log2e + c2p + p2c -----------------------------
     frag kf[4][NS];
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
       for (int s = 0; s < NS; ++s) kf[jb][s] = M::load_contig(&Ks[(16 * jb + c16) * KSTR], s, g);
     f32x4 st[2][4];
-    score_tile_T<T, D>(st, kf, qf, scr, tbl, w * WQ, l, g, c16, krh, p.krs[1], qrh, p.qrs[1], A, p.flags);
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+      for (int ib = 0; ib < 2; ++ib) {
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int s = 0; s < NS; ++s) acc = M::mma(kf[jb][s], qf[ib][s], acc);
+        st[ib][jb] = acc * sl2;
+      }
+    if (p.flags)
+      add_delta_bands_T<T, D>(st, kf, qf, cb, pb, crow, prow, w, g, c16, krh, p.krs[1], qrh, p.qrs[1], p.flags,
+                              sl2);
 
     // ---- mask + online softmax (log2 domain) --------------------------------
 #pragma unroll
@@ -166,7 +164,7 @@ __global__ __launch_bounds__(256, 1) void dsa_fwd_kernel(FwdParams p) {
           bool keep = ilive[ib] && j < Lk;
           if (MASK == MASK_KEY) keep = keep && kkb[j] != 0;
           if (MASK == MASK_PAIR) keep = keep && ((pk4 >> e) & 1u);
-          const float y = keep ? st[ib][jb][e] * sl2 : -INFINITY;
+          const float y = keep ? st[ib][jb][e] : -INFINITY;
           st[ib][jb][e] = y;
           mt = fmaxf(mt, y);
         }

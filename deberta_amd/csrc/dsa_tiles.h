@@ -209,6 +209,144 @@ DSA_DEV void score_tile_T(f32x4 (&st)[2][4], const typename Mfma<T>::frag (&kf)[
 }
 
 // ---------------------------------------------------------------------------
+// Offset-indexed ("delta") bands.
+//
+// For a 128-query x 64-key tile the offsets i - j span a window of 191
+// values; x = (i - i0) - (j - j0) + 63 indexes it.  Instead of computing the
+// relative products per table row and looking the row up per score element,
+// the bands are computed per offset: row x of the c2p band is
+// q_i . Kr[c(x)], row x of the p2c band is k_j . Qr[p(x)], with the table
+// rows gathered when the MFMA operands are loaded.  The score element (i, j)
+// then reads band row x(i, j), whose LDS offset is a compile-time constant
+// plus a per-lane base: no per-element table lookups or bounds checks.
+//   c2p: per wave, rows x in [32w, 32w + 96) x the wave's 32 queries
+//   p2c: per workgroup, rows x in [0, 192) x the 64 keys, shared by all waves
+// Band values are stored pre-multiplied by scale*log2(e) (the softmax's
+// log2-domain scale), in fp16 for bf16 inputs (saturated to the fp16 range)
+// and in fp32 for fp32 inputs.
+// ---------------------------------------------------------------------------
+template <typename T>
+struct BandType {
+  typedef float type;
+};
+template <>
+struct BandType<bf16> {
+  typedef _Float16 type;
+};
+
+template <typename B>
+DSA_DEV B to_band(float x) {
+  if constexpr (sizeof(B) == 2) {
+    x = fminf(fmaxf(x, -65504.f), 65504.f);
+  }
+  return (B)x;
+}
+
+namespace dcfg {
+constexpr int WQ = 32;          // queries per wave
+constexpr int BK = 64;          // keys per tile
+constexpr int NW = 4;           // waves per workgroup
+constexpr int BQ = NW * WQ;     // queries per workgroup
+constexpr int XW = WQ + BK;     // c2p band rows per wave (95 used)
+constexpr int XG = BQ + BK;     // p2c band rows per workgroup (191 used)
+constexpr int CBS = WQ + 1;     // c2p band row stride
+constexpr int PBS = XG + 5;     // p2c band row stride (4*PBS - 4 = 16 mod 64: 4 lane groups, distinct banks)
+constexpr int CB_ELEMS = XW * CBS;
+constexpr int PB_ELEMS = BK * PBS;
+}  // namespace dcfg
+
+// Row tables of one tile: crow[x] / prow[x] are the c2p / p2c table rows of
+// offset x (x = (i - i0) - (j - j0) + 63, i0 / j0 the tile's first query /
+// key), for x in [0, 192).
+DSA_DEV void load_row_tables(short* crow, short* prow, const int32_t* rel, int i0, int j0, int Lq, int Lk, int A,
+                             int tid) {
+  if (tid < dcfg::XG) {
+    int d = i0 - j0 - (dcfg::BK - 1) + tid;
+    d = min(max(d, -(Lk - 1)), Lq - 1);
+    int t = rel[d + Lk - 1];
+    t = min(max(t, -A), A);
+    crow[tid] = (short)c2p_row(t, A);
+    prow[tid] = (short)p2c_row(t, A);
+  }
+}
+
+// Adds the scaled c2p + p2c terms to a transposed score tile (keys down,
+// queries across; y[ib][jb][e] = key 16*jb + 4*g + e, query 32*w + 16*ib +
+// c16 of the tile).  y must already hold (q.k) * scale*log2(e).
+//   kf: A fragments of the 64 key rows, qf: B fragments of the wave's queries
+//   cb: this wave's c2p band (XW * CBS), pb: the shared p2c band (BK * PBS)
+// Contains one __syncthreads (the p2c band is shared): call it from every
+// thread of the workgroup.
+template <typename T, int D>
+DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&kf)[4][D / Mfma<T>::KSTEP],
+                               const typename Mfma<T>::frag (&qf)[2][D / Mfma<T>::KSTEP],
+                               typename BandType<T>::type* cb, typename BandType<T>::type* pb, const short* crow,
+                               const short* prow, int w, int g, int c16, const T* krh, int64_t krs, const T* qrh,
+                               int64_t qrs, int flags, float sl2) {
+  using M = Mfma<T>;
+  typedef typename M::frag frag;
+  typedef typename BandType<T>::type BT;
+  using namespace dcfg;
+  constexpr int NS = D / M::KSTEP;
+  if (flags & 1) {
+#pragma unroll
+    for (int rb = 0; rb < XW / 16; ++rb) {
+      const int row = crow[WQ * w + 16 * rb + c16];
+      frag af[NS];
+#pragma unroll
+      for (int s = 0; s < NS; ++s) af[s] = M::load_contig(krh + (int64_t)row * krs, s, g);
+#pragma unroll
+      for (int ib = 0; ib < 2; ++ib) {
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int s = 0; s < NS; ++s) acc = M::mma(af[s], qf[ib][s], acc);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) cb[(16 * rb + 4 * g + e) * CBS + 16 * ib + c16] = to_band<BT>(acc[e] * sl2);
+      }
+    }
+  }
+  if (flags & 2) {
+#pragma unroll
+    for (int t = 0; t < XG / 16 / NW; ++t) {
+      const int xb = w + NW * t;
+      const int row = prow[16 * xb + c16];
+      frag bf[NS];
+#pragma unroll
+      for (int s = 0; s < NS; ++s) bf[s] = M::load_contig(qrh + (int64_t)row * qrs, s, g);
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb) {
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int s = 0; s < NS; ++s) acc = M::mma(kf[jb][s], bf[s], acc);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pb[(16 * jb + 4 * g + e) * PBS + 16 * xb + c16] = to_band<BT>(acc[e] * sl2);
+      }
+    }
+  }
+  __syncthreads();
+  if (flags & 1) {
+    // x - 32w = (16*ib + c16) - (16*jb + 4*g + e) + 63
+    const BT* base = cb + (c16 - 4 * g + 63) * CBS + c16;
+#pragma unroll
+    for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[ib][jb][e] += (float)base[(16 * ib - 16 * jb - e) * CBS + 16 * ib];
+  }
+  if (flags & 2) {
+    // row j = 16*jb + 4*g + e, column x = 32w + (16*ib + c16) - (16*jb + 4*g + e) + 63
+    const BT* base = pb + 4 * g * PBS + WQ * w + c16 - 4 * g + 63;
+#pragma unroll
+    for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[ib][jb][e] += (float)base[(16 * jb + e) * PBS + 16 * ib - 16 * jb - e];
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Score tile in natural orientation (queries down, keys across), 64 queries
 // x 32 keys per wave.  s[jb][ib][e] is query 16*ib + 4*g + e, key
 // 16*jb + c16.
