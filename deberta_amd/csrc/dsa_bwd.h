@@ -128,319 +128,6 @@ DSA_DEV typename Mfma<T>::frag band_col_frag(const float* band, int col, int k0,
 }
 
 // ===========================================================================
-// dQ / dKr kernel
-// ===========================================================================
-template <typename T, int D, int MASK>
-__global__ __launch_bounds__(256, 1) void dsa_bwd_dq_kernel(BwdParams bp) {
-  using namespace bwdcfg;
-  using M = Mfma<T>;
-  typedef typename M::frag frag;
-  constexpr int NS = D / M::KSTEP;
-  constexpr int ND = D / 16;
-  constexpr int BQ = TILE_OWN, BK = TILE_LOOP, WQ = 32;
-  constexpr bool BF = sizeof(T) == 2;
-  constexpr int KSTR = D + Pad<T>::v;
-  constexpr int KTSTR = BK + Pad<T>::v;   // Kt: [D][BK]
-  constexpr int QTSTR = BQ + Pad<T>::v;   // Qt: [D][BQ]
-  const FwdParams& p = bp.f;
-
-  typedef typename BandType<T>::type BT;
-  constexpr int DBAND = (dcfg::NW * dcfg::CB_ELEMS + dcfg::PB_ELEMS) * (int)sizeof(BT);
-  constexpr int UNI_BYTES = (DBAND > WB * WB_STR * 4) ? DBAND : WB * WB_STR * 4;
-  __shared__ __align__(16) T Ks[BK * KSTR];
-  __shared__ __align__(16) T Vs[BK * KSTR];
-  __shared__ __align__(16) T Kt[BF ? D * KTSTR : 1];
-  __shared__ __align__(16) T Qt[BF ? D * QTSTR : 1];
-  __shared__ short tbl[TBL];
-  __shared__ short crow[dcfg::XG], prow[dcfg::XG];
-  __shared__ __align__(16) float uni[UNI_BYTES / 4];
-
-  const int tid = threadIdx.x;
-  const int w = tid >> 6, l = tid & 63, g = l >> 4, c16 = l & 15;
-  const int qt = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int Lq = p.Lq, Lk = p.Lk, A = p.A, R = 2 * A;
-  const int i0 = qt * BQ;
-  const int iw = i0 + w * WQ;
-  BT* cbw = reinterpret_cast<BT*>(uni) + w * dcfg::CB_ELEMS;
-  BT* pbs = reinterpret_cast<BT*>(uni) + dcfg::NW * dcfg::CB_ELEMS;
-  float* band = uni;
-
-  const T* qbase = (const T*)p.q + (int64_t)b * p.qs[0] + (int64_t)h * p.qs[2];
-  const T* kbase = (const T*)p.k + (int64_t)b * p.ks[0] + (int64_t)h * p.ks[2];
-  const T* vbase = (const T*)p.v + (int64_t)b * p.vs[0] + (int64_t)h * p.vs[2];
-  const T* dobase = (const T*)bp.dout + (int64_t)b * bp.dos[0] + (int64_t)h * bp.dos[2];
-  const T* krh = (p.flags & 1) ? (const T*)p.kr + (int64_t)h * p.krs[0] : nullptr;
-  const T* qrh = (p.flags & 2) ? (const T*)p.qr + (int64_t)h * p.qrs[0] : nullptr;
-  const T* krTh = (p.flags & 1) ? (const T*)bp.krT + (int64_t)h * D * bp.Rpad : nullptr;
-  const uint8_t* kkb = (MASK == MASK_KEY) ? p.kk + (int64_t)b * p.kkb : nullptr;
-  const uint8_t* pkb = (MASK == MASK_PAIR) ? p.pk + (int64_t)b * p.pkb : nullptr;
-  const float* lseb = p.lse + ((int64_t)b * p.H + h) * Lq;
-  const float* dltb = bp.delta + ((int64_t)b * p.H + h) * Lq;
-
-  int irow[2];
-  bool ilive[2];
-  float lse2[2], dlt[2];
-  frag qf[2][NS], dof[2][NS];
-#pragma unroll
-  for (int ib = 0; ib < 2; ++ib) {
-    const int i = iw + 16 * ib + c16;
-    irow[ib] = i;
-    const bool valid = i < Lq;
-    bool live = valid;
-    if (MASK == MASK_KEY && valid) live = kkb[i] != 0;
-    if (MASK == MASK_PAIR && valid) live = pkb[(int64_t)i * p.pkq + i] != 0;
-    ilive[ib] = live;
-    lse2[ib] = live ? lseb[i] * kLog2e : INFINITY;
-    dlt[ib] = valid ? dltb[i] : 0.f;
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      qf[ib][s] = valid ? M::load_contig(qbase + (int64_t)i * p.qs[1], s, g) : M::zero();
-      dof[ib][s] = valid ? M::load_contig(dobase + (int64_t)i * bp.dos[1], s, g) : M::zero();
-    }
-  }
-  if constexpr (BF) {
-    if (p.flags & 1) load_rows<T, D, BQ, 256>(nullptr, 0, Qt, QTSTR, qbase, p.qs[1], i0, Lq, tid);
-  }
-
-  f32x4 dqa[ND][2];
-#pragma unroll
-  for (int db = 0; db < ND; ++db) dqa[db][0] = dqa[db][1] = zero4();
-  f32x4 dkra[OWN_SLOTS][ND];
-#pragma unroll
-  for (int k = 0; k < OWN_SLOTS; ++k)
-#pragma unroll
-    for (int db = 0; db < ND; ++db) dkra[k][db] = zero4();
-  uint32_t touched = 0;
-
-  const float sl2 = p.scale * kLog2e;
-  const int nkt = (Lk + BK - 1) / BK;
-
-  int wg_live = 0;
-  if (tid < BQ) {
-    const int i = i0 + tid;
-    if (i < Lq) {
-      if (MASK == MASK_NONE) wg_live = 1;
-      else if (MASK == MASK_KEY) wg_live = kkb[i] != 0;
-      else wg_live = pkb[(int64_t)i * p.pkq + i] != 0;
-    }
-  }
-  const bool any_live = __syncthreads_or(wg_live);
-
-  for (int kt = 0; any_live && kt < nkt; ++kt) {
-    const int j0 = kt * BK;
-    if (MASK == MASK_KEY) {
-      int keep = 0;
-      if (tid < BK) keep = (j0 + tid < Lk) && kkb[j0 + tid];
-      if (!__syncthreads_or(keep)) continue;
-    } else if (MASK == MASK_PAIR) {
-      int keep = 0;
-      const int r = tid >> 1, half = tid & 1;
-      const int i = i0 + r;
-      if (i < Lq) {
-        const uint8_t* row = pkb + (int64_t)i * p.pkq;
-        const int jb0 = j0 + half * (BK / 2);
-        const int jend = min(jb0 + BK / 2, Lk);
-        for (int j = jb0; j < jend; ++j) keep |= row[j];
-      }
-      if (!__syncthreads_or(keep)) continue;
-    }
-    __syncthreads();
-    load_rows<T, D, BK, 256>(Ks, KSTR, BF ? Kt : nullptr, KTSTR, kbase, p.ks[1], j0, Lk, tid);
-    load_rows<T, D, BK, 256>(Vs, KSTR, nullptr, 0, vbase, p.vs[1], j0, Lk, tid);
-    if (p.flags) {
-      load_rel_window(tbl, p.rel, i0 - j0 - (BK - 1), BQ + BK - 1, Lq, Lk, A, tid, 256);
-      load_row_tables(crow, prow, p.rel, i0, j0, Lq, Lk, A, tid);
-    }
-    __syncthreads();
-
-    // ---- recompute scores (log2 domain, as the forward) ------------------------
-    frag kf[4][NS];
-#pragma unroll
-    for (int jb = 0; jb < 4; ++jb)
-#pragma unroll
-      for (int s = 0; s < NS; ++s) kf[jb][s] = M::load_contig(&Ks[(16 * jb + c16) * KSTR], s, g);
-    f32x4 st[2][4];
-#pragma unroll
-    for (int jb = 0; jb < 4; ++jb)
-#pragma unroll
-      for (int ib = 0; ib < 2; ++ib) {
-        f32x4 acc = zero4();
-#pragma unroll
-        for (int s = 0; s < NS; ++s) acc = M::mma(kf[jb][s], qf[ib][s], acc);
-        st[ib][jb] = acc * sl2;
-      }
-    if (p.flags)
-      add_delta_bands_T<T, D>(st, kf, qf, cbw, pbs, crow, prow, w, g, c16, krh, p.krs[1], qrh, p.qrs[1], p.flags,
-                              sl2);
-
-    // ---- P^T, dP^T, dS^T -----------------------------------------------------
-    f32x4 ds[2][4];
-#pragma unroll
-    for (int jb = 0; jb < 4; ++jb) {
-      frag vf[NS];
-#pragma unroll
-      for (int s = 0; s < NS; ++s) vf[s] = M::load_contig(&Vs[(16 * jb + c16) * KSTR], s, g);
-#pragma unroll
-      for (int ib = 0; ib < 2; ++ib) {
-        f32x4 dp = zero4();
-#pragma unroll
-        for (int s = 0; s < NS; ++s) dp = M::mma(vf[s], dof[ib][s], dp);
-        const int i = irow[ib];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int j = j0 + 16 * jb + 4 * g + e;
-          bool keep = ilive[ib] && j < Lk;
-          if (MASK == MASK_KEY) keep = keep && kkb[j] != 0;
-          if (MASK == MASK_PAIR) keep = keep && pkb[(int64_t)i * p.pkq + j] != 0;
-          const float pe = keep ? exp2f(st[ib][jb][e] - lse2[ib]) : 0.f;
-          ds[ib][jb][e] = pe * (dp[e] - dlt[ib]);
-        }
-      }
-    }
-
-    // ---- dQ^T += K^T dS^T ------------------------------------------------------
-#pragma unroll
-    for (int s = 0; s < BK / M::KSTEP; ++s) {
-      frag df[2];
-#pragma unroll
-      for (int ib = 0; ib < 2; ++ib) df[ib] = M::from_acc(ds[ib], s);
-#pragma unroll
-      for (int db = 0; db < ND; ++db) {
-        frag kt_f;
-        if constexpr (BF) kt_f = M::load_acc(&Kt[(16 * db + c16) * KTSTR], s, g);
-        else kt_f = load_col_acc<T>(Ks, KSTR, 16 * db + c16, s * M::KSTEP, g);
-#pragma unroll
-        for (int ib = 0; ib < 2; ++ib) dqa[db][ib] = M::mma(kt_f, df[ib], dqa[db][ib]);
-      }
-    }
-
-    // ---- c2p gradients: dQ += dSc Kr, dKr += dSc^T Q ---------------------------
-    if (p.flags & 1) {
-      int tmin, tmax;
-      wave_rel_range(tbl, 0, BQ + BK - 1, l, tmin, tmax);  // whole workgroup window
-      const int cmin = c2p_row(tmin, A), cmax = c2p_row(tmax, A);
-      int wmin, wmax;
-      wave_rel_range(tbl, w * WQ, WQ + BK - 1, l, wmin, wmax);  // this wave's window
-      const int cwmin = c2p_row(wmin, A), cwmax = c2p_row(wmax, A);
-      for (int cb = cmin; cb <= cmax; cb += WB) {
-        const int nrow = min(WB, cmax - cb + 1);
-        __syncthreads();  // scratch / previous chunk reads are done
-        for (int x = tid; x < nrow * (BQ / 4); x += 256) {
-          reinterpret_cast<f32x4*>(band)[(x / (BQ / 4)) * (WB_STR / 4) + (x % (BQ / 4))] = zero4();
-        }
-        __syncthreads();
-#pragma unroll
-        for (int ib = 0; ib < 2; ++ib)
-#pragma unroll
-          for (int jb = 0; jb < 4; ++jb)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const float v = ds[ib][jb][e];
-              if (v != 0.f) {
-                const int xi = w * WQ + (16 * ib + c16) - (16 * jb + 4 * g + e) + (BK - 1);
-                const int r = c2p_row(tbl[xi], A) - cb;
-                if (r >= 0 && r < nrow) atomicAdd(&band[r * WB_STR + w * WQ + 16 * ib + c16], v);
-              }
-            }
-        __syncthreads();
-        // dQ^T[d, i] += sum_r KrT[d, r] band[r, i] over this wave's rows
-        {
-          const int lo = max(cwmin, cb) - cb, hi = min(cwmax, cb + nrow - 1) - cb;
-          if (lo <= hi) {
-            const int rs0 = ((cb + lo) / M::KSTEP) * M::KSTEP;
-            for (int rs = rs0; rs <= cb + hi; rs += M::KSTEP) {
-              frag bfr[2];
-#pragma unroll
-              for (int ib = 0; ib < 2; ++ib) bfr[ib] = band_col_frag<T>(band, w * WQ + 16 * ib + c16, rs - cb, lo, hi, g);
-#pragma unroll
-              for (int db = 0; db < ND; ++db) {
-                const frag af = M::load_contig(krTh + (int64_t)(16 * db + c16) * bp.Rpad + rs, 0, g);
-#pragma unroll
-                for (int ib = 0; ib < 2; ++ib) dqa[db][ib] = M::mma(af, bfr[ib], dqa[db][ib]);
-              }
-            }
-          }
-        }
-        // dKr[r, d] += sum_i band[r, i] Q[i, d] for the 16-row blocks this wave owns
-        {
-          const int blo = cb >> 4, bhi = (cb + nrow - 1) >> 4;
-          for (int rbg = blo + ((w - blo % NW) + NW) % NW; rbg <= bhi; rbg += NW) {
-            f32x4 res[ND];
-#pragma unroll
-            for (int db = 0; db < ND; ++db) res[db] = zero4();
-            const int row = 16 * rbg + c16 - cb;
-#pragma unroll
-            for (int s = 0; s < BQ / M::KSTEP; ++s) {
-              const frag af = band_row_frag<T>(band, row, nrow, s * M::KSTEP, g);
-#pragma unroll
-              for (int db = 0; db < ND; ++db) {
-                frag qtf;
-                if constexpr (BF) {
-                  qtf = M::load_contig(&Qt[(16 * db + c16) * QTSTR], s, g);
-                } else {
-#pragma unroll
-                  for (int e = 0; e < 4; ++e) {
-                    const int i = i0 + s * M::KSTEP + 4 * g + e;
-                    qtf[e] = (i < Lq) ? qbase[(int64_t)i * p.qs[1] + 16 * db + c16] : 0.f;
-                  }
-                }
-                res[db] = M::mma(af, qtf, res[db]);
-              }
-            }
-            const int slot = rbg / NW;
-            bool held = false;
-#pragma unroll
-            for (int k = 0; k < OWN_SLOTS; ++k) {
-              if (slot == k) {
-#pragma unroll
-                for (int db = 0; db < ND; ++db) dkra[k][db] += res[db];
-                held = true;
-              }
-            }
-            if (held) {
-              touched |= 1u << slot;
-            } else {
-#pragma unroll
-              for (int db = 0; db < ND; ++db) res[db] *= p.scale;
-              atomic_add_block<D>(bp.dkr + (int64_t)h * R * D, R, 16 * rbg, res, g, c16);
-            }
-          }
-        }
-      }
-      __syncthreads();  // band reads done before the next tile reuses scratch
-    }
-  }
-
-  // ---- epilogue ------------------------------------------------------------------
-  T* dqbase = (T*)bp.dq + (int64_t)b * bp.dqs[0] + (int64_t)h * bp.dqs[2];
-#pragma unroll
-  for (int ib = 0; ib < 2; ++ib) {
-    const int i = irow[ib];
-    if (i < Lq) {
-      T* row = dqbase + (int64_t)i * bp.dqs[1];
-#pragma unroll
-      for (int db = 0; db < ND; ++db) {
-        typedef T vec4 __attribute__((ext_vector_type(4)));
-        vec4 v;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = (T)(dqa[db][ib][e] * p.scale);
-        *reinterpret_cast<vec4*>(row + 16 * db + 4 * g) = v;
-      }
-    }
-  }
-  if (p.flags & 1) {
-#pragma unroll
-    for (int k = 0; k < OWN_SLOTS; ++k) {
-      if (touched & (1u << k)) {
-#pragma unroll
-        for (int db = 0; db < ND; ++db) dkra[k][db] *= p.scale;
-        atomic_add_block<D>(bp.dkr + (int64_t)h * R * D, R, 16 * (NW * k + w), dkra[k], g, c16);
-      }
-    }
-  }
-}
-
-// ===========================================================================
 // dK / dV / dQr kernel
 // ===========================================================================
 template <typename T, int D, int MASK>

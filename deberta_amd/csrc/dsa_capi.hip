@@ -10,6 +10,7 @@
 
 #include "../../include/dsa.h"
 #include "dsa_bwd.h"
+#include "dsa_bwd_dq.h"
 #include "dsa_fwd.h"
 
 namespace {
@@ -129,9 +130,58 @@ int fwd_mask(const dsa::FwdParams& p, int mode, hipStream_t st) {
   }
 }
 
+// Occupancy (workgroups per CU) of the dq kernel instance these arguments select.
+template <typename T, int D>
+int dq_occupancy(int mode) {
+  int occ = 0;
+  hipError_t e = hipSuccess;
+  switch (mode) {
+    case dsa::MASK_KEY:
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)dsa::dsa_bwd_dq_kernel<T, D, dsa::MASK_KEY>,
+                                                       256, 0);
+      break;
+    case dsa::MASK_PAIR:
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)dsa::dsa_bwd_dq_kernel<T, D, dsa::MASK_PAIR>,
+                                                       256, 0);
+      break;
+    default:
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)dsa::dsa_bwd_dq_kernel<T, D, dsa::MASK_NONE>,
+                                                       256, 0);
+  }
+  return (e == hipSuccess && occ > 0) ? occ : 1;
+}
+
+int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return 256;
+  return cus;
+}
+
+// Work decomposition of the persistent dq kernel: items (head, batch, query
+// tile) with the head slowest, split into contiguous runs, one per resident
+// workgroup.
+dsa::PersistentPlan dq_plan(const dsa_fwd_args& f, int mode) {
+  dsa::PersistentPlan pl;
+  const int tiles = (f.Lq + dsa::dqcfg::BQ - 1) / dsa::dqcfg::BQ;
+  pl.per_head = f.B * tiles;
+  pl.items = f.H * pl.per_head;
+  int occ = 1;
+  if (f.dtype == DSA_BF16) occ = f.D == 64 ? dq_occupancy<dsa::bf16, 64>(mode) : dq_occupancy<dsa::bf16, 32>(mode);
+  else occ = f.D == 64 ? dq_occupancy<float, 64>(mode) : dq_occupancy<float, 32>(mode);
+  const int slots_avail = device_cus() * occ;
+  pl.grid = pl.items < slots_avail ? pl.items : slots_avail;
+  const int run = (pl.items + pl.grid - 1) / pl.grid;
+  pl.slots = (run + pl.per_head - 1) / pl.per_head + 1;
+  const int R = 2 * f.att_span;
+  pl.prow = R < 512 ? R : 512;
+  return pl;
+}
+
 struct WsLayout {
-  size_t krT, qrT, delta, total;
+  size_t krT, qrT, delta, part_dkr, total;
   int Rpad;
+  dsa::PersistentPlan dq;
 };
 
 WsLayout ws_layout(const dsa_bwd_args* a) {
@@ -139,6 +189,7 @@ WsLayout ws_layout(const dsa_bwd_args* a) {
   WsLayout w;
   const int R = f.flags ? 2 * f.att_span : 0;
   w.Rpad = (int)align_up((size_t)R, 32);
+  w.dq = dq_plan(f, mask_mode(&f));
   const size_t tab = (size_t)f.H * f.D * w.Rpad * elem_bytes(f.dtype);
   size_t off = 0;
   w.krT = off;
@@ -147,6 +198,8 @@ WsLayout ws_layout(const dsa_bwd_args* a) {
   off = align_up(off + ((f.flags & DSA_P2C) ? tab : 0), 256);
   w.delta = off;
   off = align_up(off + (size_t)f.B * f.H * f.Lq * sizeof(float), 256);
+  w.part_dkr = off;
+  if (f.flags & DSA_C2P) off = align_up(off + (size_t)w.dq.grid * w.dq.slots * w.dq.prow * f.D * sizeof(float), 256);
   w.total = off;
   return w;
 }
@@ -193,18 +246,26 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
     }
   }
   if (stages & DSA_STAGE_DQ) {
-    dim3 grid((f.Lq + dsa::bwdcfg::TILE_OWN - 1) / dsa::bwdcfg::TILE_OWN, f.H, f.B);
+    const dsa::PersistentPlan pl = ws.dq;
+    float* part = reinterpret_cast<float*>(base + ws.part_dkr);
+    dim3 grid(pl.grid);
     switch (mode) {
       case dsa::MASK_KEY:
-        hipLaunchKernelGGL((dsa::dsa_bwd_dq_kernel<T, D, dsa::MASK_KEY>), grid, dim3(256), 0, st, bp);
+        hipLaunchKernelGGL((dsa::dsa_bwd_dq_kernel<T, D, dsa::MASK_KEY>), grid, dim3(256), 0, st, bp, pl, part);
         break;
       case dsa::MASK_PAIR:
-        hipLaunchKernelGGL((dsa::dsa_bwd_dq_kernel<T, D, dsa::MASK_PAIR>), grid, dim3(256), 0, st, bp);
+        hipLaunchKernelGGL((dsa::dsa_bwd_dq_kernel<T, D, dsa::MASK_PAIR>), grid, dim3(256), 0, st, bp, pl, part);
         break;
       default:
-        hipLaunchKernelGGL((dsa::dsa_bwd_dq_kernel<T, D, dsa::MASK_NONE>), grid, dim3(256), 0, st, bp);
+        hipLaunchKernelGGL((dsa::dsa_bwd_dq_kernel<T, D, dsa::MASK_NONE>), grid, dim3(256), 0, st, bp, pl, part);
     }
     if (launch_check("dsa_bwd_dq_kernel")) return 1;
+    if (f.flags & DSA_C2P) {
+      const int64_t n = (int64_t)f.H * pl.prow * D;
+      hipLaunchKernelGGL((dsa::dsa_bwd_reduce_kernel<D>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a->dkr,
+                         part, pl, f.H, R);
+      if (launch_check("dsa_bwd_reduce_kernel")) return 1;
+    }
   }
   if (stages & DSA_STAGE_DKDV) {
     dim3 grid((f.Lk + dsa::bwdcfg::TILE_OWN - 1) / dsa::bwdcfg::TILE_OWN, f.H, f.B);

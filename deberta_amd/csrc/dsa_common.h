@@ -156,6 +156,53 @@ DSA_DEV void wave_lds_sync() {
 DSA_DEV int c2p_row(int tc, int A) { return min(max(tc + A, 0), 2 * A - 1); }
 DSA_DEV int p2c_row(int tc, int A) { return min(max(-tc + A, 0), 2 * A - 1); }
 
+// Transposed LDS reads (gfx950 ds_read_b64_tr_b16).  Within each 16-lane
+// group, lane t receives element (t % 4) of the 8-byte chunks addressed by
+// lanes 4*e + t/4 (e = 0..3).  So when lane c16 addresses
+// X[k0 + c16/4][m0 + 4*(c16 % 4)] of a row-major array X, it receives
+// X[k0 + e][m0 + c16] for e = 0..3: four consecutive k of column m0 + c16,
+// i.e. half an MFMA operand fragment of the transposed tile.
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4_tr;
+DSA_DEV bf16x4 tr4(const bf16* X, int str, int k0, int m0, int c16) {
+  const bf16* p = X + (k0 + (c16 >> 2)) * str + m0 + 4 * (c16 & 3);
+  bf16x4_tr v = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4_tr*)p);
+  return __builtin_bit_cast(bf16x4, v);
+}
+DSA_DEV f32x4 tr4(const float* X, int str, int k0, int m0, int c16) {
+  return f32x4{X[k0 * str + m0 + c16], X[(k0 + 1) * str + m0 + c16], X[(k0 + 2) * str + m0 + c16],
+               X[(k0 + 3) * str + m0 + c16]};
+}
+
+// Operand fragment of column m0 + c16 of a row-major LDS array X whose rows
+// are the k index: the CONTIG k-set (k = k0 + 8g + [0..7] for bf16,
+// k0 + 4g + [0..3] for fp32), or the ACC k-set (k0 + 4g + [0..3] and
+// k0 + 16 + 4g + [0..3] for bf16).
+DSA_DEV bf16x8 join8(bf16x4 a, bf16x4 b) {
+  bf16x8 f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    f[e] = a[e];
+    f[4 + e] = b[e];
+  }
+  return f;
+}
+template <typename T>
+DSA_DEV typename Mfma<T>::frag tr_contig(const T* X, int str, int k0, int m0, int g, int c16) {
+  if constexpr (sizeof(T) == 2) {
+    return join8(tr4(X, str, k0 + 8 * g, m0, c16), tr4(X, str, k0 + 8 * g + 4, m0, c16));
+  } else {
+    return tr4(X, str, k0 + 4 * g, m0, c16);
+  }
+}
+template <typename T>
+DSA_DEV typename Mfma<T>::frag tr_acc(const T* X, int str, int k0, int m0, int g, int c16) {
+  if constexpr (sizeof(T) == 2) {
+    return join8(tr4(X, str, k0 + 4 * g, m0, c16), tr4(X, str, k0 + 16 + 4 * g, m0, c16));
+  } else {
+    return tr4(X, str, k0 + 4 * g, m0, c16);
+  }
+}
+
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 

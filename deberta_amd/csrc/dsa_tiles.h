@@ -282,7 +282,8 @@ DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&
                                const typename Mfma<T>::frag (&qf)[2][D / Mfma<T>::KSTEP],
                                typename BandType<T>::type* cb, typename BandType<T>::type* pb, const short* crow,
                                const short* prow, int w, int g, int c16, const T* krh, int64_t krs, const T* qrh,
-                               int64_t qrs, int flags, float sl2) {
+                               int64_t qrs, int flags, float sl2, const T* krd = nullptr, int krd_str = 0,
+                               int krd_row0 = 0) {
   using M = Mfma<T>;
   typedef typename M::frag frag;
   typedef typename BandType<T>::type BT;
@@ -291,10 +292,16 @@ DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&
   if (flags & 1) {
 #pragma unroll
     for (int rb = 0; rb < XW / 16; ++rb) {
-      const int row = crow[WQ * w + 16 * rb + c16];
       frag af[NS];
+      if (krd) {  // the tile's window of Kr rows is staged in LDS (row r at r - krd_row0)
+        const int row = crow[WQ * w + 16 * rb + c16] - krd_row0;
 #pragma unroll
-      for (int s = 0; s < NS; ++s) af[s] = M::load_contig(krh + (int64_t)row * krs, s, g);
+        for (int s = 0; s < NS; ++s) af[s] = M::load_contig(krd + row * krd_str, s, g);
+      } else {
+        const int row = crow[WQ * w + 16 * rb + c16];
+#pragma unroll
+        for (int s = 0; s < NS; ++s) af[s] = M::load_contig(krh + (int64_t)row * krs, s, g);
+      }
 #pragma unroll
       for (int ib = 0; ib < 2; ++ib) {
         f32x4 acc = zero4();
