@@ -10,6 +10,7 @@
 
 #include "../../include/dsa.h"
 #include "dsa_bwd.h"
+#include "dsa_bwd_dkdv.h"
 #include "dsa_bwd_dq.h"
 #include "dsa_fwd.h"
 
@@ -130,25 +131,38 @@ int fwd_mask(const dsa::FwdParams& p, int mode, hipStream_t st) {
   }
 }
 
-// Occupancy (workgroups per CU) of the dq kernel instance these arguments select.
-template <typename T, int D>
-int dq_occupancy(int mode) {
+// Occupancy (workgroups per CU) of a kernel; 1 if the query fails.
+int occupancy_of(const void* fn) {
   int occ = 0;
-  hipError_t e = hipSuccess;
-  switch (mode) {
-    case dsa::MASK_KEY:
-      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)dsa::dsa_bwd_dq_kernel<T, D, dsa::MASK_KEY>,
-                                                       256, 0);
-      break;
-    case dsa::MASK_PAIR:
-      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)dsa::dsa_bwd_dq_kernel<T, D, dsa::MASK_PAIR>,
-                                                       256, 0);
-      break;
-    default:
-      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)dsa::dsa_bwd_dq_kernel<T, D, dsa::MASK_NONE>,
-                                                       256, 0);
-  }
+  const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, 256, 0);
   return (e == hipSuccess && occ > 0) ? occ : 1;
+}
+
+template <typename T, int D>
+const void* dq_kernel_ptr(int mode) {
+  switch (mode) {
+    case dsa::MASK_KEY: return (const void*)dsa::dsa_bwd_dq_kernel<T, D, dsa::MASK_KEY>;
+    case dsa::MASK_PAIR: return (const void*)dsa::dsa_bwd_dq_kernel<T, D, dsa::MASK_PAIR>;
+    default: return (const void*)dsa::dsa_bwd_dq_kernel<T, D, dsa::MASK_NONE>;
+  }
+}
+
+template <typename T, int D>
+const void* dkdv_kernel_ptr(int mode) {
+  switch (mode) {
+    case dsa::MASK_KEY: return (const void*)dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_KEY>;
+    case dsa::MASK_PAIR: return (const void*)dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_PAIR>;
+    default: return (const void*)dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_NONE>;
+  }
+}
+
+const void* bwd_kernel_ptr(const dsa_fwd_args& f, int mode, bool dkdv) {
+  if (f.dtype == DSA_BF16) {
+    if (f.D == 64) return dkdv ? dkdv_kernel_ptr<dsa::bf16, 64>(mode) : dq_kernel_ptr<dsa::bf16, 64>(mode);
+    return dkdv ? dkdv_kernel_ptr<dsa::bf16, 32>(mode) : dq_kernel_ptr<dsa::bf16, 32>(mode);
+  }
+  if (f.D == 64) return dkdv ? dkdv_kernel_ptr<float, 64>(mode) : dq_kernel_ptr<float, 64>(mode);
+  return dkdv ? dkdv_kernel_ptr<float, 32>(mode) : dq_kernel_ptr<float, 32>(mode);
 }
 
 int device_cus() {
@@ -158,18 +172,16 @@ int device_cus() {
   return cus;
 }
 
-// Work decomposition of the persistent dq kernel: items (head, batch, query
+// Work decomposition of a persistent backward kernel: items (head, batch,
 // tile) with the head slowest, split into contiguous runs, one per resident
 // workgroup.
-dsa::PersistentPlan dq_plan(const dsa_fwd_args& f, int mode) {
+dsa::PersistentPlan bwd_plan(const dsa_fwd_args& f, int mode, bool dkdv) {
   dsa::PersistentPlan pl;
-  const int tiles = (f.Lq + dsa::dqcfg::BQ - 1) / dsa::dqcfg::BQ;
+  const int tile = dkdv ? dsa::kvcfg::BKW : dsa::dqcfg::BQ;
+  const int tiles = ((dkdv ? f.Lk : f.Lq) + tile - 1) / tile;
   pl.per_head = f.B * tiles;
   pl.items = f.H * pl.per_head;
-  int occ = 1;
-  if (f.dtype == DSA_BF16) occ = f.D == 64 ? dq_occupancy<dsa::bf16, 64>(mode) : dq_occupancy<dsa::bf16, 32>(mode);
-  else occ = f.D == 64 ? dq_occupancy<float, 64>(mode) : dq_occupancy<float, 32>(mode);
-  const int slots_avail = device_cus() * occ;
+  const int slots_avail = device_cus() * occupancy_of(bwd_kernel_ptr(f, mode, dkdv));
   pl.grid = pl.items < slots_avail ? pl.items : slots_avail;
   const int run = (pl.items + pl.grid - 1) / pl.grid;
   pl.slots = (run + pl.per_head - 1) / pl.per_head + 1;
@@ -179,27 +191,22 @@ dsa::PersistentPlan dq_plan(const dsa_fwd_args& f, int mode) {
 }
 
 struct WsLayout {
-  size_t krT, qrT, delta, part_dkr, total;
-  int Rpad;
-  dsa::PersistentPlan dq;
+  size_t delta, part_dkr, part_dqr, total;
+  dsa::PersistentPlan dq, kv;
 };
 
 WsLayout ws_layout(const dsa_bwd_args* a) {
   const dsa_fwd_args& f = a->fwd;
   WsLayout w;
-  const int R = f.flags ? 2 * f.att_span : 0;
-  w.Rpad = (int)align_up((size_t)R, 32);
-  w.dq = dq_plan(f, mask_mode(&f));
-  const size_t tab = (size_t)f.H * f.D * w.Rpad * elem_bytes(f.dtype);
+  w.dq = bwd_plan(f, mask_mode(&f), false);
+  w.kv = bwd_plan(f, mask_mode(&f), true);
   size_t off = 0;
-  w.krT = off;
-  off = align_up(off + ((f.flags & DSA_C2P) ? tab : 0), 256);
-  w.qrT = off;
-  off = align_up(off + ((f.flags & DSA_P2C) ? tab : 0), 256);
   w.delta = off;
   off = align_up(off + (size_t)f.B * f.H * f.Lq * sizeof(float), 256);
   w.part_dkr = off;
   if (f.flags & DSA_C2P) off = align_up(off + (size_t)w.dq.grid * w.dq.slots * w.dq.prow * f.D * sizeof(float), 256);
+  w.part_dqr = off;
+  if (f.flags & DSA_P2C) off = align_up(off + (size_t)w.kv.grid * w.kv.slots * w.kv.prow * f.D * sizeof(float), 256);
   w.total = off;
   return w;
 }
@@ -222,10 +229,7 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
   bp.dkr = a->dkr;
   bp.dqr = a->dqr;
   char* base = static_cast<char*>(a->workspace);
-  bp.krT = base + ws.krT;
-  bp.qrT = base + ws.qrT;
   bp.delta = reinterpret_cast<float*>(base + ws.delta);
-  bp.Rpad = ws.Rpad;
   const int stages = a->stages ? a->stages : (DSA_STAGE_PREP | DSA_STAGE_DQ | DSA_STAGE_DKDV);
   const int R = 2 * f.att_span;
 
@@ -233,17 +237,6 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
     const int64_t n = (int64_t)f.B * f.H * f.Lq * (D / (16 / (int)sizeof(T)));
     hipLaunchKernelGGL((dsa::dsa_bwd_delta_kernel<T, D>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, bp);
     if (launch_check("dsa_bwd_delta_kernel")) return 1;
-    const int64_t nt = (int64_t)f.H * D * ws.Rpad;
-    if (f.flags & DSA_C2P) {
-      hipLaunchKernelGGL((dsa::dsa_transpose_table_kernel<T, D>), dim3((unsigned)((nt + 255) / 256)), dim3(256), 0, st,
-                         (const T*)f.kr, f.kr_strides[0], f.kr_strides[1], (T*)(base + ws.krT), f.H, R, ws.Rpad);
-      if (launch_check("dsa_transpose_table_kernel")) return 1;
-    }
-    if (f.flags & DSA_P2C) {
-      hipLaunchKernelGGL((dsa::dsa_transpose_table_kernel<T, D>), dim3((unsigned)((nt + 255) / 256)), dim3(256), 0, st,
-                         (const T*)f.qr, f.qr_strides[0], f.qr_strides[1], (T*)(base + ws.qrT), f.H, R, ws.Rpad);
-      if (launch_check("dsa_transpose_table_kernel")) return 1;
-    }
   }
   if (stages & DSA_STAGE_DQ) {
     const dsa::PersistentPlan pl = ws.dq;
@@ -268,18 +261,26 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
     }
   }
   if (stages & DSA_STAGE_DKDV) {
-    dim3 grid((f.Lk + dsa::bwdcfg::TILE_OWN - 1) / dsa::bwdcfg::TILE_OWN, f.H, f.B);
+    const dsa::PersistentPlan pl = ws.kv;
+    float* part = reinterpret_cast<float*>(base + ws.part_dqr);
+    dim3 grid(pl.grid);
     switch (mode) {
       case dsa::MASK_KEY:
-        hipLaunchKernelGGL((dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_KEY>), grid, dim3(256), 0, st, bp);
+        hipLaunchKernelGGL((dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_KEY>), grid, dim3(256), 0, st, bp, pl, part);
         break;
       case dsa::MASK_PAIR:
-        hipLaunchKernelGGL((dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_PAIR>), grid, dim3(256), 0, st, bp);
+        hipLaunchKernelGGL((dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_PAIR>), grid, dim3(256), 0, st, bp, pl, part);
         break;
       default:
-        hipLaunchKernelGGL((dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_NONE>), grid, dim3(256), 0, st, bp);
+        hipLaunchKernelGGL((dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_NONE>), grid, dim3(256), 0, st, bp, pl, part);
     }
     if (launch_check("dsa_bwd_dkdv_kernel")) return 1;
+    if (f.flags & DSA_P2C) {
+      const int64_t n = (int64_t)f.H * pl.prow * D;
+      hipLaunchKernelGGL((dsa::dsa_bwd_reduce_kernel<D>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a->dqr,
+                         part, pl, f.H, R);
+      if (launch_check("dsa_bwd_reduce_kernel")) return 1;
+    }
   }
   return 0;
 }

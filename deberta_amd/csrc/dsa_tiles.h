@@ -1,8 +1,8 @@
-// dsa_tiles.h — score-tile building blocks shared by the forward and the two
-// backward kernels: tile loaders and the disentangled score recompute
+// dsa_tiles.h — building blocks shared by the forward and the backward
+// kernels: parameter blocks, tile loaders and the relative terms of the
+// disentangled score
 //     s(i, j) = q_i.k_j + q_i.Kr[c(i-j)] + k_j.Qr[p(i-j)]
-// (deberta_v2_native.py:604 and the c2p/p2c terms of :389-410) in the two
-// orientations the kernels use.
+// (deberta_v2_native.py:604 and the c2p/p2c terms of :389-410).
 #pragma once
 
 #include "dsa_common.h"
@@ -37,31 +37,13 @@ struct BwdParams {
   int64_t dqs[3], dks[3], dvs[3];
   float* dkr;
   float* dqr;
-  const void* krT;  // [H, D, Rpad] transposed pos-key table (workspace)
-  const void* qrT;  // [H, D, Rpad] transposed pos-query table (workspace)
   float* delta;     // [B, H, Lq] rowwise dO . O (workspace)
-  int Rpad;
 };
 
 template <typename T>
 struct Pad {
   static constexpr int v = 16 / sizeof(T);  // one 16-byte pad per LDS row
 };
-
-// Relative-position window: tbl[x] = clamp(t(i - j), -A, A) for
-// i - j = dbase + x, x in [0, n).  Offsets outside the table are clamped to
-// its ends; they only occur for (i, j) pairs that are out of range and never
-// contribute.
-DSA_DEV void load_rel_window(short* tbl, const int32_t* rel, int dbase, int n, int Lq, int Lk, int A,
-                             int tid, int nthreads) {
-  for (int x = tid; x < n; x += nthreads) {
-    int d = dbase + x;
-    d = min(max(d, -(Lk - 1)), Lq - 1);
-    int t = rel[d + Lk - 1];
-    t = min(max(t, -A), A);
-    tbl[x] = (short)t;
-  }
-}
 
 // Copies rows [row0, row0 + ROWS) of a [L, D] strided matrix into LDS
 // (row-major, stride `str`), zero-filling rows >= nvalid.  If `dstT` is
@@ -86,124 +68,6 @@ DSA_DEV void load_rows(T* dst, int str, T* dstT, int strT, const T* src, int64_t
     if (dstT) {
 #pragma unroll
       for (int e = 0; e < VEC; ++e) dstT[(d0 + e) * strT + r] = x[e];
-    }
-  }
-}
-
-// Min / max of the clamped relative positions tbl[x0 .. x0 + n) over a wave.
-DSA_DEV void wave_rel_range(const short* tbl, int x0, int n, int l, int& tmin, int& tmax) {
-  int lo = INT32_MAX, hi = INT32_MIN;
-  for (int x = l; x < n; x += 64) {
-    const int t = tbl[x0 + x];
-    lo = min(lo, t);
-    hi = max(hi, t);
-  }
-  tmin = wave_min(lo);
-  tmax = wave_max(hi);
-}
-
-namespace tilecfg {
-constexpr int BAND = 96;  // band rows per chunk (>= 32 + 64 - 1)
-}
-
-// ---------------------------------------------------------------------------
-// Transposed score tile (keys down, queries across), 64 keys x 32 queries per
-// wave.  st[ib][jb][e] is key 16*jb + 4*g + e, query 16*ib + c16.
-//   kf: A fragments of the 64 key rows (CONTIG k-set over the head dim)
-//   qf: B fragments of the wave's 32 query rows
-//   xq: the wave's first query minus the tile's first query,
-//   tbl: window with x = (i - i_tile0) - (j - j0) + 63
-//   scr: per-wave scratch of max(96*33, 64*97) floats
-// ---------------------------------------------------------------------------
-template <typename T, int D>
-DSA_DEV void score_tile_T(f32x4 (&st)[2][4], const typename Mfma<T>::frag (&kf)[4][D / Mfma<T>::KSTEP],
-                          const typename Mfma<T>::frag (&qf)[2][D / Mfma<T>::KSTEP], float* scr,
-                          const short* tbl, int xq, int l, int g, int c16, const T* krh, int64_t krs,
-                          const T* qrh, int64_t qrs, int A, int flags) {
-  using M = Mfma<T>;
-  typedef typename M::frag frag;
-  constexpr int NS = D / M::KSTEP;
-  constexpr int BAND = tilecfg::BAND;
-  constexpr int CB_STR = 33;        // [r][i]
-  constexpr int PB_STR = BAND + 1;  // [j][r]
-#pragma unroll
-  for (int jb = 0; jb < 4; ++jb)
-#pragma unroll
-    for (int ib = 0; ib < 2; ++ib) {
-      f32x4 acc = zero4();
-#pragma unroll
-      for (int s = 0; s < NS; ++s) acc = M::mma(kf[jb][s], qf[ib][s], acc);
-      st[ib][jb] = acc;
-    }
-  if (!flags) return;
-
-  int tmin, tmax;
-  wave_rel_range(tbl, xq, 32 + 64 - 1, l, tmin, tmax);
-
-  if (flags & 1) {  // c2p: q_i . Kr[c(i-j)]
-    const int cmin = c2p_row(tmin, A), cmax = c2p_row(tmax, A);
-    for (int cb = cmin; cb <= cmax; cb += BAND) {
-      const int nrow = min(BAND, cmax - cb + 1);
-      const int nblk = (nrow + 15) >> 4;
-      for (int rb = 0; rb < nblk; ++rb) {
-        const int r = min(cb + 16 * rb + c16, 2 * A - 1);
-        frag af[NS];
-#pragma unroll
-        for (int s = 0; s < NS; ++s) af[s] = M::load_contig(krh + (int64_t)r * krs, s, g);
-#pragma unroll
-        for (int ib = 0; ib < 2; ++ib) {
-          f32x4 acc = zero4();
-#pragma unroll
-          for (int s = 0; s < NS; ++s) acc = M::mma(af[s], qf[ib][s], acc);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) scr[(16 * rb + 4 * g + e) * CB_STR + 16 * ib + c16] = acc[e];
-        }
-      }
-      wave_lds_sync();
-#pragma unroll
-      for (int ib = 0; ib < 2; ++ib)
-#pragma unroll
-        for (int jb = 0; jb < 4; ++jb)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int xi = xq + (16 * ib + c16) - (16 * jb + 4 * g + e) + 63;
-            const int r = c2p_row(tbl[xi], A) - cb;
-            if (r >= 0 && r < nrow) st[ib][jb][e] += scr[r * CB_STR + 16 * ib + c16];
-          }
-      wave_lds_sync();
-    }
-  }
-  if (flags & 2) {  // p2c: k_j . Qr[p(i-j)]
-    const int pmin = p2c_row(tmax, A), pmax = p2c_row(tmin, A);
-    for (int pb = pmin; pb <= pmax; pb += BAND) {
-      const int nrow = min(BAND, pmax - pb + 1);
-      const int nblk = (nrow + 15) >> 4;
-      for (int rb = 0; rb < nblk; ++rb) {
-        const int r = min(pb + 16 * rb + c16, 2 * A - 1);
-        frag bf[NS];
-#pragma unroll
-        for (int s = 0; s < NS; ++s) bf[s] = M::load_contig(qrh + (int64_t)r * qrs, s, g);
-#pragma unroll
-        for (int jb = 0; jb < 4; ++jb) {
-          f32x4 acc = zero4();
-#pragma unroll
-          for (int s = 0; s < NS; ++s) acc = M::mma(kf[jb][s], bf[s], acc);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) scr[(16 * jb + 4 * g + e) * PB_STR + 16 * rb + c16] = acc[e];
-        }
-      }
-      wave_lds_sync();
-#pragma unroll
-      for (int ib = 0; ib < 2; ++ib)
-#pragma unroll
-        for (int jb = 0; jb < 4; ++jb)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int xi = xq + (16 * ib + c16) - (16 * jb + 4 * g + e) + 63;
-            const int r = p2c_row(tbl[xi], A) - pb;
-            if (r >= 0 && r < nrow) st[ib][jb][e] += scr[(16 * jb + 4 * g + e) * PB_STR + r];
-          }
-      wave_lds_sync();
     }
   }
 }
@@ -350,109 +214,6 @@ DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&
       for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) y[ib][jb][e] += (float)base[(16 * jb + e) * PBS + 16 * ib - 16 * jb - e];
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Score tile in natural orientation (queries down, keys across), 64 queries
-// x 32 keys per wave.  s[jb][ib][e] is query 16*ib + 4*g + e, key
-// 16*jb + c16.
-//   qa: A fragments of the 64 query rows
-//   kb: B fragments of the wave's 32 key rows
-//   xk: window index offset so that x = (i - i0) - (j - j_w0) + xk, where
-//       j_w0 is the wave's first key; the wave's window is tbl[xk - 31 ..
-//       xk + 63]
-// ---------------------------------------------------------------------------
-template <typename T, int D>
-DSA_DEV void score_tile_S(f32x4 (&sc)[2][4], const typename Mfma<T>::frag (&qa)[4][D / Mfma<T>::KSTEP],
-                          const typename Mfma<T>::frag (&kb)[2][D / Mfma<T>::KSTEP], float* scr,
-                          const short* tbl, int xk, int l, int g, int c16, const T* krh, int64_t krs,
-                          const T* qrh, int64_t qrs, int A, int flags) {
-  using M = Mfma<T>;
-  typedef typename M::frag frag;
-  constexpr int NS = D / M::KSTEP;
-  constexpr int BAND = tilecfg::BAND;
-  constexpr int CB_STR = BAND + 1;  // [i][r]
-  constexpr int PB_STR = 33;        // [r][j]
-#pragma unroll
-  for (int ib = 0; ib < 4; ++ib)
-#pragma unroll
-    for (int jb = 0; jb < 2; ++jb) {
-      f32x4 acc = zero4();
-#pragma unroll
-      for (int s = 0; s < NS; ++s) acc = M::mma(qa[ib][s], kb[jb][s], acc);
-      sc[jb][ib] = acc;
-    }
-  if (!flags) return;
-
-  int tmin, tmax;
-  wave_rel_range(tbl, xk - 31, 32 + 64 - 1, l, tmin, tmax);
-
-  if (flags & 1) {  // c2p: q_i . Kr[c(i-j)]
-    const int cmin = c2p_row(tmin, A), cmax = c2p_row(tmax, A);
-    for (int cb = cmin; cb <= cmax; cb += BAND) {
-      const int nrow = min(BAND, cmax - cb + 1);
-      const int nblk = (nrow + 15) >> 4;
-      for (int rb = 0; rb < nblk; ++rb) {
-        const int r = min(cb + 16 * rb + c16, 2 * A - 1);
-        frag bf[NS];
-#pragma unroll
-        for (int s = 0; s < NS; ++s) bf[s] = M::load_contig(krh + (int64_t)r * krs, s, g);
-#pragma unroll
-        for (int ib = 0; ib < 4; ++ib) {
-          f32x4 acc = zero4();
-#pragma unroll
-          for (int s = 0; s < NS; ++s) acc = M::mma(qa[ib][s], bf[s], acc);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) scr[(16 * ib + 4 * g + e) * CB_STR + 16 * rb + c16] = acc[e];
-        }
-      }
-      wave_lds_sync();
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb)
-#pragma unroll
-        for (int ib = 0; ib < 4; ++ib)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int xi = xk + (16 * ib + 4 * g + e) - (16 * jb + c16);
-            const int r = c2p_row(tbl[xi], A) - cb;
-            if (r >= 0 && r < nrow) sc[jb][ib][e] += scr[(16 * ib + 4 * g + e) * CB_STR + r];
-          }
-      wave_lds_sync();
-    }
-  }
-  if (flags & 2) {  // p2c: k_j . Qr[p(i-j)]
-    const int pmin = p2c_row(tmax, A), pmax = p2c_row(tmin, A);
-    for (int pb = pmin; pb <= pmax; pb += BAND) {
-      const int nrow = min(BAND, pmax - pb + 1);
-      const int nblk = (nrow + 15) >> 4;
-      for (int rb = 0; rb < nblk; ++rb) {
-        const int r = min(pb + 16 * rb + c16, 2 * A - 1);
-        frag af[NS];
-#pragma unroll
-        for (int s = 0; s < NS; ++s) af[s] = M::load_contig(qrh + (int64_t)r * qrs, s, g);
-#pragma unroll
-        for (int jb = 0; jb < 2; ++jb) {
-          f32x4 acc = zero4();
-#pragma unroll
-          for (int s = 0; s < NS; ++s) acc = M::mma(af[s], kb[jb][s], acc);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) scr[(16 * rb + 4 * g + e) * PB_STR + 16 * jb + c16] = acc[e];
-        }
-      }
-      wave_lds_sync();
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb)
-#pragma unroll
-        for (int ib = 0; ib < 4; ++ib)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int xi = xk + (16 * ib + 4 * g + e) - (16 * jb + c16);
-            const int r = p2c_row(tbl[xi], A) - pb;
-            if (r >= 0 && r < nrow) sc[jb][ib][e] += scr[r * PB_STR + 16 * jb + c16];
-          }
-      wave_lds_sync();
-    }
   }
 }
 
