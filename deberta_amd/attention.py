@@ -23,6 +23,7 @@ from deberta_amd import ops  # noqa: F401  (registers the custom ops)
 from deberta_amd.config import normalize_attention_kernel, normalize_pos_att_type
 from deberta_amd.masks import kernel_masks, normalize_keep_mask
 from deberta_amd.relpos import (
+    is_monotone,
     is_toeplitz,
     normalize_relative_pos,
     relative_offset_table,
@@ -58,8 +59,9 @@ def table_for(
     device,
 ) -> torch.Tensor:
     """Offset table for the kernels from ``relative_pos`` (or the canonical
-    one when it is None).  A given matrix must depend on ``i - j`` only; this
-    is verified once per tensor version in eager mode."""
+    one when it is None).  A given matrix must depend on ``i - j`` only and
+    be non-decreasing in it (as every matrix build_relative_position returns);
+    this is verified once per tensor version in eager mode."""
     if relative_pos is None:
         return canonical_table(query_len, key_len, buckets, max_position, device)
     rp = normalize_relative_pos(relative_pos.to(device), query_len, key_len)
@@ -68,14 +70,14 @@ def table_for(
         key = (rp.data_ptr(), rp._version, tuple(rp.shape), tuple(rp.stride()), str(rp.device))
         ok = _TOEPLITZ_OK.get(key)
         if ok is None:
-            ok = is_toeplitz(rp, table)
+            ok = is_toeplitz(rp, table) and is_monotone(table)
             if len(_TOEPLITZ_OK) > 256:
                 _TOEPLITZ_OK.clear()
             _TOEPLITZ_OK[key] = ok
         if not ok:
             raise ValueError(
-                "relative_pos must depend on i - j only (as build_relative_position produces) "
-                "for the fused disentangled-attention kernels"
+                "relative_pos must depend on i - j only and be non-decreasing in it "
+                "(as build_relative_position produces) for the fused disentangled-attention kernels"
             )
     return table
 

@@ -114,3 +114,10 @@ def is_toeplitz(rp: torch.Tensor, table: Optional[torch.Tensor] = None) -> bool:
         torch.arange(Lq, device=rp.device)[:, None] - torch.arange(Lk, device=rp.device)[None, :] + (Lk - 1)
     )
     return bool(torch.equal(table.to(torch.long)[idx], rp.to(torch.long)))
+
+
+def is_monotone(table: torch.Tensor) -> bool:
+    """True if the offset table is non-decreasing in i - j (every bucketed or
+    plain relative-position table is).  Synchronises with the device."""
+    t = table.to(torch.long)
+    return bool((t[1:] >= t[:-1]).all()) if t.numel() > 1 else True

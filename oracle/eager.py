@@ -191,12 +191,15 @@ def attend(
     D = q.shape[-1]
     sf = 1 + sum(t in types for t in ("c2p", "p2c", "p2p"))
     denom = math.sqrt(float(D * sf))
-    qf, kf = q.float(), k.float()
+    # The reference scores in fp32 (query_layer.float(), :602-603); fp64
+    # inputs (used only to pin this oracle) stay in fp64.
+    score_dtype = torch.float64 if q.dtype == torch.float64 else torch.float32
+    qf, kf = q.to(score_dtype), k.to(score_dtype)
     scores = torch.matmul(qf, kf.transpose(-1, -2)) / denom
     if use_relative and (kr is not None or qr is not None):
         kr_f = kr.to(qf.dtype) if kr is not None else None
         qr_f = qr.to(qf.dtype) if qr is not None else None
-        scores = scores + relative_bias(qf, kf, kr_f, qr_f, rel, att_span, types, sf, D, variant).float()
+        scores = scores + relative_bias(qf, kf, kr_f, qr_f, rel, att_span, types, sf, D, variant).to(score_dtype)
     live = None
     if attention_mask is not None:
         keep = keep_mask(attention_mask)
@@ -280,10 +283,11 @@ class EagerDisentangledSelfAttention(nn.Module):
         if use_rel:
             Lq, Lk = q.shape[2], k.shape[2]
             rel = canonical_rel(relative_pos, Lq, Lk, self.position_buckets, self.max_relative_positions)
+            sdt = torch.float64 if q.dtype == torch.float64 else torch.float32
             if "c2p" in self.pos_att_type or "p2p" in self.pos_att_type:
-                kr = self.project_rel(rel_embeddings, use_query=False).to(torch.float32)
+                kr = self.project_rel(rel_embeddings, use_query=False).to(sdt)
             if "p2c" in self.pos_att_type or "p2p" in self.pos_att_type:
-                qr = self.project_rel(rel_embeddings, use_query=True).to(torch.float32)
+                qr = self.project_rel(rel_embeddings, use_query=True).to(sdt)
         ctx, probs = attend(
             q, k, v, kr, qr, rel, attention_mask,
             types=self.pos_att_type, att_span=self.pos_ebd_size, use_relative=use_rel, variant=self.variant,

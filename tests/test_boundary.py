@@ -1,0 +1,255 @@
+"""CPU checks of the drop-in boundary: the C ABI of libdsa.so (exports and
+struct layout against include/dsa.h), the torch.library ops (registration,
+fake-tensor shapes, tracing, loud failure off the GPU) and the host-side
+mirror of the reference interface (kernel selector, masks, module layout).
+No kernel is launched here."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+import torch
+
+import deberta_amd
+from deberta_amd import _lib, ops
+from deberta_amd.attention import DisentangledSelfAttention
+from deberta_amd.config import normalize_attention_kernel, normalize_pos_att_type
+from deberta_amd.masks import get_attention_mask, kernel_masks, normalize_keep_mask
+from oracle import eager
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "dsa.h"
+
+
+def _declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(dsa_[a-z_]+)\s*\([^;{]*\)\s*;", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIB_PATH.exists():
+        pytest.fail(f"{_lib.LIB_PATH} is not built (run python -m deberta_amd._build)")
+    return _lib.load()
+
+
+def test_header_declares_the_abi():
+    assert _declared_functions() == sorted(_lib.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+    nm = shutil.which("nm")
+    if nm:
+        out = subprocess.run([nm, "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True, text=True).stdout
+        for name in _declared_functions():
+            assert re.search(rf"\bT {name}$", out, re.M), name
+
+
+def test_version_and_error_buffer(lib):
+    assert lib.dsa_version() == _lib.EXPECTED_VERSION
+    assert _lib.last_error() == ""
+
+
+def test_argument_errors_return_codes_without_launching(lib):
+    """Validation happens before any device work, so it is testable here."""
+    assert lib.dsa_fwd(None, None) != 0
+    assert "null arguments" in _lib.last_error()
+    a = _lib.DsaFwdArgs()
+    a.B, a.H, a.Lq, a.Lk, a.D, a.dtype = 1, 1, 8, 8, 48, _lib.DSA_BF16
+    assert lib.dsa_fwd(ctypes.byref(a), None) != 0
+    assert "head dim must be 32 or 64" in _lib.last_error()
+    a.D = 64
+    assert lib.dsa_fwd(ctypes.byref(a), None) != 0
+    assert "required" in _lib.last_error()
+    a.dtype = 7
+    assert lib.dsa_fwd(ctypes.byref(a), None) != 0
+    assert "unsupported dtype" in _lib.last_error()
+
+
+C_LAYOUT_PROBE = r"""
+#include <stdio.h>
+#include <stddef.h>
+#include "dsa.h"
+#define F(s, f) printf(#s "." #f " %zu\n", offsetof(s, f));
+int main(void) {
+  printf("dsa_fwd_args %zu\n", sizeof(dsa_fwd_args));
+  printf("dsa_bwd_args %zu\n", sizeof(dsa_bwd_args));
+  %FIELDS%
+  return 0;
+}
+"""
+
+
+def test_ctypes_structs_match_the_c_header(tmp_path):
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    lines = []
+    for cname, st in (("dsa_fwd_args", _lib.DsaFwdArgs), ("dsa_bwd_args", _lib.DsaBwdArgs)):
+        for fname, _ in st._fields_:
+            lines.append(f"F({cname}, {fname})")
+    src = tmp_path / "probe.c"
+    src.write_text(C_LAYOUT_PROBE.replace("%FIELDS%", "\n  ".join(lines)))
+    exe = tmp_path / "probe"
+    subprocess.run([gcc, "-std=c99", "-I", str(HEADER.parent), str(src), "-o", str(exe)], check=True)
+    out = dict(line.rsplit(" ", 1) for line in subprocess.run([str(exe)], capture_output=True, text=True).stdout.splitlines())
+    assert int(out["dsa_fwd_args"]) == ctypes.sizeof(_lib.DsaFwdArgs)
+    assert int(out["dsa_bwd_args"]) == ctypes.sizeof(_lib.DsaBwdArgs)
+    for cname, st in (("dsa_fwd_args", _lib.DsaFwdArgs), ("dsa_bwd_args", _lib.DsaBwdArgs)):
+        for fname, _ in st._fields_:
+            assert int(out[f"{cname}.{fname}"]) == getattr(st, fname).offset, (cname, fname)
+
+
+# --- torch.library ops ----------------------------------------------------------------
+def _inputs(device="cpu", dtype=torch.bfloat16, B=2, L=64, H=2, D=64, A=16):
+    mk = lambda *s: torch.randn(*s, device=device).to(dtype)
+    q, k, v = mk(B, L, H, D), mk(B, L, H, D), mk(B, L, H, D)
+    kr, qr = mk(H, 2 * A, D), mk(H, 2 * A, D)
+    table = torch.arange(-(L - 1), L, dtype=torch.int32, device=device)
+    return q, k, v, kr, qr, table
+
+
+def test_ops_are_registered():
+    assert hasattr(torch.ops.deberta_amd, "dsa_fwd")
+    assert hasattr(torch.ops.deberta_amd, "dsa_bwd")
+
+
+def test_cpu_tensors_fail_loudly():
+    q, k, v, kr, qr, table = _inputs()
+    with pytest.raises(NotImplementedError):
+        torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, 16, 0.1)
+
+
+def test_fake_shapes():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode():
+        q, k, v, kr, qr, table = _inputs()
+        out, lse = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, 16, 0.1)
+        assert out.shape == q.shape and out.dtype == q.dtype
+        assert lse.shape == (2, 2, 64) and lse.dtype == torch.float32
+        g = torch.ops.deberta_amd.dsa_bwd(out, q, k, v, kr, qr, table, None, None, out, lse, 16, 0.1)
+        assert [t.shape for t in g] == [q.shape, k.shape, v.shape, (2, 32, 64), (2, 32, 64)]
+        assert g[3].dtype == torch.float32
+
+
+def test_trace_forward_and_backward_with_fake_tensors():
+    """make_fx in fake mode exercises the fake impls and the autograd
+    registration together (the path torch.compile takes)."""
+    from torch.fx.experimental.proxy_tensor import make_fx
+
+    def f(q, k, v, kr, qr, table, dout):
+        out, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, 16, 0.1)
+        return torch.autograd.grad(out, (q, k, v, kr, qr), dout)
+
+    q, k, v, kr, qr, table = _inputs()
+    for t in (q, k, v, kr, qr):
+        t.requires_grad_(True)
+    gm = make_fx(f, tracing_mode="fake")(q, k, v, kr, qr, table, torch.randn_like(q))
+    code = gm.code
+    assert "deberta_amd.dsa_fwd" in code and "deberta_amd.dsa_bwd" in code
+
+
+def test_python_validation():
+    q, k, v, kr, qr, table = _inputs()
+    with pytest.raises(ValueError, match="head dim"):
+        ops._validate(q[..., :48], k[..., :48], v[..., :48], None, None, None, None, None, 16)
+    with pytest.raises(ValueError, match=r"kr must be \[H"):
+        ops._validate(q, k, v, kr[:, :10], None, table, None, None, 16)
+    with pytest.raises(ValueError, match="rel_table"):
+        ops._validate(q, k, v, kr, None, None, None, None, 16)
+    with pytest.raises(TypeError, match="dtype"):
+        ops._validate(q.half(), k.half(), v.half(), None, None, None, None, None, 16)
+
+
+# --- host-side mirror of the reference interface -----------------------------------------
+@pytest.mark.parametrize(
+    "raw,canon",
+    [
+        ("dynamic", "dynamic"),
+        ("default", "dynamic"),
+        ("cached", "cached_bmm"),
+        ("cache", "cached_bmm"),
+        ("cached-bmm", "cached_bmm"),
+        ("SAFE", "stable"),
+        ("compile-safe", "stable"),
+        ("hip", "fused"),
+        ("fused", "fused"),
+    ],
+)
+def test_attention_kernel_selector(raw, canon):
+    assert normalize_attention_kernel(raw) == canon
+
+
+def test_attention_kernel_selector_rejects():
+    """test_smoke.py:2243 restated: the reference's error text."""
+    with pytest.raises(ValueError, match="model.hf.attention_kernel must be one of"):
+        normalize_attention_kernel("bad_kernel")
+
+
+def test_pos_att_type_normaliser():
+    assert normalize_pos_att_type("C2P|p2c") == ["c2p", "p2c"]
+    assert normalize_pos_att_type("c2p, p2c") == ["c2p", "p2c"]
+    assert normalize_pos_att_type(["p2c", "c2p"]) == ["p2c", "c2p"]
+    assert normalize_pos_att_type(None) == []
+
+
+def test_keep_mask_contract():
+    with pytest.raises(TypeError):
+        normalize_keep_mask([1])
+    with pytest.raises(ValueError, match="Floating-point masks are ambiguous"):
+        normalize_keep_mask(torch.ones(2))
+    assert normalize_keep_mask(torch.tensor([3, 0])).tolist() == [True, False]
+    assert get_attention_mask(torch.ones(2, 8, dtype=torch.long)).shape == (2, 1, 1, 8)
+    assert get_attention_mask(torch.ones(2, 8, 8, dtype=torch.bool)).shape == (2, 1, 8, 8)
+    assert get_attention_mask(torch.ones(2, 3, 8, 8, dtype=torch.bool)).shape == (2, 1, 8, 8)
+
+
+def test_kernel_masks():
+    keep = torch.tensor([[1, 1, 0, 1]], dtype=torch.bool)
+    kk, pk = kernel_masks(keep[:, None, None, :], 3, 4, 4)
+    assert pk is None and kk.shape == (3, 4) and kk.stride(0) == 0 and kk.dtype == torch.uint8
+    assert kk[2].tolist() == [1, 1, 0, 1]
+    dense = torch.ones(2, 1, 4, 4, dtype=torch.bool)
+    kk, pk = kernel_masks(dense, 2, 4, 4)
+    assert kk is None and pk.shape == (2, 4, 4) and pk.stride(-1) == 1
+    assert kernel_masks(None, 2, 4, 4) == (None, None)
+    with pytest.raises(ValueError, match="rank-4"):
+        kernel_masks(torch.ones(2, 4, dtype=torch.bool), 2, 4, 4)
+
+
+@pytest.mark.parametrize("share", [False, True])
+@pytest.mark.parametrize("types", ["c2p|p2c", "c2p", "p2c", "c2p|p2c|p2p"])
+def test_module_layout_matches_the_reference_shape(share, types):
+    """Same parameter names and shapes as the reference module (restated in
+    the oracle), so reference state dicts load unchanged."""
+    cfg = eager.make_config(hidden_size=64, num_attention_heads=4, share_att_key=share, pos_att_type=types)
+    ours = DisentangledSelfAttention(cfg)
+    ref = eager.EagerDisentangledSelfAttention(cfg)
+    assert {k: v.shape for k, v in ours.state_dict().items()} == {k: v.shape for k, v in ref.state_dict().items()}
+    ours.load_state_dict(ref.state_dict(), strict=True)
+    assert ours.pos_ebd_size == 256 and ours.attn_kernel == "dynamic"
+
+
+def test_module_rejects_bad_config_and_cpu():
+    with pytest.raises(ValueError, match="divisible"):
+        DisentangledSelfAttention(eager.make_config(hidden_size=30, num_attention_heads=4))
+    with pytest.raises(ValueError, match="model.hf.attention_kernel must be one of"):
+        DisentangledSelfAttention(eager.make_config(hf_attention_kernel="nope"))
+    m = DisentangledSelfAttention(eager.make_config(hidden_size=64, num_attention_heads=4))
+    with pytest.raises(RuntimeError, match="GPU"):
+        m(torch.randn(1, 8, 64), None, rel_embeddings=torch.randn(512, 64))
+    with pytest.raises(NotImplementedError, match="output_attentions"):
+        m(torch.randn(1, 8, 64), None, output_attentions=True)
+
+
+def test_package_surface():
+    for name in deberta_amd.__all__:
+        assert hasattr(deberta_amd, name), name

@@ -1,0 +1,223 @@
+"""Module-level parity on the GPU: deberta_amd.DisentangledSelfAttention
+(fused HIP kernels) against the oracle's restatement of the reference module
+with identical weights, including the gradients of the projection weights
+and of the relative-embedding table; the torch.compile path; and
+full-size properties of the op at the headline shape.
+
+Tolerances as in test_gpu_parity.py: fp32 max|err|/max|ref| <= 1e-4;
+bf16 (autocast) max|err| <= 2e-2 against the fp32 oracle.
+"""
+
+from __future__ import annotations
+
+import math
+import sys
+
+import pytest
+import torch
+
+from deberta_amd import DisentangledSelfAttention
+from oracle import eager
+from tests._cases import max_abs, max_rel
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def _pair(cfg, seed=0):
+    """Oracle module on the CPU and the fused module on the GPU with the
+    same weights (N(0, 0.02), zero biases)."""
+    torch.manual_seed(seed)
+    ref = eager.EagerDisentangledSelfAttention(cfg)
+    with torch.no_grad():
+        for n, p in ref.named_parameters():
+            p.copy_(torch.randn_like(p) * 0.02 if n.endswith("weight") else torch.zeros_like(p))
+    ours = DisentangledSelfAttention(cfg)
+    ours.load_state_dict(ref.state_dict(), strict=True)
+    return ref.eval(), ours.eval()
+
+
+def _run(module, x, mask, rel, device, autocast=False, relative_pos=None):
+    x = x.to(device).detach().clone().requires_grad_(True)
+    rel = rel.to(device).detach().clone().requires_grad_(True)
+    m = mask.to(device) if mask is not None else None
+    rp = relative_pos.to(device) if relative_pos is not None else None
+    with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+        out, _ = module(x, m, relative_pos=rp, rel_embeddings=rel)
+    g = torch.Generator(device="cpu").manual_seed(123)
+    dout = torch.randn(out.shape, generator=g).to(device=device, dtype=out.dtype)
+    names = [n for n, _ in module.named_parameters()]
+    params = [p for _, p in module.named_parameters()]
+    grads = torch.autograd.grad(out, [x, rel] + params, dout, allow_unused=True)
+    res = {"out": out.detach().float().cpu(), "dx": grads[0].float().cpu(), "drel": grads[1].float().cpu()}
+    for n, gr in zip(names, grads[2:]):
+        res["d" + n] = torch.zeros(1) if gr is None else gr.float().cpu()
+    return res
+
+
+# Biases whose exact gradient is zero: adding a vector to every key (or to
+# every row of the pos-key table) shifts each score row by a constant, which
+# softmax ignores (sum_j dS_ij = 0).  They are compared on the scale of the
+# matching weight gradient instead of their own (rounding-noise) scale.
+_SHIFT_INVARIANT = {"dkey_proj.bias": "dkey_proj.weight", "dpos_key_proj.bias": "dpos_key_proj.weight"}
+
+
+def _errors(ref: dict, got: dict) -> dict:
+    errs = {}
+    for k in ref:
+        if k in _SHIFT_INVARIANT:
+            scale = float(ref[_SHIFT_INVARIANT[k]].abs().max())
+            errs[k] = max_abs(got[k], ref[k]) / max(scale, 1e-30)
+        else:
+            errs[k] = max_rel(got[k], ref[k])
+    return errs
+
+
+def _config1(share=False, **kw):
+    return eager.make_config(
+        hidden_size=128, num_attention_heads=4, position_buckets=256, max_relative_positions=512,
+        share_att_key=share, **kw,
+    )
+
+
+@pytest.mark.parametrize("share", [False, True])
+@pytest.mark.parametrize("mask", ["none", "padding"])
+def test_config1_fp32(share, mask, gpu):
+    """BASELINE config 1 (B=2, L=128, hidden 128, 4 heads x 32, buckets 256,
+    max_rel 512, rel table [512, 128]), fp32, forward and backward."""
+    cfg = _config1(share)
+    ref, ours = _pair(cfg)
+    ours = ours.to(gpu)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(2, 128, 128, generator=g)
+    rel = torch.randn(512, 128, generator=g) * 0.02
+    m = None
+    if mask == "padding":
+        keep = torch.ones(2, 128, dtype=torch.bool)
+        keep[1, 77:] = False
+        m = keep[:, None, None, :]
+    a = _run(ref, x, m, rel, "cpu")
+    b = _run(ours, x, m, rel, gpu)
+    errs = _errors(a, b)
+    _say(f"[module fp32 share={share} mask={mask}] {errs}")
+    assert all(e <= 1e-4 for e in errs.values()), errs
+
+
+def test_bf16_autocast_base_shape(gpu):
+    """config-2 layer shape (hidden 768, 12 heads x 64) on 2 rows of 512,
+    under bf16 autocast, against the fp32 oracle: max|err|/max|ref| <= 3e-2."""
+    cfg = eager.make_config(hidden_size=768, num_attention_heads=12, share_att_key=True)
+    ref, ours = _pair(cfg, seed=1)
+    ours = ours.to(gpu)
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(2, 512, 768, generator=g)
+    rel = torch.randn(512, 768, generator=g)
+    keep = torch.ones(2, 512, dtype=torch.bool)
+    keep[1, 300:] = False
+    m = keep[:, None, None, :]
+    a = _run(ref, x, m, rel, "cpu")
+    b = _run(ours, x, m, rel, gpu, autocast=True)
+    # Under autocast the projections themselves run in bf16, so the module's
+    # gradients are compared relative to their scale (the op-level bound of
+    # 2e-2 absolute is checked in test_gpu_parity.py).
+    errs = _errors(a, b)
+    _say(f"[module bf16 autocast] {errs}")
+    assert all(e <= 3e-2 for e in errs.values()), errs
+
+
+def test_explicit_relative_pos_matches_none(gpu):
+    cfg = _config1()
+    _, ours = _pair(cfg)
+    ours = ours.to(gpu)
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(2, 128, 128, generator=g).to(gpu)
+    rel = (torch.randn(512, 128, generator=g) * 0.02).to(gpu)
+    from deberta_amd import build_relative_position
+
+    rp = build_relative_position(128, 128, bucket_size=256, max_position=512, device=gpu)
+    with torch.no_grad():
+        a, _ = ours(x, None, rel_embeddings=rel)
+        b, _ = ours(x, None, relative_pos=rp[None, None], rel_embeddings=rel)
+    assert torch.equal(a, b)
+    with pytest.raises(ValueError, match="depend on i - j only"):
+        bad = rp.clone()
+        bad[3, 5] += 1
+        ours(x, None, relative_pos=bad, rel_embeddings=rel)
+
+
+def test_none_mask_equals_all_ones_exactly(gpu):
+    cfg = _config1()
+    _, ours = _pair(cfg)
+    ours = ours.to(gpu)
+    x = torch.randn(2, 128, 128, device=gpu)
+    rel = torch.randn(512, 128, device=gpu) * 0.02
+    with torch.no_grad():
+        a, _ = ours(x, None, rel_embeddings=rel)
+        b, _ = ours(x, torch.ones(2, 1, 1, 128, dtype=torch.bool, device=gpu), rel_embeddings=rel)
+        c, _ = ours(x, torch.ones(2, 1, 128, 128, dtype=torch.bool, device=gpu), rel_embeddings=rel)
+    assert torch.equal(a, b) and torch.equal(a, c)
+
+
+@pytest.mark.parametrize("backend", ["aot_eager", "inductor"])
+def test_torch_compile(backend, gpu):
+    """The op traced by Dynamo through its fake implementation (config-5
+    style, smaller): compiled forward + backward equal the eager op."""
+    torch._dynamo.reset()
+    cfg = eager.make_config(hidden_size=256, num_attention_heads=4, share_att_key=True)
+    _, ours = _pair(cfg, seed=5)
+    ours = ours.to(gpu).train()
+    x = torch.randn(2, 256, 256, device=gpu)
+    rel = torch.randn(512, 256, device=gpu)
+
+    def loss_fn(mod, x, rel):
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            out, _ = mod(x, None, rel_embeddings=rel)
+        return out.float().square().mean()
+
+    compiled = torch.compile(ours, backend=backend, dynamic=False)
+    le = loss_fn(ours, x, rel)
+    ge = torch.autograd.grad(le, list(ours.parameters()))
+    lc = loss_fn(compiled, x, rel)
+    gc = torch.autograd.grad(lc, list(ours.parameters()))
+    assert torch.isfinite(lc) and abs(float(lc) - float(le)) <= 1e-3 * abs(float(le)) + 1e-6
+    for a, b in zip(ge, gc):
+        assert torch.isfinite(b).all()
+        assert max_abs(b, a) <= 2e-2 * max(1.0, float(a.abs().max()))
+
+
+def test_full_headline_shape_batch_consistency(gpu):
+    """At the headline shape (B=32, L=512, H=12, D=64, bf16) the op is
+    computed per (batch, head) item: the forward and dq/dk/dv of the full
+    batch equal those of each batch row run alone, bit for bit, and the
+    relative-table gradients equal the sum over rows."""
+    from deberta_amd.relpos import relative_offset_table
+
+    B, L, H, D, A = 32, 512, 12, 64, 256
+    g = torch.Generator().manual_seed(9)
+    mk = lambda *s: torch.randn(*s, generator=g).to(gpu, torch.bfloat16)
+    q, k, v, dO = mk(B, L, H, D), mk(B, L, H, D), mk(B, L, H, D), mk(B, L, H, D)
+    kr, qr = mk(H, 2 * A, D), mk(H, 2 * A, D)
+    table = relative_offset_table(L, L, bucket_size=256, max_position=512, device=gpu)
+    scale = 1 / math.sqrt(D * 3)
+
+    def run(sl):
+        ls = [t[sl].detach().clone().requires_grad_(True) for t in (q, k, v)]
+        lr = [t.detach().clone().requires_grad_(True) for t in (kr, qr)]
+        out, lse = torch.ops.deberta_amd.dsa_fwd(*ls, *lr, table, None, None, A, scale)
+        gr = torch.autograd.grad(out, ls + lr, dO[sl])
+        return out, lse, gr
+
+    out, lse, gr = run(slice(None))
+    assert torch.isfinite(out).all() and all(torch.isfinite(x).all() for x in gr)
+    dkr_sum = torch.zeros_like(gr[3], dtype=torch.float32)
+    for b in (0, 13, 31):
+        o1, l1, g1 = run(slice(b, b + 1))
+        assert torch.equal(o1, out[b : b + 1]) and torch.equal(l1, lse[b : b + 1])
+        for x, y in zip(g1[:3], gr[:3]):
+            assert torch.equal(x, y[b : b + 1])
+    for b in range(B):
+        dkr_sum += run(slice(b, b + 1))[2][3].float()
+    assert max_rel(gr[3].float(), dkr_sum) <= 2e-2
