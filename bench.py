@@ -37,6 +37,26 @@ A = BUCKETS
 R = 2 * A
 
 
+# HBM bytes per launch at this workload, from two rocprofv3 --pmc passes over
+# `bench.py --kernels-only` (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch),
+# each scaled by what the same counter reads for a plain 256 MiB device copy
+# in the same run: FETCH_SIZE reads 128 MiB for it (x2.0), WRITE_SIZE 256 MiB
+# (x1.0).  Commands and raw figures: profiles/hbm_traffic_headline.md.
+FETCH_SCALE, WRITE_SCALE = 2.0, 1.0
+TRAFFIC_KIB = {  # kernel: (FETCH_SIZE, WRITE_SIZE) as read
+    "dsa_fwd_kernel": (117981, 25344),
+    "dsa_bwd_dq_kernel": (149327, 58368),
+    "dsa_bwd_dkdv_kernel": (152589, 82948),
+}
+
+
+def hbm_bytes(kernel: str):
+    if kernel not in TRAFFIC_KIB:
+        return None
+    fetch, write = TRAFFIC_KIB[kernel]
+    return int(round((fetch * FETCH_SCALE + write * WRITE_SCALE) * 1024))
+
+
 def flops_fwd(b: int, l: int, h: int, d: int, r: int) -> float:
     return 4.0 * b * h * d * l * l + 4.0 * b * h * d * l * r
 
@@ -54,7 +74,9 @@ def cpu_model() -> str:
 
 def cpu_baseline(budget_s: float = 15.0) -> dict:
     """fp32 eager oracle fwd+bwd (the reference's op chain restated) on the
-    host's cores, on B=1 of the same shape; repeats until ~budget_s."""
+    host's cores, on a bounded sample of the same workload: batch rows of
+    the headline shape, repeated for about budget_s seconds; the value is
+    the sample's algorithmic FLOPs over its total time."""
     import torch
 
     from oracle import eager
@@ -62,7 +84,7 @@ def cpu_baseline(budget_s: float = 15.0) -> dict:
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     g = torch.Generator().manual_seed(0)
-    b = 1
+    b = 2
     q, k, v = (torch.randn(b, H, L, D, generator=g, requires_grad=True) for _ in range(3))
     kr, qr = (torch.randn(H, R, D, generator=g, requires_grad=True) for _ in range(2))
     dout = torch.randn(b, H, L, D, generator=g)
@@ -73,24 +95,23 @@ def cpu_baseline(budget_s: float = 15.0) -> dict:
         torch.autograd.grad(ctx, (q, k, v, kr, qr), dout)
 
     step()  # warm-up
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
+    runs = 0
+    t0 = time.perf_counter()
+    while True:
         step()
-        times.append(time.perf_counter() - t0)
-        if len(times) >= 50:
+        runs += 1
+        total = time.perf_counter() - t0
+        if total >= budget_s:
             break
-    times.sort()
-    med = times[len(times) // 2]
-    tflops = 3 * flops_fwd(b, L, H, D, R) / med / 1e12
+    tflops = runs * 3 * flops_fwd(b, L, H, D, R) / total / 1e12
     return {
         "value": round(tflops, 4),
         "unit": "TFLOP/s",
         "cores": cores,
         "kind": "port",
-        "sample": f"fp32 eager oracle fwd+bwd, B=1 of B={B} L={L} H={H} D={D} R={R} (no mask), "
-        f"median of {len(times)} runs = {med * 1e3:.1f} ms; CPU: {cpu_model()}",
+        "sample": f"fp32 eager oracle fwd+bwd on {runs} x {b} batch rows of B={B} L={L} H={H} D={D} R={R} "
+        f"(no mask) = {runs * b / B:.1f} steps' worth in {total:.1f} s ({total / runs * 1e3:.1f} ms per run); "
+        f"CPU: {cpu_model()}",
     }
 
 
@@ -192,12 +213,14 @@ def main() -> None:
 
         return f
 
-    run_stage(_lib.DSA_STAGE_PREP)()  # delta + transposed tables for the stage timings
+    run_stage(_lib.DSA_STAGE_PREP)()  # rowsum(dO * O) for the stage timings
+    # one kernel per stage except FOLD (two reduce launches, dkr and dqr)
     kernels = {
         "dsa_fwd_kernel": (run_fwd, f_fwd),
         "dsa_bwd_dq_kernel": (run_stage(_lib.DSA_STAGE_DQ), f_fwd),
         "dsa_bwd_dkdv_kernel": (run_stage(_lib.DSA_STAGE_DKDV), f_fwd),
-        "bwd_prep": (run_stage(_lib.DSA_STAGE_PREP), 0.0),
+        "dsa_bwd_delta_kernel": (run_stage(_lib.DSA_STAGE_PREP), 0.0),
+        "fold (2x dsa_bwd_reduce_kernel)": (run_stage(_lib.DSA_STAGE_FOLD), 0.0),
     }
     per_kernel = {}
     n_k = args.steps if args.kernels_only else max(10, args.steps)
@@ -252,7 +275,8 @@ def main() -> None:
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": hbm_bytes(dom),
+            "traffic_unit": "bytes/launch",
         },
         "wall_s_timed": round(wall, 3),
     }

@@ -20,6 +20,7 @@ DSA_P2C = 2
 DSA_STAGE_PREP = 1
 DSA_STAGE_DQ = 2
 DSA_STAGE_DKDV = 4
+DSA_STAGE_FOLD = 8
 
 EXPECTED_VERSION = 1
 

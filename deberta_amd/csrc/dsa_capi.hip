@@ -230,7 +230,7 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
   bp.dqr = a->dqr;
   char* base = static_cast<char*>(a->workspace);
   bp.delta = reinterpret_cast<float*>(base + ws.delta);
-  const int stages = a->stages ? a->stages : (DSA_STAGE_PREP | DSA_STAGE_DQ | DSA_STAGE_DKDV);
+  const int stages = a->stages ? a->stages : (DSA_STAGE_PREP | DSA_STAGE_DQ | DSA_STAGE_DKDV | DSA_STAGE_FOLD);
   const int R = 2 * f.att_span;
 
   if (stages & DSA_STAGE_PREP) {
@@ -253,12 +253,6 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
         hipLaunchKernelGGL((dsa::dsa_bwd_dq_kernel<T, D, dsa::MASK_NONE>), grid, dim3(256), 0, st, bp, pl, part);
     }
     if (launch_check("dsa_bwd_dq_kernel")) return 1;
-    if (f.flags & DSA_C2P) {
-      const int64_t n = (int64_t)f.H * pl.prow * D;
-      hipLaunchKernelGGL((dsa::dsa_bwd_reduce_kernel<D>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a->dkr,
-                         part, pl, f.H, R);
-      if (launch_check("dsa_bwd_reduce_kernel")) return 1;
-    }
   }
   if (stages & DSA_STAGE_DKDV) {
     const dsa::PersistentPlan pl = ws.kv;
@@ -275,12 +269,19 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
         hipLaunchKernelGGL((dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_NONE>), grid, dim3(256), 0, st, bp, pl, part);
     }
     if (launch_check("dsa_bwd_dkdv_kernel")) return 1;
-    if (f.flags & DSA_P2C) {
-      const int64_t n = (int64_t)f.H * pl.prow * D;
-      hipLaunchKernelGGL((dsa::dsa_bwd_reduce_kernel<D>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a->dqr,
-                         part, pl, f.H, R);
-      if (launch_check("dsa_bwd_reduce_kernel")) return 1;
-    }
+  }
+  // fold the per-workgroup partial sums of the table gradients into dkr / dqr
+  if ((stages & DSA_STAGE_FOLD) && (f.flags & DSA_C2P)) {
+    const int64_t n = (int64_t)f.H * ws.dq.prow * D;
+    hipLaunchKernelGGL((dsa::dsa_bwd_reduce_kernel<D>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a->dkr,
+                       reinterpret_cast<const float*>(base + ws.part_dkr), ws.dq, f.H, R);
+    if (launch_check("dsa_bwd_reduce_kernel")) return 1;
+  }
+  if ((stages & DSA_STAGE_FOLD) && (f.flags & DSA_P2C)) {
+    const int64_t n = (int64_t)f.H * ws.kv.prow * D;
+    hipLaunchKernelGGL((dsa::dsa_bwd_reduce_kernel<D>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a->dqr,
+                       reinterpret_cast<const float*>(base + ws.part_dqr), ws.kv, f.H, R);
+    if (launch_check("dsa_bwd_reduce_kernel")) return 1;
   }
   return 0;
 }

@@ -57,8 +57,12 @@ enum { DSA_F32 = 0, DSA_BF16 = 1 };
 /* score terms (deberta_v2_native.py:592-598, pos_att_type) */
 enum { DSA_C2P = 1, DSA_P2C = 2 };
 
-/* backward stages, for dsa_bwd_args.stages (0 means all) */
-enum { DSA_STAGE_PREP = 1, DSA_STAGE_DQ = 2, DSA_STAGE_DKDV = 4 };
+/* backward stages, for dsa_bwd_args.stages (0 means all, in this order).
+ * PREP computes rowsum(dO * O) into the workspace; DQ writes dq and DKDV
+ * writes dk, dv, each also leaving per-workgroup partial sums of dkr (DQ)
+ * or dqr (DKDV) in the workspace; FOLD adds those partial sums into dkr /
+ * dqr.  Stages run in separate calls share one workspace. */
+enum { DSA_STAGE_PREP = 1, DSA_STAGE_DQ = 2, DSA_STAGE_DKDV = 4, DSA_STAGE_FOLD = 8 };
 
 typedef struct dsa_fwd_args {
   const void* q;          /* [B, Lq, H, D] */
