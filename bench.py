@@ -213,14 +213,16 @@ def main() -> None:
 
         return f
 
-    run_stage(_lib.DSA_STAGE_PREP)()  # rowsum(dO * O) for the stage timings
-    # one kernel per stage except FOLD (two reduce launches, dkr and dqr)
+    # one stage per kernel, in dependency order (DKDV writes the dS^T that DQ and FOLD read)
+    for st in (_lib.DSA_STAGE_PREP, _lib.DSA_STAGE_DKDV):
+        run_stage(st)()
+    bh = B * H * D
     kernels = {
         "dsa_fwd_kernel": (run_fwd, f_fwd),
-        "dsa_bwd_dq_kernel": (run_stage(_lib.DSA_STAGE_DQ), f_fwd),
-        "dsa_bwd_dkdv_kernel": (run_stage(_lib.DSA_STAGE_DKDV), f_fwd),
-        "dsa_bwd_delta_kernel": (run_stage(_lib.DSA_STAGE_PREP), 0.0),
-        "fold (2x dsa_bwd_reduce_kernel)": (run_stage(_lib.DSA_STAGE_FOLD), 0.0),
+        "dsa_bwd_dkdv_kernel": (run_stage(_lib.DSA_STAGE_DKDV), bh * (6.0 * L * L + 2.0 * L * R)),
+        "dsa_bwd_dq_kernel": (run_stage(_lib.DSA_STAGE_DQ), bh * (2.0 * L * L + 2.0 * L * R)),
+        "fold (dsa_bwd_table_kernel + dsa_bwd_fold_kernel)": (run_stage(_lib.DSA_STAGE_FOLD), bh * 4.0 * L * R),
+        "prep (dsa_bwd_delta_kernel + dsa_bwd_gather_kernel)": (run_stage(_lib.DSA_STAGE_PREP), 0.0),
     }
     per_kernel = {}
     n_k = args.steps if args.kernels_only else max(10, args.steps)

@@ -1,25 +1,36 @@
-// dsa_bwd.h — backward preparation kernel (gfx950): Delta_i = dO_i . O_i.
+// dsa_bwd.h — backward of the fused disentangled attention (gfx950): the
+// math, the workspace it runs through, and the preparation kernels.
 //
-// The backward of the fused attention (ATen autograd of
-// deberta_v2_native.py:592-652 with the c2p/p2c gathers of :389-410) is
+// With s the softmax scale (ATen autograd of deberta_v2_native.py:592-652
+// and of the c2p/p2c gathers of :389-410):
 //   dP = dO V^T,  dS = P * (dP - Delta),  Delta_i = dO_i . O_i
 //   dV = P^T dO
 //   dQ = s dS K   + s sum_j dS_ij Kr[c(i-j)],   dKr[r] = s sum_{c(i-j)=r} dS_ij q_i
 //   dK = s dS^T Q + s sum_i dS_ij Qr[p(i-j)],   dQr[r] = s sum_{p(i-j)=r} dS_ij k_j
-// with s the softmax scale; masked keys and dead query rows have P = 0 and so
-// dS = 0.  dsa_bwd_dq.h computes dQ and dKr, dsa_bwd_dkdv.h dK, dV and dQr.
+// Masked keys and dead query rows have P = 0 and so dS = 0.
+//
+// Kernels, in launch order:
+//   prep   dsa_bwd_delta_kernel (Delta) and dsa_bwd_gather_kernel (krgt,
+//          qrgt: the relative tables gathered per offset d = i - j and
+//          transposed, so a run of consecutive offsets of one head-dim
+//          column is contiguous — the A operand of the offset-band products)
+//   dkdv   dsa_bwd_dkdv_kernel (dsa_bwd_dkdv.h): recomputes the scores and
+//          the softmax per (b, h, 128-key tile), writes dK, dV and dS^T
+//          (bf16 for bf16 inputs), the only (L x L) tensor of the backward
+//   dq     dsa_bwd_dq_kernel (dsa_bwd_dq.h): dQ from dS^T, K and krgt
+//   fold   dsa_bwd_table_kernel + dsa_bwd_fold_kernel (dsa_bwd_table.h):
+//          the table gradients per offset, from dS^T, Q and K, then summed
+//          onto table rows
 #pragma once
 
 #include "dsa_tiles.h"
 
 namespace dsa {
 
-// ===========================================================================
-// prep: delta_i = dO_i . O_i, and the transposed relative tables
-// ===========================================================================
+// delta_i = dO_i . O_i: D / VEC lanes per row, one 16-byte load each, then a
+// butterfly sum.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void dsa_bwd_delta_kernel(BwdParams bp) {
-  // D / VEC lanes per row, one 16-byte load each, then a butterfly sum.
   constexpr int VEC = 16 / sizeof(T);
   constexpr int LPR = D / VEC;
   typedef T vecT __attribute__((ext_vector_type(VEC)));
@@ -42,6 +53,34 @@ __global__ __launch_bounds__(256) void dsa_bwd_delta_kernel(BwdParams bp) {
 #pragma unroll
   for (int m = LPR / 2; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);
   if (row < n && part == 0) bp.delta[row] = acc;
+}
+
+// Table row of offset d (clamped into the relative-position table's range).
+DSA_DEV int offset_row(const int32_t* rel, int d, int Lq, int Lk, int A, bool p2c) {
+  d = min(max(d, -(Lk - 1)), Lq - 1);
+  const int t = min(max(rel[d + Lk - 1], -A), A);
+  return p2c ? p2c_row(t, A) : c2p_row(t, A);
+}
+
+// krgt[h][d][t] = Kr[h][c(t - OFF)][d], qrgt[h][d][t] = Qr[h][p(t - OFF)][d]
+// for t in [0, TGP); one thread per (table, h, d, t), t fastest.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void dsa_bwd_gather_kernel(BwdParams bp) {
+  const FwdParams& p = bp.f;
+  const int64_t per = (int64_t)p.H * D * bp.TGP;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= 2 * per) return;
+  const bool q = idx >= per;
+  if (q ? !(p.flags & 2) : !(p.flags & 1)) return;
+  const int64_t r = q ? idx - per : idx;
+  const int t = (int)(r % bp.TGP);
+  const int d = (int)((r / bp.TGP) % D);
+  const int h = (int)(r / ((int64_t)bp.TGP * D));
+  const int row = offset_row(p.rel, t - bp.OFF, p.Lq, p.Lk, p.A, q);
+  const T* src = q ? (const T*)p.qr + (int64_t)h * p.qrs[0] + (int64_t)row * p.qrs[1]
+                   : (const T*)p.kr + (int64_t)h * p.krs[0] + (int64_t)row * p.krs[1];
+  T* dst = (T*)(q ? bp.qrgt : bp.krgt);
+  dst[r] = src[d];
 }
 
 }  // namespace dsa

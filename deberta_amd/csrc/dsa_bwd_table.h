@@ -1,0 +1,257 @@
+// dsa_bwd_table.h — gradients of the projected relative tables (gfx950).
+//
+//   dKr[r] = s sum_{b,i,j: c(i-j)=r} dS_ij q_i,   dQr[r] = s sum_{b,i,j: p(i-j)=r} dS_ij k_j
+//
+// are computed per offset d = i - j first,
+//   Gc[d] = sum_{b,i} dS(i, i-d) q_i,   Gp[d] = sum_{b,j} dS(j+d, j) k_j,
+// and then summed onto table rows (dsa_bwd_fold_kernel): c(d) and p(d) are
+// monotone in d, so the offsets of one row form a contiguous range.
+//
+// dsa_bwd_table_kernel: one workgroup = (128-offset block [d0, d0+128),
+// head h, batch group).  For each batch and each chunk of 32 keys
+// [j0, j0+32) it stages the dS^T region rows j0.., columns i in
+// [j0 + d0, j0 + d0 + 160) — which holds every pair of the chunk with an
+// offset in the block — with the 32 key rows and a ring of query rows:
+//   Gp^T[dd] += sum_jj  K^T[jj] X[jj][jj + dd]        (X = staged region)
+//   Gc^T[dd] += sum_c   Q^T[i0 + c] X[c - dd][c]
+// Both B operands walk a diagonal of X (eight single-element LDS reads per
+// fragment); zero rows around X cover the out-of-chunk part of the walk.
+// Wave w accumulates offsets [32w, 32w + 32) of the block in registers and
+// writes them once, to a per-(block, head, batch group) partial.
+#pragma once
+
+#include "dsa_bwd.h"
+
+namespace dsa {
+
+namespace tbcfg {
+constexpr int NW = 4;
+constexpr int DBW = 128;           // offsets per block
+constexpr int JC = 32;             // keys per step
+constexpr int XC = DBW + JC;       // staged columns
+constexpr int XP = 16;             // zero rows above the staged rows
+constexpr int XROWS = XP + JC + 32;  // and 32 below
+constexpr int XCOLS = DBW + 48;    // columns a diagonal walk can touch
+constexpr int QRING = 256;         // query rows kept (power of two >= XC)
+}  // namespace tbcfg
+
+// Transposed LDS operand read (see tr_contig) from a ring of rows: logical
+// row k lives at physical row (kbase + k) % QRING.
+template <typename T>
+DSA_DEV typename Mfma<T>::frag tr_contig_ring(const T* X, int str, int kbase, int k0, int m0, int g, int c16) {
+  using namespace tbcfg;
+  if constexpr (sizeof(T) == 2) {
+    const int r0 = (kbase + k0 + 8 * g) & (QRING - 1);      // 4-aligned, so
+    const int r1 = (kbase + k0 + 8 * g + 4) & (QRING - 1);  // rows never wrap
+    return join8(tr4(X, str, r0, m0, c16), tr4(X, str, r1, m0, c16));
+  } else {
+    return tr4(X, str, (kbase + k0 + 4 * g) & (QRING - 1), m0, c16);
+  }
+}
+
+// Rows [r0, r0 + n) of a [L, D] strided matrix into ring rows (zeros for rows
+// outside [0, nvalid)).
+template <typename T, int D>
+DSA_DEV void load_ring_rows(T* ring, int str, const T* src, int64_t rs, int r0, int n, int nvalid, int tid) {
+  using namespace tbcfg;
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr int CPR = D / VEC;
+  typedef T vecT __attribute__((ext_vector_type(VEC)));
+  for (int c = tid; c < n * CPR; c += 256) {
+    const int r = r0 + c / CPR, d0 = (c % CPR) * VEC;
+    vecT x;
+    if (r >= 0 && r < nvalid) {
+      x = *reinterpret_cast<const vecT*>(src + (int64_t)r * rs + d0);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) x[e] = (T)0.0f;
+    }
+    *reinterpret_cast<vecT*>(ring + (r & (QRING - 1)) * str + d0) = x;
+  }
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
+  using namespace tbcfg;
+  using M = Mfma<T>;
+  typedef typename M::frag frag;
+  typedef T vecT __attribute__((ext_vector_type(16 / sizeof(T))));
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr int ND = D / 16;
+  constexpr int FE = M::FRAG_ELEMS;
+  constexpr int KSTR = D + Pad<T>::v;
+  constexpr int XSTR = XCOLS + Pad<T>::v;
+  constexpr int GC_STEPS = (16 + JC + M::KSTEP - 2) / M::KSTEP;  // k steps covering 16 + JC - 1 columns
+  const FwdParams& p = bp.f;
+
+  __shared__ __align__(16) T Xs[XROWS * XSTR];
+  __shared__ __align__(16) T Kc[JC * KSTR];
+  __shared__ __align__(16) T Qring[QRING * KSTR];
+
+  const int tid = threadIdx.x;
+  const int w = tid >> 6, g = (tid & 63) >> 4, c16 = tid & 15;
+  const int dblk = blockIdx.x, h = blockIdx.y, bg = blockIdx.z;
+  const int d0 = -bp.LkP + DBW * dblk;
+  const bool c2p = (p.flags & 1) != 0, p2c = (p.flags & 2) != 0;
+  const int b_lo = bg * bp.BPG, b_hi = min(p.B, b_lo + bp.BPG);
+  // key chunks whose pairs can have an offset in the block
+  int jstart = -d0 - (XC - 2);
+  jstart = jstart > 0 ? (jstart + JC - 1) / JC * JC : 0;
+  const int jend = min(p.Lk, p.Lq - d0);
+
+  // zero rows around the staged region (never overwritten)
+  {
+    constexpr int VPR = XSTR / VEC;
+    for (int c = tid; c < XP * VPR; c += 256) {
+      vecT z;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) z[e] = (T)0.0f;
+      reinterpret_cast<vecT*>(Xs)[c] = z;
+    }
+    for (int c = tid; c < (XROWS - XP - JC) * VPR; c += 256) {
+      vecT z;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) z[e] = (T)0.0f;
+      reinterpret_cast<vecT*>(Xs + (XP + JC) * XSTR)[c] = z;
+    }
+    // the ring starts finite: operand rows outside the staged window are
+    // multiplied by zeros of X, never by uninitialised LDS
+    for (int c = tid; c < QRING * KSTR / VEC; c += 256) {
+      vecT z;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) z[e] = (T)0.0f;
+      reinterpret_cast<vecT*>(Qring)[c] = z;
+    }
+  }
+
+  f32x4 gc[2][ND], gp[2][ND];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int db = 0; db < ND; ++db) gc[t][db] = gp[t][db] = zero4();
+
+  for (int b = b_lo; b < b_hi; ++b) {
+    const T* dsb = (const T*)bp.dst + (int64_t)(b * p.H + h) * bp.LkP * bp.LqP;
+    const T* qbase = (const T*)p.q + (int64_t)b * p.qs[0] + (int64_t)h * p.qs[2];
+    const T* kbase = (const T*)p.k + (int64_t)b * p.ks[0] + (int64_t)h * p.ks[2];
+    for (int j0 = jstart; j0 < jend; j0 += JC) {
+      const int ib0 = j0 + d0;  // query of staged column 0 (a multiple of 32)
+      __syncthreads();          // previous step's readers are done
+      // dS^T rows j0.., columns [ib0, ib0 + XC): 16-byte chunks, each wholly in or out of [0, LqP)
+      for (int c = tid; c < JC * (XC / VEC); c += 256) {
+        const int r = c / (XC / VEC), c0 = (c % (XC / VEC)) * VEC;
+        const int i = ib0 + c0;
+        vecT x;
+        if (i >= 0 && i < bp.LqP) {
+          x = *reinterpret_cast<const vecT*>(dsb + (int64_t)(j0 + r) * bp.LqP + i);
+        } else {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) x[e] = (T)0.0f;
+        }
+        *reinterpret_cast<vecT*>(Xs + (XP + r) * XSTR + c0) = x;
+      }
+      if (p2c) load_rows<T, D, JC, 256>(Kc, KSTR, nullptr, 0, kbase, p.ks[1], j0, p.Lk, tid);
+      if (c2p) {
+        if (j0 == jstart) load_ring_rows<T, D>(Qring, KSTR, qbase, p.qs[1], ib0, XC, p.Lq, tid);
+        else load_ring_rows<T, D>(Qring, KSTR, qbase, p.qs[1], ib0 + XC - JC, JC, p.Lq, tid);
+      }
+      __syncthreads();
+
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int c0 = 16 * (2 * w + t);  // first offset of this wave's 16-offset block
+        if (p2c) {
+          // Gp^T[d][dd] += sum_jj K^T[d][jj] X[jj][jj + dd],  jj = KSTEP*s + FE*g + e
+#pragma unroll
+          for (int s = 0; s < JC / M::KSTEP; ++s) {
+            frag bfr;
+            const T* dg = Xs + (XP + M::KSTEP * s + FE * g) * XSTR + M::KSTEP * s + FE * g + c0 + c16;
+#pragma unroll
+            for (int e = 0; e < FE; ++e) bfr[e] = dg[e * (XSTR + 1)];
+#pragma unroll
+            for (int db = 0; db < ND; ++db) {
+              const frag af = tr_contig<T>(Kc, KSTR, s * M::KSTEP, 16 * db, g, c16);
+              gp[t][db] = M::mma(af, bfr, gp[t][db]);
+            }
+          }
+        }
+        if (c2p) {
+          // Gc^T[d][dd] += sum_c Q^T[d][ib0 + c] X[c - dd][c],  c = c0 + KSTEP*s + FE*g + e
+#pragma unroll
+          for (int s = 0; s < GC_STEPS; ++s) {
+            frag bfr;
+            const int k = M::KSTEP * s + FE * g;  // c - c0 of element e = 0
+            const T* dg = Xs + (XP + k - c16) * XSTR + c0 + k;
+#pragma unroll
+            for (int e = 0; e < FE; ++e) bfr[e] = dg[e * (XSTR + 1)];
+#pragma unroll
+            for (int db = 0; db < ND; ++db) {
+              const frag af = tr_contig_ring<T>(Qring, KSTR, ib0, c0 + M::KSTEP * s, 16 * db, g, c16);
+              gc[t][db] = M::mma(af, bfr, gc[t][db]);
+            }
+          }
+        }
+      }
+    }
+  }
+
+  // partial of this (block, head, batch group): [type][dd][d], fp32
+  float* out = bp.gpart + ((int64_t)(h * bp.NDB + dblk) * bp.NBG + bg) * 2 * DBW * D;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int dd = 16 * (2 * w + t) + c16;
+#pragma unroll
+    for (int db = 0; db < ND; ++db) {
+      *reinterpret_cast<f32x4*>(out + (int64_t)dd * D + 16 * db + 4 * g) = gc[t][db];
+      *reinterpret_cast<f32x4*>(out + (int64_t)(DBW + dd) * D + 16 * db + 4 * g) = gp[t][db];
+    }
+  }
+}
+
+// tab[h][r][:] += s * sum over batch groups and offsets d with row(d) = r of
+// the partials; one thread per (table, h, r, 4 columns).
+template <int D>
+__global__ __launch_bounds__(256) void dsa_bwd_fold_kernel(BwdParams bp) {
+  using namespace tbcfg;
+  const FwdParams& p = bp.f;
+  const int R = 2 * p.A;
+  constexpr int Q4 = D / 4;
+  const int64_t per = (int64_t)p.H * R * Q4;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= 2 * per) return;
+  const bool q = idx >= per;  // false: dKr (c2p), true: dQr (p2c)
+  if (q ? !(p.flags & 2) : !(p.flags & 1)) return;
+  const int64_t rr = q ? idx - per : idx;
+  const int c4 = (int)(rr % Q4);
+  const int r = (int)((rr / Q4) % R);
+  const int h = (int)(rr / ((int64_t)Q4 * R));
+  // row(d) is non-decreasing in d for c2p and non-increasing for p2c: find
+  // the first d with row "at or past" r, then the first d past r.
+  auto past = [&](int d, bool strict) {
+    const int x = offset_row(p.rel, d, p.Lq, p.Lk, p.A, q);
+    return q ? (strict ? x < r : x <= r) : (strict ? x > r : x >= r);
+  };
+  const int dmin = -(p.Lk - 1), dmax = p.Lq - 1;
+  int lo = dmin, hi = dmax + 1;
+  while (lo < hi) {
+    const int mid = lo + ((hi - lo) >> 1);
+    if (past(mid, false)) hi = mid; else lo = mid + 1;
+  }
+  int lo2 = lo, hi2 = dmax + 1;
+  while (lo2 < hi2) {
+    const int mid = lo2 + ((hi2 - lo2) >> 1);
+    if (past(mid, true)) hi2 = mid; else lo2 = mid + 1;
+  }
+  f32x4 acc = zero4();
+  for (int d = lo; d < lo2; ++d) {
+    const int dblk = (d + bp.LkP) / DBW, dd = (d + bp.LkP) % DBW;
+    const float* src = bp.gpart + ((int64_t)(h * bp.NDB + dblk) * bp.NBG) * 2 * DBW * D +
+                       (int64_t)((q ? DBW : 0) + dd) * D + 4 * c4;
+    for (int k = 0; k < bp.NBG; ++k) acc += *reinterpret_cast<const f32x4*>(src + (int64_t)k * 2 * DBW * D);
+  }
+  float* tab = (q ? bp.dqr : bp.dkr) + ((int64_t)h * R + r) * D + 4 * c4;
+  f32x4 cur = *reinterpret_cast<f32x4*>(tab);
+  *reinterpret_cast<f32x4*>(tab) = cur + acc * p.scale;
+}
+
+}  // namespace dsa

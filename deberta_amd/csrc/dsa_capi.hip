@@ -12,6 +12,7 @@
 #include "dsa_bwd.h"
 #include "dsa_bwd_dkdv.h"
 #include "dsa_bwd_dq.h"
+#include "dsa_bwd_table.h"
 #include "dsa_fwd.h"
 
 namespace {
@@ -131,40 +132,6 @@ int fwd_mask(const dsa::FwdParams& p, int mode, hipStream_t st) {
   }
 }
 
-// Occupancy (workgroups per CU) of a kernel; 1 if the query fails.
-int occupancy_of(const void* fn) {
-  int occ = 0;
-  const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, 256, 0);
-  return (e == hipSuccess && occ > 0) ? occ : 1;
-}
-
-template <typename T, int D>
-const void* dq_kernel_ptr(int mode) {
-  switch (mode) {
-    case dsa::MASK_KEY: return (const void*)dsa::dsa_bwd_dq_kernel<T, D, dsa::MASK_KEY>;
-    case dsa::MASK_PAIR: return (const void*)dsa::dsa_bwd_dq_kernel<T, D, dsa::MASK_PAIR>;
-    default: return (const void*)dsa::dsa_bwd_dq_kernel<T, D, dsa::MASK_NONE>;
-  }
-}
-
-template <typename T, int D>
-const void* dkdv_kernel_ptr(int mode) {
-  switch (mode) {
-    case dsa::MASK_KEY: return (const void*)dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_KEY>;
-    case dsa::MASK_PAIR: return (const void*)dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_PAIR>;
-    default: return (const void*)dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_NONE>;
-  }
-}
-
-const void* bwd_kernel_ptr(const dsa_fwd_args& f, int mode, bool dkdv) {
-  if (f.dtype == DSA_BF16) {
-    if (f.D == 64) return dkdv ? dkdv_kernel_ptr<dsa::bf16, 64>(mode) : dq_kernel_ptr<dsa::bf16, 64>(mode);
-    return dkdv ? dkdv_kernel_ptr<dsa::bf16, 32>(mode) : dq_kernel_ptr<dsa::bf16, 32>(mode);
-  }
-  if (f.D == 64) return dkdv ? dkdv_kernel_ptr<float, 64>(mode) : dq_kernel_ptr<float, 64>(mode);
-  return dkdv ? dkdv_kernel_ptr<float, 32>(mode) : dq_kernel_ptr<float, 32>(mode);
-}
-
 int device_cus() {
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 256;
@@ -172,41 +139,41 @@ int device_cus() {
   return cus;
 }
 
-// Work decomposition of a persistent backward kernel: items (head, batch,
-// tile) with the head slowest, split into contiguous runs, one per resident
-// workgroup.
-dsa::PersistentPlan bwd_plan(const dsa_fwd_args& f, int mode, bool dkdv) {
-  dsa::PersistentPlan pl;
-  const int tile = dkdv ? dsa::kvcfg::BKW : dsa::dqcfg::BQ;
-  const int tiles = ((dkdv ? f.Lk : f.Lq) + tile - 1) / tile;
-  pl.per_head = f.B * tiles;
-  pl.items = f.H * pl.per_head;
-  const int slots_avail = device_cus() * occupancy_of(bwd_kernel_ptr(f, mode, dkdv));
-  pl.grid = pl.items < slots_avail ? pl.items : slots_avail;
-  const int run = (pl.items + pl.grid - 1) / pl.grid;
-  pl.slots = (run + pl.per_head - 1) / pl.per_head + 1;
-  const int R = 2 * f.att_span;
-  pl.prow = R < 512 ? R : 512;
-  return pl;
-}
+int round_up(int x, int a) { return (x + a - 1) / a * a; }
 
+// Workspace of the backward (offsets 256-byte aligned) and the padded
+// extents the kernels share.
 struct WsLayout {
-  size_t delta, part_dkr, part_dqr, total;
-  dsa::PersistentPlan dq, kv;
+  int LqP, LkP, TGP, OFF, NDB, NBG, BPG;
+  size_t delta, krgt, qrgt, dst, gpart, total;
 };
 
 WsLayout ws_layout(const dsa_bwd_args* a) {
   const dsa_fwd_args& f = a->fwd;
+  const size_t es = (size_t)elem_bytes(f.dtype);
   WsLayout w;
-  w.dq = bwd_plan(f, mask_mode(&f), false);
-  w.kv = bwd_plan(f, mask_mode(&f), true);
+  w.LqP = round_up(f.Lq, 128);
+  w.LkP = round_up(f.Lk, 128);
+  w.OFF = w.LkP - 1;            // offset origin: t = d + OFF, 32-aligned tile starts
+  w.TGP = w.LqP + w.LkP;        // offsets [-(LkP - 1), LqP] of every band window
+  w.NDB = (w.LqP + w.LkP) / dsa::tbcfg::DBW;
+  // batch groups of the table kernel: about two workgroups per CU
+  const int per = f.H * w.NDB;
+  int groups = (2 * device_cus() + per - 1) / per;
+  groups = groups < 1 ? 1 : (groups > f.B ? f.B : groups);
+  w.BPG = (f.B + groups - 1) / groups;
+  w.NBG = (f.B + w.BPG - 1) / w.BPG;
   size_t off = 0;
   w.delta = off;
   off = align_up(off + (size_t)f.B * f.H * f.Lq * sizeof(float), 256);
-  w.part_dkr = off;
-  if (f.flags & DSA_C2P) off = align_up(off + (size_t)w.dq.grid * w.dq.slots * w.dq.prow * f.D * sizeof(float), 256);
-  w.part_dqr = off;
-  if (f.flags & DSA_P2C) off = align_up(off + (size_t)w.kv.grid * w.kv.slots * w.kv.prow * f.D * sizeof(float), 256);
+  w.krgt = off;
+  if (f.flags & DSA_C2P) off = align_up(off + (size_t)f.H * f.D * w.TGP * es, 256);
+  w.qrgt = off;
+  if (f.flags & DSA_P2C) off = align_up(off + (size_t)f.H * f.D * w.TGP * es, 256);
+  w.dst = off;
+  off = align_up(off + (size_t)f.B * f.H * w.LkP * w.LqP * es, 256);
+  w.gpart = off;
+  if (f.flags) off = align_up(off + (size_t)f.H * w.NDB * w.NBG * 2 * dsa::tbcfg::DBW * f.D * sizeof(float), 256);
   w.total = off;
   return w;
 }
@@ -230,58 +197,54 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
   bp.dqr = a->dqr;
   char* base = static_cast<char*>(a->workspace);
   bp.delta = reinterpret_cast<float*>(base + ws.delta);
+  bp.krgt = base + ws.krgt;
+  bp.qrgt = base + ws.qrgt;
+  bp.dst = base + ws.dst;
+  bp.gpart = reinterpret_cast<float*>(base + ws.gpart);
+  bp.LqP = ws.LqP;
+  bp.LkP = ws.LkP;
+  bp.TGP = ws.TGP;
+  bp.OFF = ws.OFF;
+  bp.NDB = ws.NDB;
+  bp.NBG = ws.NBG;
+  bp.BPG = ws.BPG;
   const int stages = a->stages ? a->stages : (DSA_STAGE_PREP | DSA_STAGE_DQ | DSA_STAGE_DKDV | DSA_STAGE_FOLD);
-  const int R = 2 * f.att_span;
 
   if (stages & DSA_STAGE_PREP) {
     const int64_t n = (int64_t)f.B * f.H * f.Lq * (D / (16 / (int)sizeof(T)));
     hipLaunchKernelGGL((dsa::dsa_bwd_delta_kernel<T, D>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, bp);
     if (launch_check("dsa_bwd_delta_kernel")) return 1;
-  }
-  if (stages & DSA_STAGE_DQ) {
-    const dsa::PersistentPlan pl = ws.dq;
-    float* part = reinterpret_cast<float*>(base + ws.part_dkr);
-    dim3 grid(pl.grid);
-    switch (mode) {
-      case dsa::MASK_KEY:
-        hipLaunchKernelGGL((dsa::dsa_bwd_dq_kernel<T, D, dsa::MASK_KEY>), grid, dim3(256), 0, st, bp, pl, part);
-        break;
-      case dsa::MASK_PAIR:
-        hipLaunchKernelGGL((dsa::dsa_bwd_dq_kernel<T, D, dsa::MASK_PAIR>), grid, dim3(256), 0, st, bp, pl, part);
-        break;
-      default:
-        hipLaunchKernelGGL((dsa::dsa_bwd_dq_kernel<T, D, dsa::MASK_NONE>), grid, dim3(256), 0, st, bp, pl, part);
+    if (f.flags) {
+      const int64_t m = 2 * (int64_t)f.H * D * ws.TGP;
+      hipLaunchKernelGGL((dsa::dsa_bwd_gather_kernel<T, D>), dim3((unsigned)((m + 255) / 256)), dim3(256), 0, st, bp);
+      if (launch_check("dsa_bwd_gather_kernel")) return 1;
     }
-    if (launch_check("dsa_bwd_dq_kernel")) return 1;
   }
   if (stages & DSA_STAGE_DKDV) {
-    const dsa::PersistentPlan pl = ws.kv;
-    float* part = reinterpret_cast<float*>(base + ws.part_dqr);
-    dim3 grid(pl.grid);
+    dim3 grid(ws.LkP / dsa::kvcfg::BKW, f.H, f.B);
     switch (mode) {
       case dsa::MASK_KEY:
-        hipLaunchKernelGGL((dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_KEY>), grid, dim3(256), 0, st, bp, pl, part);
+        hipLaunchKernelGGL((dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_KEY>), grid, dim3(256), 0, st, bp);
         break;
       case dsa::MASK_PAIR:
-        hipLaunchKernelGGL((dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_PAIR>), grid, dim3(256), 0, st, bp, pl, part);
+        hipLaunchKernelGGL((dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_PAIR>), grid, dim3(256), 0, st, bp);
         break;
       default:
-        hipLaunchKernelGGL((dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_NONE>), grid, dim3(256), 0, st, bp, pl, part);
+        hipLaunchKernelGGL((dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_NONE>), grid, dim3(256), 0, st, bp);
     }
     if (launch_check("dsa_bwd_dkdv_kernel")) return 1;
   }
-  // fold the per-workgroup partial sums of the table gradients into dkr / dqr
-  if ((stages & DSA_STAGE_FOLD) && (f.flags & DSA_C2P)) {
-    const int64_t n = (int64_t)f.H * ws.dq.prow * D;
-    hipLaunchKernelGGL((dsa::dsa_bwd_reduce_kernel<D>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a->dkr,
-                       reinterpret_cast<const float*>(base + ws.part_dkr), ws.dq, f.H, R);
-    if (launch_check("dsa_bwd_reduce_kernel")) return 1;
+  if (stages & DSA_STAGE_DQ) {
+    dim3 grid(ws.LqP / dsa::dqcfg::BQ, f.H, f.B);
+    hipLaunchKernelGGL((dsa::dsa_bwd_dq_kernel<T, D>), grid, dim3(256), 0, st, bp);
+    if (launch_check("dsa_bwd_dq_kernel")) return 1;
   }
-  if ((stages & DSA_STAGE_FOLD) && (f.flags & DSA_P2C)) {
-    const int64_t n = (int64_t)f.H * ws.kv.prow * D;
-    hipLaunchKernelGGL((dsa::dsa_bwd_reduce_kernel<D>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a->dqr,
-                       reinterpret_cast<const float*>(base + ws.part_dqr), ws.kv, f.H, R);
-    if (launch_check("dsa_bwd_reduce_kernel")) return 1;
+  if ((stages & DSA_STAGE_FOLD) && f.flags) {
+    hipLaunchKernelGGL((dsa::dsa_bwd_table_kernel<T, D>), dim3(ws.NDB, f.H, ws.NBG), dim3(256), 0, st, bp);
+    if (launch_check("dsa_bwd_table_kernel")) return 1;
+    const int64_t n = 2 * (int64_t)f.H * (2 * f.att_span) * (D / 4);
+    hipLaunchKernelGGL((dsa::dsa_bwd_fold_kernel<D>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, bp);
+    if (launch_check("dsa_bwd_fold_kernel")) return 1;
   }
   return 0;
 }

@@ -37,7 +37,15 @@ struct BwdParams {
   int64_t dqs[3], dks[3], dvs[3];
   float* dkr;
   float* dqr;
-  float* delta;     // [B, H, Lq] rowwise dO . O (workspace)
+  // workspace
+  float* delta;     // [B, H, Lq] rowwise dO . O
+  void* dst;        // dS^T [B, H, LkP, LqP], zero outside [0, Lk) x [0, Lq)
+  void* krgt;       // [H, D, TGP]: krgt[h][d][t] = Kr[h][c(t - OFF)][d]
+  void* qrgt;       // [H, D, TGP]: qrgt[h][d][t] = Qr[h][p(t - OFF)][d]
+  float* gpart;     // table-gradient partials [H][NDB][NBG][2][128][D]
+  int LqP, LkP;     // padded query / key extents of dS^T
+  int TGP, OFF;     // row length and offset origin of krgt / qrgt
+  int NDB, NBG, BPG;  // offset blocks, batch groups, batches per group
 };
 
 template <typename T>

@@ -57,11 +57,14 @@ enum { DSA_F32 = 0, DSA_BF16 = 1 };
 /* score terms (deberta_v2_native.py:592-598, pos_att_type) */
 enum { DSA_C2P = 1, DSA_P2C = 2 };
 
-/* backward stages, for dsa_bwd_args.stages (0 means all, in this order).
- * PREP computes rowsum(dO * O) into the workspace; DQ writes dq and DKDV
- * writes dk, dv, each also leaving per-workgroup partial sums of dkr (DQ)
- * or dqr (DKDV) in the workspace; FOLD adds those partial sums into dkr /
- * dqr.  Stages run in separate calls share one workspace. */
+/* backward stages, for dsa_bwd_args.stages (0 means all).  They run in the
+ * order PREP, DKDV, DQ, FOLD and pass data through the workspace:
+ *   PREP  rowsum(dO * O) and the relative tables gathered per offset
+ *   DKDV  writes dk and dv, and dS^T into the workspace
+ *   DQ    writes dq from dS^T
+ *   FOLD  adds the relative-table gradients (from dS^T) into dkr / dqr
+ * Stages run in separate calls must keep this order and share one
+ * workspace. */
 enum { DSA_STAGE_PREP = 1, DSA_STAGE_DQ = 2, DSA_STAGE_DKDV = 4, DSA_STAGE_FOLD = 8 };
 
 typedef struct dsa_fwd_args {
