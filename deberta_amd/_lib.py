@@ -21,6 +21,7 @@ DSA_STAGE_PREP = 1
 DSA_STAGE_DQ = 2
 DSA_STAGE_DKDV = 4
 DSA_STAGE_FOLD = 8
+DSA_STAGE_DKP = 16
 
 EXPECTED_VERSION = 1
 

@@ -10,11 +10,9 @@
 //   dV^T         += dO^T P,  dK^T += Q^T dS        (dO^T, Q^T read transposed
 //                                                   from LDS)
 //   dS^T          stored to the workspace (row j, 4 consecutive queries per
-//                 lane): the dq and table kernels read it
-//   dK^T (p2c)   += sum_x qrgt[x]^T F[x][j], where F is the wave's dS stored
-//                 by offset, F[x][j] = dS(i, j) with
-//                 x = (i - i0) - (j - jw) + 31, and qrgt the Qr rows gathered
-//                 per offset (one contiguous 16-byte load per operand)
+//                 lane): the dq, dkp and table kernels read it
+// With p2c, dK is left unscaled in fp32 in the workspace and completed by
+// dsa_bwd_dkp_kernel (dsa_bwd_dkp.h), which adds the p2c term from dS^T.
 // Every query tile of the padded extent is visited, so dS^T is fully written
 // (zeros for masked pairs, dead rows and padding).
 #pragma once
@@ -31,7 +29,6 @@ constexpr int CBS = XG + 5;       // shared c2p band row stride [i][x]
 constexpr int PBS = WK + 1;       // per-wave p2c band row stride [x][j]
 constexpr int CB_ELEMS = BQ * CBS;
 constexpr int PB_ELEMS = XW * PBS;
-constexpr int DS2 = 40;           // per-wave dS-by-offset row stride [x][j]
 }  // namespace kvcfg
 
 // Row tables of offsets dbase + x, x in [0, 192).
@@ -149,9 +146,7 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void dsa_bwd_dkdv_kern
   constexpr int NS = D / M::KSTEP;
   constexpr int ND = D / 16;
   constexpr int KSTR = D + Pad<T>::v;
-  constexpr int BANDS_BYTES = (CB_ELEMS + NW * PB_ELEMS) * (int)sizeof(BT);
-  constexpr int DSD_BYTES = NW * XW * DS2 * (int)sizeof(T);
-  constexpr int UNI_BYTES = BANDS_BYTES > DSD_BYTES ? BANDS_BYTES : DSD_BYTES;
+  constexpr int UNI_BYTES = (CB_ELEMS + NW * PB_ELEMS) * (int)sizeof(BT);
   const FwdParams& p = bp.f;
 
   __shared__ __align__(16) T Qs[BQ * KSTR];
@@ -167,7 +162,6 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void dsa_bwd_dkdv_kern
   const bool p2c = (p.flags & 2) != 0;
   BT* cbs = reinterpret_cast<BT*>(uni);
   BT* pbw = reinterpret_cast<BT*>(uni) + CB_ELEMS + w * PB_ELEMS;
-  T* dsd = reinterpret_cast<T*>(uni) + w * XW * DS2;
   const float sl2 = p.scale * kLog2e;
   const int nqt = bp.LqP / BQ;
 
@@ -179,7 +173,6 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void dsa_bwd_dkdv_kern
   const T* dobase = (const T*)bp.dout + (int64_t)b * bp.dos[0] + (int64_t)h * bp.dos[2];
   const T* krh = (p.flags & 1) ? (const T*)p.kr + (int64_t)h * p.krs[0] : nullptr;
   const T* qrh = p2c ? (const T*)p.qr + (int64_t)h * p.qrs[0] : nullptr;
-  const T* qrg = p2c ? (const T*)bp.qrgt + (int64_t)h * D * bp.TGP : nullptr;
   const uint8_t* kkb = (MASK == MASK_KEY) ? p.kk + (int64_t)b * p.kkb : nullptr;
   const uint8_t* pkb = (MASK == MASK_PAIR) ? p.pk + (int64_t)b * p.pkb : nullptr;
   const float* lseb = p.lse + ((int64_t)b * p.H + h) * Lq;
@@ -212,7 +205,7 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void dsa_bwd_dkdv_kern
   f32x4 dka[ND][2], dva[ND][2];
 #pragma unroll
   for (int db = 0; db < ND; ++db) dka[db][0] = dka[db][1] = dva[db][0] = dva[db][1] = zero4();
-  f32x4 ds[2][4];
+  const f32x4 zt[2][4] = {};
 
   for (int qi = 0; qi < nqt; ++qi) {
     const int i0 = qi * BQ;
@@ -235,7 +228,7 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void dsa_bwd_dkdv_kern
       skip = !__syncthreads_or(keep);
     }
     if (skip) {
-      store_dst<T>(dstw, bp.LqP, i0, ds, true, g, c16);
+      store_dst<T>(dstw, bp.LqP, i0, zt, true, g, c16);
       continue;
     }
     __syncthreads();  // previous tile's LDS readers are done
@@ -274,83 +267,66 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void dsa_bwd_dkdv_kern
                                 sl2);
     }
 
-    // ---- P, dP, dS ----------------------------------------------------------------------
-    f32x4 pp[2][4];
+    // ---- per 32-query half: P, dP, dS, then dV^T += dO^T P, dK^T += Q^T dS ---------------
+    // (dO^T, Q^T read transposed from LDS); dS is also stored to dS^T.
+    constexpr int HALVES = 2, IBH = 4 / HALVES, SPH = IBH * 16 / M::KSTEP;
 #pragma unroll
-    for (int ib = 0; ib < 4; ++ib) {
-      frag dof[NS];
+    for (int hh = 0; hh < HALVES; ++hh) {
+      f32x4 pp[2][IBH], dsh[2][IBH];
 #pragma unroll
-      for (int s = 0; s < NS; ++s) dof[s] = M::load_contig(&dOs[(16 * ib + c16) * KSTR], s, g);
+      for (int t = 0; t < IBH; ++t) {
+        const int ib = IBH * hh + t;
+        frag dof[NS];
 #pragma unroll
-      for (int jb = 0; jb < 2; ++jb) {
-        f32x4 dp = zero4();
-#pragma unroll
-        for (int s = 0; s < NS; ++s) dp = M::mma(dof[s], vb[jb][s], dp);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int il = 16 * ib + 4 * g + e;
-          const int i = i0 + il;
-          bool keep = jkeep[jb];
-          if (MASK == MASK_PAIR) keep = keep && i < Lq && pkb[(int64_t)i * p.pkq + jcol[jb]] != 0;
-          const float pe = keep ? exp2f(sc[jb][ib][e] - rowv[il]) : 0.f;
-          pp[jb][ib][e] = pe;
-          ds[jb][ib][e] = pe * (dp[e] - rowv[BQ + il]);
-        }
-      }
-    }
-
-    // ---- dV^T += dO^T P,  dK^T += Q^T dS (dO^T, Q^T read transposed) -----------------------
-#pragma unroll
-    for (int s = 0; s < BQ / M::KSTEP; ++s) {
-      frag pf[2], df[2];
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb) {
-        pf[jb] = M::from_acc(pp[jb], s);
-        df[jb] = M::from_acc(ds[jb], s);
-      }
-#pragma unroll
-      for (int db = 0; db < ND; ++db) {
-        const frag dotf = tr_acc<T>(dOs, KSTR, s * M::KSTEP, 16 * db, g, c16);
-        const frag qtf = tr_acc<T>(Qs, KSTR, s * M::KSTEP, 16 * db, g, c16);
+        for (int s = 0; s < NS; ++s) dof[s] = M::load_contig(&dOs[(16 * ib + c16) * KSTR], s, g);
 #pragma unroll
         for (int jb = 0; jb < 2; ++jb) {
-          dva[db][jb] = M::mma(dotf, pf[jb], dva[db][jb]);
-          dka[db][jb] = M::mma(qtf, df[jb], dka[db][jb]);
+          f32x4 dp = zero4();
+#pragma unroll
+          for (int s = 0; s < NS; ++s) dp = M::mma(dof[s], vb[jb][s], dp);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int il = 16 * ib + 4 * g + e;
+            const int i = i0 + il;
+            bool keep = jkeep[jb];
+            if (MASK == MASK_PAIR) keep = keep && i < Lq && pkb[(int64_t)i * p.pkq + jcol[jb]] != 0;
+            const float pe = keep ? exp2f(sc[jb][ib][e] - rowv[il]) : 0.f;
+            pp[jb][t][e] = pe;
+            dsh[jb][t][e] = pe * (dp[e] - rowv[BQ + il]);
+          }
         }
       }
-    }
-
-    store_dst<T>(dstw, bp.LqP, i0, ds, false, g, c16);
-
-    // ---- p2c: dK^T[d][j] += sum_x qrgt[d][t0 + x] F[x][j] -------------------------------------
-    if (p2c) {
-      __syncthreads();  // every wave is done with the score bands; the union region is free
-      {
-        constexpr int DSD_V = XW * DS2 * (int)sizeof(T) / 16;
-        f32x4* z = reinterpret_cast<f32x4*>(dsd);
-        for (int x = (tid & 63); x < DSD_V; x += 64) z[x] = zero4();
-        wave_lds_sync();
-        // x_local = (16*ib + 4*g + e) - (16*jb + c16) + 31, column j_local = 16*jb + c16
-        T* base = dsd + (4 * g - c16 + 31) * DS2 + c16;
+      // dS^T rows: 4 consecutive queries per store
 #pragma unroll
-        for (int jb = 0; jb < 2; ++jb)
+      for (int jb = 0; jb < 2; ++jb) {
+        typedef T vec4 __attribute__((ext_vector_type(4)));
+        T* row = dstw + (int64_t)(16 * jb + c16) * bp.LqP + i0 + 4 * g;
 #pragma unroll
-          for (int ib = 0; ib < 4; ++ib)
+        for (int t = 0; t < IBH; ++t) {
+          vec4 v;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) base[(16 * ib + e - 16 * jb) * DS2 + 16 * jb] = (T)ds[jb][ib][e];
-        wave_lds_sync();
+          for (int e = 0; e < 4; ++e) v[e] = (T)dsh[jb][t][e];
+          *reinterpret_cast<vec4*>(row + 16 * (IBH * hh + t)) = v;
+        }
       }
-      const int t0 = i0 - jw - 31 + bp.OFF;  // qrgt column of x = 0 (a multiple of 32)
 #pragma unroll
-      for (int s = 0; s < XW / M::KSTEP; ++s) {
-        frag bfr[2];
+      for (int sh = 0; sh < SPH; ++sh) {
+        const int s = hh * SPH + sh;
+        frag pf[2], df[2];
 #pragma unroll
-        for (int jb = 0; jb < 2; ++jb) bfr[jb] = tr_contig<T>(dsd, DS2, s * M::KSTEP, 16 * jb, g, c16);
+        for (int jb = 0; jb < 2; ++jb) {
+          pf[jb] = M::from_acc(pp[jb], sh);
+          df[jb] = M::from_acc(dsh[jb], sh);
+        }
 #pragma unroll
         for (int db = 0; db < ND; ++db) {
-          const frag af = M::load_contig(qrg + (int64_t)(16 * db + c16) * bp.TGP + t0, s, g);
+          const frag dotf = tr_acc<T>(dOs, KSTR, s * M::KSTEP, 16 * db, g, c16);
+          const frag qtf = tr_acc<T>(Qs, KSTR, s * M::KSTEP, 16 * db, g, c16);
 #pragma unroll
-          for (int jb = 0; jb < 2; ++jb) dka[db][jb] = M::mma(af, bfr[jb], dka[db][jb]);
+          for (int jb = 0; jb < 2; ++jb) {
+            dva[db][jb] = M::mma(dotf, pf[jb], dva[db][jb]);
+            dka[db][jb] = M::mma(qtf, df[jb], dka[db][jb]);
+          }
         }
       }
     }
@@ -359,6 +335,7 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void dsa_bwd_dkdv_kern
   // ---- dK, dV ------------------------------------------------------------------------------
   T* dkbase = (T*)bp.dk + (int64_t)b * bp.dks[0] + (int64_t)h * bp.dks[2];
   T* dvbase = (T*)bp.dv + (int64_t)b * bp.dvs[0] + (int64_t)h * bp.dvs[2];
+  float* dkcw = p2c ? bp.dkc + ((int64_t)(b * p.H + h) * bp.LkP) * D : nullptr;
 #pragma unroll
   for (int jb = 0; jb < 2; ++jb) {
     const int j = jcol[jb];
@@ -374,7 +351,11 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void dsa_bwd_dkdv_kern
           kv[e] = (T)(dka[db][jb][e] * p.scale);
           vv[e] = (T)(dva[db][jb][e]);
         }
-        *reinterpret_cast<vec4*>(krow + 16 * db + 4 * g) = kv;
+        if (p2c) {  // content part of dK, completed by dsa_bwd_dkp_kernel
+          *reinterpret_cast<f32x4*>(dkcw + (int64_t)j * D + 16 * db + 4 * g) = dka[db][jb];
+        } else {
+          *reinterpret_cast<vec4*>(krow + 16 * db + 4 * g) = kv;
+        }
         *reinterpret_cast<vec4*>(vrow + 16 * db + 4 * g) = vv;
       }
     }

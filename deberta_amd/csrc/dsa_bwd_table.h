@@ -70,18 +70,33 @@ DSA_DEV void load_ring_rows(T* ring, int str, const T* src, int64_t rs, int r0, 
   }
 }
 
+// Number of 32-key chunks of offset block dblk that hold pairs with an
+// offset in the block, and the first of them.
+DSA_DEV void block_chunks(int dblk, int LkP, int Lq, int Lk, int* jstart, int* nch) {
+  using namespace tbcfg;
+  const int d0 = -LkP + DBW * dblk;
+  int js = -d0 - (XC - 2);  // the last staged column must reach query 0
+  js = js > 0 ? (js + JC - 1) / JC * JC : 0;
+  const int je = min(Lk, Lq - d0);
+  *jstart = js;
+  *nch = je > js ? (je - js + JC - 1) / JC : 0;
+}
+
 template <typename T, int D>
 __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
   using namespace tbcfg;
   using M = Mfma<T>;
   typedef typename M::frag frag;
-  typedef T vecT __attribute__((ext_vector_type(16 / sizeof(T))));
   constexpr int VEC = 16 / sizeof(T);
+  typedef T vecT __attribute__((ext_vector_type(VEC)));
   constexpr int ND = D / 16;
   constexpr int FE = M::FRAG_ELEMS;
   constexpr int KSTR = D + Pad<T>::v;
   constexpr int XSTR = XCOLS + Pad<T>::v;
   constexpr int GC_STEPS = (16 + JC + M::KSTEP - 2) / M::KSTEP;  // k steps covering 16 + JC - 1 columns
+  constexpr int XV = JC * XC / VEC;   // 16-byte chunks of the staged region
+  constexpr int RV = JC * D / VEC;    // 16-byte chunks of 32 key (or query) rows
+  constexpr int XCH = (XV + 255) / 256, RCH = (RV + 255) / 256;
   const FwdParams& p = bp.f;
 
   __shared__ __align__(16) T Xs[XROWS * XSTR];
@@ -90,38 +105,30 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, g = (tid & 63) >> 4, c16 = tid & 15;
-  const int dblk = blockIdx.x, h = blockIdx.y, bg = blockIdx.z;
+  // Work order: blockIdx.x enumerates (offset block, head, batch group) with
+  // the offset blocks that have the most key chunks first, so the shortest
+  // workgroups fill in at the end of the launch.
+  const int per_blk = p.H * bp.NBG;
+  const int rank = blockIdx.x / per_blk, rem = blockIdx.x % per_blk;
+  const int h = rem / bp.NBG, bg = rem % bp.NBG;
+  const int mid = (bp.NDB - 1) / 2;   // central blocks hold the most pairs
+  const int dblk = (rank & 1) ? mid + 1 + (rank >> 1) : mid - (rank >> 1);
   const int d0 = -bp.LkP + DBW * dblk;
   const bool c2p = (p.flags & 1) != 0, p2c = (p.flags & 2) != 0;
   const int b_lo = bg * bp.BPG, b_hi = min(p.B, b_lo + bp.BPG);
-  // key chunks whose pairs can have an offset in the block
-  int jstart = -d0 - (XC - 2);
-  jstart = jstart > 0 ? (jstart + JC - 1) / JC * JC : 0;
-  const int jend = min(p.Lk, p.Lq - d0);
+  int jstart, nch;
+  block_chunks(dblk, bp.LkP, p.Lq, p.Lk, &jstart, &nch);
+  const int nsteps = (b_hi > b_lo) ? (b_hi - b_lo) * nch : 0;
 
-  // zero rows around the staged region (never overwritten)
+  // zero rows around the staged region (never overwritten), and a finite ring
   {
+    vecT z;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) z[e] = (T)0.0f;
     constexpr int VPR = XSTR / VEC;
-    for (int c = tid; c < XP * VPR; c += 256) {
-      vecT z;
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) z[e] = (T)0.0f;
-      reinterpret_cast<vecT*>(Xs)[c] = z;
-    }
-    for (int c = tid; c < (XROWS - XP - JC) * VPR; c += 256) {
-      vecT z;
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) z[e] = (T)0.0f;
-      reinterpret_cast<vecT*>(Xs + (XP + JC) * XSTR)[c] = z;
-    }
-    // the ring starts finite: operand rows outside the staged window are
-    // multiplied by zeros of X, never by uninitialised LDS
-    for (int c = tid; c < QRING * KSTR / VEC; c += 256) {
-      vecT z;
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) z[e] = (T)0.0f;
-      reinterpret_cast<vecT*>(Qring)[c] = z;
-    }
+    for (int c = tid; c < XP * VPR; c += 256) reinterpret_cast<vecT*>(Xs)[c] = z;
+    for (int c = tid; c < (XROWS - XP - JC) * VPR; c += 256) reinterpret_cast<vecT*>(Xs + (XP + JC) * XSTR)[c] = z;
+    for (int c = tid; c < QRING * KSTR / VEC; c += 256) reinterpret_cast<vecT*>(Qring)[c] = z;
   }
 
   f32x4 gc[2][ND], gp[2][ND];
@@ -130,65 +137,101 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
 #pragma unroll
     for (int db = 0; db < ND; ++db) gc[t][db] = gp[t][db] = zero4();
 
-  for (int b = b_lo; b < b_hi; ++b) {
+  // Registers holding the next step's global data.
+  vecT xr[XCH], kr[RCH], qr[RCH];
+  auto step_coords = [&](int st, int& b, int& j0) {
+    b = b_lo + st / nch;
+    j0 = jstart + (st % nch) * JC;
+  };
+  auto fetch = [&](int st) {
+    int b, j0;
+    step_coords(st, b, j0);
+    const int ib0 = j0 + d0;
     const T* dsb = (const T*)bp.dst + (int64_t)(b * p.H + h) * bp.LkP * bp.LqP;
-    const T* qbase = (const T*)p.q + (int64_t)b * p.qs[0] + (int64_t)h * p.qs[2];
-    const T* kbase = (const T*)p.k + (int64_t)b * p.ks[0] + (int64_t)h * p.ks[2];
-    for (int j0 = jstart; j0 < jend; j0 += JC) {
-      const int ib0 = j0 + d0;  // query of staged column 0 (a multiple of 32)
-      __syncthreads();          // previous step's readers are done
-      // dS^T rows j0.., columns [ib0, ib0 + XC): 16-byte chunks, each wholly in or out of [0, LqP)
-      for (int c = tid; c < JC * (XC / VEC); c += 256) {
-        const int r = c / (XC / VEC), c0 = (c % (XC / VEC)) * VEC;
-        const int i = ib0 + c0;
-        vecT x;
-        if (i >= 0 && i < bp.LqP) {
-          x = *reinterpret_cast<const vecT*>(dsb + (int64_t)(j0 + r) * bp.LqP + i);
-        } else {
 #pragma unroll
-          for (int e = 0; e < VEC; ++e) x[e] = (T)0.0f;
-        }
-        *reinterpret_cast<vecT*>(Xs + (XP + r) * XSTR + c0) = x;
+    for (int k = 0; k < XCH; ++k) {
+      const int c = tid + 256 * k;
+      const int r = c / (XC / VEC), c0 = (c % (XC / VEC)) * VEC;
+      const int i = ib0 + c0;  // 16-byte chunks are wholly in or out of [0, LqP)
+      if (c < XV && i >= 0 && i < bp.LqP) {
+        xr[k] = *reinterpret_cast<const vecT*>(dsb + (int64_t)(j0 + r) * bp.LqP + i);
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) xr[k][e] = (T)0.0f;
       }
-      if (p2c) load_rows<T, D, JC, 256>(Kc, KSTR, nullptr, 0, kbase, p.ks[1], j0, p.Lk, tid);
-      if (c2p) {
-        if (j0 == jstart) load_ring_rows<T, D>(Qring, KSTR, qbase, p.qs[1], ib0, XC, p.Lq, tid);
-        else load_ring_rows<T, D>(Qring, KSTR, qbase, p.qs[1], ib0 + XC - JC, JC, p.Lq, tid);
+    }
+    const T* kbase = (const T*)p.k + (int64_t)b * p.ks[0] + (int64_t)h * p.ks[2];
+    const T* qbase = (const T*)p.q + (int64_t)b * p.qs[0] + (int64_t)h * p.qs[2];
+#pragma unroll
+    for (int k = 0; k < RCH; ++k) {
+      const int c = tid + 256 * k;
+      const int r = c / (D / VEC), c0 = (c % (D / VEC)) * VEC;
+      const int j = j0 + r, i = ib0 + XC - JC + r;  // the ring's new rows
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) kr[k][e] = qr[k][e] = (T)0.0f;
+      if (c < RV && p2c && j < p.Lk) kr[k] = *reinterpret_cast<const vecT*>(kbase + (int64_t)j * p.ks[1] + c0);
+      if (c < RV && c2p && i >= 0 && i < p.Lq) qr[k] = *reinterpret_cast<const vecT*>(qbase + (int64_t)i * p.qs[1] + c0);
+    }
+  };
+
+  if (nsteps > 0) fetch(0);
+  for (int st = 0; st < nsteps; ++st) {
+    int b, j0;
+    step_coords(st, b, j0);
+    const int ib0 = j0 + d0;  // query of staged column 0 (a multiple of 32)
+    __syncthreads();          // previous step's readers are done
+#pragma unroll
+    for (int k = 0; k < XCH; ++k) {
+      const int c = tid + 256 * k;
+      if (c < XV) *reinterpret_cast<vecT*>(Xs + (XP + c / (XC / VEC)) * XSTR + (c % (XC / VEC)) * VEC) = xr[k];
+    }
+#pragma unroll
+    for (int k = 0; k < RCH; ++k) {
+      const int c = tid + 256 * k;
+      if (c < RV) {
+        const int r = c / (D / VEC), c0 = (c % (D / VEC)) * VEC;
+        *reinterpret_cast<vecT*>(Kc + r * KSTR + c0) = kr[k];
+        *reinterpret_cast<vecT*>(Qring + ((ib0 + XC - JC + r) & (QRING - 1)) * KSTR + c0) = qr[k];
       }
-      __syncthreads();
+    }
+    if (c2p && j0 == jstart) {  // first chunk of a batch: the ring's older rows too
+      const T* qbase = (const T*)p.q + (int64_t)b * p.qs[0] + (int64_t)h * p.qs[2];
+      load_ring_rows<T, D>(Qring, KSTR, qbase, p.qs[1], ib0, XC - JC, p.Lq, tid);
+    }
+    __syncthreads();
+    if (st + 1 < nsteps) fetch(st + 1);
 
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const int c0 = 16 * (2 * w + t);  // first offset of this wave's 16-offset block
-        if (p2c) {
-          // Gp^T[d][dd] += sum_jj K^T[d][jj] X[jj][jj + dd],  jj = KSTEP*s + FE*g + e
+    for (int t = 0; t < 2; ++t) {
+      const int c0 = 16 * (2 * w + t);  // first offset of this wave's 16-offset block
+      if (p2c) {
+        // Gp^T[d][dd] += sum_jj K^T[d][jj] X[jj][jj + dd],  jj = KSTEP*s + FE*g + e
 #pragma unroll
-          for (int s = 0; s < JC / M::KSTEP; ++s) {
-            frag bfr;
-            const T* dg = Xs + (XP + M::KSTEP * s + FE * g) * XSTR + M::KSTEP * s + FE * g + c0 + c16;
+        for (int s = 0; s < JC / M::KSTEP; ++s) {
+          frag bfr;
+          const T* dg = Xs + (XP + M::KSTEP * s + FE * g) * XSTR + M::KSTEP * s + FE * g + c0 + c16;
 #pragma unroll
-            for (int e = 0; e < FE; ++e) bfr[e] = dg[e * (XSTR + 1)];
+          for (int e = 0; e < FE; ++e) bfr[e] = dg[e * (XSTR + 1)];
 #pragma unroll
-            for (int db = 0; db < ND; ++db) {
-              const frag af = tr_contig<T>(Kc, KSTR, s * M::KSTEP, 16 * db, g, c16);
-              gp[t][db] = M::mma(af, bfr, gp[t][db]);
-            }
+          for (int db = 0; db < ND; ++db) {
+            const frag af = tr_contig<T>(Kc, KSTR, s * M::KSTEP, 16 * db, g, c16);
+            gp[t][db] = M::mma(af, bfr, gp[t][db]);
           }
         }
-        if (c2p) {
-          // Gc^T[d][dd] += sum_c Q^T[d][ib0 + c] X[c - dd][c],  c = c0 + KSTEP*s + FE*g + e
+      }
+      if (c2p) {
+        // Gc^T[d][dd] += sum_c Q^T[d][ib0 + c] X[c - dd][c],  c = c0 + KSTEP*s + FE*g + e
 #pragma unroll
-          for (int s = 0; s < GC_STEPS; ++s) {
-            frag bfr;
-            const int k = M::KSTEP * s + FE * g;  // c - c0 of element e = 0
-            const T* dg = Xs + (XP + k - c16) * XSTR + c0 + k;
+        for (int s = 0; s < GC_STEPS; ++s) {
+          frag bfr;
+          const int k = M::KSTEP * s + FE * g;  // c - c0 of element e = 0
+          const T* dg = Xs + (XP + k - c16) * XSTR + c0 + k;
 #pragma unroll
-            for (int e = 0; e < FE; ++e) bfr[e] = dg[e * (XSTR + 1)];
+          for (int e = 0; e < FE; ++e) bfr[e] = dg[e * (XSTR + 1)];
 #pragma unroll
-            for (int db = 0; db < ND; ++db) {
-              const frag af = tr_contig_ring<T>(Qring, KSTR, ib0, c0 + M::KSTEP * s, 16 * db, g, c16);
-              gc[t][db] = M::mma(af, bfr, gc[t][db]);
-            }
+          for (int db = 0; db < ND; ++db) {
+            const frag af = tr_contig_ring<T>(Qring, KSTR, ib0, c0 + M::KSTEP * s, 16 * db, g, c16);
+            gc[t][db] = M::mma(af, bfr, gc[t][db]);
           }
         }
       }
