@@ -5,7 +5,9 @@
 // where dKc is the content part Q^T dS that dsa_bwd_dkdv_kernel leaves in
 // the workspace (fp32, unscaled).  One workgroup = 4 waves = one (batch b,
 // head h, 128-key tile); wave w owns keys [jw, jw + 32), jw = j0 + 32w, and
-// streams 64-query tiles of dS^T through LDS:
+// streams 64-query tiles of dS^T and the tile's qrgt window through LDS
+// (the next tile is fetched into registers while the current one is
+// computed):
 //   dK^T[d][j] += sum_x qrgt[d][t0 + x] F[x][j],   F[x][j] = dS^T[j][j + x - 31 + i0 - jw]
 // with x = (i - i0) - (j - jw) + 31 the wave's offset index and qrgt the Qr
 // rows gathered per offset and transposed.  Row j of dS^T is contiguous in
@@ -33,11 +35,14 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkp_kernel(BwdParams bp) {
   constexpr int ND = D / 16;
   constexpr int FE = M::FRAG_ELEMS;
   constexpr int TSTR = ZC + BQ + ZC + Pad<T>::v;
-  constexpr int TV = BKW * BQ / VEC;           // 16-byte chunks of one tile
-  constexpr int TCH = (TV + 255) / 256;
+  constexpr int GW = BKW - WK + XW;            // qrgt columns of the workgroup's window (192)
+  constexpr int GSTR = GW + Pad<T>::v;
+  constexpr int TV = BKW * BQ / VEC, GV = D * GW / VEC;  // 16-byte chunks per tile
+  constexpr int TCH = (TV + 255) / 256, GCH = (GV + 255) / 256;
   const FwdParams& p = bp.f;
 
   __shared__ __align__(16) T Ts[BKW * TSTR];
+  __shared__ __align__(16) T QG[D * GSTR];
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, g = (tid & 63) >> 4, c16 = tid & 15;
@@ -61,7 +66,9 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkp_kernel(BwdParams bp) {
   for (int db = 0; db < ND; ++db) acc[db][0] = acc[db][1] = zero4();
 
   const int nqt = bp.LqP / BQ;
-  vecT xr[TCH];
+  // The next query tile (dS^T columns and the qrgt window) is fetched into
+  // registers while the current one is computed.
+  vecT xr[TCH], gr[GCH];
   auto fetch = [&](int qi) {
 #pragma unroll
     for (int k = 0; k < TCH; ++k) {
@@ -71,20 +78,30 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkp_kernel(BwdParams bp) {
         xr[k] = *reinterpret_cast<const vecT*>(dsb + (int64_t)r * bp.LqP + qi * BQ + c0);
       }
     }
+    const int tw = qi * BQ - j0 - (BKW - 1) + bp.OFF;  // window column 0 (a multiple of 32)
+#pragma unroll
+    for (int k = 0; k < GCH; ++k) {
+      const int c = tid + 256 * k;
+      if (c < GV) gr[k] = *reinterpret_cast<const vecT*>(qrg + (int64_t)(c / (GW / VEC)) * bp.TGP + tw + (c % (GW / VEC)) * VEC);
+    }
   };
   fetch(0);
   for (int qi = 0; qi < nqt; ++qi) {
-    const int i0 = qi * BQ;
     __syncthreads();  // previous tile's readers are done
 #pragma unroll
     for (int k = 0; k < TCH; ++k) {
       const int c = tid + 256 * k;
       if (c < TV) *reinterpret_cast<vecT*>(Ts + (c / (BQ / VEC)) * TSTR + ZC + (c % (BQ / VEC)) * VEC) = xr[k];
     }
+#pragma unroll
+    for (int k = 0; k < GCH; ++k) {
+      const int c = tid + 256 * k;
+      if (c < GV) *reinterpret_cast<vecT*>(QG + (c / (GW / VEC)) * GSTR + (c % (GW / VEC)) * VEC) = gr[k];
+    }
     __syncthreads();
     if (qi + 1 < nqt) fetch(qi + 1);
 
-    const int t0 = i0 - jw - 31 + bp.OFF;  // qrgt column of x = 0 (a multiple of 32)
+    // qrgt column of x = 0 for this wave: i0 - jw - 31 + OFF, i.e. window column 96 - 32w
 #pragma unroll
     for (int s = 0; s < XW / M::KSTEP; ++s) {
       frag bfr[2];
@@ -98,7 +115,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkp_kernel(BwdParams bp) {
       }
 #pragma unroll
       for (int db = 0; db < ND; ++db) {
-        const frag af = M::load_contig(qrg + (int64_t)(16 * db + c16) * bp.TGP + t0, s, g);
+        const frag af = M::load_contig(QG + (16 * db + c16) * GSTR + BKW - WK - WK * w, s, g);
 #pragma unroll
         for (int jb = 0; jb < 2; ++jb) acc[db][jb] = M::mma(af, bfr[jb], acc[db][jb]);
       }

@@ -2,8 +2,9 @@
 // dS^T (gfx950).
 //
 // One workgroup = 4 waves = one (batch b, head h, 128-query tile); wave w
-// owns queries [i0 + 32w, i0 + 32w + 32) and streams 64-key tiles of dS^T
-// and K through LDS:
+// owns queries [i0 + 32w, i0 + 32w + 32) and streams 64-key tiles of dS^T,
+// K and the tile's krgt window through LDS (the next tile is fetched into
+// registers while the current one is computed):
 //   dQ^T[d][i] += sum_j K^T[d][j] dS^T[j][i]            (both operands read
 //                                                        transposed from LDS)
 //   dQ^T[d][i] += sum_x krgt[d][t0 + x] E[x][i]          (c2p)
@@ -25,35 +26,27 @@ constexpr int XW = 96;   // offset rows per wave (95 used)
 constexpr int ZP = 32;   // zero rows above and below the dS^T tile
 }  // namespace dqcfg
 
-// Copies rows [r0, r0 + ROWS) x columns [c0, c0 + COLS) of a row-major
-// matrix (row stride rs) into LDS (row stride str).  Every row and column is
-// in range: the caller pads the source.
-template <typename T, int ROWS, int COLS, int NT>
-DSA_DEV void copy_tile(T* dst, int str, const T* src, int64_t rs, int tid) {
-  constexpr int VEC = 16 / sizeof(T);
-  constexpr int CPR = COLS / VEC;
-  typedef T vecT __attribute__((ext_vector_type(VEC)));
-#pragma unroll
-  for (int c = tid; c < ROWS * CPR; c += NT) {
-    const int r = c / CPR, c0 = (c % CPR) * VEC;
-    *reinterpret_cast<vecT*>(dst + r * str + c0) = *reinterpret_cast<const vecT*>(src + (int64_t)r * rs + c0);
-  }
-}
-
 template <typename T, int D>
 __global__ __launch_bounds__(256, 2) void dsa_bwd_dq_kernel(BwdParams bp) {
   using namespace dqcfg;
   using M = Mfma<T>;
   typedef typename M::frag frag;
+  constexpr int VEC = 16 / sizeof(T);
+  typedef T vecT __attribute__((ext_vector_type(VEC)));
   constexpr int ND = D / 16;
   constexpr int FE = M::FRAG_ELEMS;               // k indices per lane per step
   constexpr int KSTR = D + Pad<T>::v;             // K tile row stride
   constexpr int SSTR = BQ + Pad<T>::v;            // dS^T tile row stride
   constexpr int SROWS = ZP + BK + ZP;
+  constexpr int GW = BQ + XW - WQ;                // krgt columns of the workgroup's window (192)
+  constexpr int GSTR = GW + Pad<T>::v;
+  constexpr int SV = BK * BQ / VEC, KV = BK * D / VEC, GV = D * GW / VEC;  // 16-byte chunks per tile
+  constexpr int SCH = (SV + 255) / 256, KCH = (KV + 255) / 256, GCH = (GV + 255) / 256;
   const FwdParams& p = bp.f;
 
   __shared__ __align__(16) T Ss[SROWS * SSTR];
   __shared__ __align__(16) T Ks[BK * KSTR];
+  __shared__ __align__(16) T KG[D * GSTR];
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, g = (tid & 63) >> 4, c16 = tid & 15;
@@ -67,12 +60,11 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dq_kernel(BwdParams bp) {
 
   // zero pad rows (never overwritten)
   {
-    typedef T vecT __attribute__((ext_vector_type(16 / sizeof(T))));
-    constexpr int VPR = SSTR * (int)sizeof(T) / 16;
-    for (int c = tid; c < ZP * VPR; c += 256) {
-      vecT z;
+    constexpr int VPR = SSTR / VEC;
+    vecT z;
 #pragma unroll
-      for (int e = 0; e < 16 / (int)sizeof(T); ++e) z[e] = (T)0.0f;
+    for (int e = 0; e < VEC; ++e) z[e] = (T)0.0f;
+    for (int c = tid; c < ZP * VPR; c += 256) {
       reinterpret_cast<vecT*>(Ss)[c] = z;
       reinterpret_cast<vecT*>(Ss + (ZP + BK) * SSTR)[c] = z;
     }
@@ -82,13 +74,58 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dq_kernel(BwdParams bp) {
 #pragma unroll
   for (int db = 0; db < ND; ++db) dqa[db][0] = dqa[db][1] = zero4();
 
+  // The next key tile (dS^T rows, K rows, krgt window) is fetched into
+  // registers while the current one is computed.
+  vecT sr[SCH], kr[KCH], gr[GCH];
+  auto fetch = [&](int kt) {
+    const int j0 = kt * BK;
+#pragma unroll
+    for (int k = 0; k < SCH; ++k) {
+      const int c = tid + 256 * k;
+      if (c < SV) sr[k] = *reinterpret_cast<const vecT*>(dsb + (int64_t)(j0 + c / (BQ / VEC)) * bp.LqP + (c % (BQ / VEC)) * VEC);
+    }
+#pragma unroll
+    for (int k = 0; k < KCH; ++k) {
+      const int c = tid + 256 * k;
+      const int j = j0 + c / (D / VEC);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) kr[k][e] = (T)0.0f;
+      if (c < KV && j < p.Lk) kr[k] = *reinterpret_cast<const vecT*>(kbase + (int64_t)j * p.ks[1] + (c % (D / VEC)) * VEC);
+    }
+    if (c2p) {
+      const int tw = i0 - j0 - 63 + bp.OFF;  // window column 0 (a multiple of 32)
+#pragma unroll
+      for (int k = 0; k < GCH; ++k) {
+        const int c = tid + 256 * k;
+        if (c < GV) gr[k] = *reinterpret_cast<const vecT*>(krg + (int64_t)(c / (GW / VEC)) * bp.TGP + tw + (c % (GW / VEC)) * VEC);
+      }
+    }
+  };
+
   const int nkt = bp.LkP / BK;
+  fetch(0);
   for (int kt = 0; kt < nkt; ++kt) {
     const int j0 = kt * BK;
     __syncthreads();  // previous tile's readers are done
-    copy_tile<T, BK, BQ, 256>(St, SSTR, dsb + (int64_t)j0 * bp.LqP, bp.LqP, tid);
-    load_rows<T, D, BK, 256>(Ks, KSTR, nullptr, 0, kbase, p.ks[1], j0, p.Lk, tid);
+#pragma unroll
+    for (int k = 0; k < SCH; ++k) {
+      const int c = tid + 256 * k;
+      if (c < SV) *reinterpret_cast<vecT*>(St + (c / (BQ / VEC)) * SSTR + (c % (BQ / VEC)) * VEC) = sr[k];
+    }
+#pragma unroll
+    for (int k = 0; k < KCH; ++k) {
+      const int c = tid + 256 * k;
+      if (c < KV) *reinterpret_cast<vecT*>(Ks + (c / (D / VEC)) * KSTR + (c % (D / VEC)) * VEC) = kr[k];
+    }
+    if (c2p) {
+#pragma unroll
+      for (int k = 0; k < GCH; ++k) {
+        const int c = tid + 256 * k;
+        if (c < GV) *reinterpret_cast<vecT*>(KG + (c / (GW / VEC)) * GSTR + (c % (GW / VEC)) * VEC) = gr[k];
+      }
+    }
     __syncthreads();
+    if (kt + 1 < nkt) fetch(kt + 1);
 
     // ---- dQ^T += K^T dS^T -------------------------------------------------------------
 #pragma unroll
@@ -106,7 +143,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dq_kernel(BwdParams bp) {
 
     // ---- c2p: dQ^T += krgt[t0 + x]^T E[x] ---------------------------------------------------
     if (c2p) {
-      const int t0 = iw - j0 - 63 + bp.OFF;  // krgt column of x = 0 (a multiple of 32)
+      // krgt column of x = 0 for this wave: iw - j0 - 63 + OFF, i.e. window column 32w
 #pragma unroll
       for (int s = 0; s < XW / M::KSTEP; ++s) {
         frag bfr[2];
@@ -119,7 +156,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dq_kernel(BwdParams bp) {
         }
 #pragma unroll
         for (int db = 0; db < ND; ++db) {
-          const frag af = M::load_contig(krg + (int64_t)(16 * db + c16) * bp.TGP + t0, s, g);
+          const frag af = M::load_contig(KG + (16 * db + c16) * GSTR + WQ * w, s, g);
 #pragma unroll
           for (int ib = 0; ib < 2; ++ib) dqa[db][ib] = M::mma(af, bfr[ib], dqa[db][ib]);
         }
