@@ -46,7 +46,8 @@ DSA_DEV void load_row_tables_at(short* crow, short* prow, const int32_t* rel, in
 // (queries down, keys across; y[jb][ib][e] = query 16*ib + 4*g + e, key
 // 32*w + 16*jb + c16 of the tile).  y holds (q.k) * scale*log2e.
 //   qa: A fragments of the 64 query rows, kb: B fragments of the wave's keys
-//   cbs: shared c2p band (BQ * CBS), pbw: this wave's p2c band (XW * PBS)
+//   cbs: shared c2p band (BQ * CBS), pbw: this wave's p2c band (XW * PBS),
+//   both unscaled; sl2 is applied as the band values are added
 // Contains one __syncthreads.
 template <typename T, int D>
 DSA_DEV void add_delta_bands_S(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&qa)[4][D / Mfma<T>::KSTEP],
@@ -72,8 +73,7 @@ DSA_DEV void add_delta_bands_S(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&
         f32x4 acc = zero4();
 #pragma unroll
         for (int s = 0; s < NS; ++s) acc = M::mma(qa[ib][s], bf[s], acc);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) cbs[(16 * ib + 4 * g + e) * CBS + 16 * xb + c16] = to_band<BT>(acc[e] * sl2);
+        store_band4<BT>(cbs + (16 * ib + 4 * g) * CBS + 16 * xb + c16, CBS, acc);
       }
     }
   }
@@ -90,8 +90,7 @@ DSA_DEV void add_delta_bands_S(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&
         f32x4 acc = zero4();
 #pragma unroll
         for (int s = 0; s < NS; ++s) acc = M::mma(af[s], kb[jb][s], acc);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) pbw[(16 * xb + 4 * g + e) * PBS + 16 * jb + c16] = to_band<BT>(acc[e] * sl2);
+        store_band4<BT>(pbw + (16 * xb + 4 * g) * PBS + 16 * jb + c16, PBS, acc);
       }
     }
   }
@@ -104,7 +103,8 @@ DSA_DEV void add_delta_bands_S(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&
 #pragma unroll
       for (int ib = 0; ib < 4; ++ib)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) y[jb][ib][e] += (float)base[(16 * ib + e) * CBS + 16 * ib + e - 16 * jb];
+        for (int e = 0; e < 4; ++e)
+          y[jb][ib][e] = __builtin_fmaf((float)base[(16 * ib + e) * CBS + 16 * ib + e - 16 * jb], sl2, y[jb][ib][e]);
   }
   if (flags & 2) {
     // x_local = (16*ib + 4*g + e) - (16*jb + c16) + 31, column j_local = 16*jb + c16
@@ -114,7 +114,8 @@ DSA_DEV void add_delta_bands_S(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&
 #pragma unroll
       for (int ib = 0; ib < 4; ++ib)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) y[jb][ib][e] += (float)base[(16 * ib + e - 16 * jb) * PBS + 16 * jb];
+        for (int e = 0; e < 4; ++e)
+          y[jb][ib][e] = __builtin_fmaf((float)base[(16 * ib + e - 16 * jb) * PBS + 16 * jb], sl2, y[jb][ib][e]);
   }
 }
 
@@ -290,7 +291,7 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 2 : 1) void dsa_bwd_dkdv_kern
             const int i = i0 + il;
             bool keep = jkeep[jb];
             if (MASK == MASK_PAIR) keep = keep && i < Lq && pkb[(int64_t)i * p.pkq + jcol[jb]] != 0;
-            const float pe = keep ? exp2f(sc[jb][ib][e] - rowv[il]) : 0.f;
+            const float pe = keep ? __builtin_amdgcn_exp2f(sc[jb][ib][e] - rowv[il]) : 0.f;
             pp[jb][t][e] = pe;
             dsh[jb][t][e] = pe * (dp[e] - rowv[BQ + il]);
           }

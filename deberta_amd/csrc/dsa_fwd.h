@@ -173,13 +173,13 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
       const float mnew = fmaxf(mrow[ib], mt);
       float alpha = 1.f;
       if (mnew != -INFINITY) {
-        alpha = exp2f(mrow[ib] - mnew);  // 0 when mrow was -inf
+        alpha = __builtin_amdgcn_exp2f(mrow[ib] - mnew);  // 0 when mrow was -inf
         float ls = 0.f;
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float pe = exp2f(st[ib][jb][e] - mnew);
+            const float pe = __builtin_amdgcn_exp2f(st[ib][jb][e] - mnew);
             st[ib][jb][e] = pe;
             ls += pe;
           }

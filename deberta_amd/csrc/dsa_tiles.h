@@ -94,9 +94,9 @@ DSA_DEV void load_rows(T* dst, int str, T* dstT, int strT, const T* src, int64_t
 // plus a per-lane base: no per-element table lookups or bounds checks.
 //   c2p: per wave, rows x in [32w, 32w + 96) x the wave's 32 queries
 //   p2c: per workgroup, rows x in [0, 192) x the 64 keys, shared by all waves
-// Band values are stored pre-multiplied by scale*log2(e) (the softmax's
-// log2-domain scale), in fp16 for bf16 inputs (saturated to the fp16 range)
-// and in fp32 for fp32 inputs.
+// Band values are stored unscaled, in fp16 for bf16 inputs (saturated to the
+// fp16 range) and in fp32 for fp32 inputs; the gather multiplies them by the
+// softmax's log2-domain scale as it adds them (one mixed-precision FMA).
 // ---------------------------------------------------------------------------
 template <typename T>
 struct BandType {
@@ -107,12 +107,23 @@ struct BandType<bf16> {
   typedef _Float16 type;
 };
 
+// Stores the four values of a C-tile column (rows 4g + e) at p[e * stride].
+// fp16 bands are converted two at a time with round-toward-zero, which also
+// saturates: a finite value never rounds to infinity.
 template <typename B>
-DSA_DEV B to_band(float x) {
+DSA_DEV void store_band4(B* p, int stride, const f32x4& v) {
   if constexpr (sizeof(B) == 2) {
-    x = fminf(fmaxf(x, -65504.f), 65504.f);
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 a = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(v[0], v[1]));
+    const h2 c = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(v[2], v[3]));
+    p[0] = a[0];
+    p[stride] = a[1];
+    p[2 * stride] = c[0];
+    p[3 * stride] = c[1];
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) p[e * stride] = v[e];
   }
-  return (B)x;
 }
 
 namespace dcfg {
@@ -180,8 +191,7 @@ DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&
         f32x4 acc = zero4();
 #pragma unroll
         for (int s = 0; s < NS; ++s) acc = M::mma(af[s], qf[ib][s], acc);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) cb[(16 * rb + 4 * g + e) * CBS + 16 * ib + c16] = to_band<BT>(acc[e] * sl2);
+        store_band4<BT>(cb + (16 * rb + 4 * g) * CBS + 16 * ib + c16, CBS, acc);
       }
     }
   }
@@ -198,8 +208,7 @@ DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&
         f32x4 acc = zero4();
 #pragma unroll
         for (int s = 0; s < NS; ++s) acc = M::mma(kf[jb][s], bf[s], acc);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) pb[(16 * jb + 4 * g + e) * PBS + 16 * xb + c16] = to_band<BT>(acc[e] * sl2);
+        store_band4<BT>(pb + (16 * jb + 4 * g) * PBS + 16 * xb + c16, PBS, acc);
       }
     }
   }
@@ -212,7 +221,8 @@ DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&
 #pragma unroll
       for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) y[ib][jb][e] += (float)base[(16 * ib - 16 * jb - e) * CBS + 16 * ib];
+        for (int e = 0; e < 4; ++e)
+          y[ib][jb][e] = __builtin_fmaf((float)base[(16 * ib - 16 * jb - e) * CBS + 16 * ib], sl2, y[ib][jb][e]);
   }
   if (flags & 2) {
     // row j = 16*jb + 4*g + e, column x = 32w + (16*ib + c16) - (16*jb + 4*g + e) + 63
@@ -222,7 +232,8 @@ DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&
 #pragma unroll
       for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) y[ib][jb][e] += (float)base[(16 * jb + e) * PBS + 16 * ib - 16 * jb - e];
+        for (int e = 0; e < 4; ++e)
+          y[ib][jb][e] = __builtin_fmaf((float)base[(16 * jb + e) * PBS + 16 * ib - 16 * jb - e], sl2, y[ib][jb][e]);
   }
 }
 
