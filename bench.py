@@ -161,7 +161,7 @@ def main() -> None:
     leaves = (q, k, v, kr, qr)
 
     def step():
-        out, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, A, scale)
+        out, _, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, A, scale)
         return torch.autograd.grad(out, leaves, dout)
 
     if args.copy_probe_mib:
@@ -193,11 +193,11 @@ def main() -> None:
 
     # ---- per-kernel times: each launch timed on the stream it runs on ------------
     stream = torch.cuda.current_stream(dev)
-    out, lse = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, A, scale)
+    out, lse, bias = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, A, scale)
     f32 = dict(dtype=torch.float32, device=dev)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     dkr, dqr = torch.zeros((H, R, D), **f32), torch.zeros((H, R, D), **f32)
-    bargs = ops.fill_bwd_args(dout, q, k, v, kr, qr, table, None, None, out, lse, A, scale, dq, dk, dv, dkr, dqr)
+    bargs = ops.fill_bwd_args(dout, q, k, v, kr, qr, table, None, None, out, lse, bias, A, scale, dq, dk, dv, dkr, dqr)
     ws = torch.empty((ops.bwd_workspace_bytes(bargs),), dtype=torch.uint8, device=dev)
     bargs.workspace, bargs.workspace_bytes = ws.data_ptr(), ws.numel()
     fargs = bargs.fwd

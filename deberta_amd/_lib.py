@@ -41,6 +41,7 @@ class DsaFwdArgs(ctypes.Structure):
         ("pair_keep", ctypes.c_void_p),
         ("out", ctypes.c_void_p),
         ("lse", ctypes.c_void_p),
+        ("bias", ctypes.c_void_p),
         ("q_strides", _i64x3),
         ("k_strides", _i64x3),
         ("v_strides", _i64x3),
@@ -81,7 +82,14 @@ class DsaBwdArgs(ctypes.Structure):
 
 
 # Every entry point include/dsa.h declares.
-EXPORTS = ("dsa_fwd", "dsa_bwd", "dsa_bwd_workspace_bytes", "dsa_last_error", "dsa_version")
+EXPORTS = (
+    "dsa_fwd",
+    "dsa_bwd",
+    "dsa_bwd_workspace_bytes",
+    "dsa_fwd_bias_bytes",
+    "dsa_last_error",
+    "dsa_version",
+)
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
@@ -111,6 +119,8 @@ def load() -> ctypes.CDLL:
         lib.dsa_bwd.restype = ctypes.c_int
         lib.dsa_bwd_workspace_bytes.argtypes = [ctypes.POINTER(DsaBwdArgs)]
         lib.dsa_bwd_workspace_bytes.restype = ctypes.c_size_t
+        lib.dsa_fwd_bias_bytes.argtypes = [ctypes.POINTER(DsaFwdArgs)]
+        lib.dsa_fwd_bias_bytes.restype = ctypes.c_size_t
         lib.dsa_last_error.argtypes = []
         lib.dsa_last_error.restype = ctypes.c_char_p
         lib.dsa_version.argtypes = []

@@ -111,7 +111,13 @@ def fused_attention(
         qr = qr.to(q.dtype)
     if kr is None and qr is None:
         table = None
-    out, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, key_keep, pair_keep, int(att_span), float(scale))
+    # The relative term is saved only when a backward can follow.
+    save_bias = torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad for t in (q, k, v, kr, qr)
+    )
+    out, _, _ = torch.ops.deberta_amd.dsa_fwd(
+        q, k, v, kr, qr, table, key_keep, pair_keep, int(att_span), float(scale), save_bias
+    )
     return out
 
 

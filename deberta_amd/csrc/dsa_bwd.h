@@ -10,7 +10,7 @@
 // Masked keys and dead query rows have P = 0 and so dS = 0.
 //
 // Kernels, in launch order:
-//   prep   dsa_bwd_delta_kernel (Delta) and dsa_bwd_gather_kernel (krgt,
+//   prep   dsa_bwd_delta_kernel (lse and Delta per row) and dsa_bwd_gather_kernel (krgt,
 //          qrgt: the relative tables gathered per offset d = i - j and
 //          transposed, so a run of consecutive offsets of one head-dim
 //          column is contiguous — the A operand of the offset-band products)
@@ -27,32 +27,40 @@
 
 namespace dsa {
 
-// delta_i = dO_i . O_i: D / VEC lanes per row, one 16-byte load each, then a
-// butterfly sum.
+// rowinfo[b][h][i] = (lse_i * log2 e, dO_i . O_i) for i < LqP: D / VEC lanes
+// per row, one 16-byte load each, then a butterfly sum.  Rows past Lq get
+// (inf, 0); dead rows already have lse = inf.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void dsa_bwd_delta_kernel(BwdParams bp) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int LPR = D / VEC;
   typedef T vecT __attribute__((ext_vector_type(VEC)));
   const FwdParams& p = bp.f;
-  const int64_t n = (int64_t)p.B * p.H * p.Lq;
+  const int64_t n = (int64_t)p.B * p.H * p.LqP;
   const int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) / LPR;
   const int part = threadIdx.x % LPR;
   float acc = 0.f;
+  int i = 0, h = 0, b = 0;
   if (row < n) {
-    const int i = (int)(row % p.Lq);
-    const int h = (int)((row / p.Lq) % p.H);
-    const int b = (int)(row / ((int64_t)p.Lq * p.H));
-    const T* o = (const T*)p.out + (int64_t)b * p.os[0] + (int64_t)i * p.os[1] + (int64_t)h * p.os[2];
-    const T* d = (const T*)bp.dout + (int64_t)b * bp.dos[0] + (int64_t)i * bp.dos[1] + (int64_t)h * bp.dos[2];
-    const vecT ov = *reinterpret_cast<const vecT*>(o + part * VEC);
-    const vecT dv = *reinterpret_cast<const vecT*>(d + part * VEC);
+    i = (int)(row % p.LqP);
+    h = (int)((row / p.LqP) % p.H);
+    b = (int)(row / ((int64_t)p.LqP * p.H));
+    if (i < p.Lq) {
+      const T* o = (const T*)p.out + (int64_t)b * p.os[0] + (int64_t)i * p.os[1] + (int64_t)h * p.os[2];
+      const T* d = (const T*)bp.dout + (int64_t)b * bp.dos[0] + (int64_t)i * bp.dos[1] + (int64_t)h * bp.dos[2];
+      const vecT ov = *reinterpret_cast<const vecT*>(o + part * VEC);
+      const vecT dv = *reinterpret_cast<const vecT*>(d + part * VEC);
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) acc += (float)ov[e] * (float)dv[e];
+      for (int e = 0; e < VEC; ++e) acc += (float)ov[e] * (float)dv[e];
+    }
   }
 #pragma unroll
   for (int m = LPR / 2; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);
-  if (row < n && part == 0) bp.delta[row] = acc;
+  if (row < n && part == 0) {
+    const float lse2 = (i < p.Lq) ? p.lse[((int64_t)b * p.H + h) * p.Lq + i] * kLog2e : INFINITY;
+    bp.rowinfo[2 * row] = lse2;
+    bp.rowinfo[2 * row + 1] = acc;
+  }
 }
 
 // Table row of offset d (clamped into the relative-position table's range).

@@ -48,7 +48,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkp_kernel(BwdParams bp) {
   const int w = tid >> 6, g = (tid & 63) >> 4, c16 = tid & 15;
   const int kt = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int j0 = kt * BKW, jw = j0 + w * WK;
-  const T* dsb = (const T*)bp.dst + ((int64_t)(b * p.H + h) * bp.LkP + j0) * bp.LqP;
+  const T* dsb = (const T*)bp.dst + ((int64_t)(b * p.H + h) * bp.f.LkP + j0) * bp.f.LqP;
   const T* qrg = (const T*)bp.qrgt + (int64_t)h * D * bp.TGP;
 
   // zero columns (never overwritten)
@@ -65,7 +65,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkp_kernel(BwdParams bp) {
 #pragma unroll
   for (int db = 0; db < ND; ++db) acc[db][0] = acc[db][1] = zero4();
 
-  const int nqt = bp.LqP / BQ;
+  const int nqt = bp.f.LqP / BQ;
   // The next query tile (dS^T columns and the qrgt window) is fetched into
   // registers while the current one is computed.
   vecT xr[TCH], gr[GCH];
@@ -75,7 +75,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkp_kernel(BwdParams bp) {
       const int c = tid + 256 * k;
       if (c < TV) {
         const int r = c / (BQ / VEC), c0 = (c % (BQ / VEC)) * VEC;
-        xr[k] = *reinterpret_cast<const vecT*>(dsb + (int64_t)r * bp.LqP + qi * BQ + c0);
+        xr[k] = *reinterpret_cast<const vecT*>(dsb + (int64_t)r * bp.f.LqP + qi * BQ + c0);
       }
     }
     const int tw = qi * BQ - j0 - (BKW - 1) + bp.OFF;  // window column 0 (a multiple of 32)
@@ -123,7 +123,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkp_kernel(BwdParams bp) {
   }
 
   // dK = s (dKc + p2c term); lanes hold 4 consecutive head-dim columns of key j
-  const float* dkc = bp.dkc + ((int64_t)(b * p.H + h) * bp.LkP) * D;
+  const float* dkc = bp.dkc + ((int64_t)(b * p.H + h) * bp.f.LkP) * D;
   T* dkbase = (T*)bp.dk + (int64_t)b * bp.dks[0] + (int64_t)h * bp.dks[2];
 #pragma unroll
   for (int jb = 0; jb < 2; ++jb) {

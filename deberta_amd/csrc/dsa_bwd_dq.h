@@ -54,7 +54,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dq_kernel(BwdParams bp) {
   const int i0 = qt * BQ, iw = i0 + w * WQ;
   const bool c2p = (p.flags & 1) != 0;
   const T* kbase = (const T*)p.k + (int64_t)b * p.ks[0] + (int64_t)h * p.ks[2];
-  const T* dsb = (const T*)bp.dst + (int64_t)(b * p.H + h) * bp.LkP * bp.LqP + i0;
+  const T* dsb = (const T*)bp.dst + (int64_t)(b * p.H + h) * bp.f.LkP * bp.f.LqP + i0;
   const T* krg = c2p ? (const T*)bp.krgt + (int64_t)h * D * bp.TGP : nullptr;
   T* St = Ss + ZP * SSTR;  // row 0 of the tile
 
@@ -82,7 +82,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dq_kernel(BwdParams bp) {
 #pragma unroll
     for (int k = 0; k < SCH; ++k) {
       const int c = tid + 256 * k;
-      if (c < SV) sr[k] = *reinterpret_cast<const vecT*>(dsb + (int64_t)(j0 + c / (BQ / VEC)) * bp.LqP + (c % (BQ / VEC)) * VEC);
+      if (c < SV) sr[k] = *reinterpret_cast<const vecT*>(dsb + (int64_t)(j0 + c / (BQ / VEC)) * bp.f.LqP + (c % (BQ / VEC)) * VEC);
     }
 #pragma unroll
     for (int k = 0; k < KCH; ++k) {
@@ -102,7 +102,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dq_kernel(BwdParams bp) {
     }
   };
 
-  const int nkt = bp.LkP / BK;
+  const int nkt = bp.f.LkP / BK;
   fetch(0);
   for (int kt = 0; kt < nkt; ++kt) {
     const int j0 = kt * BK;

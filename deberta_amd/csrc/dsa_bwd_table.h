@@ -113,11 +113,11 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
   const int h = rem / bp.NBG, bg = rem % bp.NBG;
   const int mid = (bp.NDB - 1) / 2;   // central blocks hold the most pairs
   const int dblk = (rank & 1) ? mid + 1 + (rank >> 1) : mid - (rank >> 1);
-  const int d0 = -bp.LkP + DBW * dblk;
+  const int d0 = -bp.f.LkP + DBW * dblk;
   const bool c2p = (p.flags & 1) != 0, p2c = (p.flags & 2) != 0;
   const int b_lo = bg * bp.BPG, b_hi = min(p.B, b_lo + bp.BPG);
   int jstart, nch;
-  block_chunks(dblk, bp.LkP, p.Lq, p.Lk, &jstart, &nch);
+  block_chunks(dblk, bp.f.LkP, p.Lq, p.Lk, &jstart, &nch);
   const int nsteps = (b_hi > b_lo) ? (b_hi - b_lo) * nch : 0;
 
   // zero rows around the staged region (never overwritten), and a finite ring
@@ -147,14 +147,14 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
     int b, j0;
     step_coords(st, b, j0);
     const int ib0 = j0 + d0;
-    const T* dsb = (const T*)bp.dst + (int64_t)(b * p.H + h) * bp.LkP * bp.LqP;
+    const T* dsb = (const T*)bp.dst + (int64_t)(b * p.H + h) * bp.f.LkP * bp.f.LqP;
 #pragma unroll
     for (int k = 0; k < XCH; ++k) {
       const int c = tid + 256 * k;
       const int r = c / (XC / VEC), c0 = (c % (XC / VEC)) * VEC;
       const int i = ib0 + c0;  // 16-byte chunks are wholly in or out of [0, LqP)
-      if (c < XV && i >= 0 && i < bp.LqP) {
-        xr[k] = *reinterpret_cast<const vecT*>(dsb + (int64_t)(j0 + r) * bp.LqP + i);
+      if (c < XV && i >= 0 && i < bp.f.LqP) {
+        xr[k] = *reinterpret_cast<const vecT*>(dsb + (int64_t)(j0 + r) * bp.f.LqP + i);
       } else {
 #pragma unroll
         for (int e = 0; e < VEC; ++e) xr[k][e] = (T)0.0f;
@@ -287,7 +287,7 @@ __global__ __launch_bounds__(256) void dsa_bwd_fold_kernel(BwdParams bp) {
   }
   f32x4 acc = zero4();
   for (int d = lo; d < lo2; ++d) {
-    const int dblk = (d + bp.LkP) / DBW, dd = (d + bp.LkP) % DBW;
+    const int dblk = (d + bp.f.LkP) / DBW, dd = (d + bp.f.LkP) % DBW;
     const float* src = bp.gpart + ((int64_t)(h * bp.NDB + dblk) * bp.NBG) * 2 * DBW * D +
                        (int64_t)((q ? DBW : 0) + dd) * D + 4 * c4;
     for (int k = 0; k < bp.NBG; ++k) acc += *reinterpret_cast<const f32x4*>(src + (int64_t)k * 2 * DBW * D);

@@ -35,6 +35,8 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+int round_up(int x, int a) { return (x + a - 1) / a * a; }
+
 int elem_bytes(int dtype) { return dtype == DSA_BF16 ? 2 : 4; }
 
 // Checks shared by forward and backward.  Shapes are validated on the host
@@ -84,6 +86,7 @@ dsa::FwdParams to_params(const dsa_fwd_args* a) {
   p.pk = a->pair_keep;
   p.out = a->out;
   p.lse = a->lse;
+  p.bias = a->bias;
   for (int s = 0; s < 3; ++s) {
     p.qs[s] = a->q_strides[s];
     p.ks[s] = a->k_strides[s];
@@ -103,6 +106,8 @@ dsa::FwdParams to_params(const dsa_fwd_args* a) {
   p.Lk = a->Lk;
   p.A = a->flags ? a->att_span : 1;
   p.flags = a->flags;
+  p.LqP = round_up(a->Lq, 128);
+  p.LkP = round_up(a->Lk, 128);
   p.scale = a->scale;
   return p;
 }
@@ -140,13 +145,11 @@ int device_cus() {
   return cus;
 }
 
-int round_up(int x, int a) { return (x + a - 1) / a * a; }
-
 // Workspace of the backward (offsets 256-byte aligned) and the padded
 // extents the kernels share.
 struct WsLayout {
   int LqP, LkP, TGP, OFF, NDB, NBG, BPG;
-  size_t delta, krgt, qrgt, dst, gpart, dkc, total;
+  size_t rowinfo, krgt, qrgt, dst, gpart, dkc, total;
 };
 
 WsLayout ws_layout(const dsa_bwd_args* a) {
@@ -165,8 +168,8 @@ WsLayout ws_layout(const dsa_bwd_args* a) {
   w.BPG = (f.B + groups - 1) / groups;
   w.NBG = (f.B + w.BPG - 1) / w.BPG;
   size_t off = 0;
-  w.delta = off;
-  off = align_up(off + (size_t)f.B * f.H * f.Lq * sizeof(float), 256);
+  w.rowinfo = off;
+  off = align_up(off + (size_t)f.B * f.H * w.LqP * 2 * sizeof(float), 256);
   w.krgt = off;
   if (f.flags & DSA_C2P) off = align_up(off + (size_t)f.H * f.D * w.TGP * es, 256);
   w.qrgt = off;
@@ -199,14 +202,12 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
   bp.dkr = a->dkr;
   bp.dqr = a->dqr;
   char* base = static_cast<char*>(a->workspace);
-  bp.delta = reinterpret_cast<float*>(base + ws.delta);
+  bp.rowinfo = reinterpret_cast<float*>(base + ws.rowinfo);
   bp.krgt = base + ws.krgt;
   bp.qrgt = base + ws.qrgt;
   bp.dst = base + ws.dst;
   bp.gpart = reinterpret_cast<float*>(base + ws.gpart);
   bp.dkc = reinterpret_cast<float*>(base + ws.dkc);
-  bp.LqP = ws.LqP;
-  bp.LkP = ws.LkP;
   bp.TGP = ws.TGP;
   bp.OFF = ws.OFF;
   bp.NDB = ws.NDB;
@@ -216,7 +217,7 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
       a->stages ? a->stages : (DSA_STAGE_PREP | DSA_STAGE_DQ | DSA_STAGE_DKDV | DSA_STAGE_DKP | DSA_STAGE_FOLD);
 
   if (stages & DSA_STAGE_PREP) {
-    const int64_t n = (int64_t)f.B * f.H * f.Lq * (D / (16 / (int)sizeof(T)));
+    const int64_t n = (int64_t)f.B * f.H * ws.LqP * (D / (16 / (int)sizeof(T)));
     hipLaunchKernelGGL((dsa::dsa_bwd_delta_kernel<T, D>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, bp);
     if (launch_check("dsa_bwd_delta_kernel")) return 1;
     if (f.flags) {
@@ -279,6 +280,11 @@ int dsa_fwd(const dsa_fwd_args* a, void* stream) {
   return a->D == 64 ? fwd_mask<float, 64>(p, mode, st) : fwd_mask<float, 32>(p, mode, st);
 }
 
+size_t dsa_fwd_bias_bytes(const dsa_fwd_args* a) {
+  if (!a || !a->flags) return 0;
+  return (size_t)a->B * a->H * round_up(a->Lq, 128) * round_up(a->Lk, 128) * (a->dtype == DSA_BF16 ? 2 : 4);
+}
+
 size_t dsa_bwd_workspace_bytes(const dsa_bwd_args* a) {
   if (!a) return 0;
   return ws_layout(a).total;
@@ -292,6 +298,8 @@ int dsa_bwd(const dsa_bwd_args* a, void* stream) {
   if (!a->dout || !a->dq || !a->dk || !a->dv) return fail("dsa: dout, dq, dk and dv are required");
   if ((f.flags & DSA_C2P) && !a->dkr) return fail("dsa: c2p backward needs dkr");
   if ((f.flags & DSA_P2C) && !a->dqr) return fail("dsa: p2c backward needs dqr");
+  if (f.flags && !f.bias) return fail("dsa: the backward needs the relative term saved by dsa_fwd (fwd.bias)");
+  if (f.flags && !aligned16(f.bias)) return fail("dsa: fwd.bias must be 16-byte aligned");
   const int vec = 16 / elem_bytes(f.dtype);
   const void* ptrs[] = {a->dout, a->dq, a->dk, a->dv};
   const int64_t* strides[] = {a->do_strides, a->dq_strides, a->dk_strides, a->dv_strides};

@@ -173,10 +173,6 @@ DSA_DEV f32x4 tr4(const float* X, int str, int k0, int m0, int c16) {
                X[(k0 + 3) * str + m0 + c16]};
 }
 
-// Operand fragment of column m0 + c16 of a row-major LDS array X whose rows
-// are the k index: the CONTIG k-set (k = k0 + 8g + [0..7] for bf16,
-// k0 + 4g + [0..3] for fp32), or the ACC k-set (k0 + 4g + [0..3] and
-// k0 + 16 + 4g + [0..3] for bf16).
 DSA_DEV bf16x8 join8(bf16x4 a, bf16x4 b) {
   bf16x8 f;
 #pragma unroll
@@ -186,6 +182,72 @@ DSA_DEV bf16x8 join8(bf16x4 a, bf16x4 b) {
   }
   return f;
 }
+
+// ds_read_b64_tr_b16 at an address the caller computed (see tr4).
+DSA_DEV bf16x4 tr4_at(const bf16* p) {
+  bf16x4_tr v = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4_tr*)p);
+  return __builtin_bit_cast(bf16x4, v);
+}
+
+// 16-byte copy global -> LDS without registers (gfx950 global_load_lds_dwordx4):
+// lane l of the wave writes lds_wave + 16 * l, where lds_wave is the same for
+// every lane of the wave.  Completion is tracked by vmcnt (lds_dma_wait).
+DSA_DEV void lds_dma16(const void* src, void* lds_wave) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_wave, 16, 0, 0);
+}
+// Waits for this wave's outstanding global loads, the LDS copies included.
+DSA_DEV void lds_dma_wait() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0) only
+
+// Row-major LDS tile with COLS elements per row whose 16-byte chunks are
+// XOR-swizzled by row (chunk c of row r stored at chunk c ^ (r % CPR)), so that
+// column reads across rows and row reads across lanes spread over the banks
+// without padding.  Filled with lds_dma16, which writes 16-byte chunks in
+// lane order.
+template <typename T, int COLS>
+struct Swz {
+  static constexpr int VEC = 16 / sizeof(T);
+  static constexpr int CPR = COLS / VEC;
+  static_assert((CPR & (CPR - 1)) == 0, "chunks per row must be a power of two");
+  DSA_DEV static int off(int r, int c) { return r * COLS + (((c / VEC) ^ (r & (CPR - 1))) * VEC) + (c % VEC); }
+  // CONTIG k-set of row r (k = KSTEP*s + FE*g + [0, FE)) as an operand fragment
+  DSA_DEV static typename Mfma<T>::frag row_frag(const T* X, int r, int s, int g) {
+    constexpr int FE = Mfma<T>::FRAG_ELEMS;
+    return *reinterpret_cast<const typename Mfma<T>::frag*>(X + off(r, Mfma<T>::KSTEP * s + FE * g));
+  }
+  // four consecutive rows k0 + e of column m0 + c16 (as tr4)
+  DSA_DEV static f32x4 col4_f32(const float* X, int k0, int m0, int c16) {
+    return f32x4{X[off(k0, m0 + c16)], X[off(k0 + 1, m0 + c16)], X[off(k0 + 2, m0 + c16)], X[off(k0 + 3, m0 + c16)]};
+  }
+  // ACC k-set of column m0 + c16 read transposed (as tr_acc)
+  DSA_DEV static typename Mfma<T>::frag col_acc(const T* X, int k0, int m0, int g, int c16) {
+    if constexpr (sizeof(T) == 2) {
+      const int r0 = k0 + 4 * g + (c16 >> 2), r1 = r0 + 16, c = m0 + 4 * (c16 & 3);
+      return join8(tr4_at(reinterpret_cast<const bf16*>(X) + off(r0, c)),
+                   tr4_at(reinterpret_cast<const bf16*>(X) + off(r1, c)));
+    } else {
+      return col4_f32(reinterpret_cast<const float*>(X), k0 + 4 * g, m0, c16);
+    }
+  }
+};
+
+// Four consecutive rows k0 + e (e = 0..3) of column m0 + c16 of a row-major
+// LDS array X as fp32, for 16-bit (fp16 / bf16) or fp32 elements.
+template <typename B>
+DSA_DEV f32x4 tr4_f32(const B* X, int str, int k0, int m0, int c16) {
+  if constexpr (sizeof(B) == 2) {
+    typedef B b4 __attribute__((ext_vector_type(4)));
+    const bf16x4 r = tr4(reinterpret_cast<const bf16*>(X), str, k0, m0, c16);
+    const b4 v = __builtin_bit_cast(b4, r);
+    return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+  } else {
+    return tr4(X, str, k0, m0, c16);
+  }
+}
+
+// Operand fragment of column m0 + c16 of a row-major LDS array X whose rows
+// are the k index: the CONTIG k-set (k = k0 + 8g + [0..7] for bf16,
+// k0 + 4g + [0..3] for fp32), or the ACC k-set (k0 + 4g + [0..3] and
+// k0 + 16 + 4g + [0..3] for bf16).
 template <typename T>
 DSA_DEV typename Mfma<T>::frag tr_contig(const T* X, int str, int k0, int m0, int g, int c16) {
   if constexpr (sizeof(T) == 2) {

@@ -83,6 +83,10 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
 
   const float sl2 = p.scale * kLog2e;
   const int nkt = (Lk + BK - 1) / BK;
+  // this lane's first element of the saved relative term in each key tile
+  BT* biasl = (p.bias && p.flags) ? (BT*)p.bias + bias_tile_offset(b, h, p.H, qt, 0, p.LqP, p.LkP) + w * 2048 +
+                                        c16 * 16 + g * 4
+                                  : nullptr;
 
   // Is any query row of this workgroup live?  If not, nothing to compute.
   int wg_live = 0;
@@ -140,7 +144,7 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
       }
     if (p.flags)
       add_delta_bands_T<T, D>(st, kf, qf, cb, pb, crow, prow, w, g, c16, krh, p.krs[1], qrh, p.qrs[1], p.flags,
-                              sl2);
+                              sl2, biasl ? biasl + (int64_t)kt * 8192 : nullptr);
 
     // ---- mask + online softmax (log2 domain) --------------------------------
 #pragma unroll

@@ -5,6 +5,8 @@
 // (deberta_v2_native.py:604 and the c2p/p2c terms of :389-410).
 #pragma once
 
+#include <type_traits>
+
 #include "dsa_common.h"
 
 namespace dsa {
@@ -20,10 +22,12 @@ struct FwdParams {
   const uint8_t* pk;
   void* out;
   float* lse;
+  void* bias;       // saved relative term [B, H, LqP, LkP] or null
   int64_t qs[3], ks[3], vs[3], os[3];
   int64_t krs[2], qrs[2];
   int64_t kkb, pkb, pkq;
   int B, H, Lq, Lk, A, flags;
+  int LqP, LkP;     // Lq, Lk rounded up to 128 (extents of bias and dS^T)
   float scale;
 };
 
@@ -38,13 +42,12 @@ struct BwdParams {
   float* dkr;
   float* dqr;
   // workspace
-  float* delta;     // [B, H, Lq] rowwise dO . O
-  void* dst;        // dS^T [B, H, LkP, LqP], zero outside [0, Lk) x [0, Lq)
+  float* rowinfo;   // [B, H, LqP, 2]: lse*log2e (inf: dead or padding row), dO . O
+  void* dst;        // dS^T [B, H, f.LkP, f.LqP], zero outside [0, Lk) x [0, Lq)
   void* krgt;       // [H, D, TGP]: krgt[h][d][t] = Kr[h][c(t - OFF)][d]
   void* qrgt;       // [H, D, TGP]: qrgt[h][d][t] = Qr[h][p(t - OFF)][d]
   float* gpart;     // table-gradient partials [H][NDB][NBG][2][128][D]
   float* dkc;       // content part of dK (fp32, unscaled) [B, H, LkP, D], when p2c
-  int LqP, LkP;     // padded query / key extents of dS^T
   int TGP, OFF;     // row length and offset origin of krgt / qrgt
   int NDB, NBG, BPG;  // offset blocks, batch groups, batches per group
 };
@@ -154,11 +157,40 @@ DSA_DEV void load_row_tables(short* crow, short* prow, const int32_t* rel, int i
   }
 }
 
+// The saved relative term (dsa_fwd_args.bias) is stored per forward tile of
+// 128 queries x 64 keys, 8192 elements in the order in which the forward's
+// lanes hold them, so every store instruction writes 512 contiguous bytes:
+//   element (i, j) of tile (i / 128, j / 64) is at
+//   ((((w * 2 + ib) * 4 + jb) * 16 + c16) * 4 + g) * 4 + e
+// with w = i % 128 / 32, ib = i % 32 / 16, c16 = i % 16, jb = j % 64 / 16,
+// g = j % 16 / 4, e = j % 4.  Offset of the first element of a tile:
+DSA_DEV int64_t bias_tile_offset(int b, int h, int H, int qt, int kt, int LqP, int LkP) {
+  return (((int64_t)(b * H + h) * (LqP / 128) + qt) * (LkP / 64) + kt) * 8192;
+}
+
+// Stores four values at p[0..3] (fp16: round-toward-zero pair conversion,
+// saturating as in store_band4).
+template <typename B>
+DSA_DEV void store4_contig(B* p, const f32x4& v) {
+  if constexpr (sizeof(B) == 2) {
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 a = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(v[0], v[1]));
+    const h2 c = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(v[2], v[3]));
+    *reinterpret_cast<h4*>(p) = h4{a[0], a[1], c[0], c[1]};
+  } else {
+    *reinterpret_cast<f32x4*>(p) = v;
+  }
+}
+
 // Adds the scaled c2p + p2c terms to a transposed score tile (keys down,
 // queries across; y[ib][jb][e] = key 16*jb + 4*g + e, query 32*w + 16*ib +
 // c16 of the tile).  y must already hold (q.k) * scale*log2(e).
 //   kf: A fragments of the 64 key rows, qf: B fragments of the wave's queries
 //   cb: this wave's c2p band (XW * CBS), pb: the shared p2c band (BK * PBS)
+//   bias: if not null, where this lane's part of the tile's saved relative
+//         term goes (see bias_tile_offset): the unscaled c2p + p2c values,
+//         stored for the backward
 // Contains one __syncthreads (the p2c band is shared): call it from every
 // thread of the workgroup.
 template <typename T, int D>
@@ -166,8 +198,7 @@ DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&
                                const typename Mfma<T>::frag (&qf)[2][D / Mfma<T>::KSTEP],
                                typename BandType<T>::type* cb, typename BandType<T>::type* pb, const short* crow,
                                const short* prow, int w, int g, int c16, const T* krh, int64_t krs, const T* qrh,
-                               int64_t qrs, int flags, float sl2, const T* krd = nullptr, int krd_str = 0,
-                               int krd_row0 = 0) {
+                               int64_t qrs, int flags, float sl2, typename BandType<T>::type* bias = nullptr) {
   using M = Mfma<T>;
   typedef typename M::frag frag;
   typedef typename BandType<T>::type BT;
@@ -176,16 +207,10 @@ DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&
   if (flags & 1) {
 #pragma unroll
     for (int rb = 0; rb < XW / 16; ++rb) {
+      const int row = crow[WQ * w + 16 * rb + c16];
       frag af[NS];
-      if (krd) {  // the tile's window of Kr rows is staged in LDS (row r at r - krd_row0)
-        const int row = crow[WQ * w + 16 * rb + c16] - krd_row0;
 #pragma unroll
-        for (int s = 0; s < NS; ++s) af[s] = M::load_contig(krd + row * krd_str, s, g);
-      } else {
-        const int row = crow[WQ * w + 16 * rb + c16];
-#pragma unroll
-        for (int s = 0; s < NS; ++s) af[s] = M::load_contig(krh + (int64_t)row * krs, s, g);
-      }
+      for (int s = 0; s < NS; ++s) af[s] = M::load_contig(krh + (int64_t)row * krs, s, g);
 #pragma unroll
       for (int ib = 0; ib < 2; ++ib) {
         f32x4 acc = zero4();
@@ -213,28 +238,40 @@ DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&
     }
   }
   __syncthreads();
-  if (flags & 1) {
-    // x - 32w = (16*ib + c16) - (16*jb + 4*g + e) + 63
-    const BT* base = cb + (c16 - 4 * g + 63) * CBS + c16;
+  // c2p: x - 32w = (16*ib + c16) - (16*jb + 4*g + e) + 63
+  const BT* cbase = cb + (c16 - 4 * g + 63) * CBS + c16;
+  // p2c: row j = 16*jb + 4*g + e, column x = 32w + (16*ib + c16) - (16*jb + 4*g + e) + 63
+  const BT* pbase = pb + 4 * g * PBS + WQ * w + c16 - 4 * g + 63;
+  // The two terms are summed in the band type (for fp16: one rounding of the
+  // exact sum, which is also the value saved), then scaled into the score
+  // with one mixed-precision FMA per element.  The uniform flag test sits
+  // outside the loops.
+  auto gather = [&](auto with_c, auto with_p) {
 #pragma unroll
     for (int ib = 0; ib < 2; ++ib)
 #pragma unroll
-      for (int jb = 0; jb < 4; ++jb)
+      for (int jb = 0; jb < 4; ++jb) {
+        BT bs[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          y[ib][jb][e] = __builtin_fmaf((float)base[(16 * ib - 16 * jb - e) * CBS + 16 * ib], sl2, y[ib][jb][e]);
-  }
-  if (flags & 2) {
-    // row j = 16*jb + 4*g + e, column x = 32w + (16*ib + c16) - (16*jb + 4*g + e) + 63
-    const BT* base = pb + 4 * g * PBS + WQ * w + c16 - 4 * g + 63;
+        for (int e = 0; e < 4; ++e) {
+          BT v = (BT)0.0f;
+          if constexpr (decltype(with_c)::value) v = cbase[(16 * ib - 16 * jb - e) * CBS + 16 * ib];
+          if constexpr (decltype(with_p)::value) v = v + pbase[(16 * jb + e) * PBS + 16 * ib - 16 * jb - e];
+          bs[e] = v;
+        }
 #pragma unroll
-    for (int ib = 0; ib < 2; ++ib)
-#pragma unroll
-      for (int jb = 0; jb < 4; ++jb)
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          y[ib][jb][e] = __builtin_fmaf((float)base[(16 * jb + e) * PBS + 16 * ib - 16 * jb - e], sl2, y[ib][jb][e]);
-  }
+        for (int e = 0; e < 4; ++e) y[ib][jb][e] = __builtin_fmaf((float)bs[e], sl2, y[ib][jb][e]);
+        if (bias) {
+          typedef BT b4 __attribute__((ext_vector_type(4)));
+          *reinterpret_cast<b4*>(bias + (ib * 4 + jb) * 256) = b4{bs[0], bs[1], bs[2], bs[3]};
+        }
+      }
+  };
+  using yes = std::true_type;
+  using no = std::false_type;
+  if ((flags & 3) == 3) gather(yes{}, yes{});
+  else if (flags & 1) gather(yes{}, no{});
+  else gather(no{}, yes{});
 }
 
 }  // namespace dsa

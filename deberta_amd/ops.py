@@ -15,6 +15,9 @@ Tensor layouts (see include/dsa.h):
   pair_keep         uint8 [B, Lq, Lk] or None (pairwise keep mask)
   out               [B, Lq, H, D] contiguous, dtype of q
   lse               float32 [B, H, Lq]
+  bias              [B, H, pad128(Lq), pad128(Lk)] the relative score term
+                    c2p + p2c saved for the backward (float16 for bfloat16
+                    inputs, float32 for float32); empty when not saved
 """
 
 from __future__ import annotations
@@ -55,6 +58,19 @@ def _flags(kr: Optional[Tensor], qr: Optional[Tensor]) -> int:
     return (_lib.DSA_C2P if kr is not None else 0) | (_lib.DSA_P2C if qr is not None else 0)
 
 
+def _pad128(n: int) -> int:
+    return (n + 127) // 128 * 128
+
+
+def bias_shape(q: Tensor, k: Tensor) -> tuple[int, int, int, int]:
+    """Shape of the saved relative term (``dsa_fwd_args.bias``)."""
+    return (q.shape[0], q.shape[2], _pad128(q.shape[1]), _pad128(k.shape[1]))
+
+
+def bias_dtype(dtype: torch.dtype) -> torch.dtype:
+    return torch.float16 if dtype == torch.bfloat16 else torch.float32
+
+
 def _fill_fwd_args(
     q: Tensor,
     k: Tensor,
@@ -68,6 +84,7 @@ def _fill_fwd_args(
     lse: Tensor,
     att_span: int,
     scale: float,
+    bias: Optional[Tensor] = None,
 ) -> _lib.DsaFwdArgs:
     B, Lq, H, D = q.shape
     Lk = k.shape[1]
@@ -77,6 +94,7 @@ def _fill_fwd_args(
     a.rel_table = _ptr(rel_table)
     a.key_keep, a.pair_keep = _ptr(key_keep), _ptr(pair_keep)
     a.out, a.lse = out.data_ptr(), lse.data_ptr()
+    a.bias = _ptr(bias) if bias is not None and bias.numel() else None
     a.q_strides[:] = _strides3(q)
     a.k_strides[:] = _strides3(k)
     a.v_strides[:] = _strides3(v)
@@ -142,7 +160,11 @@ def dsa_fwd(
     pair_keep: Optional[Tensor],
     att_span: int,
     scale: float,
-) -> tuple[Tensor, Tensor]:
+    save_bias: bool = True,
+) -> tuple[Tensor, Tensor, Tensor]:
+    """(out, lse, bias).  With c2p/p2c and ``save_bias`` the relative score
+    term is written to ``bias`` for the backward (which needs it); else
+    ``bias`` is empty."""
     _validate(q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span)
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
     kr = None if kr is None else _kernel_ready(kr)
@@ -150,19 +172,27 @@ def dsa_fwd(
     B, Lq, H, D = q.shape
     out = torch.empty((B, Lq, H, D), dtype=q.dtype, device=q.device)
     lse = torch.empty((B, H, Lq), dtype=torch.float32, device=q.device)
-    args = _fill_fwd_args(q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, att_span, scale)
+    if save_bias and (kr is not None or qr is not None):
+        bias = torch.empty(bias_shape(q, k), dtype=bias_dtype(q.dtype), device=q.device)
+    else:
+        bias = torch.empty((0,), dtype=bias_dtype(q.dtype), device=q.device)
+    args = _fill_fwd_args(q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, att_span, scale, bias)
     lib = _lib.load()
     stream = torch.cuda.current_stream(q.device).cuda_stream
     _lib.check(lib.dsa_fwd(ctypes.byref(args), ctypes.c_void_p(stream)), "dsa_fwd")
-    return out, lse
+    return out, lse, bias
 
 
 @dsa_fwd.register_fake
-def _dsa_fwd_fake(q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, scale):
+def _dsa_fwd_fake(q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias=True):
     B, Lq, H, D = q.shape
     out = q.new_empty((B, Lq, H, D))
     lse = q.new_empty((B, H, Lq), dtype=torch.float32)
-    return out, lse
+    if save_bias and (kr is not None or qr is not None):
+        bias = q.new_empty(bias_shape(q, k), dtype=bias_dtype(q.dtype))
+    else:
+        bias = q.new_empty((0,), dtype=bias_dtype(q.dtype))
+    return out, lse, bias
 
 
 def bwd_workspace_bytes(args: _lib.DsaBwdArgs) -> int:
@@ -181,6 +211,7 @@ def fill_bwd_args(
     pair_keep: Optional[Tensor],
     out: Tensor,
     lse: Tensor,
+    bias: Optional[Tensor],
     att_span: int,
     scale: float,
     dq: Tensor,
@@ -190,7 +221,7 @@ def fill_bwd_args(
     dqr: Optional[Tensor],
 ) -> _lib.DsaBwdArgs:
     a = _lib.DsaBwdArgs()
-    a.fwd = _fill_fwd_args(q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, att_span, scale)
+    a.fwd = _fill_fwd_args(q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, att_span, scale, bias)
     a.dout = dout.data_ptr()
     a.do_strides[:] = _strides3(dout)
     a.dq, a.dk, a.dv = dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
@@ -215,14 +246,18 @@ def dsa_bwd(
     pair_keep: Optional[Tensor],
     out: Tensor,
     lse: Tensor,
+    bias: Tensor,
     att_span: int,
     scale: float,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     """Gradients (dq, dk, dv, dkr, dqr).  dkr/dqr are float32 [H, 2A, D]
-    (empty when the matching table is None)."""
+    (empty when the matching table is None).  ``bias`` is the relative term
+    dsa_fwd saved (required with c2p/p2c)."""
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
     kr = None if kr is None else _kernel_ready(kr)
     qr = None if qr is None else _kernel_ready(qr)
+    if (kr is not None or qr is not None) and tuple(bias.shape) != bias_shape(q, k):
+        raise RuntimeError("dsa_bwd: the relative term saved by dsa_fwd (save_bias=True) is required")
     dout = _kernel_ready(dout.to(q.dtype))
     out = _kernel_ready(out)
     B, Lq, H, D = q.shape
@@ -234,7 +269,7 @@ def dsa_bwd(
     dkr = torch.zeros((H, R, D), **f32) if kr is not None else torch.empty((0,), **f32)
     dqr = torch.zeros((H, R, D), **f32) if qr is not None else torch.empty((0,), **f32)
     args = fill_bwd_args(
-        dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, att_span, scale,
+        dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, att_span, scale,
         dq, dk, dv, dkr if kr is not None else None, dqr if qr is not None else None,
     )
     ws = torch.empty((max(bwd_workspace_bytes(args), 16),), dtype=torch.uint8, device=q.device)
@@ -247,7 +282,7 @@ def dsa_bwd(
 
 
 @dsa_bwd.register_fake
-def _dsa_bwd_fake(dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, att_span, scale):
+def _dsa_bwd_fake(dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, att_span, scale):
     H, D = q.shape[2], q.shape[3]
     R = 2 * int(att_span)
     f32 = dict(dtype=torch.float32)
@@ -263,22 +298,22 @@ def _dsa_bwd_fake(dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, ls
 
 
 def _setup_context(ctx, inputs, output):
-    q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, scale = inputs
-    out, lse = output
-    ctx.mark_non_differentiable(lse)
-    ctx.save_for_backward(q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse)
+    q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias = inputs
+    out, lse, bias = output
+    ctx.mark_non_differentiable(lse, bias)
+    ctx.save_for_backward(q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias)
     ctx.att_span = att_span
     ctx.scale = scale
 
 
-def _backward(ctx, dout, dlse):
-    q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse = ctx.saved_tensors
+def _backward(ctx, dout, dlse, dbias):
+    q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias = ctx.saved_tensors
     dq, dk, dv, dkr, dqr = dsa_bwd(
-        dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, ctx.att_span, ctx.scale
+        dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, ctx.att_span, ctx.scale
     )
     gkr = dkr.to(kr.dtype) if kr is not None else None
     gqr = dqr.to(qr.dtype) if qr is not None else None
-    return dq, dk, dv, gkr, gqr, None, None, None, None, None
+    return dq, dk, dv, gkr, gqr, None, None, None, None, None, None
 
 
 torch.library.register_autograd("deberta_amd::dsa_fwd", _backward, setup_context=_setup_context)

@@ -80,6 +80,10 @@ typedef struct dsa_fwd_args {
   const uint8_t* pair_keep; /* [B, Lq, Lk] or NULL */
   void* out;              /* [B, Lq, H, D], same dtype as q */
   float* lse;             /* [B, H, Lq] contiguous, natural-log logsumexp */
+  void* bias;             /* optional [B, H, round_up(Lq, 128), round_up(Lk, 128)]
+                             contiguous: the relative score term c2p + p2c
+                             (unscaled; fp16 for bf16 inputs, fp32 for fp32),
+                             written for dsa_bwd.  NULL: not written. */
   int64_t q_strides[3];   /* element strides of b, l, h */
   int64_t k_strides[3];
   int64_t v_strides[3];
@@ -128,6 +132,11 @@ int dsa_bwd(const dsa_bwd_args* args, void* stream);
 
 /* Workspace bytes dsa_bwd needs for these arguments. */
 size_t dsa_bwd_workspace_bytes(const dsa_bwd_args* args);
+
+/* Bytes of dsa_fwd_args.bias for these arguments (0 without c2p / p2c).
+ * No counterpart in the reference, which keeps its (B, H, L, L) relative
+ * terms alive for autograd instead. */
+size_t dsa_fwd_bias_bytes(const dsa_fwd_args* args);
 
 /* Thread-local description of the last error (empty string if none). */
 const char* dsa_last_error(void);

@@ -118,7 +118,7 @@ def hip_run(c: Case, x: dict, dtype: torch.dtype, device, grads: bool = True) ->
     kk, pk = kernel_masks(mask, c.B, c.L, Lk)
     sf = 1 + sum(t in types for t in ("c2p", "p2c", "p2p"))
     scale = 1.0 / math.sqrt(c.D * sf)
-    out, lse = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, kk, pk, c.A, scale)
+    out, lse, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, kk, pk, c.A, scale)
     res = {"out": out.detach().float().cpu(), "lse": lse.detach().cpu()}
     if grads:
         dout = x["dout"].to(device=device, dtype=dtype)

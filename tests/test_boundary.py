@@ -132,10 +132,11 @@ def test_fake_shapes():
 
     with FakeTensorMode():
         q, k, v, kr, qr, table = _inputs()
-        out, lse = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, 16, 0.1)
+        out, lse, bias = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, 16, 0.1)
         assert out.shape == q.shape and out.dtype == q.dtype
         assert lse.shape == (2, 2, 64) and lse.dtype == torch.float32
-        g = torch.ops.deberta_amd.dsa_bwd(out, q, k, v, kr, qr, table, None, None, out, lse, 16, 0.1)
+        assert bias.shape == (2, 2, 128, 128) and bias.dtype == torch.float16
+        g = torch.ops.deberta_amd.dsa_bwd(out, q, k, v, kr, qr, table, None, None, out, lse, bias, 16, 0.1)
         assert [t.shape for t in g] == [q.shape, k.shape, v.shape, (2, 32, 64), (2, 32, 64)]
         assert g[3].dtype == torch.float32
 
@@ -146,7 +147,7 @@ def test_trace_forward_and_backward_with_fake_tensors():
     from torch.fx.experimental.proxy_tensor import make_fx
 
     def f(q, k, v, kr, qr, table, dout):
-        out, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, 16, 0.1)
+        out, _, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, 16, 0.1)
         return torch.autograd.grad(out, (q, k, v, kr, qr), dout)
 
     q, k, v, kr, qr, table = _inputs()
