@@ -92,7 +92,10 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
   constexpr int ND = D / 16;
   constexpr int FE = M::FRAG_ELEMS;
   constexpr int KSTR = D + Pad<T>::v;
-  constexpr int XSTR = XCOLS + Pad<T>::v;
+  // Row stride of X chosen for few LDS bank conflicts in its diagonal walks
+  // (178: two-way at most; rows are then only 4-byte aligned).
+  constexpr int XSTR = sizeof(T) == 2 ? 178 : XCOLS + Pad<T>::v;
+  constexpr int QSTR = KSTR;
   constexpr int GC_STEPS = (16 + JC + M::KSTEP - 2) / M::KSTEP;  // k steps covering 16 + JC - 1 columns
   constexpr int XV = JC * XC / VEC;   // 16-byte chunks of the staged region
   constexpr int RV = JC * D / VEC;    // 16-byte chunks of 32 key (or query) rows
@@ -101,7 +104,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
 
   __shared__ __align__(16) T Xs[XROWS * XSTR];
   __shared__ __align__(16) T Kc[JC * KSTR];
-  __shared__ __align__(16) T Qring[QRING * KSTR];
+  __shared__ __align__(16) T Qring[QRING * QSTR];
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, g = (tid & 63) >> 4, c16 = tid & 15;
@@ -125,10 +128,9 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
     vecT z;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) z[e] = (T)0.0f;
-    constexpr int VPR = XSTR / VEC;
-    for (int c = tid; c < XP * VPR; c += 256) reinterpret_cast<vecT*>(Xs)[c] = z;
-    for (int c = tid; c < (XROWS - XP - JC) * VPR; c += 256) reinterpret_cast<vecT*>(Xs + (XP + JC) * XSTR)[c] = z;
-    for (int c = tid; c < QRING * KSTR / VEC; c += 256) reinterpret_cast<vecT*>(Qring)[c] = z;
+    static_assert(XROWS * XSTR % VEC == 0 && QRING * QSTR % VEC == 0, "whole 16-byte chunks");
+    for (int c = tid; c < XROWS * XSTR / VEC; c += 256) reinterpret_cast<vecT*>(Xs)[c] = z;
+    for (int c = tid; c < QRING * QSTR / VEC; c += 256) reinterpret_cast<vecT*>(Qring)[c] = z;
   }
 
   f32x4 gc[2][ND], gp[2][ND];
@@ -183,7 +185,11 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
 #pragma unroll
     for (int k = 0; k < XCH; ++k) {
       const int c = tid + 256 * k;
-      if (c < XV) *reinterpret_cast<vecT*>(Xs + (XP + c / (XC / VEC)) * XSTR + (c % (XC / VEC)) * VEC) = xr[k];
+      if (c < XV) {
+        const int r = c / (XC / VEC), c0 = (c % (XC / VEC)) * VEC;
+        *reinterpret_cast<vecT*>(Xs + (XP + r) * XSTR + c0) = xr[k];
+
+      }
     }
 #pragma unroll
     for (int k = 0; k < RCH; ++k) {
@@ -191,12 +197,12 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
       if (c < RV) {
         const int r = c / (D / VEC), c0 = (c % (D / VEC)) * VEC;
         *reinterpret_cast<vecT*>(Kc + r * KSTR + c0) = kr[k];
-        *reinterpret_cast<vecT*>(Qring + ((ib0 + XC - JC + r) & (QRING - 1)) * KSTR + c0) = qr[k];
+        *reinterpret_cast<vecT*>(Qring + ((ib0 + XC - JC + r) & (QRING - 1)) * QSTR + c0) = qr[k];
       }
     }
     if (c2p && j0 == jstart) {  // first chunk of a batch: the ring's older rows too
       const T* qbase = (const T*)p.q + (int64_t)b * p.qs[0] + (int64_t)h * p.qs[2];
-      load_ring_rows<T, D>(Qring, KSTR, qbase, p.qs[1], ib0, XC - JC, p.Lq, tid);
+      load_ring_rows<T, D>(Qring, QSTR, qbase, p.qs[1], ib0, XC - JC, p.Lq, tid);
     }
     __syncthreads();
     if (st + 1 < nsteps) fetch(st + 1);
@@ -230,7 +236,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
           for (int e = 0; e < FE; ++e) bfr[e] = dg[e * (XSTR + 1)];
 #pragma unroll
           for (int db = 0; db < ND; ++db) {
-            const frag af = tr_contig_ring<T>(Qring, KSTR, ib0, c0 + M::KSTEP * s, 16 * db, g, c16);
+            const frag af = tr_contig_ring<T>(Qring, QSTR, ib0, c0 + M::KSTEP * s, 16 * db, g, c16);
             gc[t][db] = M::mma(af, bfr, gc[t][db]);
           }
         }

@@ -7,7 +7,10 @@
 //   + c2p band (per wave)            MFMA  Kr[c(x)] Q^T  -> LDS (fp16) -> gather
 //   + p2c band (per workgroup)       MFMA  K Qr[p(x)]^T  -> LDS (fp16) -> gather
 //   mask, online softmax (exp2)      fp32, per query column
-//   O^T += V^T P^T                   MFMA, P fed from registers (ACC k-set)
+//   O^T += V^T P^T                   MFMA, P fed from registers (ACC k-set),
+//                                    V^T read transposed from LDS
+// The next key tile is fetched into registers while the current one is
+// computed.
 //
 // The score tile is kept transposed (keys down, queries across) so that the
 // probabilities a lane holds are already the B operand of the PV product.
@@ -27,13 +30,16 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
   typedef typename M::frag frag;
   typedef typename BandType<T>::type BT;
   constexpr int NS = D / M::KSTEP;        // k steps over the head dim
-  constexpr int KSTR = D + Pad<T>::v;      // Ks row stride
-  constexpr int VSTR = BK + Pad<T>::v;     // Vt row stride
+  constexpr int KSTR = D + Pad<T>::v;      // Ks / Vs row stride
   constexpr int ND = D / 16;               // 16-wide tiles over the head dim
   constexpr int PV_STEPS = BK / M::KSTEP;  // k steps over the key tile
+  constexpr int VEC = 16 / sizeof(T);
+  typedef T vecT __attribute__((ext_vector_type(VEC)));
+  constexpr int KV = BK * D / VEC;         // 16-byte chunks of a K (or V) tile
+  constexpr int KCH = (KV + 255) / 256;
 
   __shared__ __align__(16) T Ks[BK * KSTR];
-  __shared__ __align__(16) T Vt[D * VSTR];
+  __shared__ __align__(16) T Vs[BK * KSTR];
   __shared__ short crow[XG], prow[XG];
   __shared__ __align__(16) BT cb_all[NW * CB_ELEMS];
   __shared__ __align__(16) BT pb[PB_ELEMS];
@@ -100,6 +106,27 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
   }
   const bool any_live = __syncthreads_or(wg_live);
 
+  // The next key tile (K and V rows) is fetched into registers while the
+  // current one is computed.
+  vecT kr[KCH], vr[KCH];
+  int kfetched = -1;
+  auto fetch = [&](int kt) {
+    const int j0 = kt * BK;
+#pragma unroll
+    for (int k = 0; k < KCH; ++k) {
+      const int c = tid + 256 * k;
+      const int j = j0 + c / (D / VEC), c0 = (c % (D / VEC)) * VEC;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) kr[k][e] = vr[k][e] = (T)0.0f;
+      if (c < KV && j < Lk) {
+        kr[k] = *reinterpret_cast<const vecT*>(kbase + (int64_t)j * p.ks[1] + c0);
+        vr[k] = *reinterpret_cast<const vecT*>(vbase + (int64_t)j * p.vs[1] + c0);
+      }
+    }
+    kfetched = kt;
+  };
+  if (any_live) fetch(0);
+
   for (int kt = 0; any_live && kt < nkt; ++kt) {
     const int j0 = kt * BK;
     // Skip key tiles that every query row of the workgroup masks out: their
@@ -121,10 +148,19 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
       if (!__syncthreads_or(keep)) continue;
     }
     __syncthreads();  // previous tile's LDS reads are done
-    load_rows<T, D, BK, 256>(Ks, KSTR, nullptr, 0, kbase, p.ks[1], j0, Lk, tid);
-    load_rows<T, D, BK, 256>(nullptr, 0, Vt, VSTR, vbase, p.vs[1], j0, Lk, tid);
+    if (kt != kfetched) fetch(kt);  // a tile after skipped ones was not prefetched
+#pragma unroll
+    for (int k = 0; k < KCH; ++k) {
+      const int c = tid + 256 * k;
+      if (c < KV) {
+        const int r = c / (D / VEC), c0 = (c % (D / VEC)) * VEC;
+        *reinterpret_cast<vecT*>(Ks + r * KSTR + c0) = kr[k];
+        *reinterpret_cast<vecT*>(Vs + r * KSTR + c0) = vr[k];
+      }
+    }
     if (p.flags) load_row_tables(crow, prow, p.rel, i0, j0, Lq, Lk, A, tid);
     __syncthreads();
+    if (kt + 1 < nkt) fetch(kt + 1);
 
     // ---- y = (K Q^T) * scale*log2e + c2p + p2c -----------------------------
     frag kf[4][NS];
@@ -205,7 +241,7 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
       for (int ib = 0; ib < 2; ++ib) pf[ib] = M::from_acc(st[ib], s);
 #pragma unroll
       for (int db = 0; db < ND; ++db) {
-        const frag vf = M::load_acc(&Vt[(16 * db + c16) * VSTR], s, g);
+        const frag vf = tr_acc<T>(Vs, KSTR, s * M::KSTEP, 16 * db, g, c16);
 #pragma unroll
         for (int ib = 0; ib < 2; ++ib) o[db][ib] = M::mma(vf, pf[ib], o[db][ib]);
       }
