@@ -6,7 +6,8 @@
 //   S^T = K Q^T                      MFMA, K tile from LDS, Q^T in registers
 //   + c2p band (per wave)            MFMA  Kr[c(x)] Q^T  -> LDS (fp16) -> gather
 //   + p2c band (per workgroup)       MFMA  K Qr[p(x)]^T  -> LDS (fp16) -> gather
-//   mask, online softmax (exp2)      fp32, per query column
+//   mask, online softmax (exp2)      fp32, per query column, with a lazily
+//                                    raised reference max
 //   O^T += V^T P^T                   MFMA, P fed from registers (ACC k-set),
 //                                    V^T read transposed from LDS
 // The next key tile is fetched into registers while the current one is
@@ -81,13 +82,14 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
     for (int s = 0; s < NS; ++s)
       qf[ib][s] = (irow[ib] < Lq) ? M::load_contig(qbase + (int64_t)irow[ib] * p.qs[1], s, g) : M::zero();
 
-  float mrow[2] = {-INFINITY, -INFINITY};
+  float mref[2] = {-INFINITY, -INFINITY};  // reference max of the unscaled scores
   float lrow[2] = {0.f, 0.f};
   f32x4 o[ND][2];
 #pragma unroll
   for (int db = 0; db < ND; ++db) o[db][0] = o[db][1] = zero4();
 
   const float sl2 = p.scale * kLog2e;
+  const float thr = 8.f / sl2;  // reference-max slack (unscaled): p <= 2^8
   const int nkt = (Lk + BK - 1) / BK;
   // this lane's first element of the saved relative term in each key tile
   BT* biasl = (p.bias && p.flags) ? (BT*)p.bias + bias_tile_offset(b, h, p.H, qt, 0, p.LqP, p.LkP) + w * 2048 +
@@ -109,9 +111,11 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
   // The next key tile (K and V rows) is fetched into registers while the
   // current one is computed.
   vecT kr[KCH], vr[KCH];
+  int relv = 0;  // this thread's relative position of the fetched tile (tid < XG)
   int kfetched = -1;
   auto fetch = [&](int kt) {
     const int j0 = kt * BK;
+    if (p.flags && tid < XG) relv = rel_of_tile(p.rel, i0, j0, Lq, Lk, tid);
 #pragma unroll
     for (int k = 0; k < KCH; ++k) {
       const int c = tid + 256 * k;
@@ -158,11 +162,11 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
         *reinterpret_cast<vecT*>(Vs + r * KSTR + c0) = vr[k];
       }
     }
-    if (p.flags) load_row_tables(crow, prow, p.rel, i0, j0, Lq, Lk, A, tid);
+    if (p.flags) store_row_tables(crow, prow, relv, A, tid);
     __syncthreads();
     if (kt + 1 < nkt) fetch(kt + 1);
 
-    // ---- y = (K Q^T) * scale*log2e + c2p + p2c -----------------------------
+    // ---- y = K Q^T + c2p + p2c (unscaled) -------------------------------------
     frag kf[4][NS];
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb)
@@ -176,61 +180,81 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
         f32x4 acc = zero4();
 #pragma unroll
         for (int s = 0; s < NS; ++s) acc = M::mma(kf[jb][s], qf[ib][s], acc);
-        st[ib][jb] = acc * sl2;
+        st[ib][jb] = acc;
       }
     if (p.flags)
       add_delta_bands_T<T, D>(st, kf, qf, cb, pb, crow, prow, w, g, c16, krh, p.krs[1], qrh, p.qrs[1], p.flags,
-                              sl2, biasl ? biasl + (int64_t)kt * 8192 : nullptr);
+                              biasl ? biasl + (int64_t)kt * 8192 : nullptr);
 
-    // ---- mask + online softmax (log2 domain) --------------------------------
+    // ---- mask: only where a key or query of the tile can be masked out ------
+    if (MASK != MASK_NONE || j0 + BK > Lk) {
 #pragma unroll
-    for (int ib = 0; ib < 2; ++ib) {
-      const int i = irow[ib];
-      float mt = -INFINITY;
+      for (int ib = 0; ib < 2; ++ib) {
+        const int i = irow[ib];
 #pragma unroll
-      for (int jb = 0; jb < 4; ++jb) {
-        uint32_t pk4 = 0;
-        if (MASK == MASK_PAIR && ilive[ib]) {
-          const uint8_t* row = pkb + (int64_t)i * p.pkq;
+        for (int jb = 0; jb < 4; ++jb) {
+          uint32_t pk4 = 0;
+          if (MASK == MASK_PAIR && ilive[ib]) {
+            const uint8_t* row = pkb + (int64_t)i * p.pkq;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int j = j0 + 16 * jb + 4 * g + e;
+              pk4 |= (j < Lk && row[j]) ? (1u << e) : 0u;
+            }
+          }
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int j = j0 + 16 * jb + 4 * g + e;
-            pk4 |= (j < Lk && row[j]) ? (1u << e) : 0u;
+            bool keep = ilive[ib] && j < Lk;
+            if (MASK == MASK_KEY) keep = keep && kkb[j] != 0;
+            if (MASK == MASK_PAIR) keep = keep && ((pk4 >> e) & 1u);
+            if (!keep) st[ib][jb][e] = -INFINITY;
           }
         }
+      }
+    }
+
+    // ---- online softmax -------------------------------------------------------
+    // Scores stay unscaled; p = exp2((y - m) * scale*log2e) against a
+    // reference max m per query that is raised (and O, l rescaled) only when
+    // a score exceeds it by more than thr, so p <= 2^8.  Queries whose keys
+    // are all masked so far keep m = -inf and p = 0.
+    float lm[2];
+    bool raise = false;
+#pragma unroll
+    for (int ib = 0; ib < 2; ++ib) {
+      float mt = -INFINITY;
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) mt = fmaxf(mt, st[ib][jb][e]);
+      lm[ib] = mt;
+      raise = raise || mt > mref[ib] + thr;
+    }
+    if (__any(raise)) {
+#pragma unroll
+      for (int ib = 0; ib < 2; ++ib) {
+        const float mnew = fmaxf(mref[ib], col_max(lm[ib]));
+        const float alpha = (mref[ib] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((mref[ib] - mnew) * sl2);
+        lrow[ib] *= alpha;
+#pragma unroll
+        for (int db = 0; db < ND; ++db) o[db][ib] *= alpha;
+        mref[ib] = mnew;
+      }
+    }
+#pragma unroll
+    for (int ib = 0; ib < 2; ++ib) {
+      const float mb = (mref[ib] == -INFINITY) ? 0.f : mref[ib] * sl2;
+      float ls = 0.f;
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int j = j0 + 16 * jb + 4 * g + e;
-          bool keep = ilive[ib] && j < Lk;
-          if (MASK == MASK_KEY) keep = keep && kkb[j] != 0;
-          if (MASK == MASK_PAIR) keep = keep && ((pk4 >> e) & 1u);
-          const float y = keep ? st[ib][jb][e] : -INFINITY;
-          st[ib][jb][e] = y;
-          mt = fmaxf(mt, y);
+          const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(st[ib][jb][e], sl2, -mb));
+          st[ib][jb][e] = pe;
+          ls += pe;
         }
-      }
-      mt = col_max(mt);
-      const float mnew = fmaxf(mrow[ib], mt);
-      float alpha = 1.f;
-      if (mnew != -INFINITY) {
-        alpha = __builtin_amdgcn_exp2f(mrow[ib] - mnew);  // 0 when mrow was -inf
-        float ls = 0.f;
-#pragma unroll
-        for (int jb = 0; jb < 4; ++jb)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float pe = __builtin_amdgcn_exp2f(st[ib][jb][e] - mnew);
-            st[ib][jb][e] = pe;
-            ls += pe;
-          }
-        lrow[ib] = lrow[ib] * alpha + ls;
-        mrow[ib] = mnew;
-      } else {
-#pragma unroll
-        for (int jb = 0; jb < 4; ++jb) st[ib][jb] = zero4();
-      }
-#pragma unroll
-      for (int db = 0; db < ND; ++db) o[db][ib] *= alpha;
+      lrow[ib] += ls;
     }
 
     // ---- O^T += V^T P^T -------------------------------------------------------
@@ -266,7 +290,7 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
         for (int e = 0; e < 4; ++e) v[e] = (T)(o[db][ib][e] * inv);
         *reinterpret_cast<vec4*>(orow + 16 * db + 4 * g) = v;
       }
-      if (g == 0) p.lse[((int64_t)b * p.H + h) * Lq + i] = ok ? (mrow[ib] * kLn2 + logf(lsum)) : INFINITY;
+      if (g == 0) p.lse[((int64_t)b * p.H + h) * Lq + i] = ok ? (mref[ib] * p.scale + logf(lsum)) : INFINITY;
     }
   }
 }

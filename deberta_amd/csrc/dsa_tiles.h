@@ -98,8 +98,8 @@ DSA_DEV void load_rows(T* dst, int str, T* dstT, int strT, const T* src, int64_t
 //   c2p: per wave, rows x in [32w, 32w + 96) x the wave's 32 queries
 //   p2c: per workgroup, rows x in [0, 192) x the 64 keys, shared by all waves
 // Band values are stored unscaled, in fp16 for bf16 inputs (saturated to the
-// fp16 range) and in fp32 for fp32 inputs; the gather multiplies them by the
-// softmax's log2-domain scale as it adds them (one mixed-precision FMA).
+// fp16 range) and in fp32 for fp32 inputs; the gather adds them to the
+// unscaled score (one mixed-precision FMA).
 // ---------------------------------------------------------------------------
 template <typename T>
 struct BandType {
@@ -145,12 +145,16 @@ constexpr int PB_ELEMS = BK * PBS;
 // Row tables of one tile: crow[x] / prow[x] are the c2p / p2c table rows of
 // offset x (x = (i - i0) - (j - j0) + 63, i0 / j0 the tile's first query /
 // key), for x in [0, 192).
-DSA_DEV void load_row_tables(short* crow, short* prow, const int32_t* rel, int i0, int j0, int Lq, int Lk, int A,
-                             int tid) {
+// rel_of_tile reads thread tid's relative position (tid < XG), store_row_tables
+// turns it into the two table rows.
+DSA_DEV int rel_of_tile(const int32_t* rel, int i0, int j0, int Lq, int Lk, int tid) {
+  int d = i0 - j0 - (dcfg::BK - 1) + tid;
+  d = min(max(d, -(Lk - 1)), Lq - 1);
+  return rel[d + Lk - 1];
+}
+
+DSA_DEV void store_row_tables(short* crow, short* prow, int t, int A, int tid) {
   if (tid < dcfg::XG) {
-    int d = i0 - j0 - (dcfg::BK - 1) + tid;
-    d = min(max(d, -(Lk - 1)), Lq - 1);
-    int t = rel[d + Lk - 1];
     t = min(max(t, -A), A);
     crow[tid] = (short)c2p_row(t, A);
     prow[tid] = (short)p2c_row(t, A);
@@ -183,9 +187,10 @@ DSA_DEV void store4_contig(B* p, const f32x4& v) {
   }
 }
 
-// Adds the scaled c2p + p2c terms to a transposed score tile (keys down,
+// Adds the c2p + p2c terms to a transposed score tile (keys down,
 // queries across; y[ib][jb][e] = key 16*jb + 4*g + e, query 32*w + 16*ib +
-// c16 of the tile).  y must already hold (q.k) * scale*log2(e).
+// c16 of the tile).  y holds q.k on entry and q.k + c2p + p2c (unscaled)
+// on return.
 //   kf: A fragments of the 64 key rows, qf: B fragments of the wave's queries
 //   cb: this wave's c2p band (XW * CBS), pb: the shared p2c band (BK * PBS)
 //   bias: if not null, where this lane's part of the tile's saved relative
@@ -198,7 +203,7 @@ DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&
                                const typename Mfma<T>::frag (&qf)[2][D / Mfma<T>::KSTEP],
                                typename BandType<T>::type* cb, typename BandType<T>::type* pb, const short* crow,
                                const short* prow, int w, int g, int c16, const T* krh, int64_t krs, const T* qrh,
-                               int64_t qrs, int flags, float sl2, typename BandType<T>::type* bias = nullptr) {
+                               int64_t qrs, int flags, typename BandType<T>::type* bias = nullptr) {
   using M = Mfma<T>;
   typedef typename M::frag frag;
   typedef typename BandType<T>::type BT;
@@ -243,8 +248,8 @@ DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&
   // p2c: row j = 16*jb + 4*g + e, column x = 32w + (16*ib + c16) - (16*jb + 4*g + e) + 63
   const BT* pbase = pb + 4 * g * PBS + WQ * w + c16 - 4 * g + 63;
   // The two terms are summed in the band type (for fp16: one rounding of the
-  // exact sum, which is also the value saved), then scaled into the score
-  // with one mixed-precision FMA per element.  The uniform flag test sits
+  // exact sum, which is also the value saved), then added to the score with
+  // one mixed-precision FMA per element.  The uniform flag test sits
   // outside the loops.
   auto gather = [&](auto with_c, auto with_p) {
 #pragma unroll
@@ -260,7 +265,7 @@ DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&
           bs[e] = v;
         }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) y[ib][jb][e] = __builtin_fmaf((float)bs[e], sl2, y[ib][jb][e]);
+        for (int e = 0; e < 4; ++e) y[ib][jb][e] = __builtin_fmaf((float)bs[e], 1.0f, y[ib][jb][e]);
         if (bias) {
           typedef BT b4 __attribute__((ext_vector_type(4)));
           *reinterpret_cast<b4*>(bias + (ib * 4 + jb) * 256) = b4{bs[0], bs[1], bs[2], bs[3]};
