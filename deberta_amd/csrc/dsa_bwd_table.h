@@ -16,6 +16,8 @@
 //   Gc^T[dd] += sum_c   Q^T[i0 + c] X[c - dd][c]
 // Both B operands walk a diagonal of X (eight single-element LDS reads per
 // fragment); zero rows around X cover the out-of-chunk part of the walk.
+// A wave's two offset blocks share their A operands (the c2p one over 64
+// staged columns, with diagonal elements outside the chunk read as zeros).
 // Wave w accumulates offsets [32w, 32w + 32) of the block in registers and
 // writes them once, to a per-(block, head, batch group) partial.
 #pragma once
@@ -29,7 +31,7 @@ constexpr int NW = 4;
 constexpr int DBW = 128;           // offsets per block
 constexpr int JC = 32;             // keys per step
 constexpr int XC = DBW + JC;       // staged columns
-constexpr int XP = 16;             // zero rows above the staged rows
+constexpr int XP = 32;             // zero rows above the staged rows
 constexpr int XROWS = XP + JC + 32;  // and 32 below
 constexpr int XCOLS = DBW + 48;    // columns a diagonal walk can touch
 constexpr int QRING = 256;         // query rows kept (power of two >= XC)
@@ -96,7 +98,8 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
   // (178: two-way at most; rows are then only 4-byte aligned).
   constexpr int XSTR = sizeof(T) == 2 ? 178 : XCOLS + Pad<T>::v;
   constexpr int QSTR = KSTR;
-  constexpr int GC_STEPS = (16 + JC + M::KSTEP - 2) / M::KSTEP;  // k steps covering 16 + JC - 1 columns
+  constexpr int GC_STEPS = 64 / M::KSTEP;  // k steps over the 64 staged columns a wave's two blocks read
+  constexpr int GP_STEPS = JC / M::KSTEP;
   constexpr int XV = JC * XC / VEC;   // 16-byte chunks of the staged region
   constexpr int RV = JC * D / VEC;    // 16-byte chunks of 32 key (or query) rows
   constexpr int XCH = (XV + 255) / 256, RCH = (RV + 255) / 256;
@@ -207,38 +210,49 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
     __syncthreads();
     if (st + 1 < nsteps) fetch(st + 1);
 
+    // A operands, shared by the wave's two 16-offset blocks: K^T of the 32
+    // keys, and Q^T of staged columns [32w, 32w + 64).
+    frag ka[GP_STEPS][ND], qa[GC_STEPS][ND];
+    if (p2c) {
+#pragma unroll
+      for (int s = 0; s < GP_STEPS; ++s)
+#pragma unroll
+        for (int db = 0; db < ND; ++db) ka[s][db] = tr_contig<T>(Kc, KSTR, s * M::KSTEP, 16 * db, g, c16);
+    }
+    if (c2p) {
+#pragma unroll
+      for (int s = 0; s < GC_STEPS; ++s)
+#pragma unroll
+        for (int db = 0; db < ND; ++db)
+          qa[s][db] = tr_contig_ring<T>(Qring, QSTR, ib0, 32 * w + M::KSTEP * s, 16 * db, g, c16);
+    }
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int c0 = 16 * (2 * w + t);  // first offset of this wave's 16-offset block
       if (p2c) {
         // Gp^T[d][dd] += sum_jj K^T[d][jj] X[jj][jj + dd],  jj = KSTEP*s + FE*g + e
 #pragma unroll
-        for (int s = 0; s < JC / M::KSTEP; ++s) {
+        for (int s = 0; s < GP_STEPS; ++s) {
           frag bfr;
           const T* dg = Xs + (XP + M::KSTEP * s + FE * g) * XSTR + M::KSTEP * s + FE * g + c0 + c16;
 #pragma unroll
           for (int e = 0; e < FE; ++e) bfr[e] = dg[e * (XSTR + 1)];
 #pragma unroll
-          for (int db = 0; db < ND; ++db) {
-            const frag af = tr_contig<T>(Kc, KSTR, s * M::KSTEP, 16 * db, g, c16);
-            gp[t][db] = M::mma(af, bfr, gp[t][db]);
-          }
+          for (int db = 0; db < ND; ++db) gp[t][db] = M::mma(ka[s][db], bfr, gp[t][db]);
         }
       }
       if (c2p) {
-        // Gc^T[d][dd] += sum_c Q^T[d][ib0 + c] X[c - dd][c],  c = c0 + KSTEP*s + FE*g + e
+        // Gc^T[d][dd] += sum_c Q^T[d][ib0 + c] X[c - dd][c],  c = 32w + KSTEP*s + FE*g + e;
+        // X rows c - dd in [-31, 64) (zero outside [0, JC)).
 #pragma unroll
         for (int s = 0; s < GC_STEPS; ++s) {
           frag bfr;
-          const int k = M::KSTEP * s + FE * g;  // c - c0 of element e = 0
-          const T* dg = Xs + (XP + k - c16) * XSTR + c0 + k;
+          const int c = 32 * w + M::KSTEP * s + FE * g;  // column of element e = 0
+          const T* dg = Xs + (XP + c - c0 - c16) * XSTR + c;
 #pragma unroll
           for (int e = 0; e < FE; ++e) bfr[e] = dg[e * (XSTR + 1)];
 #pragma unroll
-          for (int db = 0; db < ND; ++db) {
-            const frag af = tr_contig_ring<T>(Qring, QSTR, ib0, c0 + M::KSTEP * s, 16 * db, g, c16);
-            gc[t][db] = M::mma(af, bfr, gc[t][db]);
-          }
+          for (int db = 0; db < ND; ++db) gc[t][db] = M::mma(qa[s][db], bfr, gc[t][db]);
         }
       }
     }

@@ -26,6 +26,7 @@ class Case:
     seed: int = 0
     Lk: Optional[int] = None
     std: float = 1.0
+    ramp: float = 0.0  # key j scaled by 1 + ramp * j / Lk (score maxima grow along the keys)
 
     @property
     def A(self) -> int:
@@ -47,6 +48,8 @@ def make_inputs(c: Case) -> dict:
     kr = torch.randn(c.H, 2 * c.A, c.D, generator=g) * c.std
     qr = torch.randn(c.H, 2 * c.A, c.D, generator=g) * c.std
     dout = torch.randn(c.B, c.L, c.H, c.D, generator=g)
+    if c.ramp:
+        k = k * (1 + c.ramp * torch.arange(Lk, dtype=torch.float32) / Lk)[None, :, None, None]
     mask = None
     if c.mask == "key":
         lens = torch.randint(max(1, c.L // 8), c.L + 1, (c.B,), generator=g)

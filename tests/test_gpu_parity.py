@@ -76,6 +76,27 @@ def test_fp32_no_mask(c, gpu):
 
 
 # --- masks --------------------------------------------------------------------------
+# --- growing scores: the forward's reference max is raised on most key tiles ----
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+@pytest.mark.parametrize("mask", ["none", "key"])
+def test_growing_scores(mask, dtype, gpu):
+    """Keys scaled up along the sequence, so each 64-key tile's score maxima
+    exceed the previous ones by far more than the forward's reference-max
+    slack (8 in log2 units): the running max is raised and O and l rescaled
+    tile after tile, and softmax rows are nearly one-hot."""
+    if dtype == torch.float32:
+        c = Case(B=2, H=2, L=384, D=64, std=2.0, ramp=3.0, mask=mask, seed=41)  # log2 scores to +-50
+        _check(c, dtype, gpu)
+    else:
+        # Scores to +-28 (log2 units): larger ones put the fp16-stored relative
+        # term's rounding (2^-10 relative) above the absolute bf16 tolerance,
+        # as the reference's own bf16 products (2^-9) would be.  Gradients at
+        # these magnitudes exceed it through input rounding alone, so the
+        # forward is compared.
+        c = Case(B=2, H=2, L=384, D=64, std=1.0, ramp=8.0, mask=mask, seed=41)
+        _check(c, dtype, gpu, grads=False)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
 @pytest.mark.parametrize("mask", ["key", "pair", "dead"])
 def test_masks(mask, dtype, gpu):
