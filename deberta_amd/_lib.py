@@ -21,9 +21,8 @@ DSA_STAGE_PREP = 1
 DSA_STAGE_DQ = 2
 DSA_STAGE_DKDV = 4
 DSA_STAGE_FOLD = 8
-DSA_STAGE_DKP = 16
 
-EXPECTED_VERSION = 1
+EXPECTED_VERSION = 2
 
 _i64x3 = ctypes.c_int64 * 3
 _i64x2 = ctypes.c_int64 * 2

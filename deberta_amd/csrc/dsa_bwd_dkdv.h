@@ -3,18 +3,25 @@
 //
 // One workgroup = 4 waves = one (batch b, head h, 128-key tile); wave w owns
 // keys [j0 + 32w, j0 + 32w + 32) and streams 32-query tiles.  The tiles (Q,
-// dO, the saved relative term, lse and Delta) are double-buffered in LDS and
-// filled by direct global-to-LDS copies issued one tile ahead; K and V of the
-// workgroup's keys stay in LDS.  Per tile:
+// dO, the saved relative term, lse and Delta, and a 32-offset block of
+// qrgt) are double-buffered in LDS and filled by direct global-to-LDS copies
+// issued one tile ahead; K and V of the wave's keys stay in registers.  Per
+// tile:
 //   scores        y = (Q K^T + bias) * scale*log2e, queries down / keys
 //                 across, where bias = c2p + p2c is the relative term the
 //                 forward saved (read transposed from the LDS tile)
 //   P, dP, dS     P = exp2(y - lse*log2e), dP = dO V^T, dS = P (dP - Delta)
 //   dS^T          stored to the workspace (row j, 4 consecutive queries per
-//                 lane): the dq, dkp and table kernels read it
+//                 lane): the dq and table kernels read it
 //   dV^T         += dO^T P,  dK^T += Q^T dS        (dO^T, Q^T read transposed)
-// With p2c, dK is left unscaled in fp32 in the workspace and completed by
-// dsa_bwd_dkp_kernel (dsa_bwd_dkp.h), which adds the p2c term from dS^T.
+//   p2c          dK^T[d][j] += sum_x qrgt[d][t0 + x] F[x][j], F[x][j] =
+//                dS(i0 + x + (j - jw) - 31, j): x = (i - i0) - (j - jw) + 31 is
+//                the wave's offset index and qrgt holds the Qr rows gathered
+//                per offset and transposed.  The wave keeps its dS^T tile in
+//                LDS (rows j, 32 zero columns before each row), so F's
+//                operand is eight consecutive elements of one row; the
+//                qrgt window (160 offsets of the workgroup) is a ring of
+//                32-offset blocks, one new block per tile.
 // Every query tile of the padded extent is visited, so dS^T is fully written
 // (zeros for masked pairs, dead rows and padding).
 #pragma once
@@ -36,11 +43,22 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
   using SQ = Swz<T, D>;
   constexpr int NS = D / M::KSTEP;
   constexpr int ND = D / 16;
-  constexpr int KSTR = D + Pad<T>::v;
+  constexpr int VEC = 16 / (int)sizeof(T);
   constexpr int QCH = BQ * D * (int)sizeof(T) / 16;   // 16-byte chunks of a Q (or dO) tile
   constexpr int QCW = QCH / NW;                         // ... per wave
   constexpr int BE = 2 * 2048;                          // saved-bias elements of a tile
   constexpr int BCW = BE * (int)sizeof(BT) / 16 / NW;   // bias chunks per wave
+  constexpr int FE = M::FRAG_ELEMS;
+  // dS^T tile of a wave: rows j (32 + 1), ZL zero columns, 32 data columns,
+  // the rest of the stride zero; a row's right-hand zeros continue into the
+  // next row's leading ones.
+  constexpr int ZL = 32;
+  constexpr int SROW = sizeof(T) == 2 ? 72 : 76;         // few bank conflicts for 16-byte row reads
+  constexpr int SW = (WK + 1) * SROW;
+  // qrgt ring: NRB blocks of 32 offsets, each stored [chunk c][d][VEC] so that
+  // a fragment read (one chunk of 16 consecutive d rows) is contiguous.
+  constexpr int NRB = 6, RBE = 32 * D;
+  constexpr int RCPB = RBE / VEC;                        // 16-byte chunks per block
   const FwdParams& p = bp.f;
 
   // Double-buffered tiles, filled by LDS copies issued one tile ahead.
@@ -48,8 +66,8 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
   __shared__ __align__(16) T dOs[2][BQ * D];
   __shared__ __align__(16) BT Bs[2][BE];
   __shared__ __align__(16) float Rs[2][2 * BQ];   // per query: lse*log2e (inf: no probabilities), Delta
-  __shared__ __align__(16) T Kw[BKW * KSTR];      // the workgroup's keys and values
-  __shared__ __align__(16) T Vw[BKW * KSTR];
+  __shared__ __align__(16) T Ring[NRB * RBE];     // qrgt window (p2c)
+  __shared__ __align__(16) T Stg[NW * SW];        // each wave's dS^T tile (p2c)
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = tid >> 6, g = (tid & 63) >> 4, c16 = tid & 15;
@@ -70,6 +88,11 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
   const uint8_t* kkb = (MASK == MASK_KEY) ? p.kk + (int64_t)b * p.kkb : nullptr;
   const uint8_t* pkb = (MASK == MASK_PAIR) ? p.pk + (int64_t)b * p.pkb : nullptr;
   T* dstw = (T*)bp.dst + ((int64_t)(b * p.H + h) * p.LkP + jw) * p.LqP;
+  const T* qrg = p2c ? (const T*)bp.qrgt + (int64_t)h * D * bp.TGP : nullptr;
+  // qrgt column of the workgroup window's first offset at query tile 0
+  // (a multiple of 32: t = d + OFF with d = -j0 - 127)
+  const int tw0 = -j0 - (BKW - 1) + bp.OFF;
+  T* stg = Stg + w * SW;
 
   int jcol[2];
   bool jkeep[2];
@@ -89,6 +112,20 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
   f32x4 dka[ND][2], dva[ND][2];
 #pragma unroll
   for (int db = 0; db < ND; ++db) dka[db][0] = dka[db][1] = dva[db][0] = dva[db][1] = zero4();
+
+  // Issues the LDS copies of qrgt block rb (columns [32 rb, 32 rb + 32)) into
+  // ring slot rb % NRB: chunk c of row d at ((c * D) + d) * VEC.
+  auto issue_ring = [&](int rb) {
+    T* slot = Ring + (rb % NRB) * RBE;
+#pragma unroll
+    for (int k = 0; k < (RCPB + 255) / 256; ++k) {
+      const int pc = 256 * k + w * 64 + lane;
+      if (256 * k + w * 64 < RCPB) {
+        const int c = pc / D, d = pc % D;
+        lds_dma16(qrg + (int64_t)d * bp.TGP + 32 * rb + c * VEC, (char*)(slot + (256 * k + w * 64) * VEC));
+      }
+    }
+  };
 
   // Issues the LDS copies of query tile qi into buffer bf (lane order =
   // physical chunk order; Q and dO rows are clamped to Lq - 1, where
@@ -119,6 +156,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
       }
     }
     if (w == 0 && lane < 2 * BQ * 4 / 16) lds_dma16(rib + 2 * i0 + 4 * lane, (char*)Rs[bf]);
+    if (p2c) issue_ring(tw0 / 32 + qi + 4);
   };
 
   if (!any_key) {
@@ -130,9 +168,29 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
         for (int ib = 0; ib < BQ / 16; ++ib)
           *reinterpret_cast<vec4*>(dstw + (int64_t)(16 * jb + c16) * p.LqP + qi * BQ + 16 * ib + 4 * g) = vec4{};
   } else {
-    // K and V rows of the workgroup's keys stay in LDS (B operands)
-    load_rows<T, D, BKW, 256>(Kw, KSTR, nullptr, 0, kbase, p.ks[1], j0, Lk, tid);
-    load_rows<T, D, BKW, 256>(Vw, KSTR, nullptr, 0, vbase, p.vs[1], j0, Lk, tid);
+    // K and V rows of the wave's keys stay in registers (B operands)
+    frag kf[2][NS], vf[2][NS];
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb) {
+      const int j = jcol[jb];
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        kf[jb][s] = (j < Lk) ? M::load_contig(kbase + (int64_t)j * p.ks[1], s, g) : M::zero();
+        vf[jb][s] = (j < Lk) ? M::load_contig(vbase + (int64_t)j * p.vs[1], s, g) : M::zero();
+      }
+    }
+    if (p2c) {
+      // zero the wave's dS^T tile (its zero columns are never written), and
+      // fill the ring with the first window's older blocks
+      typedef T vecT __attribute__((ext_vector_type(VEC)));
+      vecT z;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) z[e] = (T)0.0f;
+      static_assert(SW % VEC == 0, "whole chunks");
+      for (int c = lane; c < SW / VEC; c += 64) reinterpret_cast<vecT*>(stg)[c] = z;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) issue_ring(tw0 / 32 + r);
+    }
     issue(0, 0);
     for (int qi = 0; qi < nqt; ++qi) {
       const int i0 = qi * BQ, bf = qi & 1;
@@ -183,7 +241,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
           f32x4 acc = zero4();
 #pragma unroll
           for (int s = 0; s < NS; ++s)
-            acc = M::mma(qa[s], M::load_contig(&Kw[(WK * w + 16 * jb + c16) * KSTR], s, g), acc);
+            acc = M::mma(qa[s], kf[jb][s], acc);
           if (p.flags) {
             // rows 16*ib + 4*g + e of key column 32w + 16*jb + c16 (forward tile order)
             const int jl = WK * w + 16 * jb;
@@ -217,7 +275,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
           f32x4 dp = zero4();
 #pragma unroll
           for (int s = 0; s < NS; ++s)
-            dp = M::mma(dof[s], M::load_contig(&Vw[(WK * w + 16 * jb + c16) * KSTR], s, g), dp);
+            dp = M::mma(dof[s], vf[jb][s], dp);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int il = 16 * ib + 4 * g + e;
@@ -240,6 +298,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) v[e] = (T)dsh[jb][ib][e];
           *reinterpret_cast<vec4*>(dstw + (int64_t)(16 * jb + c16) * p.LqP + i0 + 16 * ib + 4 * g) = v;
+          if (p2c) *reinterpret_cast<vec4*>(stg + (16 * jb + c16) * SROW + ZL + 16 * ib + 4 * g) = v;
         }
 
       // ---- dV^T += dO^T P,  dK^T += Q^T dS (dO^T, Q^T read transposed) -----------------------
@@ -262,13 +321,38 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
           }
         }
       }
+
+      // ---- p2c: dK^T += qrgt[t0 + x]^T F[x] ------------------------------------------------
+      if (p2c) {
+        // qrgt column of x = 0 for this wave: i0 - jw - 31 + OFF (a multiple of 32)
+        const int t0 = tw0 + i0 + BKW - WK - WK * w;
+#pragma unroll
+        for (int s = 0; s < 2 * WK / M::KSTEP; ++s) {
+          frag bfr[2];
+#pragma unroll
+          for (int jb = 0; jb < 2; ++jb) {
+            // k = x = KSTEP*s + FE*g + e  ->  staged column (i - i0) = x + (j - jw) - 31
+            const int jl = 16 * jb + c16;
+            const T* row = stg + jl * SROW + ZL + M::KSTEP * s + FE * g + jl - 31;
+#pragma unroll
+            for (int e = 0; e < FE; ++e) bfr[jb][e] = row[e];
+          }
+          const int t = t0 + M::KSTEP * s + FE * g;  // this lane's first k column
+          const T* blk = Ring + ((t >> 5) % NRB) * RBE + ((t & 31) / VEC) * D * VEC;
+#pragma unroll
+          for (int db = 0; db < ND; ++db) {
+            const frag af = *reinterpret_cast<const frag*>(blk + (16 * db + c16) * VEC);
+#pragma unroll
+            for (int jb = 0; jb < 2; ++jb) dka[db][jb] = M::mma(af, bfr[jb], dka[db][jb]);
+          }
+        }
+      }
     }
   }
 
   // ---- dK, dV ------------------------------------------------------------------------------
   T* dkbase = (T*)bp.dk + (int64_t)b * bp.dks[0] + (int64_t)h * bp.dks[2];
   T* dvbase = (T*)bp.dv + (int64_t)b * bp.dvs[0] + (int64_t)h * bp.dvs[2];
-  float* dkcw = p2c ? bp.dkc + ((int64_t)(b * p.H + h) * p.LkP) * D : nullptr;
 #pragma unroll
   for (int jb = 0; jb < 2; ++jb) {
     const int j = jcol[jb];
@@ -284,11 +368,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
           kv[e] = (T)(dka[db][jb][e] * p.scale);
           vv[e] = (T)(dva[db][jb][e]);
         }
-        if (p2c) {  // content part of dK, completed by dsa_bwd_dkp_kernel
-          *reinterpret_cast<f32x4*>(dkcw + (int64_t)j * D + 16 * db + 4 * g) = dka[db][jb];
-        } else {
-          *reinterpret_cast<vec4*>(krow + 16 * db + 4 * g) = kv;
-        }
+        *reinterpret_cast<vec4*>(krow + 16 * db + 4 * g) = kv;
         *reinterpret_cast<vec4*>(vrow + 16 * db + 4 * g) = vv;
       }
     }

@@ -11,7 +11,6 @@
 #include "../../include/dsa.h"
 #include "dsa_bwd.h"
 #include "dsa_bwd_dkdv.h"
-#include "dsa_bwd_dkp.h"
 #include "dsa_bwd_dq.h"
 #include "dsa_bwd_table.h"
 #include "dsa_fwd.h"
@@ -149,7 +148,7 @@ int device_cus() {
 // extents the kernels share.
 struct WsLayout {
   int LqP, LkP, TGP, OFF, NDB, NBG, BPG;
-  size_t rowinfo, krgt, qrgt, dst, gpart, dkc, total;
+  size_t rowinfo, krgt, qrgt, dst, gpart, total;
 };
 
 WsLayout ws_layout(const dsa_bwd_args* a) {
@@ -178,8 +177,6 @@ WsLayout ws_layout(const dsa_bwd_args* a) {
   off = align_up(off + (size_t)f.B * f.H * w.LkP * w.LqP * es, 256);
   w.gpart = off;
   if (f.flags) off = align_up(off + (size_t)f.H * w.NDB * w.NBG * 2 * dsa::tbcfg::DBW * f.D * sizeof(float), 256);
-  w.dkc = off;
-  if (f.flags & DSA_P2C) off = align_up(off + (size_t)f.B * f.H * w.LkP * f.D * sizeof(float), 256);
   w.total = off;
   return w;
 }
@@ -207,14 +204,13 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
   bp.qrgt = base + ws.qrgt;
   bp.dst = base + ws.dst;
   bp.gpart = reinterpret_cast<float*>(base + ws.gpart);
-  bp.dkc = reinterpret_cast<float*>(base + ws.dkc);
   bp.TGP = ws.TGP;
   bp.OFF = ws.OFF;
   bp.NDB = ws.NDB;
   bp.NBG = ws.NBG;
   bp.BPG = ws.BPG;
   const int stages =
-      a->stages ? a->stages : (DSA_STAGE_PREP | DSA_STAGE_DQ | DSA_STAGE_DKDV | DSA_STAGE_DKP | DSA_STAGE_FOLD);
+      a->stages ? a->stages : (DSA_STAGE_PREP | DSA_STAGE_DQ | DSA_STAGE_DKDV | DSA_STAGE_FOLD);
 
   if (stages & DSA_STAGE_PREP) {
     const int64_t n = (int64_t)f.B * f.H * ws.LqP * (D / (16 / (int)sizeof(T)));
@@ -245,11 +241,6 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
     hipLaunchKernelGGL((dsa::dsa_bwd_dq_kernel<T, D>), grid, dim3(256), 0, st, bp);
     if (launch_check("dsa_bwd_dq_kernel")) return 1;
   }
-  if ((stages & DSA_STAGE_DKP) && (f.flags & DSA_P2C)) {
-    dim3 grid(ws.LkP / dsa::dkpcfg::BKW, f.H, f.B);
-    hipLaunchKernelGGL((dsa::dsa_bwd_dkp_kernel<T, D>), grid, dim3(256), 0, st, bp);
-    if (launch_check("dsa_bwd_dkp_kernel")) return 1;
-  }
   if ((stages & DSA_STAGE_FOLD) && f.flags) {
     hipLaunchKernelGGL((dsa::dsa_bwd_table_kernel<T, D>), dim3(ws.NDB * f.H * ws.NBG), dim3(256), 0, st, bp);
     if (launch_check("dsa_bwd_table_kernel")) return 1;
@@ -264,7 +255,7 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
 
 extern "C" {
 
-int dsa_version(void) { return 1; }
+int dsa_version(void) { return 2; }
 
 const char* dsa_last_error(void) { return g_err.c_str(); }
 

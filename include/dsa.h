@@ -58,16 +58,14 @@ enum { DSA_F32 = 0, DSA_BF16 = 1 };
 enum { DSA_C2P = 1, DSA_P2C = 2 };
 
 /* backward stages, for dsa_bwd_args.stages (0 means all).  They run in the
- * order PREP, DKDV, DQ, DKP, FOLD and pass data through the workspace:
+ * order PREP, DKDV, DQ, FOLD and pass data through the workspace:
  *   PREP  rowsum(dO * O) and the relative tables gathered per offset
- *   DKDV  writes dv, dk (with p2c: its content part, into the workspace)
- *         and dS^T into the workspace
+ *   DKDV  writes dv, dk and dS^T (into the workspace)
  *   DQ    writes dq from dS^T
- *   DKP   with p2c: completes dk with its p2c term from dS^T
  *   FOLD  adds the relative-table gradients (from dS^T) into dkr / dqr
  * Stages run in separate calls must keep this order and share one
  * workspace. */
-enum { DSA_STAGE_PREP = 1, DSA_STAGE_DQ = 2, DSA_STAGE_DKDV = 4, DSA_STAGE_FOLD = 8, DSA_STAGE_DKP = 16 };
+enum { DSA_STAGE_PREP = 1, DSA_STAGE_DQ = 2, DSA_STAGE_DKDV = 4, DSA_STAGE_FOLD = 8 };
 
 typedef struct dsa_fwd_args {
   const void* q;          /* [B, Lq, H, D] */
