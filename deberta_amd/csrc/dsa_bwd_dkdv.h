@@ -72,7 +72,9 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = tid >> 6, g = (tid & 63) >> 4, c16 = tid & 15;
   const int Lq = p.Lq, Lk = p.Lk;
-  const int kt = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int NKT = p.LkP / BKW;
+  const int m = xcd_remap(blockIdx.x, gridDim.x);  // (b, h, kt), kt fastest
+  const int kt = m % NKT, h = (m / NKT) % p.H, b = m / (NKT * p.H);
   const bool p2c = (p.flags & 2) != 0;
   const float sl2 = p.scale * kLog2e;
   const int nqt = p.LqP / BQ;

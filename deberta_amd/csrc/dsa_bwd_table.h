@@ -113,7 +113,9 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
   const int w = tid >> 6, g = (tid & 63) >> 4, c16 = tid & 15;
   // Work order: blockIdx.x enumerates (offset block, head, batch group) with
   // the offset blocks that have the most key chunks first, so the shortest
-  // workgroups fill in at the end of the launch.
+  // workgroups fill in at the end of the launch.  (Grouping a (head, batch
+  // group)'s offset blocks on one XCD instead measured slower: the long
+  // blocks then finish last.)
   const int per_blk = p.H * bp.NBG;
   const int rank = blockIdx.x / per_blk, rem = blockIdx.x % per_blk;
   const int h = rem / bp.NBG, bg = rem % bp.NBG;

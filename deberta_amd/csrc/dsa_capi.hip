@@ -47,6 +47,9 @@ int check_fwd(const dsa_fwd_args* a) {
   if (a->B < 1 || a->H < 1 || a->Lq < 1 || a->Lk < 1)
     return fail("dsa: empty shape B=%d H=%d Lq=%d Lk=%d", a->B, a->H, a->Lq, a->Lk);
   if (a->B > 65535 || a->H > 65535) return fail("dsa: B and H must be <= 65535");
+  // 1-D grids of (tile, head, batch) workgroups
+  if ((int64_t)a->B * a->H * (((a->Lq > a->Lk ? a->Lq : a->Lk) + 127) / 128) > 0x7fffffff)
+    return fail("dsa: B * H * tiles exceeds the 1-D grid range");
   if (!a->q || !a->k || !a->v || !a->out || !a->lse) return fail("dsa: q, k, v, out and lse are required");
   if ((a->flags & ~(DSA_C2P | DSA_P2C)) != 0) return fail("dsa: unknown flags 0x%x", a->flags);
   if (a->flags) {
@@ -123,7 +126,7 @@ int launch_check(const char* what) {
 
 template <typename T, int D, int MASK>
 int launch_fwd(const dsa::FwdParams& p, hipStream_t st) {
-  dim3 grid((p.Lq + dsa::dcfg::BQ - 1) / dsa::dcfg::BQ, p.H, p.B);
+  dim3 grid((unsigned)((p.Lq + dsa::dcfg::BQ - 1) / dsa::dcfg::BQ * p.H * p.B));
   hipLaunchKernelGGL((dsa::dsa_fwd_kernel<T, D, MASK>), grid, dim3(256), 0, st, p);
   return launch_check("dsa_fwd_kernel");
 }
@@ -223,7 +226,7 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
     }
   }
   if (stages & DSA_STAGE_DKDV) {
-    dim3 grid(ws.LkP / dsa::kvcfg::BKW, f.H, f.B);
+    dim3 grid((unsigned)(ws.LkP / dsa::kvcfg::BKW * f.H * f.B));
     switch (mode) {
       case dsa::MASK_KEY:
         hipLaunchKernelGGL((dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_KEY>), grid, dim3(256), 0, st, bp);
@@ -237,7 +240,7 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
     if (launch_check("dsa_bwd_dkdv_kernel")) return 1;
   }
   if (stages & DSA_STAGE_DQ) {
-    dim3 grid(ws.LqP / dsa::dqcfg::BQ, f.H, f.B);
+    dim3 grid((unsigned)(ws.LqP / dsa::dqcfg::BQ * f.H * f.B));
     hipLaunchKernelGGL((dsa::dsa_bwd_dq_kernel<T, D>), grid, dim3(256), 0, st, bp);
     if (launch_check("dsa_bwd_dq_kernel")) return 1;
   }

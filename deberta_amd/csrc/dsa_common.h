@@ -265,6 +265,19 @@ DSA_DEV typename Mfma<T>::frag tr_acc(const T* X, int str, int k0, int m0, int g
   }
 }
 
+// Workgroups are dispatched to the 8 XCDs in turn (workgroup n to XCD
+// n % 8), and each XCD has its own L2.  xcd_remap gives workgroup n of a
+// G-workgroup 1-D grid the logical index that makes each XCD run one
+// contiguous range of logical indices, in order, so workgroups that are
+// neighbours in logical order (the tiles of one batch and head, which read
+// the same K/V or Q/dO) run on one XCD at about the same time and share its
+// L2.  A bijection on [0, G).
+DSA_DEV int xcd_remap(int n, int G) {
+  constexpr int NX = 8;
+  const int per = G / NX;
+  return n < per * NX ? (n % NX) * per + n / NX : n;
+}
+
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 

@@ -47,7 +47,9 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, g = (tid & 63) >> 4, c16 = tid & 15;
-  const int qt = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int NQT = (p.Lq + BQ - 1) / BQ;
+  const int m = xcd_remap(blockIdx.x, gridDim.x);  // (b, h, qt), qt fastest
+  const int qt = m % NQT, h = (m / NQT) % p.H, b = m / (NQT * p.H);
   const int Lq = p.Lq, Lk = p.Lk, A = p.A;
   const int i0 = qt * BQ;
   const int iw = i0 + w * WQ;
