@@ -44,17 +44,22 @@ R = 2 * A
 # (x1.0).  Commands and raw figures: profiles/hbm_traffic_headline.md.
 FETCH_SCALE, WRITE_SCALE = 2.0, 1.0
 TRAFFIC_KIB = {  # kernel: (FETCH_SIZE, WRITE_SIZE) as read
-    "dsa_fwd_kernel": (117981, 25344),
-    "dsa_bwd_dq_kernel": (149327, 58368),
-    "dsa_bwd_dkdv_kernel": (152589, 82948),
+    "dsa_fwd_kernel": (52303, 221952),
+    "dsa_bwd_dkdv_kernel": (178774, 284099),
+    "dsa_bwd_dq_kernel": (126758, 24576),
+    "dsa_bwd_table_kernel": (179810, 36864),
+    "dsa_bwd_fold_kernel": (19995, 3072),
+    "dsa_bwd_delta_kernel": (24997, 1536),
+    "dsa_bwd_gather_kernel": (1571, 3072),
 }
 
 
-def hbm_bytes(kernel: str):
-    if kernel not in TRAFFIC_KIB:
+def hbm_bytes(stage: str):
+    """HBM bytes per launch of a bench stage (the sum over its kernels)."""
+    names = [k for k in TRAFFIC_KIB if k in stage]
+    if not names:
         return None
-    fetch, write = TRAFFIC_KIB[kernel]
-    return int(round((fetch * FETCH_SCALE + write * WRITE_SCALE) * 1024))
+    return int(round(sum(TRAFFIC_KIB[k][0] * FETCH_SCALE + TRAFFIC_KIB[k][1] * WRITE_SCALE for k in names) * 1024))
 
 
 def flops_fwd(b: int, l: int, h: int, d: int, r: int) -> float:
@@ -174,7 +179,13 @@ def main() -> None:
         del src_t, dst_t
 
     ms_step = wall = float("nan")
-    if not args.kernels_only:
+    if args.kernels_only:
+        # the same sustained load before the per-kernel timing as in a full
+        # run (the GPU's clocks settle under it)
+        for _ in range(args.warmup + args.steps):
+            step()
+        torch.cuda.synchronize()
+    else:
         for _ in range(args.warmup):
             step()
         torch.cuda.synchronize()
