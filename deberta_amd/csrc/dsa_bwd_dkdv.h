@@ -61,11 +61,15 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
   constexpr int RCPB = RBE / VEC;                        // 16-byte chunks per block
   const FwdParams& p = bp.f;
 
-  // Double-buffered tiles, filled by LDS copies issued one tile ahead.
-  __shared__ __align__(16) T Qs[2][BQ * D];
-  __shared__ __align__(16) T dOs[2][BQ * D];
-  __shared__ __align__(16) BT Bs[2][BE];
-  __shared__ __align__(16) float Rs[2][2 * BQ];   // per query: lse*log2e (inf: no probabilities), Delta
+  // Double-buffered tiles, filled by LDS copies issued one tile ahead.  The
+  // two buffers are distinct arrays and the loop is unrolled by two, so the
+  // compiler sees that a tile's reads do not touch the buffer the next
+  // tile's copies are landing in (it would otherwise wait for those copies
+  // before every read).
+  __shared__ __align__(16) T Qs0[BQ * D], Qs1[BQ * D];
+  __shared__ __align__(16) T dOs0[BQ * D], dOs1[BQ * D];
+  __shared__ __align__(16) BT Bs0[BE], Bs1[BE];
+  __shared__ __align__(16) float Rs0[2 * BQ], Rs1[2 * BQ];  // per query: lse*log2e (inf: no probabilities), Delta
   __shared__ __align__(16) T Ring[NRB * RBE];     // qrgt window (p2c)
   __shared__ __align__(16) T Stg[NW * SW];        // each wave's dS^T tile (p2c)
 
@@ -117,6 +121,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
 
   // Issues the LDS copies of qrgt block rb (columns [32 rb, 32 rb + 32)) into
   // ring slot rb % NRB: chunk c of row d at ((c * D) + d) * VEC.
+  typedef T vecT __attribute__((ext_vector_type(VEC)));
   auto issue_ring = [&](int rb) {
     T* slot = Ring + (rb % NRB) * RBE;
 #pragma unroll
@@ -129,10 +134,11 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
     }
   };
 
-  // Issues the LDS copies of query tile qi into buffer bf (lane order =
-  // physical chunk order; Q and dO rows are clamped to Lq - 1, where
-  // probabilities are zero anyway).
-  auto issue = [&](int qi, int bf) {
+  // Issues the LDS copies of query tile qi into the given buffers (lane
+  // order = physical chunk order; Q and dO rows are clamped to Lq - 1, where
+  // probabilities are zero anyway), and its qrgt block (whose ring slot was
+  // last read two tiles earlier).
+  auto issue = [&](int qi, T* Qd, T* dOd, BT* Bd, float* Rd) {
     const int i0 = qi * BQ;
 #pragma unroll
     for (int k = 0; k < (QCW + 63) / 64; ++k) {
@@ -140,8 +146,8 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
       if (64 * k + lane < QCW) {
         const int r = pc / SQ::CPR, lc = (pc % SQ::CPR) ^ (r & (SQ::CPR - 1));
         const int64_t i = min(i0 + r, Lq - 1);
-        lds_dma16(qbase + i * p.qs[1] + lc * SQ::VEC, (char*)Qs[bf] + (w * QCW + 64 * k) * 16);
-        lds_dma16(dobase + i * bp.dos[1] + lc * SQ::VEC, (char*)dOs[bf] + (w * QCW + 64 * k) * 16);
+        lds_dma16(qbase + i * p.qs[1] + lc * SQ::VEC, (char*)Qd + (w * QCW + 64 * k) * 16);
+        lds_dma16(dobase + i * bp.dos[1] + lc * SQ::VEC, (char*)dOd + (w * QCW + 64 * k) * 16);
       }
     }
     if (p.flags) {
@@ -154,10 +160,10 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
         const int kk = pc / CPB;
         const BT* src = biasb + bias_tile_offset(b, h, p.H, i0 / 128, j0 / 64 + kk, p.LqP, p.LkP) +
                         ((i0 % 128) / 32) * 2048 + (pc % CPB) * (16 / (int)sizeof(BT));
-        lds_dma16(src, (char*)Bs[bf] + (w * BCW + 64 * k) * 16);
+        lds_dma16(src, (char*)Bd + (w * BCW + 64 * k) * 16);
       }
     }
-    if (w == 0 && lane < 2 * BQ * 4 / 16) lds_dma16(rib + 2 * i0 + 4 * lane, (char*)Rs[bf]);
+    if (w == 0 && lane < 2 * BQ * 4 / 16) lds_dma16(rib + 2 * i0 + 4 * lane, (char*)Rd);
     if (p2c) issue_ring(tw0 / 32 + qi + 4);
   };
 
@@ -184,21 +190,24 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
     if (p2c) {
       // zero the wave's dS^T tile (its zero columns are never written), and
       // fill the ring with the first window's older blocks
-      typedef T vecT __attribute__((ext_vector_type(VEC)));
       vecT z;
 #pragma unroll
       for (int e = 0; e < VEC; ++e) z[e] = (T)0.0f;
       static_assert(SW % VEC == 0, "whole chunks");
       for (int c = lane; c < SW / VEC; c += 64) reinterpret_cast<vecT*>(stg)[c] = z;
-#pragma unroll
       for (int r = 0; r < 4; ++r) issue_ring(tw0 / 32 + r);
     }
-    issue(0, 0);
-    for (int qi = 0; qi < nqt; ++qi) {
-      const int i0 = qi * BQ, bf = qi & 1;
-      lds_dma_wait();   // this wave's copies of tile qi have landed
+    issue(0, Qs0, dOs0, Bs0, Rs0);
+    lds_dma_wait();
+    auto tile = [&](int qi, const T* Q, const T* dO, const BT* Bt, const float* R, T* nQ, T* ndO, BT* nBt,
+                    float* nR) {
+      const int i0 = qi * BQ;
+      // This wave's copies of tile qi have landed: they were issued before
+      // the previous tile's four dS^T stores, its last vector-memory
+      // instructions (tile 0 was waited for before the loop).
+      vm_wait<4>();
       __syncthreads();  // ... every wave's, and tile qi - 1 is no longer read
-      if (qi + 1 < nqt) issue(qi + 1, bf ^ 1);
+      if (qi + 1 < nqt) issue(qi + 1, nQ, ndO, nBt, nR);
       // Tiles without a kept (query, key) pair store zeros.
       bool skip = i0 >= Lq;
       if (!skip && MASK == MASK_KEY) {
@@ -224,12 +233,8 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
 #pragma unroll
           for (int ib = 0; ib < BQ / 16; ++ib)
             *reinterpret_cast<vec4*>(dstw + (int64_t)(16 * jb + c16) * p.LqP + i0 + 16 * ib + 4 * g) = vec4{};
-        continue;
+        return;
       }
-      const T* Q = Qs[bf];
-      const T* dO = dOs[bf];
-      const BT* Bt = Bs[bf];
-      const float* R = Rs[bf];
 
       // ---- scores (queries down, keys across): (Q K^T + saved bias) * scale*log2e -------------
       f32x4 sc[2][BQ / 16];
@@ -349,6 +354,10 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
           }
         }
       }
+    };
+    for (int qi = 0; qi < nqt; qi += 2) {
+      tile(qi, Qs0, dOs0, Bs0, Rs0, Qs1, dOs1, Bs1, Rs1);
+      if (qi + 1 < nqt) tile(qi + 1, Qs1, dOs1, Bs1, Rs1, Qs0, dOs0, Bs0, Rs0);
     }
   }
 

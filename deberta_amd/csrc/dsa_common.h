@@ -191,12 +191,25 @@ DSA_DEV bf16x4 tr4_at(const bf16* p) {
 
 // 16-byte copy global -> LDS without registers (gfx950 global_load_lds_dwordx4):
 // lane l of the wave writes lds_wave + 16 * l, where lds_wave is the same for
-// every lane of the wave.  Completion is tracked by vmcnt (lds_dma_wait).
+// every lane of the wave.  Completion is tracked by vmcnt only, and the
+// caller waits for it explicitly (lds_dma_wait, vm_wait): the copy is
+// issued from inline assembly because the compiler, which cannot tell which
+// LDS bytes a copy writes, would otherwise wait for every outstanding copy
+// before each LDS read, including reads of other buffers.
 DSA_DEV void lds_dma16(const void* src, void* lds_wave) {
-  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_wave, 16, 0, 0);
+  const unsigned lds =
+      __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(__attribute__((address_space(3))) void*)lds_wave);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
 }
-// Waits for this wave's outstanding global loads, the LDS copies included.
-DSA_DEV void lds_dma_wait() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0) only
+// Waits until at most N of this wave's vector-memory instructions are
+// outstanding (they complete in issue order).
+template <int N>
+DSA_DEV void vm_wait() {
+  static_assert(N >= 0 && N < 16, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | N);  // vmcnt(N), expcnt and lgkmcnt not waited for
+}
+// Waits for all of this wave's outstanding global loads, the LDS copies included.
+DSA_DEV void lds_dma_wait() { vm_wait<0>(); }
 
 // Row-major LDS tile with COLS elements per row whose 16-byte chunks are
 // XOR-swizzled by row (chunk c of row r stored at chunk c ^ (r % CPR)), so that
