@@ -97,6 +97,24 @@ def test_growing_scores(mask, dtype, gpu):
         _check(c, dtype, gpu, grads=False)
 
 
+# --- long sequences (config-4 length, with its document-block mask) and the
+# config-5 head count: 32 query tiles, 64 offset blocks, the ring of qrgt
+# blocks wrapping many times, tile skipping over whole documents
+@pytest.mark.parametrize(
+    "c,dtype",
+    [
+        (Case(B=1, H=2, L=4096, D=64, mask="pair", seed=51), torch.bfloat16),
+        (Case(B=1, H=2, L=4096, D=64, mask="pair", seed=52), torch.float32),
+        (Case(B=1, H=2, L=4096, D=64, seed=53), torch.bfloat16),
+        (Case(B=2, H=2, L=2048, D=64, mask="key", seed=54), torch.float32),
+        (Case(B=2, H=16, L=512, D=64, seed=55), torch.bfloat16),
+    ],
+    ids=["L4096-doc-bf16", "L4096-doc-fp32", "L4096-bf16", "L2048-key-fp32", "H16-bf16"],
+)
+def test_long_sequences(c, dtype, gpu):
+    _check(c, dtype, gpu)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
 @pytest.mark.parametrize("mask", ["key", "pair", "dead"])
 def test_masks(mask, dtype, gpu):
