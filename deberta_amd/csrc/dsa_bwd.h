@@ -15,11 +15,12 @@
 //          transposed, so a run of consecutive offsets of one head-dim
 //          column is contiguous — the A operand of the offset-band products)
 //   dkdv   dsa_bwd_dkdv_kernel (dsa_bwd_dkdv.h): recomputes the scores and
-//          the softmax per (b, h, 128-key tile), writes dK, dV and dS^T
-//          (bf16 for bf16 inputs), the only (L x L) tensor of the backward
-//   dq     dsa_bwd_dq_kernel (dsa_bwd_dq.h): dQ from dS^T, K and krgt
+//          the softmax per (b, h, 128-key tile), writes dK, dV and dS
+//          (rows = queries; bf16 for bf16 inputs), the only (L x L) tensor
+//          the backward passes between its kernels
+//   dq     dsa_bwd_dq_kernel (dsa_bwd_dq.h): dQ from dS, K and krgt
 //   fold   dsa_bwd_table_kernel + dsa_bwd_fold_kernel (dsa_bwd_table.h):
-//          the table gradients per offset, from dS^T, Q and K, then summed
+//          the table gradients per offset, from dS, Q and K, then summed
 //          onto table rows
 #pragma once
 
@@ -70,8 +71,10 @@ DSA_DEV int offset_row(const int32_t* rel, int d, int Lq, int Lk, int A, bool p2
   return p2c ? p2c_row(t, A) : c2p_row(t, A);
 }
 
-// krgt[h][d][t] = Kr[h][c(t - OFF)][d], qrgt[h][d][t] = Qr[h][p(t - OFF)][d]
-// for t in [0, TGP); one thread per (table, h, d, t), t fastest.
+// krgt[h][d][t] = Kr[h][c(t' - OFF)][d] with t' = t ^ (VEC - 1) (each
+// aligned group of VEC = 16 / sizeof(T) offsets reversed: the dq kernel's
+// operand order), qrgt[h][d][t] = Qr[h][p(t - OFF)][d], for t in [0, TGP);
+// one thread per (table, h, d, t), t fastest.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void dsa_bwd_gather_kernel(BwdParams bp) {
   const FwdParams& p = bp.f;
@@ -84,7 +87,8 @@ __global__ __launch_bounds__(256) void dsa_bwd_gather_kernel(BwdParams bp) {
   const int t = (int)(r % bp.TGP);
   const int d = (int)((r / bp.TGP) % D);
   const int h = (int)(r / ((int64_t)bp.TGP * D));
-  const int row = offset_row(p.rel, t - bp.OFF, p.Lq, p.Lk, p.A, q);
+  constexpr int VEC = 16 / sizeof(T);
+  const int row = offset_row(p.rel, (q ? t : (t ^ (VEC - 1))) - bp.OFF, p.Lq, p.Lk, p.A, q);
   const T* src = q ? (const T*)p.qr + (int64_t)h * p.qrs[0] + (int64_t)row * p.qrs[1]
                    : (const T*)p.kr + (int64_t)h * p.krs[0] + (int64_t)row * p.krs[1];
   T* dst = (T*)(q ? bp.qrgt : bp.krgt);

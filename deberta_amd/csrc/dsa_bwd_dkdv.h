@@ -1,4 +1,4 @@
-// dsa_bwd_dkdv.h — dK, dV and dS^T of the fused disentangled attention
+// dsa_bwd_dkdv.h — dK, dV and dS of the fused disentangled attention
 // (gfx950).
 //
 // One workgroup = 4 waves = one (batch b, head h, 128-key tile); wave w owns
@@ -11,18 +11,20 @@
 //                 across, where bias = c2p + p2c is the relative term the
 //                 forward saved (read transposed from the LDS tile)
 //   P, dP, dS     P = exp2(y - lse*log2e), dP = dO V^T, dS = P (dP - Delta)
-//   dS^T          stored to the workspace (row j, 4 consecutive queries per
-//                 lane): the dq and table kernels read it
+//   dS            staged transposed in the wave's LDS tile (rows j), then
+//                 stored to the workspace in rows i (4 consecutive keys per
+//                 lane, read back transposed): the dq and table kernels
+//                 read it
 //   dV^T         += dO^T P,  dK^T += Q^T dS        (dO^T, Q^T read transposed)
 //   p2c          dK^T[d][j] += sum_x qrgt[d][t0 + x] F[x][j], F[x][j] =
 //                dS(i0 + x + (j - jw) - 31, j): x = (i - i0) - (j - jw) + 31 is
 //                the wave's offset index and qrgt holds the Qr rows gathered
-//                per offset and transposed.  The wave keeps its dS^T tile in
-//                LDS (rows j, 32 zero columns before each row), so F's
-//                operand is eight consecutive elements of one row; the
+//                per offset and transposed.  The wave's dS^T tile in LDS
+//                (rows j, 32 zero columns before each row) makes F's
+//                operand eight consecutive elements of one row; the
 //                qrgt window (160 offsets of the workgroup) is a ring of
 //                32-offset blocks, one new block per tile.
-// Every query tile of the padded extent is visited, so dS^T is fully written
+// Every query tile of the padded extent is visited, so dS is fully written
 // (zeros for masked pairs, dead rows and padding).
 #pragma once
 
@@ -71,7 +73,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
   __shared__ __align__(16) BT Bs0[BE], Bs1[BE];
   __shared__ __align__(16) float Rs0[2 * BQ], Rs1[2 * BQ];  // per query: lse*log2e (inf: no probabilities), Delta
   __shared__ __align__(16) T Ring[NRB * RBE];     // qrgt window (p2c)
-  __shared__ __align__(16) T Stg[NW * SW];        // each wave's dS^T tile (p2c)
+  __shared__ __align__(16) T Stg[NW * SW];        // each wave's dS^T tile
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = tid >> 6, g = (tid & 63) >> 4, c16 = tid & 15;
@@ -93,7 +95,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
   const float* rib = bp.rowinfo + (int64_t)(b * p.H + h) * p.LqP * 2;
   const uint8_t* kkb = (MASK == MASK_KEY) ? p.kk + (int64_t)b * p.kkb : nullptr;
   const uint8_t* pkb = (MASK == MASK_PAIR) ? p.pk + (int64_t)b * p.pkb : nullptr;
-  T* dstw = (T*)bp.dst + ((int64_t)(b * p.H + h) * p.LkP + jw) * p.LqP;
+  T* dsw = (T*)bp.ds + (int64_t)(b * p.H + h) * p.LqP * p.LkP + jw;  // dS column jw, row 0
   const T* qrg = p2c ? (const T*)bp.qrgt + (int64_t)h * D * bp.TGP : nullptr;
   // qrgt column of the workgroup window's first offset at query tile 0
   // (a multiple of 32: t = d + OFF with d = -j0 - 127)
@@ -167,14 +169,18 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
     if (p2c) issue_ring(tw0 / 32 + qi + 4);
   };
 
+  // dS rows i of the wave's 32 keys: lane (g, c16) writes keys jw + 16 kk +
+  // 4g + [0, 4) of query i0 + 16 mi + c16.
+  typedef T vec4 __attribute__((ext_vector_type(4)));
+  auto store_ds = [&](int i0, int kk, int mi, const vec4& v) {
+    *reinterpret_cast<vec4*>(dsw + (int64_t)(i0 + 16 * mi + c16) * p.LkP + 16 * kk + 4 * g) = v;
+  };
   if (!any_key) {
-    typedef T vec4 __attribute__((ext_vector_type(4)));
     for (int qi = 0; qi < nqt; ++qi)
 #pragma unroll
-      for (int jb = 0; jb < 2; ++jb)
+      for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-        for (int ib = 0; ib < BQ / 16; ++ib)
-          *reinterpret_cast<vec4*>(dstw + (int64_t)(16 * jb + c16) * p.LqP + qi * BQ + 16 * ib + 4 * g) = vec4{};
+        for (int mi = 0; mi < BQ / 16; ++mi) store_ds(qi * BQ, kk, mi, vec4{});
   } else {
     // K and V rows of the wave's keys stay in registers (B operands)
     frag kf[2][NS], vf[2][NS];
@@ -187,23 +193,24 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
         vf[jb][s] = (j < Lk) ? M::load_contig(vbase + (int64_t)j * p.vs[1], s, g) : M::zero();
       }
     }
-    if (p2c) {
-      // zero the wave's dS^T tile (its zero columns are never written), and
-      // fill the ring with the first window's older blocks
+    {
+      // zero the wave's dS^T tile (its zero columns are never written)
       vecT z;
 #pragma unroll
       for (int e = 0; e < VEC; ++e) z[e] = (T)0.0f;
       static_assert(SW % VEC == 0, "whole chunks");
       for (int c = lane; c < SW / VEC; c += 64) reinterpret_cast<vecT*>(stg)[c] = z;
-      for (int r = 0; r < 4; ++r) issue_ring(tw0 / 32 + r);
     }
+    // the ring's first window, older blocks
+    if (p2c)
+      for (int r = 0; r < 4; ++r) issue_ring(tw0 / 32 + r);
     issue(0, Qs0, dOs0, Bs0, Rs0);
     lds_dma_wait();
     auto tile = [&](int qi, const T* Q, const T* dO, const BT* Bt, const float* R, T* nQ, T* ndO, BT* nBt,
                     float* nR) {
       const int i0 = qi * BQ;
       // This wave's copies of tile qi have landed: they were issued before
-      // the previous tile's four dS^T stores, its last vector-memory
+      // the previous tile's four dS stores, its last vector-memory
       // instructions (tile 0 was waited for before the loop).
       vm_wait<4>();
       __syncthreads();  // ... every wave's, and tile qi - 1 is no longer read
@@ -226,13 +233,11 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
         }
         skip = !__syncthreads_or(keep);
       }
-      typedef T vec4 __attribute__((ext_vector_type(4)));
       if (skip) {
 #pragma unroll
-        for (int jb = 0; jb < 2; ++jb)
+        for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-          for (int ib = 0; ib < BQ / 16; ++ib)
-            *reinterpret_cast<vec4*>(dstw + (int64_t)(16 * jb + c16) * p.LqP + i0 + 16 * ib + 4 * g) = vec4{};
+          for (int mi = 0; mi < BQ / 16; ++mi) store_ds(i0, kk, mi, vec4{});
         return;
       }
 
@@ -270,7 +275,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
         }
       }
 
-      // ---- P, dP, dS; dS^T rows stored (4 consecutive queries per lane) ------------------------
+      // ---- P, dP, dS -----------------------------------------------------------------------------
       f32x4 pp[2][BQ / 16], dsh[2][BQ / 16];
 #pragma unroll
       for (int ib = 0; ib < BQ / 16; ++ib) {
@@ -297,6 +302,8 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
           }
         }
       }
+      // dS^T of the tile into the wave's LDS tile (rows j), then dS rows to
+      // the workspace, four consecutive keys per lane read transposed
 #pragma unroll
       for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
@@ -304,9 +311,13 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
           vec4 v;
 #pragma unroll
           for (int e = 0; e < 4; ++e) v[e] = (T)dsh[jb][ib][e];
-          *reinterpret_cast<vec4*>(dstw + (int64_t)(16 * jb + c16) * p.LqP + i0 + 16 * ib + 4 * g) = v;
-          if (p2c) *reinterpret_cast<vec4*>(stg + (16 * jb + c16) * SROW + ZL + 16 * ib + 4 * g) = v;
+          *reinterpret_cast<vec4*>(stg + (16 * jb + c16) * SROW + ZL + 16 * ib + 4 * g) = v;
         }
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int mi = 0; mi < BQ / 16; ++mi)
+          store_ds(i0, kk, mi, __builtin_bit_cast(vec4, tr4(stg + ZL, SROW, 16 * kk + 4 * g, 16 * mi, c16)));
 
       // ---- dV^T += dO^T P,  dK^T += Q^T dS (dO^T, Q^T read transposed) -----------------------
 #pragma unroll
@@ -341,8 +352,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
             // k = x = KSTEP*s + FE*g + e  ->  staged column (i - i0) = x + (j - jw) - 31
             const int jl = 16 * jb + c16;
             const T* row = stg + jl * SROW + ZL + M::KSTEP * s + FE * g + jl - 31;
-#pragma unroll
-            for (int e = 0; e < FE; ++e) bfr[jb][e] = row[e];
+            lds_read_elems<T, FE>(bfr[jb], row);
           }
           const int t = t0 + M::KSTEP * s + FE * g;  // this lane's first k column
           const T* blk = Ring + ((t >> 5) % NRB) * RBE + ((t & 31) / VEC) * D * VEC;

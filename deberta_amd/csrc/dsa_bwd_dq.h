@@ -1,19 +1,21 @@
-// dsa_bwd_dq.h — dQ of the fused disentangled attention from the stored
-// dS^T (gfx950).
+// dsa_bwd_dq.h — dQ of the fused disentangled attention from the stored dS
+// (gfx950).
 //
 // One workgroup = 4 waves = one (batch b, head h, 128-query tile); wave w
-// owns queries [i0 + 32w, i0 + 32w + 32) and streams 64-key tiles of dS^T,
-// K and the tile's krgt window through LDS (the next tile is fetched into
-// registers while the current one is computed):
-//   dQ^T[d][i] += sum_j K^T[d][j] dS^T[j][i]            (both operands read
-//                                                        transposed from LDS)
+// owns queries [i0 + 32w, i0 + 32w + 32) and streams 64-key tiles of dS
+// (rows = queries), K and the tile's krgt window through LDS (fetched into
+// registers two tiles ahead):
+//   dQ^T[d][i] += sum_j K^T[d][j] dS[i][j]              (K^T read transposed,
+//                                                        dS rows contiguous)
 //   dQ^T[d][i] += sum_x krgt[d][t0 + x] E[x][i]          (c2p)
 // where x = (i - iw) - (j - j0) + 63 is the wave's offset index, E[x][i] =
-// dS(i, j) is read straight from the dS^T tile (eight rows of column i per
-// operand), and krgt holds the Kr rows gathered per offset and transposed.
-// The tile is stored with 32 zero rows above and below so that offsets
-// outside the tile read zeros.  No softmax state is needed: dS^T already
-// holds zeros for masked pairs and dead rows.
+// dS(i, j), and krgt holds the Kr rows gathered per offset and transposed.
+// For one query, consecutive x are consecutive keys (descending), so E's
+// operand is eight consecutive elements of one staged dS row; krgt stores
+// each aligned group of eight offsets reversed, so the A operand's k order
+// matches (ascending keys).  32 zero columns before each staged row (and
+// the next row's, after it) cover offsets outside the tile.  No softmax
+// state is needed: dS holds zeros for masked pairs and dead rows.
 #pragma once
 
 #include "dsa_bwd.h"
@@ -23,7 +25,7 @@ namespace dsa {
 namespace dqcfg {
 constexpr int NW = 4, WQ = 32, BQ = 128, BK = 64;
 constexpr int XW = 96;   // offset rows per wave (95 used)
-constexpr int ZP = 32;   // zero rows above and below the dS^T tile
+constexpr int ZC = 32;   // zero columns before each staged dS row
 }  // namespace dqcfg
 
 template <typename T, int D>
@@ -35,16 +37,20 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dq_kernel(BwdParams bp) {
   typedef T vecT __attribute__((ext_vector_type(VEC)));
   constexpr int ND = D / 16;
   constexpr int FE = M::FRAG_ELEMS;               // k indices per lane per step
+  static_assert(FE == VEC, "a fragment is one 16-byte chunk");
   constexpr int KSTR = D + Pad<T>::v;             // K tile row stride
-  constexpr int SSTR = BQ + Pad<T>::v;            // dS^T tile row stride
-  constexpr int SROWS = ZP + BK + ZP;
+  // Staged dS row: ZC zeros, BK keys, zeros up to the stride, and then the
+  // next row's leading zeros; the stride makes 16 rows' 16-byte reads hit
+  // distinct banks.  The c2p walk reads key columns [BK - XW, WQ + BK - 2].
+  constexpr int SSTR = sizeof(T) == 2 ? 104 : 100;
+  static_assert(ZC + BK - XW >= 0 && WQ + BK - 2 < SSTR && ZC + BK <= SSTR, "zero columns cover the walk");
   constexpr int GW = BQ + XW - WQ;                // krgt columns of the workgroup's window (192)
   constexpr int GSTR = GW + Pad<T>::v;
-  constexpr int SV = BK * BQ / VEC, KV = BK * D / VEC, GV = D * GW / VEC;  // 16-byte chunks per tile
+  constexpr int SV = BQ * BK / VEC, KV = BK * D / VEC, GV = D * GW / VEC;  // 16-byte chunks per tile
   constexpr int SCH = (SV + 255) / 256, KCH = (KV + 255) / 256, GCH = (GV + 255) / 256;
   const FwdParams& p = bp.f;
 
-  __shared__ __align__(16) T Ss[SROWS * SSTR];
+  __shared__ __align__(16) T Ss[(BQ + 1) * SSTR];
   __shared__ __align__(16) T Ks[BK * KSTR];
   __shared__ __align__(16) T KG[D * GSTR];
 
@@ -56,35 +62,39 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dq_kernel(BwdParams bp) {
   const int i0 = qt * BQ, iw = i0 + w * WQ;
   const bool c2p = (p.flags & 1) != 0;
   const T* kbase = (const T*)p.k + (int64_t)b * p.ks[0] + (int64_t)h * p.ks[2];
-  const T* dsb = (const T*)bp.dst + (int64_t)(b * p.H + h) * bp.f.LkP * bp.f.LqP + i0;
+  const T* dsb = (const T*)bp.ds + ((int64_t)(b * p.H + h) * bp.f.LqP + i0) * bp.f.LkP;
   const T* krg = c2p ? (const T*)bp.krgt + (int64_t)h * D * bp.TGP : nullptr;
-  T* St = Ss + ZP * SSTR;  // row 0 of the tile
 
-  // zero pad rows (never overwritten)
+  // zeros everywhere; the key columns are overwritten per tile
   {
-    constexpr int VPR = SSTR / VEC;
     vecT z;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) z[e] = (T)0.0f;
-    for (int c = tid; c < ZP * VPR; c += 256) {
-      reinterpret_cast<vecT*>(Ss)[c] = z;
-      reinterpret_cast<vecT*>(Ss + (ZP + BK) * SSTR)[c] = z;
-    }
+    static_assert((BQ + 1) * SSTR % VEC == 0, "whole chunks");
+    for (int c = tid; c < (BQ + 1) * SSTR / VEC; c += 256) reinterpret_cast<vecT*>(Ss)[c] = z;
   }
 
   f32x4 dqa[ND][2];
 #pragma unroll
   for (int db = 0; db < ND; ++db) dqa[db][0] = dqa[db][1] = zero4();
 
-  // The next key tile (dS^T rows, K rows, krgt window) is fetched into
-  // registers while the current one is computed.
-  vecT sr[SCH], kr[KCH], gr[GCH];
-  auto fetch = [&](int kt) {
+  // Key tiles (dS columns, K rows, krgt window) are fetched into registers
+  // two tiles ahead, into two register sets used in turn (a tile's compute
+  // alone is too short to cover the loads' latency).
+  struct Regs {
+    vecT s[SCH], k[KCH], g[GCH];
+  };
+  Regs ra, rb;
+  auto fetch = [&](int kt, Regs& r) {
+    vecT(&sr)[SCH] = r.s;
+    vecT(&kr)[KCH] = r.k;
+    vecT(&gr)[GCH] = r.g;
     const int j0 = kt * BK;
 #pragma unroll
     for (int k = 0; k < SCH; ++k) {
       const int c = tid + 256 * k;
-      if (c < SV) sr[k] = *reinterpret_cast<const vecT*>(dsb + (int64_t)(j0 + c / (BQ / VEC)) * bp.f.LqP + (c % (BQ / VEC)) * VEC);
+      if (c < SV)
+        sr[k] = *reinterpret_cast<const vecT*>(dsb + (int64_t)(c / (BK / VEC)) * bp.f.LkP + j0 + (c % (BK / VEC)) * VEC);
     }
 #pragma unroll
     for (int k = 0; k < KCH; ++k) {
@@ -105,36 +115,35 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dq_kernel(BwdParams bp) {
   };
 
   const int nkt = bp.f.LkP / BK;
-  fetch(0);
-  for (int kt = 0; kt < nkt; ++kt) {
-    const int j0 = kt * BK;
+  auto tile = [&](int kt, Regs& r) {
     __syncthreads();  // previous tile's readers are done
 #pragma unroll
     for (int k = 0; k < SCH; ++k) {
       const int c = tid + 256 * k;
-      if (c < SV) *reinterpret_cast<vecT*>(St + (c / (BQ / VEC)) * SSTR + (c % (BQ / VEC)) * VEC) = sr[k];
+      if (c < SV) *reinterpret_cast<vecT*>(Ss + (c / (BK / VEC)) * SSTR + ZC + (c % (BK / VEC)) * VEC) = r.s[k];
     }
 #pragma unroll
     for (int k = 0; k < KCH; ++k) {
       const int c = tid + 256 * k;
-      if (c < KV) *reinterpret_cast<vecT*>(Ks + (c / (D / VEC)) * KSTR + (c % (D / VEC)) * VEC) = kr[k];
+      if (c < KV) *reinterpret_cast<vecT*>(Ks + (c / (D / VEC)) * KSTR + (c % (D / VEC)) * VEC) = r.k[k];
     }
     if (c2p) {
 #pragma unroll
       for (int k = 0; k < GCH; ++k) {
         const int c = tid + 256 * k;
-        if (c < GV) *reinterpret_cast<vecT*>(KG + (c / (GW / VEC)) * GSTR + (c % (GW / VEC)) * VEC) = gr[k];
+        if (c < GV) *reinterpret_cast<vecT*>(KG + (c / (GW / VEC)) * GSTR + (c % (GW / VEC)) * VEC) = r.g[k];
       }
     }
     __syncthreads();
-    if (kt + 1 < nkt) fetch(kt + 1);
+    if (kt + 2 < nkt) fetch(kt + 2, r);
 
-    // ---- dQ^T += K^T dS^T -------------------------------------------------------------
+    // ---- dQ^T += K^T dS^T: B = dS row i, keys KSTEP*s + FE*g + [0, FE) -----------------------
 #pragma unroll
     for (int s = 0; s < BK / M::KSTEP; ++s) {
       frag bfr[2];
 #pragma unroll
-      for (int ib = 0; ib < 2; ++ib) bfr[ib] = tr_contig<T>(St, SSTR, s * M::KSTEP, WQ * w + 16 * ib, g, c16);
+      for (int ib = 0; ib < 2; ++ib)
+        bfr[ib] = *reinterpret_cast<const frag*>(Ss + (WQ * w + 16 * ib + c16) * SSTR + ZC + M::KSTEP * s + FE * g);
 #pragma unroll
       for (int db = 0; db < ND; ++db) {
         const frag af = tr_contig<T>(Ks, KSTR, s * M::KSTEP, 16 * db, g, c16);
@@ -145,25 +154,34 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dq_kernel(BwdParams bp) {
 
     // ---- c2p: dQ^T += krgt[t0 + x]^T E[x] ---------------------------------------------------
     if (c2p) {
-      // krgt column of x = 0 for this wave: iw - j0 - 63 + OFF, i.e. window column 32w
+      // krgt column of x = 0 for this wave: iw - j0 - 63 + OFF, i.e. window
+      // column 32w.  Element e of the fragment whose first offset is
+      // xb = KSTEP*s + FE*g holds offset x = xb + FE - 1 - e, i.e. key
+      // column (i - iw) + BK - FE - xb + e.
 #pragma unroll
       for (int s = 0; s < XW / M::KSTEP; ++s) {
+        const int xb = M::KSTEP * s + FE * g;
         frag bfr[2];
 #pragma unroll
         for (int ib = 0; ib < 2; ++ib) {
-          // k = x = KSTEP*s + FE*g + e  ->  tile row j = (16*ib + c16) - x + 63
-          const T* col = Ss + (ZP + 16 * ib + c16 + 63 - M::KSTEP * s - FE * g) * SSTR + WQ * w + 16 * ib + c16;
-#pragma unroll
-          for (int e = 0; e < FE; ++e) bfr[ib][e] = col[-e * SSTR];
+          const int il = 16 * ib + c16;  // i - iw
+          const T* row = Ss + (WQ * w + il) * SSTR + ZC + il + BK - FE - xb;
+          lds_read_elems<T, FE>(bfr[ib], row);
         }
 #pragma unroll
         for (int db = 0; db < ND; ++db) {
-          const frag af = M::load_contig(KG + (16 * db + c16) * GSTR + WQ * w, s, g);
+          const frag af = *reinterpret_cast<const frag*>(KG + (16 * db + c16) * GSTR + WQ * w + xb);
 #pragma unroll
           for (int ib = 0; ib < 2; ++ib) dqa[db][ib] = M::mma(af, bfr[ib], dqa[db][ib]);
         }
       }
     }
+  };
+  fetch(0, ra);
+  if (nkt > 1) fetch(1, rb);
+  for (int kt = 0; kt < nkt; kt += 2) {
+    tile(kt, ra);
+    if (kt + 1 < nkt) tile(kt + 1, rb);
   }
 
   // ---- dQ ---------------------------------------------------------------------------------

@@ -8,18 +8,20 @@
 // monotone in d, so the offsets of one row form a contiguous range.
 //
 // dsa_bwd_table_kernel: one workgroup = (128-offset block [d0, d0+128),
-// head h, batch group).  For each batch and each chunk of 32 keys
-// [j0, j0+32) it stages the dS^T region rows j0.., columns i in
-// [j0 + d0, j0 + d0 + 160) — which holds every pair of the chunk with an
-// offset in the block — with the 32 key rows and a ring of query rows:
-//   Gp^T[dd] += sum_jj  K^T[jj] X[jj][jj + dd]        (X = staged region)
-//   Gc^T[dd] += sum_c   Q^T[i0 + c] X[c - dd][c]
+// head h, batch group).  For each batch and each chunk of 32 queries
+// [i0, i0+32) it stages the region of dS (rows = queries) with rows i0..,
+// keys j in [jb, jb + 160), jb = i0 - d0 - 128 — which holds every pair of
+// the chunk with an offset in the block — with the 32 query rows and a ring
+// of key rows.  Element (r, c) of the staged region X has offset
+// d = d0 + 127 - (c - r - 1); with e = c - r - 1 (so d = d0 + 127 - e):
+//   Gc^T[e] += sum_r  Q^T[i0 + r] X[r][r + 1 + e]
+//   Gp^T[e] += sum_c  K^T[jb + c] X[c - 1 - e][c]
 // Both B operands walk a diagonal of X (eight single-element LDS reads per
 // fragment); zero rows around X cover the out-of-chunk part of the walk.
-// A wave's two offset blocks share their A operands (the c2p one over 64
+// A wave's two offset blocks share their A operands (the p2c one over 64
 // staged columns, with diagonal elements outside the chunk read as zeros).
-// Wave w accumulates offsets [32w, 32w + 32) of the block in registers and
-// writes them once, to a per-(block, head, batch group) partial.
+// Wave w accumulates e in [32w, 32w + 32) in registers and writes them once,
+// to a per-(block, head, batch group) partial.
 #pragma once
 
 #include "dsa_bwd.h"
@@ -29,12 +31,12 @@ namespace dsa {
 namespace tbcfg {
 constexpr int NW = 4;
 constexpr int DBW = 128;           // offsets per block
-constexpr int JC = 32;             // keys per step
+constexpr int JC = 32;             // queries per step
 constexpr int XC = DBW + JC;       // staged columns
 constexpr int XP = 32;             // zero rows above the staged rows
 constexpr int XROWS = XP + JC + 32;  // and 32 below
 constexpr int XCOLS = DBW + 48;    // columns a diagonal walk can touch
-constexpr int QRING = 256;         // query rows kept (power of two >= XC)
+constexpr int QRING = 256;         // ring rows kept (power of two >= XC)
 }  // namespace tbcfg
 
 // Transposed LDS operand read (see tr_contig) from a ring of rows: logical
@@ -72,16 +74,16 @@ DSA_DEV void load_ring_rows(T* ring, int str, const T* src, int64_t rs, int r0, 
   }
 }
 
-// Number of 32-key chunks of offset block dblk that hold pairs with an
-// offset in the block, and the first of them.
-DSA_DEV void block_chunks(int dblk, int LkP, int Lq, int Lk, int* jstart, int* nch) {
+// Number of 32-query chunks of offset block dblk that hold pairs with an
+// offset in the block, and the first of them: rows i >= d0 (a key j = i - d
+// >= 0 exists) and i0 - d0 - 127 <= Lk - 1 (a key j < Lk exists).
+DSA_DEV void block_chunks(int dblk, int LkP, int Lq, int Lk, int* istart, int* nch) {
   using namespace tbcfg;
-  const int d0 = -LkP + DBW * dblk;
-  int js = -d0 - (XC - 2);  // the last staged column must reach query 0
-  js = js > 0 ? (js + JC - 1) / JC * JC : 0;
-  const int je = min(Lk, Lq - d0);
-  *jstart = js;
-  *nch = je > js ? (je - js + JC - 1) / JC : 0;
+  const int d0 = -LkP + DBW * dblk;  // a multiple of 128
+  const int is = d0 > 0 ? d0 : 0;
+  const int ie = min(Lq, Lk + d0 + DBW - 1);
+  *istart = is;
+  *nch = ie > is ? (ie - is + JC - 1) / JC : 0;
 }
 
 template <typename T, int D>
@@ -97,22 +99,22 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
   // Row stride of X chosen for few LDS bank conflicts in its diagonal walks
   // (178: two-way at most; rows are then only 4-byte aligned).
   constexpr int XSTR = sizeof(T) == 2 ? 178 : XCOLS + Pad<T>::v;
-  constexpr int QSTR = KSTR;
-  constexpr int GC_STEPS = 64 / M::KSTEP;  // k steps over the 64 staged columns a wave's two blocks read
-  constexpr int GP_STEPS = JC / M::KSTEP;
+  constexpr int RSTR = KSTR;
+  constexpr int GP_STEPS = 64 / M::KSTEP;  // k steps over the 64 staged columns a wave's two blocks read
+  constexpr int GC_STEPS = JC / M::KSTEP;
   constexpr int XV = JC * XC / VEC;   // 16-byte chunks of the staged region
-  constexpr int RV = JC * D / VEC;    // 16-byte chunks of 32 key (or query) rows
+  constexpr int RV = JC * D / VEC;    // 16-byte chunks of 32 query (or key) rows
   constexpr int XCH = (XV + 255) / 256, RCH = (RV + 255) / 256;
   const FwdParams& p = bp.f;
 
   __shared__ __align__(16) T Xs[XROWS * XSTR];
-  __shared__ __align__(16) T Kc[JC * KSTR];
-  __shared__ __align__(16) T Qring[QRING * QSTR];
+  __shared__ __align__(16) T Qc[JC * KSTR];          // the chunk's query rows
+  __shared__ __align__(16) T Kring[QRING * RSTR];    // key rows of the staged columns
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, g = (tid & 63) >> 4, c16 = tid & 15;
   // Work order: blockIdx.x enumerates (offset block, head, batch group) with
-  // the offset blocks that have the most key chunks first, so the shortest
+  // the offset blocks that have the most chunks first, so the shortest
   // workgroups fill in at the end of the launch.  (Grouping a (head, batch
   // group)'s offset blocks on one XCD instead measured slower: the long
   // blocks then finish last.)
@@ -124,8 +126,8 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
   const int d0 = -bp.f.LkP + DBW * dblk;
   const bool c2p = (p.flags & 1) != 0, p2c = (p.flags & 2) != 0;
   const int b_lo = bg * bp.BPG, b_hi = min(p.B, b_lo + bp.BPG);
-  int jstart, nch;
-  block_chunks(dblk, bp.f.LkP, p.Lq, p.Lk, &jstart, &nch);
+  int istart, nch;
+  block_chunks(dblk, bp.f.LkP, p.Lq, p.Lk, &istart, &nch);
   const int nsteps = (b_hi > b_lo) ? (b_hi - b_lo) * nch : 0;
 
   // zero rows around the staged region (never overwritten), and a finite ring
@@ -133,9 +135,9 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
     vecT z;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) z[e] = (T)0.0f;
-    static_assert(XROWS * XSTR % VEC == 0 && QRING * QSTR % VEC == 0, "whole 16-byte chunks");
+    static_assert(XROWS * XSTR % VEC == 0 && QRING * RSTR % VEC == 0, "whole 16-byte chunks");
     for (int c = tid; c < XROWS * XSTR / VEC; c += 256) reinterpret_cast<vecT*>(Xs)[c] = z;
-    for (int c = tid; c < QRING * QSTR / VEC; c += 256) reinterpret_cast<vecT*>(Qring)[c] = z;
+    for (int c = tid; c < QRING * RSTR / VEC; c += 256) reinterpret_cast<vecT*>(Kring)[c] = z;
   }
 
   f32x4 gc[2][ND], gp[2][ND];
@@ -145,55 +147,54 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
     for (int db = 0; db < ND; ++db) gc[t][db] = gp[t][db] = zero4();
 
   // Registers holding the next step's global data.
-  vecT xr[XCH], kr[RCH], qr[RCH];
-  auto step_coords = [&](int st, int& b, int& j0) {
+  vecT xr[XCH], qr[RCH], kr[RCH];
+  auto step_coords = [&](int st, int& b, int& i0) {
     b = b_lo + st / nch;
-    j0 = jstart + (st % nch) * JC;
+    i0 = istart + (st % nch) * JC;
   };
   auto fetch = [&](int st) {
-    int b, j0;
-    step_coords(st, b, j0);
-    const int ib0 = j0 + d0;
-    const T* dsb = (const T*)bp.dst + (int64_t)(b * p.H + h) * bp.f.LkP * bp.f.LqP;
+    int b, i0;
+    step_coords(st, b, i0);
+    const int jb = i0 - d0 - DBW;  // key of staged column 0 (a multiple of 32)
+    const T* dsb = (const T*)bp.ds + (int64_t)(b * p.H + h) * bp.f.LqP * bp.f.LkP;
 #pragma unroll
     for (int k = 0; k < XCH; ++k) {
       const int c = tid + 256 * k;
       const int r = c / (XC / VEC), c0 = (c % (XC / VEC)) * VEC;
-      const int i = ib0 + c0;  // 16-byte chunks are wholly in or out of [0, LqP)
-      if (c < XV && i >= 0 && i < bp.f.LqP) {
-        xr[k] = *reinterpret_cast<const vecT*>(dsb + (int64_t)(j0 + r) * bp.f.LqP + i);
+      const int j = jb + c0;  // 16-byte chunks are wholly in or out of [0, LkP)
+      if (c < XV && j >= 0 && j < bp.f.LkP) {
+        xr[k] = *reinterpret_cast<const vecT*>(dsb + (int64_t)(i0 + r) * bp.f.LkP + j);
       } else {
 #pragma unroll
         for (int e = 0; e < VEC; ++e) xr[k][e] = (T)0.0f;
       }
     }
-    const T* kbase = (const T*)p.k + (int64_t)b * p.ks[0] + (int64_t)h * p.ks[2];
     const T* qbase = (const T*)p.q + (int64_t)b * p.qs[0] + (int64_t)h * p.qs[2];
+    const T* kbase = (const T*)p.k + (int64_t)b * p.ks[0] + (int64_t)h * p.ks[2];
 #pragma unroll
     for (int k = 0; k < RCH; ++k) {
       const int c = tid + 256 * k;
       const int r = c / (D / VEC), c0 = (c % (D / VEC)) * VEC;
-      const int j = j0 + r, i = ib0 + XC - JC + r;  // the ring's new rows
+      const int i = i0 + r, j = jb + XC - JC + r;  // the ring's new rows
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) kr[k][e] = qr[k][e] = (T)0.0f;
-      if (c < RV && p2c && j < p.Lk) kr[k] = *reinterpret_cast<const vecT*>(kbase + (int64_t)j * p.ks[1] + c0);
-      if (c < RV && c2p && i >= 0 && i < p.Lq) qr[k] = *reinterpret_cast<const vecT*>(qbase + (int64_t)i * p.qs[1] + c0);
+      for (int e = 0; e < VEC; ++e) qr[k][e] = kr[k][e] = (T)0.0f;
+      if (c < RV && c2p && i < p.Lq) qr[k] = *reinterpret_cast<const vecT*>(qbase + (int64_t)i * p.qs[1] + c0);
+      if (c < RV && p2c && j >= 0 && j < p.Lk) kr[k] = *reinterpret_cast<const vecT*>(kbase + (int64_t)j * p.ks[1] + c0);
     }
   };
 
   if (nsteps > 0) fetch(0);
   for (int st = 0; st < nsteps; ++st) {
-    int b, j0;
-    step_coords(st, b, j0);
-    const int ib0 = j0 + d0;  // query of staged column 0 (a multiple of 32)
-    __syncthreads();          // previous step's readers are done
+    int b, i0;
+    step_coords(st, b, i0);
+    const int jb = i0 - d0 - DBW;  // key of staged column 0
+    __syncthreads();               // previous step's readers are done
 #pragma unroll
     for (int k = 0; k < XCH; ++k) {
       const int c = tid + 256 * k;
       if (c < XV) {
         const int r = c / (XC / VEC), c0 = (c % (XC / VEC)) * VEC;
         *reinterpret_cast<vecT*>(Xs + (XP + r) * XSTR + c0) = xr[k];
-
       }
     }
 #pragma unroll
@@ -201,60 +202,60 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
       const int c = tid + 256 * k;
       if (c < RV) {
         const int r = c / (D / VEC), c0 = (c % (D / VEC)) * VEC;
-        *reinterpret_cast<vecT*>(Kc + r * KSTR + c0) = kr[k];
-        *reinterpret_cast<vecT*>(Qring + ((ib0 + XC - JC + r) & (QRING - 1)) * QSTR + c0) = qr[k];
+        *reinterpret_cast<vecT*>(Qc + r * KSTR + c0) = qr[k];
+        *reinterpret_cast<vecT*>(Kring + ((jb + XC - JC + r) & (QRING - 1)) * RSTR + c0) = kr[k];
       }
     }
-    if (c2p && j0 == jstart) {  // first chunk of a batch: the ring's older rows too
-      const T* qbase = (const T*)p.q + (int64_t)b * p.qs[0] + (int64_t)h * p.qs[2];
-      load_ring_rows<T, D>(Qring, QSTR, qbase, p.qs[1], ib0, XC - JC, p.Lq, tid);
+    if (p2c && i0 == istart) {  // first chunk of a batch: the ring's older rows too
+      const T* kbase = (const T*)p.k + (int64_t)b * p.ks[0] + (int64_t)h * p.ks[2];
+      load_ring_rows<T, D>(Kring, RSTR, kbase, p.ks[1], jb, XC - JC, p.Lk, tid);
     }
     __syncthreads();
     if (st + 1 < nsteps) fetch(st + 1);
 
-    // A operands, shared by the wave's two 16-offset blocks: K^T of the 32
-    // keys, and Q^T of staged columns [32w, 32w + 64).
-    frag ka[GP_STEPS][ND], qa[GC_STEPS][ND];
-    if (p2c) {
-#pragma unroll
-      for (int s = 0; s < GP_STEPS; ++s)
-#pragma unroll
-        for (int db = 0; db < ND; ++db) ka[s][db] = tr_contig<T>(Kc, KSTR, s * M::KSTEP, 16 * db, g, c16);
-    }
+    // A operands, shared by the wave's two 16-offset blocks: Q^T of the 32
+    // queries, and K^T of staged columns [32w, 32w + 64).
+    frag qa[GC_STEPS][ND], ka[GP_STEPS][ND];
     if (c2p) {
 #pragma unroll
       for (int s = 0; s < GC_STEPS; ++s)
 #pragma unroll
+        for (int db = 0; db < ND; ++db) qa[s][db] = tr_contig<T>(Qc, KSTR, s * M::KSTEP, 16 * db, g, c16);
+    }
+    if (p2c) {
+#pragma unroll
+      for (int s = 0; s < GP_STEPS; ++s)
+#pragma unroll
         for (int db = 0; db < ND; ++db)
-          qa[s][db] = tr_contig_ring<T>(Qring, QSTR, ib0, 32 * w + M::KSTEP * s, 16 * db, g, c16);
+          ka[s][db] = tr_contig_ring<T>(Kring, RSTR, jb, 32 * w + M::KSTEP * s, 16 * db, g, c16);
     }
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      const int c0 = 16 * (2 * w + t);  // first offset of this wave's 16-offset block
-      if (p2c) {
-        // Gp^T[d][dd] += sum_jj K^T[d][jj] X[jj][jj + dd],  jj = KSTEP*s + FE*g + e
-#pragma unroll
-        for (int s = 0; s < GP_STEPS; ++s) {
-          frag bfr;
-          const T* dg = Xs + (XP + M::KSTEP * s + FE * g) * XSTR + M::KSTEP * s + FE * g + c0 + c16;
-#pragma unroll
-          for (int e = 0; e < FE; ++e) bfr[e] = dg[e * (XSTR + 1)];
-#pragma unroll
-          for (int db = 0; db < ND; ++db) gp[t][db] = M::mma(ka[s][db], bfr, gp[t][db]);
-        }
-      }
+      const int e0 = 16 * (2 * w + t);  // first e of this wave's 16-offset block
       if (c2p) {
-        // Gc^T[d][dd] += sum_c Q^T[d][ib0 + c] X[c - dd][c],  c = 32w + KSTEP*s + FE*g + e;
-        // X rows c - dd in [-31, 64) (zero outside [0, JC)).
+        // Gc^T[d][e] += sum_r Q^T[d][i0 + r] X[r][r + 1 + e],  r = KSTEP*s + FE*g + u
 #pragma unroll
         for (int s = 0; s < GC_STEPS; ++s) {
           frag bfr;
-          const int c = 32 * w + M::KSTEP * s + FE * g;  // column of element e = 0
-          const T* dg = Xs + (XP + c - c0 - c16) * XSTR + c;
+          const T* dg = Xs + (XP + M::KSTEP * s + FE * g) * XSTR + M::KSTEP * s + FE * g + 1 + e0 + c16;
 #pragma unroll
-          for (int e = 0; e < FE; ++e) bfr[e] = dg[e * (XSTR + 1)];
+          for (int u = 0; u < FE; ++u) bfr[u] = dg[u * (XSTR + 1)];
 #pragma unroll
           for (int db = 0; db < ND; ++db) gc[t][db] = M::mma(qa[s][db], bfr, gc[t][db]);
+        }
+      }
+      if (p2c) {
+        // Gp^T[d][e] += sum_c K^T[d][jb + c] X[c - 1 - e][c],  c = 32w + KSTEP*s + FE*g + u;
+        // X rows c - 1 - e in [-32, 63) (zero outside [0, JC)).
+#pragma unroll
+        for (int s = 0; s < GP_STEPS; ++s) {
+          frag bfr;
+          const int c = 32 * w + M::KSTEP * s + FE * g;  // column of element u = 0
+          const T* dg = Xs + (XP + c - 1 - e0 - c16) * XSTR + c;
+#pragma unroll
+          for (int u = 0; u < FE; ++u) bfr[u] = dg[u * (XSTR + 1)];
+#pragma unroll
+          for (int db = 0; db < ND; ++db) gp[t][db] = M::mma(ka[s][db], bfr, gp[t][db]);
         }
       }
     }
@@ -264,7 +265,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
   float* out = bp.gpart + ((int64_t)(h * bp.NDB + dblk) * bp.NBG + bg) * 2 * DBW * D;
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    const int dd = 16 * (2 * w + t) + c16;
+    const int dd = DBW - 1 - (16 * (2 * w + t) + c16);  // offset d0 + dd
 #pragma unroll
     for (int db = 0; db < ND; ++db) {
       *reinterpret_cast<f32x4*>(out + (int64_t)dd * D + 16 * db + 4 * g) = gc[t][db];

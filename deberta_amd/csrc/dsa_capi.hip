@@ -151,7 +151,7 @@ int device_cus() {
 // extents the kernels share.
 struct WsLayout {
   int LqP, LkP, TGP, OFF, NDB, NBG, BPG;
-  size_t rowinfo, krgt, qrgt, dst, gpart, total;
+  size_t rowinfo, krgt, qrgt, ds, gpart, total;
 };
 
 WsLayout ws_layout(const dsa_bwd_args* a) {
@@ -176,7 +176,7 @@ WsLayout ws_layout(const dsa_bwd_args* a) {
   if (f.flags & DSA_C2P) off = align_up(off + (size_t)f.H * f.D * w.TGP * es, 256);
   w.qrgt = off;
   if (f.flags & DSA_P2C) off = align_up(off + (size_t)f.H * f.D * w.TGP * es, 256);
-  w.dst = off;
+  w.ds = off;
   off = align_up(off + (size_t)f.B * f.H * w.LkP * w.LqP * es, 256);
   w.gpart = off;
   if (f.flags) off = align_up(off + (size_t)f.H * w.NDB * w.NBG * 2 * dsa::tbcfg::DBW * f.D * sizeof(float), 256);
@@ -205,7 +205,7 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
   bp.rowinfo = reinterpret_cast<float*>(base + ws.rowinfo);
   bp.krgt = base + ws.krgt;
   bp.qrgt = base + ws.qrgt;
-  bp.dst = base + ws.dst;
+  bp.ds = base + ws.ds;
   bp.gpart = reinterpret_cast<float*>(base + ws.gpart);
   bp.TGP = ws.TGP;
   bp.OFF = ws.OFF;

@@ -183,6 +183,17 @@ DSA_DEV bf16x8 join8(bf16x4 a, bf16x4 b) {
   return f;
 }
 
+// FE consecutive LDS elements starting at an element (not 16-byte) aligned
+// address, one single-element read each.  The compiler would merge them
+// into one unaligned 16-byte read, which this LDS serves far more slowly
+// than separate aligned reads; the volatile LDS-space access keeps them
+// apart.
+template <typename T, int FE, typename F>
+DSA_DEV void lds_read_elems(F& f, const T* p) {
+#pragma unroll
+  for (int e = 0; e < FE; ++e) f[e] = *(volatile const __attribute__((address_space(3))) T*)(p + e);
+}
+
 // ds_read_b64_tr_b16 at an address the caller computed (see tr4).
 DSA_DEV bf16x4 tr4_at(const bf16* p) {
   bf16x4_tr v = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4_tr*)p);

@@ -43,7 +43,7 @@ struct BwdParams {
   float* dqr;
   // workspace
   float* rowinfo;   // [B, H, LqP, 2]: lse*log2e (inf: dead or padding row), dO . O
-  void* dst;        // dS^T [B, H, f.LkP, f.LqP], zero outside [0, Lk) x [0, Lq)
+  void* ds;         // dS [B, H, f.LqP, f.LkP] (rows = queries), zero outside [0, Lq) x [0, Lk)
   void* krgt;       // [H, D, TGP]: krgt[h][d][t] = Kr[h][c(t - OFF)][d]
   void* qrgt;       // [H, D, TGP]: qrgt[h][d][t] = Qr[h][p(t - OFF)][d]
   float* gpart;     // table-gradient partials [H][NDB][NBG][2][128][D]
