@@ -184,14 +184,30 @@ DSA_DEV bf16x8 join8(bf16x4 a, bf16x4 b) {
 }
 
 // FE consecutive LDS elements starting at an element (not 16-byte) aligned
-// address, one single-element read each.  The compiler would merge them
-// into one unaligned 16-byte read, which this LDS serves far more slowly
-// than separate aligned reads; the volatile LDS-space access keeps them
-// apart.
+// address.  A 16-byte read at such an address is served far more slowly
+// than aligned reads, so 16-bit elements are read as the FE/2 + 1 dwords
+// that cover them (two-dword reads at the dword-aligned address below) and
+// shifted into place with v_alignbit (by 16 bits when the address is odd in
+// 16-bit units); 32-bit elements are read one by one.
 template <typename T, int FE, typename F>
 DSA_DEV void lds_read_elems(F& f, const T* p) {
+  if constexpr (sizeof(T) == 2) {
+    typedef const __attribute__((address_space(3))) unsigned* lds_u32;
+    const uintptr_t a = (uintptr_t)p;
+    const lds_u32 q = (lds_u32)(a & ~(uintptr_t)3);
+    unsigned d[FE / 2 + 1];
 #pragma unroll
-  for (int e = 0; e < FE; ++e) f[e] = *(volatile const __attribute__((address_space(3))) T*)(p + e);
+    for (int k = 0; k < FE / 2 + 1; ++k) d[k] = q[k];
+    const unsigned sh = (a & 2) ? 16u : 0u;
+    typedef unsigned u_n __attribute__((ext_vector_type(FE / 2)));
+    u_n r;
+#pragma unroll
+    for (int k = 0; k < FE / 2; ++k) r[k] = __builtin_amdgcn_alignbit(d[k + 1], d[k], sh);
+    f = __builtin_bit_cast(F, r);
+  } else {
+#pragma unroll
+    for (int e = 0; e < FE; ++e) f[e] = *(volatile const __attribute__((address_space(3))) T*)(p + e);
+  }
 }
 
 // ds_read_b64_tr_b16 at an address the caller computed (see tr4).
