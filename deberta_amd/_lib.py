@@ -22,7 +22,7 @@ DSA_STAGE_DQ = 2
 DSA_STAGE_DKDV = 4
 DSA_STAGE_FOLD = 8
 
-EXPECTED_VERSION = 2
+EXPECTED_VERSION = 3
 
 _i64x3 = ctypes.c_int64 * 3
 _i64x2 = ctypes.c_int64 * 2
@@ -77,6 +77,8 @@ class DsaBwdArgs(ctypes.Structure):
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_size_t),
         ("stages", ctypes.c_int32),
+        ("dtab_dtype", ctypes.c_int32),
+        ("dtab_overwrite", ctypes.c_int32),
     ]
 
 

@@ -274,8 +274,9 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
   }
 }
 
-// tab[h][r][:] += s * sum over batch groups and offsets d with row(d) = r of
-// the partials; one thread per (table, h, r, 4 columns).
+// tab[h][r][:] (+)= s * sum over batch groups and offsets d with row(d) = r
+// of the partials (accumulated into fp32, or written in fp32 or bf16); one
+// thread per (table, h, r, 4 columns).
 template <int D>
 __global__ __launch_bounds__(256) void dsa_bwd_fold_kernel(BwdParams bp) {
   using namespace tbcfg;
@@ -315,9 +316,18 @@ __global__ __launch_bounds__(256) void dsa_bwd_fold_kernel(BwdParams bp) {
                        (int64_t)((q ? DBW : 0) + dd) * D + 4 * c4;
     for (int k = 0; k < bp.NBG; ++k) acc += *reinterpret_cast<const f32x4*>(src + (int64_t)k * 2 * DBW * D);
   }
-  float* tab = (q ? bp.dqr : bp.dkr) + ((int64_t)h * R + r) * D + 4 * c4;
-  f32x4 cur = *reinterpret_cast<f32x4*>(tab);
-  *reinterpret_cast<f32x4*>(tab) = cur + acc * p.scale;
+  const int64_t o = ((int64_t)h * R + r) * D + 4 * c4;
+  void* tab = q ? bp.dqr : bp.dkr;
+  if (bp.dtab_bf16) {
+    typedef bf16 b4 __attribute__((ext_vector_type(4)));
+    const f32x4 v = acc * p.scale;
+    *reinterpret_cast<b4*>((bf16*)tab + o) = b4{(bf16)v[0], (bf16)v[1], (bf16)v[2], (bf16)v[3]};
+  } else if (bp.dtab_overwrite) {
+    *reinterpret_cast<f32x4*>((float*)tab + o) = acc * p.scale;
+  } else {
+    f32x4* t = reinterpret_cast<f32x4*>((float*)tab + o);
+    *t = *t + acc * p.scale;
+  }
 }
 
 }  // namespace dsa

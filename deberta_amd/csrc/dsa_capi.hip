@@ -201,6 +201,8 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
   bp.dv = a->dv;
   bp.dkr = a->dkr;
   bp.dqr = a->dqr;
+  bp.dtab_bf16 = a->dtab_dtype == DSA_BF16;
+  bp.dtab_overwrite = a->dtab_overwrite != 0;
   char* base = static_cast<char*>(a->workspace);
   bp.rowinfo = reinterpret_cast<float*>(base + ws.rowinfo);
   bp.krgt = base + ws.krgt;
@@ -258,7 +260,7 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
 
 extern "C" {
 
-int dsa_version(void) { return 2; }
+int dsa_version(void) { return 3; }
 
 const char* dsa_last_error(void) { return g_err.c_str(); }
 
@@ -292,6 +294,9 @@ int dsa_bwd(const dsa_bwd_args* a, void* stream) {
   if (!a->dout || !a->dq || !a->dk || !a->dv) return fail("dsa: dout, dq, dk and dv are required");
   if ((f.flags & DSA_C2P) && !a->dkr) return fail("dsa: c2p backward needs dkr");
   if ((f.flags & DSA_P2C) && !a->dqr) return fail("dsa: p2c backward needs dqr");
+  if (a->dtab_dtype != DSA_F32 && a->dtab_dtype != DSA_BF16) return fail("dsa: unsupported dtab_dtype %d", a->dtab_dtype);
+  if (a->dtab_dtype == DSA_BF16 && !a->dtab_overwrite)
+    return fail("dsa: bf16 table gradients are written, not accumulated (set dtab_overwrite)");
   if (f.flags && !f.bias) return fail("dsa: the backward needs the relative term saved by dsa_fwd (fwd.bias)");
   if (f.flags && !aligned16(f.bias)) return fail("dsa: fwd.bias must be 16-byte aligned");
   const int vec = 16 / elem_bytes(f.dtype);

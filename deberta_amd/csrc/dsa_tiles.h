@@ -39,8 +39,9 @@ struct BwdParams {
   void* dk;
   void* dv;
   int64_t dqs[3], dks[3], dvs[3];
-  float* dkr;
-  float* dqr;
+  void* dkr;        // table gradients: fp32 accumulated, or fp32 / bf16 overwritten
+  void* dqr;
+  int dtab_bf16, dtab_overwrite;
   // workspace
   float* rowinfo;   // [B, H, LqP, 2]: lse*log2e (inf: dead or padding row), dO . O
   void* ds;         // dS [B, H, f.LqP, f.LkP] (rows = queries), zero outside [0, Lq) x [0, Lk)

@@ -219,7 +219,10 @@ def fill_bwd_args(
     dv: Tensor,
     dkr: Optional[Tensor],
     dqr: Optional[Tensor],
+    dtab_overwrite: bool = False,
 ) -> _lib.DsaBwdArgs:
+    """Backward arguments.  dkr / dqr are fp32 and accumulated into, or, with
+    ``dtab_overwrite``, written (fp32 or bf16, their dtype)."""
     a = _lib.DsaBwdArgs()
     a.fwd = _fill_fwd_args(q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, att_span, scale, bias)
     a.dout = dout.data_ptr()
@@ -230,6 +233,9 @@ def fill_bwd_args(
     a.dv_strides[:] = _strides3(dv)
     a.dkr, a.dqr = _ptr(dkr), _ptr(dqr)
     a.stages = 0
+    tab = dkr if dkr is not None else dqr
+    a.dtab_dtype = _DTYPES[tab.dtype] if tab is not None else _lib.DSA_F32
+    a.dtab_overwrite = int(dtab_overwrite)
     return a
 
 
@@ -250,8 +256,8 @@ def dsa_bwd(
     att_span: int,
     scale: float,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
-    """Gradients (dq, dk, dv, dkr, dqr).  dkr/dqr are float32 [H, 2A, D]
-    (empty when the matching table is None).  ``bias`` is the relative term
+    """Gradients (dq, dk, dv, dkr, dqr).  dkr/dqr are [H, 2A, D] in the
+    tables' dtype (empty when the matching table is None).  ``bias`` is the relative term
     dsa_fwd saved (required with c2p/p2c)."""
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
     kr = None if kr is None else _kernel_ready(kr)
@@ -265,12 +271,13 @@ def dsa_bwd(
     dq = torch.empty_like(q, memory_format=torch.contiguous_format)
     dk = torch.empty_like(k, memory_format=torch.contiguous_format)
     dv = torch.empty_like(v, memory_format=torch.contiguous_format)
-    f32 = dict(dtype=torch.float32, device=q.device)
-    dkr = torch.zeros((H, R, D), **f32) if kr is not None else torch.empty((0,), **f32)
-    dqr = torch.zeros((H, R, D), **f32) if qr is not None else torch.empty((0,), **f32)
+    # the table gradients are written in the tables' dtype (no zeroing, no cast)
+    tab = dict(dtype=q.dtype, device=q.device)
+    dkr = torch.empty((H, R, D), **tab) if kr is not None else torch.empty((0,), **tab)
+    dqr = torch.empty((H, R, D), **tab) if qr is not None else torch.empty((0,), **tab)
     args = fill_bwd_args(
         dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, att_span, scale,
-        dq, dk, dv, dkr if kr is not None else None, dqr if qr is not None else None,
+        dq, dk, dv, dkr if kr is not None else None, dqr if qr is not None else None, dtab_overwrite=True,
     )
     ws = torch.empty((max(bwd_workspace_bytes(args), 16),), dtype=torch.uint8, device=q.device)
     args.workspace = ws.data_ptr()
@@ -285,9 +292,8 @@ def dsa_bwd(
 def _dsa_bwd_fake(dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, att_span, scale):
     H, D = q.shape[2], q.shape[3]
     R = 2 * int(att_span)
-    f32 = dict(dtype=torch.float32)
-    dkr = q.new_empty((H, R, D), **f32) if kr is not None else q.new_empty((0,), **f32)
-    dqr = q.new_empty((H, R, D), **f32) if qr is not None else q.new_empty((0,), **f32)
+    dkr = q.new_empty((H, R, D)) if kr is not None else q.new_empty((0,))
+    dqr = q.new_empty((H, R, D)) if qr is not None else q.new_empty((0,))
     return (
         q.new_empty(q.shape),
         k.new_empty(k.shape),
@@ -301,6 +307,9 @@ def _setup_context(ctx, inputs, output):
     q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias = inputs
     out, lse, bias = output
     ctx.mark_non_differentiable(lse, bias)
+    # lse and the saved term get no gradient: do not materialise zeros for
+    # them (the saved term is (B, H, L, L)-sized)
+    ctx.set_materialize_grads(False)
     ctx.save_for_backward(q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias)
     ctx.att_span = att_span
     ctx.scale = scale
@@ -308,12 +317,12 @@ def _setup_context(ctx, inputs, output):
 
 def _backward(ctx, dout, dlse, dbias):
     q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias = ctx.saved_tensors
+    if dout is None:  # the output itself received no gradient
+        return (None,) * 11
     dq, dk, dv, dkr, dqr = dsa_bwd(
         dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, ctx.att_span, ctx.scale
     )
-    gkr = dkr.to(kr.dtype) if kr is not None else None
-    gqr = dqr.to(qr.dtype) if qr is not None else None
-    return dq, dk, dv, gkr, gqr, None, None, None, None, None, None
+    return dq, dk, dv, (dkr if kr is not None else None), (dqr if qr is not None else None), None, None, None, None, None, None
 
 
 torch.library.register_autograd("deberta_amd::dsa_fwd", _backward, setup_context=_setup_context)

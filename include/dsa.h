@@ -109,12 +109,15 @@ typedef struct dsa_bwd_args {
   int64_t dq_strides[3];
   int64_t dk_strides[3];
   int64_t dv_strides[3];
-  float* dkr;             /* [H, R, D] fp32 contiguous, accumulated (+=); NULL if !C2P */
-  float* dqr;             /* [H, R, D] fp32 contiguous, accumulated (+=); NULL if !P2C */
+  void* dkr;              /* [H, R, D] contiguous; NULL if !C2P */
+  void* dqr;              /* [H, R, D] contiguous; NULL if !P2C */
   /* workspace: dsa_bwd_workspace_bytes() bytes, caller-allocated */
   void* workspace;
   size_t workspace_bytes;
   int32_t stages;         /* DSA_STAGE_* mask; 0 = all */
+  int32_t dtab_dtype;     /* dtype of dkr / dqr: DSA_F32 (0) or DSA_BF16 */
+  int32_t dtab_overwrite; /* 0: dkr / dqr are fp32 and accumulated (+=) into;
+                             1: they are overwritten (=), either dtype */
 } dsa_bwd_args;
 
 /* Forward: out = softmax(mask((QK^T + c2p + p2c) * scale)) V and its
@@ -123,8 +126,8 @@ typedef struct dsa_bwd_args {
 int dsa_fwd(const dsa_fwd_args* args, void* stream);
 
 /* Backward of dsa_fwd: dq, dk, dv and the gradients of the projected
- * relative tables (dkr, dqr, accumulated into fp32 buffers the caller has
- * zeroed).  Replaces ATen autograd through deberta_v2_native.py:592-652 and
+ * relative tables (dkr, dqr: accumulated into fp32 buffers, or written in
+ * fp32 or bf16, per dtab_dtype / dtab_overwrite).  Replaces ATen autograd through deberta_v2_native.py:592-652 and
  * the einsum/bmm + gather bias path (:349-528). */
 int dsa_bwd(const dsa_bwd_args* args, void* stream);
 

@@ -138,7 +138,7 @@ def test_fake_shapes():
         assert bias.shape == (2, 2, 128, 128) and bias.dtype == torch.float16
         g = torch.ops.deberta_amd.dsa_bwd(out, q, k, v, kr, qr, table, None, None, out, lse, bias, 16, 0.1)
         assert [t.shape for t in g] == [q.shape, k.shape, v.shape, (2, 32, 64), (2, 32, 64)]
-        assert g[3].dtype == torch.float32
+        assert g[3].dtype == q.dtype
 
 
 def test_trace_forward_and_backward_with_fake_tensors():
