@@ -233,7 +233,7 @@ def main() -> None:
         "dsa_bwd_dkdv_kernel": (run_stage(_lib.DSA_STAGE_DKDV), bh * (6.0 * L * L + 2.0 * L * R)),
         "dsa_bwd_dq_kernel": (run_stage(_lib.DSA_STAGE_DQ), bh * (2.0 * L * L + 2.0 * L * R)),
         "fold (dsa_bwd_table_kernel + dsa_bwd_fold_kernel)": (run_stage(_lib.DSA_STAGE_FOLD), bh * 4.0 * L * R),
-        "prep (dsa_bwd_delta_kernel + dsa_bwd_gather_kernel)": (run_stage(_lib.DSA_STAGE_PREP), 0.0),
+        "prep (dsa_bwd_delta_kernel + dsa_bwd_gather_kernel + dsa_bwd_segments_kernel)": (run_stage(_lib.DSA_STAGE_PREP), 0.0),
     }
     per_kernel = {}
     n_k = args.steps if args.kernels_only else max(10, args.steps)

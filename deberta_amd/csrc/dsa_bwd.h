@@ -10,10 +10,11 @@
 // Masked keys and dead query rows have P = 0 and so dS = 0.
 //
 // Kernels, in launch order:
-//   prep   dsa_bwd_delta_kernel (lse and Delta per row) and dsa_bwd_gather_kernel (krgt,
+//   prep   dsa_bwd_delta_kernel (lse and Delta per row), dsa_bwd_gather_kernel (krgt,
 //          qrgt: the relative tables gathered per offset d = i - j and
 //          transposed, so a run of consecutive offsets of one head-dim
 //          column is contiguous — the A operand of the offset-band products)
+//          and dsa_bwd_segments_kernel (the offset range of each table row)
 //   dkdv   dsa_bwd_dkdv_kernel (dsa_bwd_dkdv.h): recomputes the scores and
 //          the softmax per (b, h, 128-key tile), writes dK, dV and dS
 //          (rows = queries; bf16 for bf16 inputs), the only (L x L) tensor
@@ -93,6 +94,32 @@ __global__ __launch_bounds__(256) void dsa_bwd_gather_kernel(BwdParams bp) {
                    : (const T*)p.kr + (int64_t)h * p.krs[0] + (int64_t)row * p.krs[1];
   T* dst = (T*)(q ? bp.qrgt : bp.krgt);
   dst[r] = src[d];
+}
+
+// seg[t][0][r], seg[t][1][r]: the offsets [begin, end) whose table row is r
+// (t = 0: c2p, whose row is non-decreasing in the offset; t = 1: p2c,
+// non-increasing).  One thread per (table, offset d), plus one past the
+// last offset: it starts the rows above the previous offset's row, up to
+// its own, and ends the rows from the previous offset's row up to (not
+// including) its own.
+__global__ __launch_bounds__(256) void dsa_bwd_segments_kernel(BwdParams bp) {
+  const FwdParams& p = bp.f;
+  const int R = 2 * p.A, n = p.Lq + p.Lk - 1, dmin = -(p.Lk - 1);
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= 2 * (int64_t)(n + 1)) return;
+  const int t = (int)(idx / (n + 1)), u = (int)(idx % (n + 1));
+  if (!(p.flags & (1 << t))) return;
+  // rows counted so that they are non-decreasing in d
+  auto rank = [&](int d) {
+    const int x = offset_row(p.rel, d, p.Lq, p.Lk, p.A, t == 1);
+    return t ? R - 1 - x : x;
+  };
+  const int cur = u < n ? rank(dmin + u) : R;
+  const int prev = u > 0 ? rank(dmin + u - 1) : -1;
+  int* beg = bp.seg + (2 * t) * R;
+  int* end = beg + R;
+  for (int q = prev + 1; q <= min(cur, R - 1); ++q) beg[t ? R - 1 - q : q] = dmin + u;
+  for (int q = max(prev, 0); q < min(cur, R); ++q) end[t ? R - 1 - q : q] = dmin + u;
 }
 
 }  // namespace dsa

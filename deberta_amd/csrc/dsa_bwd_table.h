@@ -5,7 +5,8 @@
 // are computed per offset d = i - j first,
 //   Gc[d] = sum_{b,i} dS(i, i-d) q_i,   Gp[d] = sum_{b,j} dS(j+d, j) k_j,
 // and then summed onto table rows (dsa_bwd_fold_kernel): c(d) and p(d) are
-// monotone in d, so the offsets of one row form a contiguous range.
+// monotone in d, so the offsets of one row form a contiguous range
+// (dsa_bwd_segments_kernel finds them).
 //
 // dsa_bwd_table_kernel: one workgroup = (128-offset block [d0, d0+128),
 // head h, batch group).  For each batch and each chunk of 32 queries
@@ -275,58 +276,44 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
 }
 
 // tab[h][r][:] (+)= s * sum over batch groups and offsets d with row(d) = r
-// of the partials (accumulated into fp32, or written in fp32 or bf16); one
-// thread per (table, h, r, 4 columns).
+// of the partials (accumulated into fp32, or written in fp32 or bf16).  One
+// wave per (table, h, r): 64 / (D/4) parts split the row's offset range
+// [begin, end) (from dsa_bwd_segments_kernel) and are summed with lane
+// shuffles; lanes of a part hold 4 columns each.
 template <int D>
-__global__ __launch_bounds__(256) void dsa_bwd_fold_kernel(BwdParams bp) {
+__global__ __launch_bounds__(64) void dsa_bwd_fold_kernel(BwdParams bp) {
   using namespace tbcfg;
   const FwdParams& p = bp.f;
   const int R = 2 * p.A;
-  constexpr int Q4 = D / 4;
-  const int64_t per = (int64_t)p.H * R * Q4;
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= 2 * per) return;
-  const bool q = idx >= per;  // false: dKr (c2p), true: dQr (p2c)
-  if (q ? !(p.flags & 2) : !(p.flags & 1)) return;
-  const int64_t rr = q ? idx - per : idx;
-  const int c4 = (int)(rr % Q4);
-  const int r = (int)((rr / Q4) % R);
-  const int h = (int)(rr / ((int64_t)Q4 * R));
-  // row(d) is non-decreasing in d for c2p and non-increasing for p2c: find
-  // the first d with row "at or past" r, then the first d past r.
-  auto past = [&](int d, bool strict) {
-    const int x = offset_row(p.rel, d, p.Lq, p.Lk, p.A, q);
-    return q ? (strict ? x < r : x <= r) : (strict ? x > r : x >= r);
-  };
-  const int dmin = -(p.Lk - 1), dmax = p.Lq - 1;
-  int lo = dmin, hi = dmax + 1;
-  while (lo < hi) {
-    const int mid = lo + ((hi - lo) >> 1);
-    if (past(mid, false)) hi = mid; else lo = mid + 1;
-  }
-  int lo2 = lo, hi2 = dmax + 1;
-  while (lo2 < hi2) {
-    const int mid = lo2 + ((hi2 - lo2) >> 1);
-    if (past(mid, true)) hi2 = mid; else lo2 = mid + 1;
-  }
+  constexpr int Q4 = D / 4, NP = 64 / Q4;
+  const int t = blockIdx.x / (p.H * R), h = (blockIdx.x / R) % p.H, r = blockIdx.x % R;
+  if (!(p.flags & (1 << t))) return;
+  const bool q = t == 1;  // false: dKr (c2p), true: dQr (p2c)
+  const int c4 = threadIdx.x % Q4, part = threadIdx.x / Q4;
+  const int beg = bp.seg[(2 * t) * R + r], end = bp.seg[(2 * t + 1) * R + r];
   f32x4 acc = zero4();
-  for (int d = lo; d < lo2; ++d) {
+  for (int d = beg + part; d < end; d += NP) {
     const int dblk = (d + bp.f.LkP) / DBW, dd = (d + bp.f.LkP) % DBW;
     const float* src = bp.gpart + ((int64_t)(h * bp.NDB + dblk) * bp.NBG) * 2 * DBW * D +
                        (int64_t)((q ? DBW : 0) + dd) * D + 4 * c4;
     for (int k = 0; k < bp.NBG; ++k) acc += *reinterpret_cast<const f32x4*>(src + (int64_t)k * 2 * DBW * D);
   }
+#pragma unroll
+  for (int m = Q4; m < 64; m <<= 1)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] += __shfl_xor(acc[e], m);
+  if (part != 0) return;
   const int64_t o = ((int64_t)h * R + r) * D + 4 * c4;
   void* tab = q ? bp.dqr : bp.dkr;
+  const f32x4 v = acc * p.scale;
   if (bp.dtab_bf16) {
     typedef bf16 b4 __attribute__((ext_vector_type(4)));
-    const f32x4 v = acc * p.scale;
     *reinterpret_cast<b4*>((bf16*)tab + o) = b4{(bf16)v[0], (bf16)v[1], (bf16)v[2], (bf16)v[3]};
   } else if (bp.dtab_overwrite) {
-    *reinterpret_cast<f32x4*>((float*)tab + o) = acc * p.scale;
+    *reinterpret_cast<f32x4*>((float*)tab + o) = v;
   } else {
-    f32x4* t = reinterpret_cast<f32x4*>((float*)tab + o);
-    *t = *t + acc * p.scale;
+    f32x4* tp = reinterpret_cast<f32x4*>((float*)tab + o);
+    *tp = *tp + v;
   }
 }
 

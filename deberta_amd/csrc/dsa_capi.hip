@@ -151,7 +151,7 @@ int device_cus() {
 // extents the kernels share.
 struct WsLayout {
   int LqP, LkP, TGP, OFF, NDB, NBG, BPG;
-  size_t rowinfo, krgt, qrgt, ds, gpart, total;
+  size_t rowinfo, krgt, qrgt, ds, gpart, seg, total;
 };
 
 WsLayout ws_layout(const dsa_bwd_args* a) {
@@ -180,6 +180,8 @@ WsLayout ws_layout(const dsa_bwd_args* a) {
   off = align_up(off + (size_t)f.B * f.H * w.LkP * w.LqP * es, 256);
   w.gpart = off;
   if (f.flags) off = align_up(off + (size_t)f.H * w.NDB * w.NBG * 2 * dsa::tbcfg::DBW * f.D * sizeof(float), 256);
+  w.seg = off;
+  if (f.flags) off = align_up(off + (size_t)2 * 2 * (2 * f.att_span) * sizeof(int), 256);
   w.total = off;
   return w;
 }
@@ -209,6 +211,7 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
   bp.qrgt = base + ws.qrgt;
   bp.ds = base + ws.ds;
   bp.gpart = reinterpret_cast<float*>(base + ws.gpart);
+  bp.seg = reinterpret_cast<int*>(base + ws.seg);
   bp.TGP = ws.TGP;
   bp.OFF = ws.OFF;
   bp.NDB = ws.NDB;
@@ -225,6 +228,9 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
       const int64_t m = 2 * (int64_t)f.H * D * ws.TGP;
       hipLaunchKernelGGL((dsa::dsa_bwd_gather_kernel<T, D>), dim3((unsigned)((m + 255) / 256)), dim3(256), 0, st, bp);
       if (launch_check("dsa_bwd_gather_kernel")) return 1;
+      const int64_t ns = 2 * (int64_t)(f.Lq + f.Lk);
+      hipLaunchKernelGGL((dsa::dsa_bwd_segments_kernel), dim3((unsigned)((ns + 255) / 256)), dim3(256), 0, st, bp);
+      if (launch_check("dsa_bwd_segments_kernel")) return 1;
     }
   }
   if (stages & DSA_STAGE_DKDV) {
@@ -249,8 +255,7 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
   if ((stages & DSA_STAGE_FOLD) && f.flags) {
     hipLaunchKernelGGL((dsa::dsa_bwd_table_kernel<T, D>), dim3(ws.NDB * f.H * ws.NBG), dim3(256), 0, st, bp);
     if (launch_check("dsa_bwd_table_kernel")) return 1;
-    const int64_t n = 2 * (int64_t)f.H * (2 * f.att_span) * (D / 4);
-    hipLaunchKernelGGL((dsa::dsa_bwd_fold_kernel<D>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, bp);
+    hipLaunchKernelGGL((dsa::dsa_bwd_fold_kernel<D>), dim3((unsigned)(2 * f.H * (2 * f.att_span))), dim3(64), 0, st, bp);
     if (launch_check("dsa_bwd_fold_kernel")) return 1;
   }
   return 0;

@@ -48,6 +48,7 @@ struct BwdParams {
   void* krgt;       // [H, D, TGP]: krgt[h][d][t] = Kr[h][c(t - OFF)][d]
   void* qrgt;       // [H, D, TGP]: qrgt[h][d][t] = Qr[h][p(t - OFF)][d]
   float* gpart;     // table-gradient partials [H][NDB][NBG][2][128][D]
+  int* seg;         // [2][2][R]: offsets [begin, end) of each table row (c2p, p2c)
   int TGP, OFF;     // row length and offset origin of krgt / qrgt
   int NDB, NBG, BPG;  // offset blocks, batch groups, batches per group
 };
