@@ -137,9 +137,12 @@ constexpr int NW = 4;           // waves per workgroup
 constexpr int BQ = NW * WQ;     // queries per workgroup
 constexpr int XW = WQ + BK;     // c2p band rows per wave (95 used)
 constexpr int XG = BQ + BK;     // p2c band rows per workgroup (191 used)
-constexpr int CBS = WQ + 1;     // c2p band row stride
+// c2p band, stored per query (row i, offsets x contiguous) so that a lane's
+// four MFMA results are one write; the stride puts 16 rows' 8-byte chunks
+// in distinct banks
+constexpr int CTS = 104;
 constexpr int PBS = XG + 5;     // p2c band row stride (4*PBS - 4 = 16 mod 64: 4 lane groups, distinct banks)
-constexpr int CB_ELEMS = XW * CBS;
+constexpr int CB_ELEMS = WQ * CTS;
 constexpr int PB_ELEMS = BK * PBS;
 }  // namespace dcfg
 
@@ -193,7 +196,7 @@ DSA_DEV void store4_contig(B* p, const f32x4& v) {
 // c16 of the tile).  y holds q.k on entry and q.k + c2p + p2c (unscaled)
 // on return.
 //   kf: A fragments of the 64 key rows, qf: B fragments of the wave's queries
-//   cb: this wave's c2p band (XW * CBS), pb: the shared p2c band (BK * PBS)
+//   cb: this wave's c2p band (WQ * CTS), pb: the shared p2c band (BK * PBS)
 //   bias: if not null, where this lane's part of the tile's saved relative
 //         term goes (see bias_tile_offset): the unscaled c2p + p2c values,
 //         stored for the backward
@@ -222,7 +225,7 @@ DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&
         f32x4 acc = zero4();
 #pragma unroll
         for (int s = 0; s < NS; ++s) acc = M::mma(af[s], qf[ib][s], acc);
-        store_band4<BT>(cb + (16 * rb + 4 * g) * CBS + 16 * ib + c16, CBS, acc);
+        store4_contig<BT>(cb + (16 * ib + c16) * CTS + 16 * rb + 4 * g, acc);
       }
     }
   }
@@ -244,8 +247,9 @@ DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&
     }
   }
   __syncthreads();
-  // c2p: x - 32w = (16*ib + c16) - (16*jb + 4*g + e) + 63
-  const BT* cbase = cb + (c16 - 4 * g + 63) * CBS + c16;
+  // c2p: x - 32w = (16*ib + c16) - (16*jb + 4*g + e) + 63; the four e are
+  // consecutive x (descending) of one query row
+  const BT* cbase = cb + c16 * CTS + c16 - 4 * g + 60;
   // p2c: row j = 16*jb + 4*g + e, column x = 32w + (16*ib + c16) - (16*jb + 4*g + e) + 63
   const BT* pbase = pb + 4 * g * PBS + WQ * w + c16 - 4 * g + 63;
   // The two terms are summed in the band type (for fp16: one rounding of the
@@ -257,18 +261,20 @@ DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&
     for (int ib = 0; ib < 2; ++ib)
 #pragma unroll
       for (int jb = 0; jb < 4; ++jb) {
+        typedef BT b4 __attribute__((ext_vector_type(4)));
+        b4 cv;
+        if constexpr (decltype(with_c)::value) lds_read_elems<BT, 4>(cv, cbase + 16 * ib * CTS + 16 * (ib - jb));
         BT bs[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           BT v = (BT)0.0f;
-          if constexpr (decltype(with_c)::value) v = cbase[(16 * ib - 16 * jb - e) * CBS + 16 * ib];
+          if constexpr (decltype(with_c)::value) v = cv[3 - e];
           if constexpr (decltype(with_p)::value) v = v + pbase[(16 * jb + e) * PBS + 16 * ib - 16 * jb - e];
           bs[e] = v;
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) y[ib][jb][e] = __builtin_fmaf((float)bs[e], 1.0f, y[ib][jb][e]);
         if (bias) {
-          typedef BT b4 __attribute__((ext_vector_type(4)));
           *reinterpret_cast<b4*>(bias + (ib * 4 + jb) * 256) = b4{bs[0], bs[1], bs[2], bs[3]};
         }
       }
