@@ -19,6 +19,30 @@ namespace {
 
 thread_local std::string g_err;
 
+// A side stream (default priority) and two events per device and host
+// thread, for running the DQ stage beside the FOLD stage: both only read
+// the workspace after DKDV.  Created on first use, kept for the thread's
+// lifetime.
+struct SideStream {
+  int device = -1;
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+thread_local SideStream g_side[16];
+
+SideStream* side_stream() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return nullptr;
+  SideStream& s = g_side[dev];
+  if (s.device != dev) {
+    if (hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking) != hipSuccess) return nullptr;
+    if (hipEventCreateWithFlags(&s.fork, hipEventDisableTiming) != hipSuccess) return nullptr;
+    if (hipEventCreateWithFlags(&s.join, hipEventDisableTiming) != hipSuccess) return nullptr;
+    s.device = dev;
+  }
+  return &s;
+}
+
 int fail(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
 int fail(const char* fmt, ...) {
   char buf[512];
@@ -247,17 +271,30 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
     }
     if (launch_check("dsa_bwd_dkdv_kernel")) return 1;
   }
-  if (stages & DSA_STAGE_DQ) {
-    dim3 grid((unsigned)(ws.LqP / dsa::dqcfg::BQ * f.H * f.B));
-    hipLaunchKernelGGL((dsa::dsa_bwd_dq_kernel<T, D>), grid, dim3(256), 0, st, bp);
-    if (launch_check("dsa_bwd_dq_kernel")) return 1;
-  }
-  if ((stages & DSA_STAGE_FOLD) && f.flags) {
+  // DQ and FOLD both only read dS: with both requested, DQ runs on a side
+  // stream (forked from and joined back into the caller's stream) so that
+  // the two kernels share the GPU; the table kernel, whose workgroups are
+  // longer, is launched first.
+  const bool fold = (stages & DSA_STAGE_FOLD) && f.flags;
+  SideStream* side = ((stages & DSA_STAGE_DQ) && fold) ? side_stream() : nullptr;
+  if (side && (hipEventRecord(side->fork, st) != hipSuccess || hipStreamWaitEvent(side->stream, side->fork, 0) != hipSuccess))
+    return fail("dsa: side stream fork failed");
+  if (fold) {
     hipLaunchKernelGGL((dsa::dsa_bwd_table_kernel<T, D>), dim3(ws.NDB * f.H * ws.NBG), dim3(256), 0, st, bp);
     if (launch_check("dsa_bwd_table_kernel")) return 1;
+  }
+  if (stages & DSA_STAGE_DQ) {
+    hipStream_t sq = side ? side->stream : st;
+    dim3 grid((unsigned)(ws.LqP / dsa::dqcfg::BQ * f.H * f.B));
+    hipLaunchKernelGGL((dsa::dsa_bwd_dq_kernel<T, D>), grid, dim3(256), 0, sq, bp);
+    if (launch_check("dsa_bwd_dq_kernel")) return 1;
+    if (side && hipEventRecord(side->join, sq) != hipSuccess) return fail("dsa: side stream join failed");
+  }
+  if (fold) {
     hipLaunchKernelGGL((dsa::dsa_bwd_fold_kernel<D>), dim3((unsigned)(2 * f.H * (2 * f.att_span))), dim3(64), 0, st, bp);
     if (launch_check("dsa_bwd_fold_kernel")) return 1;
   }
+  if (side && hipStreamWaitEvent(st, side->join, 0) != hipSuccess) return fail("dsa: side stream join failed");
   return 0;
 }
 
