@@ -30,9 +30,14 @@ struct SideStream {
 };
 thread_local SideStream g_side[16];
 
-SideStream* side_stream() {
+SideStream* side_stream(hipStream_t st) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return nullptr;
+  // Under graph capture the stages run in order on the caller's stream: a
+  // fork/join across streams inside a capture ended in a host crash in the
+  // runtime's capture end.
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
   SideStream& s = g_side[dev];
   if (s.device != dev) {
     if (hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking) != hipSuccess) return nullptr;
@@ -276,7 +281,7 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
   // the two kernels share the GPU; the table kernel, whose workgroups are
   // longer, is launched first.
   const bool fold = (stages & DSA_STAGE_FOLD) && f.flags;
-  SideStream* side = ((stages & DSA_STAGE_DQ) && fold) ? side_stream() : nullptr;
+  SideStream* side = ((stages & DSA_STAGE_DQ) && fold) ? side_stream(st) : nullptr;
   if (side && (hipEventRecord(side->fork, st) != hipSuccess || hipStreamWaitEvent(side->stream, side->fork, 0) != hipSuccess))
     return fail("dsa: side stream fork failed");
   if (fold) {
