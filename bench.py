@@ -44,13 +44,14 @@ R = 2 * A
 # (x1.0).  Commands and raw figures: profiles/hbm_traffic_headline.md.
 FETCH_SCALE, WRITE_SCALE = 2.0, 1.0
 TRAFFIC_KIB = {  # kernel: (FETCH_SIZE, WRITE_SIZE) as read
-    "dsa_fwd_kernel": (52303, 221952),
-    "dsa_bwd_dkdv_kernel": (178774, 284099),
-    "dsa_bwd_dq_kernel": (126758, 24576),
-    "dsa_bwd_table_kernel": (179810, 36864),
-    "dsa_bwd_fold_kernel": (19995, 3072),
-    "dsa_bwd_delta_kernel": (24997, 1536),
-    "dsa_bwd_gather_kernel": (1571, 3072),
+    "dsa_fwd_kernel": (52587, 221952),
+    "dsa_bwd_dkdv_kernel": (180717, 245885),
+    "dsa_bwd_dq_kernel": (127076, 24576),
+    "dsa_bwd_table_kernel": (178500, 36864),
+    "dsa_bwd_fold_kernel": (19420, 2458),
+    "dsa_bwd_delta_kernel": (24993, 1536),
+    "dsa_bwd_gather_kernel": (6184, 3072),
+    "dsa_bwd_segments_kernel": (26, 8),
 }
 
 

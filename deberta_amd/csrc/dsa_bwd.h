@@ -74,26 +74,34 @@ DSA_DEV int offset_row(const int32_t* rel, int d, int Lq, int Lk, int A, bool p2
 
 // krgt[h][d][t] = Kr[h][c(t' - OFF)][d] with t' = t ^ (VEC - 1) (each
 // aligned group of VEC = 16 / sizeof(T) offsets reversed: the dq kernel's
-// operand order), qrgt[h][d][t] = Qr[h][p(t - OFF)][d], for t in [0, TGP);
-// one thread per (table, h, d, t), t fastest.
+// operand order), qrgt[h][d][t] = Qr[h][p(t - OFF)][d], for t in [0, TGP).
+// One thread per (table, h, d, group of VEC consecutive t): VEC gathered
+// elements, one 16-byte store.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void dsa_bwd_gather_kernel(BwdParams bp) {
+  constexpr int VEC = 16 / sizeof(T);
+  typedef T vecT __attribute__((ext_vector_type(VEC)));
   const FwdParams& p = bp.f;
-  const int64_t per = (int64_t)p.H * D * bp.TGP;
+  const int NG = bp.TGP / VEC;
+  const int64_t per = (int64_t)p.H * D * NG;
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= 2 * per) return;
   const bool q = idx >= per;
   if (q ? !(p.flags & 2) : !(p.flags & 1)) return;
   const int64_t r = q ? idx - per : idx;
-  const int t = (int)(r % bp.TGP);
-  const int d = (int)((r / bp.TGP) % D);
-  const int h = (int)(r / ((int64_t)bp.TGP * D));
-  constexpr int VEC = 16 / sizeof(T);
-  const int row = offset_row(p.rel, (q ? t : (t ^ (VEC - 1))) - bp.OFF, p.Lq, p.Lk, p.A, q);
-  const T* src = q ? (const T*)p.qr + (int64_t)h * p.qrs[0] + (int64_t)row * p.qrs[1]
-                   : (const T*)p.kr + (int64_t)h * p.krs[0] + (int64_t)row * p.krs[1];
-  T* dst = (T*)(q ? bp.qrgt : bp.krgt);
-  dst[r] = src[d];
+  const int t0 = (int)(r % NG) * VEC;
+  const int d = (int)((r / NG) % D);
+  const int h = (int)(r / ((int64_t)NG * D));
+  const T* src = q ? (const T*)p.qr + (int64_t)h * p.qrs[0] : (const T*)p.kr + (int64_t)h * p.krs[0];
+  const int64_t rs = q ? p.qrs[1] : p.krs[1];
+  vecT v;
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) {
+    const int t = t0 + (q ? e : (VEC - 1 - e));
+    v[e] = src[(int64_t)offset_row(p.rel, t - bp.OFF, p.Lq, p.Lk, p.A, q) * rs + d];
+  }
+  T* dst = (T*)(q ? bp.qrgt : bp.krgt) + ((int64_t)h * D + d) * bp.TGP + t0;
+  *reinterpret_cast<vecT*>(dst) = v;
 }
 
 // seg[t][0][r], seg[t][1][r]: the offsets [begin, end) whose table row is r

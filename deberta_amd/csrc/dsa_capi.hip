@@ -254,7 +254,7 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
     hipLaunchKernelGGL((dsa::dsa_bwd_delta_kernel<T, D>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, bp);
     if (launch_check("dsa_bwd_delta_kernel")) return 1;
     if (f.flags) {
-      const int64_t m = 2 * (int64_t)f.H * D * ws.TGP;
+      const int64_t m = 2 * (int64_t)f.H * D * (ws.TGP / (16 / (int)sizeof(T)));
       hipLaunchKernelGGL((dsa::dsa_bwd_gather_kernel<T, D>), dim3((unsigned)((m + 255) / 256)), dim3(256), 0, st, bp);
       if (launch_check("dsa_bwd_gather_kernel")) return 1;
       const int64_t ns = 2 * (int64_t)(f.Lq + f.Lk);
