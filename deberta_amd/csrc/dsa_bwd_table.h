@@ -9,20 +9,27 @@
 // (dsa_bwd_segments_kernel finds them).
 //
 // dsa_bwd_table_kernel: one workgroup = (128-offset block [d0, d0+128),
-// head h, batch group).  For each batch and each chunk of 32 queries
-// [i0, i0+32) it stages the region of dS (rows = queries) with rows i0..,
-// keys j in [jb, jb + 160), jb = i0 - d0 - 128 — which holds every pair of
-// the chunk with an offset in the block — with the 32 query rows and a ring
-// of key rows.  Element (r, c) of the staged region X has offset
-// d = d0 + 127 - (c - r - 1); with e = c - r - 1 (so d = d0 + 127 - e):
-//   Gc^T[e] += sum_r  Q^T[i0 + r] X[r][r + 1 + e]
-//   Gp^T[e] += sum_c  K^T[jb + c] X[c - 1 - e][c]
-// Both B operands walk a diagonal of X (eight single-element LDS reads per
-// fragment); zero rows around X cover the out-of-chunk part of the walk.
-// A wave's two offset blocks share their A operands (the p2c one over 64
-// staged columns, with diagonal elements outside the chunk read as zeros).
-// Wave w accumulates e in [32w, 32w + 32) in registers and writes them once,
-// to a per-(block, head, batch group) partial.
+// head h, batch group).  Waves 0 and 1 compute Gc, waves 2 and 3 Gp, each
+// wave on its own items, staged into its own part of LDS (no workgroup
+// barrier until the end).  An item is one batch and 32 rows:
+//   Gc item: queries [i0, i0+32); region X[r][c] = dS(i0 + r, i0 - d0 - 128 + c)
+//            (32 x 168); the pair (r, r + e + 1) has offset d0 + 127 - e, so
+//            Gc^T[:, e] += sum_r Q^T[:, i0 + r] X[r][r + e + 1]
+//   Gp item: keys [j0, j0+32); region X[rho][c] = dS(j0 + d0 + rho, j0 + c)
+//            (160 x 32); the pair (c + e, c) has offset d0 + e, so
+//            Gp^T[:, e] += sum_c K^T[:, j0 + c] X[c + e][c]
+// Every pair of a batch with an offset in the block lies in exactly one item
+// of each kind.  The B operands walk diagonals of X (one 16-bit LDS read per
+// element, at compile-time offsets from a per-lane base); the k index of the
+// products (the 32 rows of an item) is assigned to lane groups interleaved
+// (group g holds rows 2g, 2g+1, 2g+8, 2g+9, ...), which spreads the four
+// groups' diagonal reads over distinct LDS banks.  A wave keeps all 128
+// offsets x D in registers (fp32) and prefetches its next item's global
+// data into registers while it computes.  The two waves of a kind sum their
+// accumulators through LDS and write one fp32 partial per (block, head,
+// batch group, kind).  The Gc and Gp waves of a workgroup sweep the same
+// batch's band of dS together, so the second reader of each dS line
+// finds it in L2.
 #pragma once
 
 #include "dsa_bwd.h"
@@ -31,60 +38,61 @@ namespace dsa {
 
 namespace tbcfg {
 constexpr int NW = 4;
-constexpr int DBW = 128;           // offsets per block
-constexpr int JC = 32;             // queries per step
-constexpr int XC = DBW + JC;       // staged columns
-constexpr int XP = 32;             // zero rows above the staged rows
-constexpr int XROWS = XP + JC + 32;  // and 32 below
-constexpr int XCOLS = DBW + 48;    // columns a diagonal walk can touch
-constexpr int QRING = 256;         // ring rows kept (power of two >= XC)
+constexpr int DBW = 128;          // offsets per block
+constexpr int CH = 32;            // rows of an item (Gc: queries, Gp: keys)
+constexpr int XS_C = DBW + 40;    // Gc region row stride (elements; 160 columns used)
+constexpr int PR = DBW + CH;      // Gp region rows (160; 159 used)
+constexpr int XS_P = 40;          // Gp region row stride (elements; 32 columns used)
 }  // namespace tbcfg
 
-// Transposed LDS operand read (see tr_contig) from a ring of rows: logical
-// row k lives at physical row (kbase + k) % QRING.
+// k index (row of an item) of element u of a B fragment of lane group g in
+// k-step s, as the sum of a per-lane part (tab_kg) and a compile-time part
+// (tab_ku).  bf16: groups interleaved in pairs (rows 2g + {0,1} + 8m); fp32:
+// the contiguous k-set (rows 4g + u).
 template <typename T>
-DSA_DEV typename Mfma<T>::frag tr_contig_ring(const T* X, int str, int kbase, int k0, int m0, int g, int c16) {
-  using namespace tbcfg;
+DSA_DEV int tab_kg(int g) {
+  return sizeof(T) == 2 ? 2 * g : 4 * g;
+}
+template <typename T>
+constexpr int tab_ku(int s, int u) {
+  return sizeof(T) == 2 ? 32 * s + (u & 1) + 8 * (u >> 1) : 16 * s + u;
+}
+
+// A operand (rows of an item, transposed): lane (c16, g) gets
+// R[k(s, g, u)][col0 + c16] for its k-set, R row-major with stride str.
+template <typename T>
+DSA_DEV typename Mfma<T>::frag tab_afrag(const T* R, int str, int s, int col0, int g, int c16) {
   if constexpr (sizeof(T) == 2) {
-    const int r0 = (kbase + k0 + 8 * g) & (QRING - 1);      // 4-aligned, so
-    const int r1 = (kbase + k0 + 8 * g + 4) & (QRING - 1);  // rows never wrap
-    return join8(tr4(X, str, r0, m0, c16), tr4(X, str, r1, m0, c16));
+    // ds_read_b64_tr_b16: lane 4e + q addresses the 4-column chunk q of the
+    // row that lane group g needs as its e-th k value
+    const int e = c16 >> 2, q = c16 & 3;
+    const int row = 32 * s + 2 * g + (e & 1) + 8 * (e >> 1);
+    const T* p = R + row * str + col0 + 4 * q;
+    return join8(tr4_at(p), tr4_at(p + 16 * str));
   } else {
-    return tr4(X, str, (kbase + k0 + 4 * g) & (QRING - 1), m0, c16);
+    const int row = 16 * s + 4 * g;
+    const T* p = R + row * str + col0 + c16;
+    return f32x4{p[0], p[str], p[2 * str], p[3 * str]};
   }
 }
 
-// Rows [r0, r0 + n) of a [L, D] strided matrix into ring rows (zeros for rows
-// outside [0, nvalid)).
-template <typename T, int D>
-DSA_DEV void load_ring_rows(T* ring, int str, const T* src, int64_t rs, int r0, int n, int nvalid, int tid) {
-  using namespace tbcfg;
-  constexpr int VEC = 16 / sizeof(T);
-  constexpr int CPR = D / VEC;
-  typedef T vecT __attribute__((ext_vector_type(VEC)));
-  for (int c = tid; c < n * CPR; c += 256) {
-    const int r = r0 + c / CPR, d0 = (c % CPR) * VEC;
-    vecT x;
-    if (r >= 0 && r < nvalid) {
-      x = *reinterpret_cast<const vecT*>(src + (int64_t)r * rs + d0);
-    } else {
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) x[e] = (T)0.0f;
-    }
-    *reinterpret_cast<vecT*>(ring + (r & (QRING - 1)) * str + d0) = x;
-  }
-}
-
-// Number of 32-query chunks of offset block dblk that hold pairs with an
-// offset in the block, and the first of them: rows i >= d0 (a key j = i - d
-// >= 0 exists) and i0 - d0 - 127 <= Lk - 1 (a key j < Lk exists).
-DSA_DEV void block_chunks(int dblk, int LkP, int Lq, int Lk, int* istart, int* nch) {
+// Number of 32-row items of each kind in offset block dblk and the first
+// item row: Gc items start at query rows i >= max(d0, 0) and end where no key
+// j = i - d < Lk is left; Gp items start at the first key with a query
+// j + d >= 0 and end where no query j + d < Lq is left.
+DSA_DEV void block_items(int dblk, int LkP, int Lq, int Lk, bool p2c, int* start, int* n) {
   using namespace tbcfg;
   const int d0 = -LkP + DBW * dblk;  // a multiple of 128
-  const int is = d0 > 0 ? d0 : 0;
-  const int ie = min(Lq, Lk + d0 + DBW - 1);
-  *istart = is;
-  *nch = ie > is ? (ie - is + JC - 1) / JC : 0;
+  int s, e;
+  if (!p2c) {
+    s = d0 > 0 ? d0 : 0;
+    e = min(Lq, Lk + d0 + DBW - 1);
+  } else {
+    s = max(0, -(d0 + DBW - 1)) / CH * CH;
+    e = min(Lk, Lq - d0);
+  }
+  *start = s;
+  *n = e > s ? (e - s + CH - 1) / CH : 0;
 }
 
 template <typename T, int D>
@@ -95,182 +103,213 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
   constexpr int VEC = 16 / sizeof(T);
   typedef T vecT __attribute__((ext_vector_type(VEC)));
   constexpr int ND = D / 16;
+  constexpr int NEB = DBW / 16;         // 16-offset blocks
   constexpr int FE = M::FRAG_ELEMS;
-  constexpr int KSTR = D + Pad<T>::v;
-  // Row stride of X chosen for few LDS bank conflicts in its diagonal walks
-  // (178: two-way at most; rows are then only 4-byte aligned).
-  constexpr int XSTR = sizeof(T) == 2 ? 178 : XCOLS + Pad<T>::v;
-  constexpr int RSTR = KSTR;
-  constexpr int GP_STEPS = 64 / M::KSTEP;  // k steps over the 64 staged columns a wave's two blocks read
-  constexpr int GC_STEPS = JC / M::KSTEP;
-  constexpr int XV = JC * XC / VEC;   // 16-byte chunks of the staged region
-  constexpr int RV = JC * D / VEC;    // 16-byte chunks of 32 query (or key) rows
-  constexpr int XCH = (XV + 255) / 256, RCH = (RV + 255) / 256;
+  constexpr int NS = CH / M::KSTEP;     // k steps per item
+  constexpr int KSTR = D + Pad<T>::v;   // item rows (Q or K) stride
+  constexpr int DCH = D / VEC;          // 16-byte chunks per item row
+  constexpr int XELEMS = (CH * XS_C > PR * XS_P) ? CH * XS_C : PR * XS_P;
+  constexpr int WELEMS = XELEMS + CH * KSTR;  // per wave
+  constexpr bool PREFETCH = sizeof(T) == 2;
+  static_assert((XS_C * sizeof(T)) % 16 == 0 && (XS_P * sizeof(T)) % 16 == 0, "16-byte rows");
+  static_assert(NW * WELEMS * sizeof(T) >= 2 * NEB * ND * 64 * 16, "LDS holds two waves' accumulators");
   const FwdParams& p = bp.f;
 
-  __shared__ __align__(16) T Xs[XROWS * XSTR];
-  __shared__ __align__(16) T Qc[JC * KSTR];          // the chunk's query rows
-  __shared__ __align__(16) T Kring[QRING * RSTR];    // key rows of the staged columns
+  __shared__ __align__(16) T lds[NW * WELEMS];
 
   const int tid = threadIdx.x;
-  const int w = tid >> 6, g = (tid & 63) >> 4, c16 = tid & 15;
+  // the wave index, known to the compiler as uniform (the item loop's
+  // buffer resources are then scalar)
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 4, c16 = lane & 15;
+  const bool p2c = w >= 2;  // wave kind: 0, 1 -> Gc; 2, 3 -> Gp
+  const int sub = w & 1;
   // Work order: blockIdx.x enumerates (offset block, head, batch group) with
-  // the offset blocks that have the most chunks first, so the shortest
-  // workgroups fill in at the end of the launch.  (Grouping a (head, batch
-  // group)'s offset blocks on one XCD instead measured slower: the long
-  // blocks then finish last.)
+  // the offset blocks that have the most items first, so the shortest
+  // workgroups fill in at the end of the launch.
   const int per_blk = p.H * bp.NBG;
   const int rank = blockIdx.x / per_blk, rem = blockIdx.x % per_blk;
   const int h = rem / bp.NBG, bg = rem % bp.NBG;
-  const int mid = (bp.NDB - 1) / 2;   // central blocks hold the most pairs
+  const int mid = (bp.NDB - 1) / 2;  // central blocks hold the most pairs
   const int dblk = (rank & 1) ? mid + 1 + (rank >> 1) : mid - (rank >> 1);
-  const int d0 = -bp.f.LkP + DBW * dblk;
-  const bool c2p = (p.flags & 1) != 0, p2c = (p.flags & 2) != 0;
+  const int d0 = -p.LkP + DBW * dblk;
+  const bool active = (p.flags & (p2c ? 2 : 1)) != 0;
   const int b_lo = bg * bp.BPG, b_hi = min(p.B, b_lo + bp.BPG);
-  int istart, nch;
-  block_chunks(dblk, bp.f.LkP, p.Lq, p.Lk, &istart, &nch);
-  const int nsteps = (b_hi > b_lo) ? (b_hi - b_lo) * nch : 0;
+  int rstart, nch;
+  block_items(dblk, p.LkP, p.Lq, p.Lk, p2c, &rstart, &nch);
+  const int nitems = (active && b_hi > b_lo) ? (b_hi - b_lo) * nch : 0;
 
-  // zero rows around the staged region (never overwritten), and a finite ring
-  {
-    vecT z;
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) z[e] = (T)0.0f;
-    static_assert(XROWS * XSTR % VEC == 0 && QRING * RSTR % VEC == 0, "whole 16-byte chunks");
-    for (int c = tid; c < XROWS * XSTR / VEC; c += 256) reinterpret_cast<vecT*>(Xs)[c] = z;
-    for (int c = tid; c < QRING * RSTR / VEC; c += 256) reinterpret_cast<vecT*>(Kring)[c] = z;
-  }
+  T* X = lds + w * WELEMS;  // this wave's region
+  T* Rw = X + XELEMS;       // and its item rows (Q for Gc, K for Gp)
 
-  f32x4 gc[2][ND], gp[2][ND];
+  f32x4 acc[NEB][ND];
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+  for (int eb = 0; eb < NEB; ++eb)
 #pragma unroll
-    for (int db = 0; db < ND; ++db) gc[t][db] = gp[t][db] = zero4();
+    for (int db = 0; db < ND; ++db) acc[eb][db] = zero4();
 
-  // Registers holding the next step's global data.
-  vecT xr[XCH], qr[RCH], kr[RCH];
-  auto step_coords = [&](int st, int& b, int& i0) {
-    b = b_lo + st / nch;
-    i0 = istart + (st % nch) * JC;
-  };
-  auto fetch = [&](int st) {
-    int b, i0;
-    step_coords(st, b, i0);
-    const int jb = i0 - d0 - DBW;  // key of staged column 0 (a multiple of 32)
-    const T* dsb = (const T*)bp.ds + (int64_t)(b * p.H + h) * bp.f.LqP * bp.f.LkP;
-#pragma unroll
-    for (int k = 0; k < XCH; ++k) {
-      const int c = tid + 256 * k;
-      const int r = c / (XC / VEC), c0 = (c % (XC / VEC)) * VEC;
-      const int j = jb + c0;  // 16-byte chunks are wholly in or out of [0, LkP)
-      if (c < XV && j >= 0 && j < bp.f.LkP) {
-        xr[k] = *reinterpret_cast<const vecT*>(dsb + (int64_t)(i0 + r) * bp.f.LkP + j);
+  // The item loop of one kind (P: Gp).
+  //
+  // Staging of an item, in 16-byte chunks: the region, then the item rows
+  // (Q for Gc, K for Gp).  Each is a block of rows x CPR chunks walked in
+  // passes of 64 / CPR rows, one chunk per lane, so a lane's byte offset
+  // moves by a uniform stride from pass to pass.  The loads are buffer
+  // loads whose range check returns zeros: for chunks outside the (b, h)
+  // slice of dS (rows before 0 or past LqP: negative offsets are huge as
+  // unsigned), for Gc chunks whose columns lie outside [0, LkP) (their
+  // offset is pushed past the range), and for item rows past Lq / Lk.
+  auto run = [&](auto kind) {
+    constexpr bool P = decltype(kind)::value;
+    constexpr int CPR = P ? CH / VEC : (DBW + CH) / VEC;  // Gc region: 160 columns read per row
+    constexpr int RPI = 64 / CPR;
+    constexpr int NXR = P ? PR : CH;                      // region rows
+    constexpr int NP_X = (NXR + RPI - 1) / RPI;
+    constexpr int RPI_R = 64 / DCH, NP_R = (CH + RPI_R - 1) / RPI_R;
+    constexpr int NSLOT = NP_X + NP_R;
+    constexpr int XS = P ? XS_P : XS_C;
+    constexpr unsigned OOB = 0x80000000u;  // at least every range below
+    const int lr = lane / CPR, lc = lane % CPR;  // region: row in pass, chunk
+    const int rr = lane / DCH, rc = lane % DCH;  // item rows: row in pass, chunk
+    const int64_t qks = P ? p.ks[1] : p.qs[1];
+    const T* qkh = P ? (const T*)p.k + (int64_t)h * p.ks[2] : (const T*)p.q + (int64_t)h * p.qs[2];
+    const int64_t qkbs = P ? p.ks[0] : p.qs[0];
+    const int Lrow = P ? p.Lk : p.Lq;
+    const unsigned xstride = (unsigned)(RPI * p.LkP * (int)sizeof(T));  // bytes per pass
+    const unsigned rstride = (unsigned)(RPI_R * qks * (int64_t)sizeof(T));
+    auto bload = [&](__amdgpu_buffer_rsrc_t rs, unsigned off) {
+      return __builtin_bit_cast(vecT, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, 0));
+    };
+    // buffer resources and pass-0 byte offsets of item it
+    struct ItemSrc {
+      __amdgpu_buffer_rsrc_t xs, rs;
+      unsigned xoff, roff;
+    };
+    auto item_src = [&](int it) {
+      const int b = b_lo + it / nch, r0 = rstart + (it % nch) * CH;
+      ItemSrc o;
+      const T* dsb = (const T*)bp.ds + (int64_t)(b * p.H + h) * p.LqP * p.LkP;
+      o.xs = __builtin_amdgcn_make_buffer_rsrc((void*)dsb, 0, p.LqP * p.LkP * (int)sizeof(T), 0x00020000);
+      if constexpr (!P) {
+        const int j = r0 - d0 - DBW + lc * VEC;  // a multiple of VEC: chunks lie wholly in or out
+        const bool ok = lr < RPI && j >= 0 && j < p.LkP;
+        o.xoff = ok ? (unsigned)(((r0 + lr) * p.LkP + j) * (int)sizeof(T)) : OOB;
       } else {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) xr[k][e] = (T)0.0f;
+        o.xoff = (unsigned)(((r0 + d0 + lr) * p.LkP + r0 + lc * VEC) * (int)sizeof(T));
       }
+      const T* rb = qkh + (int64_t)b * qkbs;
+      o.rs = __builtin_amdgcn_make_buffer_rsrc((void*)rb, 0, (int)(((int64_t)(Lrow - 1) * qks + D) * sizeof(T)),
+                                               0x00020000);
+      o.roff = (unsigned)(((int64_t)(r0 + rr) * qks + rc * VEC) * sizeof(T));
+      return o;
+    };
+    T* const xd = X + lr * XS + lc * VEC;       // LDS destinations: pass t adds t * RPI rows
+    T* const rd = Rw + rr * KSTR + rc * VEC;
+    auto xok = [&](int t) { return lr < RPI && lr + RPI * t < NXR; };
+    auto rok = [&](int t) { return rr + RPI_R * t < CH; };
+
+    vecT pre[PREFETCH ? NSLOT : 1];
+    auto fetch = [&](int it) {
+      const ItemSrc o = item_src(it);
+#pragma unroll
+      for (int t = 0; t < NP_X; ++t) pre[t] = bload(o.xs, o.xoff + t * xstride);
+#pragma unroll
+      for (int t = 0; t < NP_R; ++t) pre[NP_X + t] = bload(o.rs, o.roff + t * rstride);
+    };
+    auto commit = [&]() {
+#pragma unroll
+      for (int t = 0; t < NP_X; ++t)
+        if (xok(t)) *reinterpret_cast<vecT*>(xd + t * RPI * XS) = pre[t];
+#pragma unroll
+      for (int t = 0; t < NP_R; ++t)
+        if (rok(t)) *reinterpret_cast<vecT*>(rd + t * RPI_R * KSTR) = pre[NP_X + t];
+    };
+    auto stage_direct = [&](int it) {
+      const ItemSrc o = item_src(it);
+      for (int t = 0; t < NP_X; ++t)
+        if (xok(t)) *reinterpret_cast<vecT*>(xd + t * RPI * XS) = bload(o.xs, o.xoff + t * xstride);
+      for (int t = 0; t < NP_R; ++t)
+        if (rok(t)) *reinterpret_cast<vecT*>(rd + t * RPI_R * KSTR) = bload(o.rs, o.roff + t * rstride);
+    };
+
+    // B fragment of 16-offset block eb, k-step s: Gc reads X[k][k + e + 1],
+    // Gp reads X[k + e][k], k = kg + tab_ku(s, u), e = 16 eb + c16: one
+    // per-lane base and compile-time offsets
+    const int kg = tab_kg<T>(g);
+    const T* xb = X + (P ? c16 * XS + kg * (XS + 1) : kg * (XS + 1) + c16 + 1);
+    auto bfrag = [&](int eb, int s) {
+      frag f;
+#pragma unroll
+      for (int u = 0; u < FE; ++u) f[u] = xb[(P ? 16 * eb * XS : 16 * eb) + tab_ku<T>(s, u) * (XS + 1)];
+      return f;
+    };
+
+    int it = sub;
+    if constexpr (PREFETCH) {
+      if (it < nitems) fetch(it);
     }
-    const T* qbase = (const T*)p.q + (int64_t)b * p.qs[0] + (int64_t)h * p.qs[2];
-    const T* kbase = (const T*)p.k + (int64_t)b * p.ks[0] + (int64_t)h * p.ks[2];
+    for (; it < nitems; it += 2) {
+      if constexpr (PREFETCH) {
+        commit();
+        if (it + 2 < nitems) fetch(it + 2);
+      } else {
+        stage_direct(it);
+      }
+      wave_lds_sync();
+      frag af[NS][ND];
 #pragma unroll
-    for (int k = 0; k < RCH; ++k) {
-      const int c = tid + 256 * k;
-      const int r = c / (D / VEC), c0 = (c % (D / VEC)) * VEC;
-      const int i = i0 + r, j = jb + XC - JC + r;  // the ring's new rows
+      for (int s = 0; s < NS; ++s)
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) qr[k][e] = kr[k][e] = (T)0.0f;
-      if (c < RV && c2p && i < p.Lq) qr[k] = *reinterpret_cast<const vecT*>(qbase + (int64_t)i * p.qs[1] + c0);
-      if (c < RV && p2c && j >= 0 && j < p.Lk) kr[k] = *reinterpret_cast<const vecT*>(kbase + (int64_t)j * p.ks[1] + c0);
+        for (int db = 0; db < ND; ++db) af[s][db] = tab_afrag<T>(Rw, KSTR, s, 16 * db, g, c16);
+      // one block ahead: the next block's reads are issued before this
+      // block's products (the scheduling barrier keeps the compiler from
+      // hoisting more of them, which would cost registers)
+      frag bcur[NS];
+#pragma unroll
+      for (int s = 0; s < NS; ++s) bcur[s] = bfrag(0, s);
+#pragma unroll
+      for (int eb = 0; eb < NEB; ++eb) {
+        frag bnext[NS];
+        if (eb + 1 < NEB) {
+#pragma unroll
+          for (int s = 0; s < NS; ++s) bnext[s] = bfrag(eb + 1, s);
+        }
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+#pragma unroll
+          for (int db = 0; db < ND; ++db) acc[eb][db] = M::mma(af[s][db], bcur[s], acc[eb][db]);
+        __builtin_amdgcn_sched_barrier(0);
+        if (eb + 1 < NEB) {
+#pragma unroll
+          for (int s = 0; s < NS; ++s) bcur[s] = bnext[s];
+        }
+      }
+      wave_lds_sync();  // the region is rewritten by the next item
     }
   };
+  if (p2c) run(std::true_type{});
+  else run(std::false_type{});
 
-  if (nsteps > 0) fetch(0);
-  for (int st = 0; st < nsteps; ++st) {
-    int b, i0;
-    step_coords(st, b, i0);
-    const int jb = i0 - d0 - DBW;  // key of staged column 0
-    __syncthreads();               // previous step's readers are done
+  // Sum the two waves of each kind (1 into 0, 3 into 2) through LDS, then
+  // store the partial of this (block, head, batch group): [kind][dd][d], fp32.
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(lds);
+  if (sub == 1) {
+    f32x4* dst = reinterpret_cast<f32x4*>(red) + (w >> 1) * (NEB * ND * 64) + lane;
 #pragma unroll
-    for (int k = 0; k < XCH; ++k) {
-      const int c = tid + 256 * k;
-      if (c < XV) {
-        const int r = c / (XC / VEC), c0 = (c % (XC / VEC)) * VEC;
-        *reinterpret_cast<vecT*>(Xs + (XP + r) * XSTR + c0) = xr[k];
-      }
-    }
+    for (int eb = 0; eb < NEB; ++eb)
 #pragma unroll
-    for (int k = 0; k < RCH; ++k) {
-      const int c = tid + 256 * k;
-      if (c < RV) {
-        const int r = c / (D / VEC), c0 = (c % (D / VEC)) * VEC;
-        *reinterpret_cast<vecT*>(Qc + r * KSTR + c0) = qr[k];
-        *reinterpret_cast<vecT*>(Kring + ((jb + XC - JC + r) & (QRING - 1)) * RSTR + c0) = kr[k];
-      }
-    }
-    if (p2c && i0 == istart) {  // first chunk of a batch: the ring's older rows too
-      const T* kbase = (const T*)p.k + (int64_t)b * p.ks[0] + (int64_t)h * p.ks[2];
-      load_ring_rows<T, D>(Kring, RSTR, kbase, p.ks[1], jb, XC - JC, p.Lk, tid);
-    }
-    __syncthreads();
-    if (st + 1 < nsteps) fetch(st + 1);
-
-    // A operands, shared by the wave's two 16-offset blocks: Q^T of the 32
-    // queries, and K^T of staged columns [32w, 32w + 64).
-    frag qa[GC_STEPS][ND], ka[GP_STEPS][ND];
-    if (c2p) {
-#pragma unroll
-      for (int s = 0; s < GC_STEPS; ++s)
-#pragma unroll
-        for (int db = 0; db < ND; ++db) qa[s][db] = tr_contig<T>(Qc, KSTR, s * M::KSTEP, 16 * db, g, c16);
-    }
-    if (p2c) {
-#pragma unroll
-      for (int s = 0; s < GP_STEPS; ++s)
-#pragma unroll
-        for (int db = 0; db < ND; ++db)
-          ka[s][db] = tr_contig_ring<T>(Kring, RSTR, jb, 32 * w + M::KSTEP * s, 16 * db, g, c16);
-    }
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int e0 = 16 * (2 * w + t);  // first e of this wave's 16-offset block
-      if (c2p) {
-        // Gc^T[d][e] += sum_r Q^T[d][i0 + r] X[r][r + 1 + e],  r = KSTEP*s + FE*g + u
-#pragma unroll
-        for (int s = 0; s < GC_STEPS; ++s) {
-          frag bfr;
-          const T* dg = Xs + (XP + M::KSTEP * s + FE * g) * XSTR + M::KSTEP * s + FE * g + 1 + e0 + c16;
-#pragma unroll
-          for (int u = 0; u < FE; ++u) bfr[u] = dg[u * (XSTR + 1)];
-#pragma unroll
-          for (int db = 0; db < ND; ++db) gc[t][db] = M::mma(qa[s][db], bfr, gc[t][db]);
-        }
-      }
-      if (p2c) {
-        // Gp^T[d][e] += sum_c K^T[d][jb + c] X[c - 1 - e][c],  c = 32w + KSTEP*s + FE*g + u;
-        // X rows c - 1 - e in [-32, 63) (zero outside [0, JC)).
-#pragma unroll
-        for (int s = 0; s < GP_STEPS; ++s) {
-          frag bfr;
-          const int c = 32 * w + M::KSTEP * s + FE * g;  // column of element u = 0
-          const T* dg = Xs + (XP + c - 1 - e0 - c16) * XSTR + c;
-#pragma unroll
-          for (int u = 0; u < FE; ++u) bfr[u] = dg[u * (XSTR + 1)];
-#pragma unroll
-          for (int db = 0; db < ND; ++db) gp[t][db] = M::mma(ka[s][db], bfr, gp[t][db]);
-        }
-      }
-    }
+      for (int db = 0; db < ND; ++db) dst[(eb * ND + db) * 64] = acc[eb][db];
   }
-
-  // partial of this (block, head, batch group): [type][dd][d], fp32
-  float* out = bp.gpart + ((int64_t)(h * bp.NDB + dblk) * bp.NBG + bg) * 2 * DBW * D;
+  __syncthreads();
+  if (sub == 0 && active) {
+    const f32x4* src = reinterpret_cast<const f32x4*>(red) + (w >> 1) * (NEB * ND * 64) + lane;
+    float* out = bp.gpart + ((int64_t)(h * bp.NDB + dblk) * bp.NBG + bg) * 2 * DBW * D + (p2c ? DBW * D : 0);
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int dd = DBW - 1 - (16 * (2 * w + t) + c16);  // offset d0 + dd
+    for (int eb = 0; eb < NEB; ++eb) {
+      const int e = 16 * eb + c16;
+      const int dd = p2c ? e : DBW - 1 - e;  // offset d0 + dd
 #pragma unroll
-    for (int db = 0; db < ND; ++db) {
-      *reinterpret_cast<f32x4*>(out + (int64_t)dd * D + 16 * db + 4 * g) = gc[t][db];
-      *reinterpret_cast<f32x4*>(out + (int64_t)(DBW + dd) * D + 16 * db + 4 * g) = gp[t][db];
+      for (int db = 0; db < ND; ++db)
+        *reinterpret_cast<f32x4*>(out + (int64_t)dd * D + 16 * db + 4 * g) = acc[eb][db] + src[(eb * ND + db) * 64];
     }
   }
 }

@@ -192,9 +192,10 @@ WsLayout ws_layout(const dsa_bwd_args* a) {
   w.OFF = w.LkP - 1;            // offset origin: t = d + OFF, 32-aligned tile starts
   w.TGP = w.LqP + w.LkP;        // offsets [-(LkP - 1), LqP] of every band window
   w.NDB = (w.LqP + w.LkP) / dsa::tbcfg::DBW;
-  // batch groups of the table kernel: about two workgroups per CU
+  // batch groups of the table kernel: about three workgroups per CU (two
+  // run at a time; the workgroups of the outer offset blocks are short)
   const int per = f.H * w.NDB;
-  int groups = (2 * device_cus() + per - 1) / per;
+  int groups = (3 * device_cus() + per - 1) / per;
   groups = groups < 1 ? 1 : (groups > f.B ? f.B : groups);
   w.BPG = (f.B + groups - 1) / groups;
   w.NBG = (f.B + w.BPG - 1) / w.BPG;
@@ -355,6 +356,14 @@ int dsa_bwd(const dsa_bwd_args* a, void* stream) {
       if (strides[t][s] % vec != 0) return fail("dsa: dout/dq/dk/dv strides must be multiples of %d elements", vec);
   }
   const WsLayout ws = ws_layout(a);
+  // the table kernel addresses one (b, h) slice of dS, and the rows of q and
+  // k of one (b, h), with 32-bit byte offsets
+  const int64_t es = elem_bytes(f.dtype);
+  if ((int64_t)ws.LqP * ws.LkP * es > 0x7fffffffLL)
+    return fail("dsa: Lq x Lk too large for the backward (padded (b, h) slice of dS over 2 GiB)");
+  if (((int64_t)(f.Lq - 1) * f.q_strides[1] + f.D) * es > 0x7fffffffLL ||
+      ((int64_t)(f.Lk - 1) * f.k_strides[1] + f.D) * es > 0x7fffffffLL)
+    return fail("dsa: q / k sequence stride too large for the backward (rows of one (b, h) over 2 GiB)");
   if (!a->workspace || a->workspace_bytes < ws.total)
     return fail("dsa: workspace of %zu bytes required, got %zu", ws.total, a->workspace_bytes);
   if (!aligned16(a->workspace)) return fail("dsa: workspace must be 16-byte aligned");
