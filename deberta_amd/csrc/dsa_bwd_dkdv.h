@@ -7,10 +7,11 @@
 // qrgt) are double-buffered in LDS and filled by direct global-to-LDS copies
 // issued one tile ahead; K and V of the wave's keys stay in registers.  Per
 // tile:
-//   scores        y = (Q K^T + bias) * scale*log2e, queries down / keys
-//                 across, where bias = c2p + p2c is the relative term the
-//                 forward saved (read transposed from the LDS tile)
-//   P, dP, dS     P = exp2(y - lse*log2e), dP = dO V^T, dS = P (dP - Delta)
+//   scores        y = Q K^T + bias (unscaled), queries down / keys across,
+//                 where bias = c2p + p2c is the relative term the forward
+//                 saved (read transposed from the LDS tile)
+//   P, dP, dS     P = exp2(y * scale*log2e - lse*log2e), dP = dO V^T,
+//                 dS = P (dP - Delta)
 //   dS            staged transposed in the wave's LDS tile (rows j), then
 //                 stored to the workspace in rows i (4 consecutive keys per
 //                 lane, read back transposed): the dq and table kernels
@@ -241,7 +242,8 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
         return;
       }
 
-      // ---- scores (queries down, keys across): (Q K^T + saved bias) * scale*log2e -------------
+      // ---- scores (queries down, keys across): Q K^T + saved bias (unscaled) --------------------
+      const float one = opaque_one();
       f32x4 sc[2][BQ / 16];
 #pragma unroll
       for (int ib = 0; ib < BQ / 16; ++ib) {
@@ -258,20 +260,19 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
             // rows 16*ib + 4*g + e of key column 32w + 16*jb + c16 (forward tile order)
             const int jl = WK * w + 16 * jb;
             const int o = (jl / 64) * 2048 + ib * 1024 + ((jl % 64) / 16) * 256;
-            f32x4 bv;
             if constexpr (sizeof(BT) == 2) {
+              // one mixed-precision FMA per element adds the fp16 term
               typedef _Float16 h4 __attribute__((ext_vector_type(4)));
               const h4 v = __builtin_bit_cast(
                   h4, tr4_at(reinterpret_cast<const bf16*>(Bt) + o + (4 * g + (c16 >> 2)) * 16 + (c16 & 3) * 4));
-              bv = f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+#pragma unroll
+              for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf((float)v[e], one, acc[e]);
             } else {
 #pragma unroll
-              for (int e = 0; e < 4; ++e) bv[e] = Bt[o + (4 * g + e) * 16 + c16];
+              for (int e = 0; e < 4; ++e) acc[e] += Bt[o + (4 * g + e) * 16 + c16];
             }
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc[e] += bv[e];
           }
-          sc[jb][ib] = acc * sl2;
+          sc[jb][ib] = acc;
         }
       }
 
@@ -296,7 +297,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
             // unwritten saved term: they are never exponentiated
             bool keep = jkeep[jb] && lr != INFINITY;
             if (MASK == MASK_PAIR) keep = keep && pkb[(int64_t)min(i0 + il, Lq - 1) * p.pkq + jcol[jb]] != 0;
-            const float pe = keep ? __builtin_amdgcn_exp2f(sc[jb][ib][e] - lr) : 0.f;
+            const float pe = keep ? __builtin_amdgcn_exp2f(__builtin_fmaf(sc[jb][ib][e], sl2, -lr)) : 0.f;
             pp[jb][ib][e] = pe;
             dsh[jb][ib][e] = pe * (dp[e] - R[2 * il + 1]);
           }

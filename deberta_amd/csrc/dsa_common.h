@@ -318,6 +318,15 @@ DSA_DEV int xcd_remap(int n, int G) {
   return n < per * NX ? (n % NX) * per + n / NX : n;
 }
 
+// 1.0f that the compiler cannot see through: fma(fp16 -> fp32 x, one, y)
+// then stays one mixed-precision FMA (v_fma_mix_f32) instead of being
+// folded into a conversion and an add.
+DSA_DEV float opaque_one() {
+  float one;
+  asm volatile("v_mov_b32 %0, 1.0" : "=v"(one));
+  return one;
+}
+
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 

@@ -111,25 +111,6 @@ struct BandType<bf16> {
   typedef _Float16 type;
 };
 
-// Stores the four values of a C-tile column (rows 4g + e) at p[e * stride].
-// fp16 bands are converted two at a time with round-toward-zero, which also
-// saturates: a finite value never rounds to infinity.
-template <typename B>
-DSA_DEV void store_band4(B* p, int stride, const f32x4& v) {
-  if constexpr (sizeof(B) == 2) {
-    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-    const h2 a = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(v[0], v[1]));
-    const h2 c = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(v[2], v[3]));
-    p[0] = a[0];
-    p[stride] = a[1];
-    p[2 * stride] = c[0];
-    p[3 * stride] = c[1];
-  } else {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) p[e * stride] = v[e];
-  }
-}
-
 namespace dcfg {
 constexpr int WQ = 32;          // queries per wave
 constexpr int BK = 64;          // keys per tile
@@ -141,9 +122,13 @@ constexpr int XG = BQ + BK;     // p2c band rows per workgroup (191 used)
 // four MFMA results are one write; the stride puts 16 rows' 8-byte chunks
 // in distinct banks
 constexpr int CTS = 104;
-constexpr int PBS = XG + 5;     // p2c band row stride (4*PBS - 4 = 16 mod 64: 4 lane groups, distinct banks)
+// p2c band, stored per offset (row x, the 64 keys contiguous) so that a
+// lane's four MFMA results (four consecutive keys) are two 4-byte writes;
+// the odd dword stride (33 for fp16) spreads the gather's 16 consecutive
+// offsets over distinct banks
+constexpr int PBT = BK + 2;
 constexpr int CB_ELEMS = WQ * CTS;
-constexpr int PB_ELEMS = BK * PBS;
+constexpr int PB_ELEMS = XG * PBT;
 }  // namespace dcfg
 
 // Row tables of one tile: crow[x] / prow[x] are the c2p / p2c table rows of
@@ -176,8 +161,25 @@ DSA_DEV int64_t bias_tile_offset(int b, int h, int H, int qt, int kt, int LqP, i
   return (((int64_t)(b * H + h) * (LqP / 128) + qt) * (LkP / 64) + kt) * 8192;
 }
 
+// Stores four values at p[0..3] as two halves of two elements (p only
+// 4-byte aligned for fp16, 8-byte aligned for fp32).  fp16 values are
+// converted two at a time with round-toward-zero, which also saturates: a
+// finite value never rounds to infinity.
+template <typename B>
+DSA_DEV void store4_halves(B* p, const f32x4& v) {
+  if constexpr (sizeof(B) == 2) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    *reinterpret_cast<h2*>(p) = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(v[0], v[1]));
+    *reinterpret_cast<h2*>(p + 2) = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(v[2], v[3]));
+  } else {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    *reinterpret_cast<f2*>(p) = f2{v[0], v[1]};
+    *reinterpret_cast<f2*>(p + 2) = f2{v[2], v[3]};
+  }
+}
+
 // Stores four values at p[0..3] (fp16: round-toward-zero pair conversion,
-// saturating as in store_band4).
+// saturating as in store4_halves).
 template <typename B>
 DSA_DEV void store4_contig(B* p, const f32x4& v) {
   if constexpr (sizeof(B) == 2) {
@@ -196,7 +198,7 @@ DSA_DEV void store4_contig(B* p, const f32x4& v) {
 // c16 of the tile).  y holds q.k on entry and q.k + c2p + p2c (unscaled)
 // on return.
 //   kf: A fragments of the 64 key rows, qf: B fragments of the wave's queries
-//   cb: this wave's c2p band (WQ * CTS), pb: the shared p2c band (BK * PBS)
+//   cb: this wave's c2p band (WQ * CTS), pb: the shared p2c band (XG * PBT)
 //   bias: if not null, where this lane's part of the tile's saved relative
 //         term goes (see bias_tile_offset): the unscaled c2p + p2c values,
 //         stored for the backward
@@ -242,7 +244,7 @@ DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&
         f32x4 acc = zero4();
 #pragma unroll
         for (int s = 0; s < NS; ++s) acc = M::mma(kf[jb][s], bf[s], acc);
-        store_band4<BT>(pb + (16 * jb + 4 * g) * PBS + 16 * xb + c16, PBS, acc);
+        store4_halves<BT>(pb + (16 * xb + c16) * PBT + 16 * jb + 4 * g, acc);
       }
     }
   }
@@ -250,12 +252,13 @@ DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&
   // c2p: x - 32w = (16*ib + c16) - (16*jb + 4*g + e) + 63; the four e are
   // consecutive x (descending) of one query row
   const BT* cbase = cb + c16 * CTS + c16 - 4 * g + 60;
-  // p2c: row j = 16*jb + 4*g + e, column x = 32w + (16*ib + c16) - (16*jb + 4*g + e) + 63
-  const BT* pbase = pb + 4 * g * PBS + WQ * w + c16 - 4 * g + 63;
+  // p2c: row x = 32w + (16*ib + c16) - (16*jb + 4*g + e) + 63, key 16*jb + 4*g + e
+  const BT* pbase = pb + (WQ * w + c16 - 4 * g + 63) * PBT + 4 * g;
   // The two terms are summed in the band type (for fp16: one rounding of the
   // exact sum, which is also the value saved), then added to the score with
   // one mixed-precision FMA per element.  The uniform flag test sits
   // outside the loops.
+  const float one = opaque_one();
   auto gather = [&](auto with_c, auto with_p) {
 #pragma unroll
     for (int ib = 0; ib < 2; ++ib)
@@ -269,11 +272,11 @@ DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&
         for (int e = 0; e < 4; ++e) {
           BT v = (BT)0.0f;
           if constexpr (decltype(with_c)::value) v = cv[3 - e];
-          if constexpr (decltype(with_p)::value) v = v + pbase[(16 * jb + e) * PBS + 16 * ib - 16 * jb - e];
+          if constexpr (decltype(with_p)::value) v = v + pbase[(16 * ib - 16 * jb - e) * PBT + 16 * jb + e];
           bs[e] = v;
         }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) y[ib][jb][e] = __builtin_fmaf((float)bs[e], 1.0f, y[ib][jb][e]);
+        for (int e = 0; e < 4; ++e) y[ib][jb][e] = __builtin_fmaf((float)bs[e], one, y[ib][jb][e]);
         if (bias) {
           *reinterpret_cast<b4*>(bias + (ib * 4 + jb) * 256) = b4{bs[0], bs[1], bs[2], bs[3]};
         }
