@@ -49,9 +49,7 @@ TRAFFIC_KIB = {  # kernel: (FETCH_SIZE, WRITE_SIZE) as read
     "dsa_bwd_dq_kernel": (127076, 24576),
     "dsa_bwd_table_kernel": (178500, 36864),
     "dsa_bwd_fold_kernel": (19420, 2458),
-    "dsa_bwd_delta_kernel": (24993, 1536),
-    "dsa_bwd_gather_kernel": (6184, 3072),
-    "dsa_bwd_segments_kernel": (26, 8),
+    "dsa_bwd_prep_kernel": (31203, 4616),
 }
 
 
@@ -234,7 +232,7 @@ def main() -> None:
         "dsa_bwd_dkdv_kernel": (run_stage(_lib.DSA_STAGE_DKDV), bh * (6.0 * L * L + 2.0 * L * R)),
         "dsa_bwd_dq_kernel": (run_stage(_lib.DSA_STAGE_DQ), bh * (2.0 * L * L + 2.0 * L * R)),
         "fold (dsa_bwd_table_kernel + dsa_bwd_fold_kernel)": (run_stage(_lib.DSA_STAGE_FOLD), bh * 4.0 * L * R),
-        "prep (dsa_bwd_delta_kernel + dsa_bwd_gather_kernel + dsa_bwd_segments_kernel)": (run_stage(_lib.DSA_STAGE_PREP), 0.0),
+        "prep (dsa_bwd_prep_kernel)": (run_stage(_lib.DSA_STAGE_PREP), 0.0),
     }
     per_kernel = {}
     n_k = args.steps if args.kernels_only else max(10, args.steps)

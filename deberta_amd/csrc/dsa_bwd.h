@@ -10,11 +10,12 @@
 // Masked keys and dead query rows have P = 0 and so dS = 0.
 //
 // Kernels, in launch order:
-//   prep   dsa_bwd_delta_kernel (lse and Delta per row), dsa_bwd_gather_kernel (krgt,
-//          qrgt: the relative tables gathered per offset d = i - j and
-//          transposed, so a run of consecutive offsets of one head-dim
-//          column is contiguous — the A operand of the offset-band products)
-//          and dsa_bwd_segments_kernel (the offset range of each table row)
+//   prep   dsa_bwd_prep_kernel, one launch of three parts: prep_delta (lse
+//          and Delta per row), prep_gather (krgt, qrgt: the relative tables
+//          gathered per offset d = i - j and transposed, so a run of
+//          consecutive offsets of one head-dim column is contiguous — the A
+//          operand of the offset-band products) and prep_segments (the
+//          offset range of each table row)
 //   dkdv   dsa_bwd_dkdv_kernel (dsa_bwd_dkdv.h): recomputes the scores and
 //          the softmax per (b, h, 128-key tile), writes dK, dV and dS
 //          (rows = queries; bf16 for bf16 inputs), the only (L x L) tensor
@@ -31,15 +32,15 @@ namespace dsa {
 
 // rowinfo[b][h][i] = (lse_i * log2 e, dO_i . O_i) for i < LqP: D / VEC lanes
 // per row, one 16-byte load each, then a butterfly sum.  Rows past Lq get
-// (inf, 0); dead rows already have lse = inf.
+// (inf, 0); dead rows already have lse = inf.  Block blk of 256 threads.
 template <typename T, int D>
-__global__ __launch_bounds__(256) void dsa_bwd_delta_kernel(BwdParams bp) {
+DSA_DEV void prep_delta(const BwdParams& bp, int blk) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int LPR = D / VEC;
   typedef T vecT __attribute__((ext_vector_type(VEC)));
   const FwdParams& p = bp.f;
   const int64_t n = (int64_t)p.B * p.H * p.LqP;
-  const int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) / LPR;
+  const int64_t row = ((int64_t)blk * 256 + threadIdx.x) / LPR;
   const int part = threadIdx.x % LPR;
   float acc = 0.f;
   int i = 0, h = 0, b = 0;
@@ -76,15 +77,15 @@ DSA_DEV int offset_row(const int32_t* rel, int d, int Lq, int Lk, int A, bool p2
 // aligned group of VEC = 16 / sizeof(T) offsets reversed: the dq kernel's
 // operand order), qrgt[h][d][t] = Qr[h][p(t - OFF)][d], for t in [0, TGP).
 // One thread per (table, h, d, group of VEC consecutive t): VEC gathered
-// elements, one 16-byte store.
+// elements, one 16-byte store.  Block blk of 256 threads.
 template <typename T, int D>
-__global__ __launch_bounds__(256) void dsa_bwd_gather_kernel(BwdParams bp) {
+DSA_DEV void prep_gather(const BwdParams& bp, int blk) {
   constexpr int VEC = 16 / sizeof(T);
   typedef T vecT __attribute__((ext_vector_type(VEC)));
   const FwdParams& p = bp.f;
   const int NG = bp.TGP / VEC;
   const int64_t per = (int64_t)p.H * D * NG;
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t idx = (int64_t)blk * 256 + threadIdx.x;
   if (idx >= 2 * per) return;
   const bool q = idx >= per;
   if (q ? !(p.flags & 2) : !(p.flags & 1)) return;
@@ -109,11 +110,11 @@ __global__ __launch_bounds__(256) void dsa_bwd_gather_kernel(BwdParams bp) {
 // non-increasing).  One thread per (table, offset d), plus one past the
 // last offset: it starts the rows above the previous offset's row, up to
 // its own, and ends the rows from the previous offset's row up to (not
-// including) its own.
-__global__ __launch_bounds__(256) void dsa_bwd_segments_kernel(BwdParams bp) {
+// including) its own.  Block blk of 256 threads.
+DSA_DEV void prep_segments(const BwdParams& bp, int blk) {
   const FwdParams& p = bp.f;
   const int R = 2 * p.A, n = p.Lq + p.Lk - 1, dmin = -(p.Lk - 1);
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t idx = (int64_t)blk * 256 + threadIdx.x;
   if (idx >= 2 * (int64_t)(n + 1)) return;
   const int t = (int)(idx / (n + 1)), u = (int)(idx % (n + 1));
   if (!(p.flags & (1 << t))) return;
@@ -128,6 +129,25 @@ __global__ __launch_bounds__(256) void dsa_bwd_segments_kernel(BwdParams bp) {
   int* end = beg + R;
   for (int q = prev + 1; q <= min(cur, R - 1); ++q) beg[t ? R - 1 - q : q] = dmin + u;
   for (int q = max(prev, 0); q < min(cur, R); ++q) end[t ? R - 1 - q : q] = dmin + u;
+}
+
+// The preparation stage in one launch: blocks [0, nb_gather) gather the
+// tables, the next nb_seg blocks find the row segments, the rest compute
+// rowinfo.  The short gather and segment blocks go first and run beside
+// the rowinfo blocks.
+struct PrepBlocks {
+  int gather, seg, delta;
+};
+template <typename T, int D>
+__global__ __launch_bounds__(256) void dsa_bwd_prep_kernel(BwdParams bp, PrepBlocks nb) {
+  const int blk = blockIdx.x;
+  if (blk < nb.gather) {
+    prep_gather<T, D>(bp, blk);
+  } else if (blk < nb.gather + nb.seg) {
+    prep_segments(bp, blk - nb.gather);
+  } else {
+    prep_delta<T, D>(bp, blk - nb.gather - nb.seg);
+  }
 }
 
 }  // namespace dsa

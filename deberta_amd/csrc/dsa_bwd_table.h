@@ -6,7 +6,7 @@
 //   Gc[d] = sum_{b,i} dS(i, i-d) q_i,   Gp[d] = sum_{b,j} dS(j+d, j) k_j,
 // and then summed onto table rows (dsa_bwd_fold_kernel): c(d) and p(d) are
 // monotone in d, so the offsets of one row form a contiguous range
-// (dsa_bwd_segments_kernel finds them).
+// (prep_segments in dsa_bwd_prep_kernel finds them).
 //
 // dsa_bwd_table_kernel: one workgroup = (128-offset block [d0, d0+128),
 // head h, batch group).  Waves 0 and 1 compute Gc, waves 2 and 3 Gp, each
@@ -316,9 +316,9 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
 
 // tab[h][r][:] (+)= s * sum over batch groups and offsets d with row(d) = r
 // of the partials (accumulated into fp32, or written in fp32 or bf16).  One
-// wave per (table, h, r): 64 / (D/4) parts split the row's offset range
-// [begin, end) (from dsa_bwd_segments_kernel) and are summed with lane
-// shuffles; lanes of a part hold 4 columns each.
+// wave per (table, h, r): 64 / (D/4) parts split the (offset, batch group)
+// pairs of the row's offset range [begin, end) (from prep_segments) and are
+// summed with lane shuffles; lanes of a part hold 4 columns each.
 template <int D>
 __global__ __launch_bounds__(64) void dsa_bwd_fold_kernel(BwdParams bp) {
   using namespace tbcfg;
@@ -331,11 +331,12 @@ __global__ __launch_bounds__(64) void dsa_bwd_fold_kernel(BwdParams bp) {
   const int c4 = threadIdx.x % Q4, part = threadIdx.x / Q4;
   const int beg = bp.seg[(2 * t) * R + r], end = bp.seg[(2 * t + 1) * R + r];
   f32x4 acc = zero4();
-  for (int d = beg + part; d < end; d += NP) {
+  const int npairs = (end - beg) * bp.NBG;
+  for (int it = part; it < npairs; it += NP) {
+    const int d = beg + it / bp.NBG, k = it % bp.NBG;
     const int dblk = (d + bp.f.LkP) / DBW, dd = (d + bp.f.LkP) % DBW;
-    const float* src = bp.gpart + ((int64_t)(h * bp.NDB + dblk) * bp.NBG) * 2 * DBW * D +
-                       (int64_t)((q ? DBW : 0) + dd) * D + 4 * c4;
-    for (int k = 0; k < bp.NBG; ++k) acc += *reinterpret_cast<const f32x4*>(src + (int64_t)k * 2 * DBW * D);
+    acc += *reinterpret_cast<const f32x4*>(bp.gpart + ((int64_t)(h * bp.NDB + dblk) * bp.NBG + k) * 2 * DBW * D +
+                                           (int64_t)((q ? DBW : 0) + dd) * D + 4 * c4);
   }
 #pragma unroll
   for (int m = Q4; m < 64; m <<= 1)

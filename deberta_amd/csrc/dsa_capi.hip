@@ -251,17 +251,19 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
       a->stages ? a->stages : (DSA_STAGE_PREP | DSA_STAGE_DQ | DSA_STAGE_DKDV | DSA_STAGE_FOLD);
 
   if (stages & DSA_STAGE_PREP) {
+    dsa::PrepBlocks nb;
     const int64_t n = (int64_t)f.B * f.H * ws.LqP * (D / (16 / (int)sizeof(T)));
-    hipLaunchKernelGGL((dsa::dsa_bwd_delta_kernel<T, D>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, bp);
-    if (launch_check("dsa_bwd_delta_kernel")) return 1;
+    nb.delta = (int)((n + 255) / 256);
+    nb.gather = nb.seg = 0;
     if (f.flags) {
       const int64_t m = 2 * (int64_t)f.H * D * (ws.TGP / (16 / (int)sizeof(T)));
-      hipLaunchKernelGGL((dsa::dsa_bwd_gather_kernel<T, D>), dim3((unsigned)((m + 255) / 256)), dim3(256), 0, st, bp);
-      if (launch_check("dsa_bwd_gather_kernel")) return 1;
+      nb.gather = (int)((m + 255) / 256);
       const int64_t ns = 2 * (int64_t)(f.Lq + f.Lk);
-      hipLaunchKernelGGL((dsa::dsa_bwd_segments_kernel), dim3((unsigned)((ns + 255) / 256)), dim3(256), 0, st, bp);
-      if (launch_check("dsa_bwd_segments_kernel")) return 1;
+      nb.seg = (int)((ns + 255) / 256);
     }
+    hipLaunchKernelGGL((dsa::dsa_bwd_prep_kernel<T, D>), dim3((unsigned)(nb.gather + nb.seg + nb.delta)), dim3(256), 0,
+                       st, bp, nb);
+    if (launch_check("dsa_bwd_prep_kernel")) return 1;
   }
   if (stages & DSA_STAGE_DKDV) {
     dim3 grid((unsigned)(ws.LkP / dsa::kvcfg::BKW * f.H * f.B));
