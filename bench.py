@@ -44,12 +44,12 @@ R = 2 * A
 # (x1.0).  Commands and raw figures: profiles/hbm_traffic_headline.md.
 FETCH_SCALE, WRITE_SCALE = 2.0, 1.0
 TRAFFIC_KIB = {  # kernel: (FETCH_SIZE, WRITE_SIZE) as read
-    "dsa_fwd_kernel": (52587, 221952),
-    "dsa_bwd_dkdv_kernel": (180717, 245885),
-    "dsa_bwd_dq_kernel": (127076, 24576),
-    "dsa_bwd_table_kernel": (178500, 36864),
-    "dsa_bwd_fold_kernel": (19420, 2458),
-    "dsa_bwd_prep_kernel": (31203, 4616),
+    "dsa_fwd_kernel": (52860, 221952),
+    "dsa_bwd_dkdv_kernel": (180884, 245912),
+    "dsa_bwd_dq_kernel": (127165, 24576),
+    "dsa_bwd_table_kernel": (222911, 49166),
+    "dsa_bwd_fold_kernel": (25559, 2458),
+    "dsa_bwd_prep_kernel": (31177, 4616),
 }
 
 
