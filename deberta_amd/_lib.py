@@ -22,7 +22,7 @@ DSA_STAGE_DQ = 2
 DSA_STAGE_DKDV = 4
 DSA_STAGE_FOLD = 8
 
-EXPECTED_VERSION = 3
+EXPECTED_VERSION = 4
 
 _i64x3 = ctypes.c_int64 * 3
 _i64x2 = ctypes.c_int64 * 2
@@ -58,6 +58,8 @@ class DsaFwdArgs(ctypes.Structure):
         ("dtype", ctypes.c_int32),
         ("flags", ctypes.c_int32),
         ("scale", ctypes.c_float),
+        ("seg", ctypes.c_void_p),
+        ("seg_stride_b", ctypes.c_int64),
     ]
 
 

@@ -21,7 +21,7 @@ import torch.nn as nn
 
 from deberta_amd import ops  # noqa: F401  (registers the custom ops)
 from deberta_amd.config import normalize_attention_kernel, normalize_pos_att_type
-from deberta_amd.masks import kernel_masks, normalize_keep_mask
+from deberta_amd.masks import SegmentMask, kernel_masks, normalize_keep_mask
 from deberta_amd.relpos import (
     is_monotone,
     is_toeplitz,
@@ -104,7 +104,7 @@ def fused_attention(
     _require_gpu(q)
     B, Lq = q.shape[0], q.shape[1]
     Lk = k.shape[1]
-    key_keep, pair_keep = kernel_masks(attention_mask, B, Lq, Lk)
+    key_keep, pair_keep = kernel_masks(attention_mask, B, Lq, Lk, q.device)
     if kr is not None:
         kr = kr.to(q.dtype)
     if qr is not None:
@@ -172,7 +172,7 @@ def disentangled_attention(
         table = table_for(relative_pos, q.shape[1], k.shape[1], position_buckets, max_relative_positions, q.device)
     else:
         att_span, table = 1, None
-    if attention_mask is not None:
+    if attention_mask is not None and not isinstance(attention_mask, SegmentMask):
         attention_mask = normalize_keep_mask(attention_mask)
         if attention_mask.ndim != 4:
             raise ValueError(
@@ -308,7 +308,7 @@ class DisentangledSelfAttention(nn.Module):
                     q.device,
                 )
 
-        if attention_mask is not None:
+        if attention_mask is not None and not isinstance(attention_mask, SegmentMask):
             attention_mask = normalize_keep_mask(attention_mask)
             if attention_mask.ndim != 4:
                 raise ValueError(

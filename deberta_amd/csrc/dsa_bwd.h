@@ -125,18 +125,42 @@ DSA_DEV void prep_segments(const BwdParams& bp, int blk) {
   };
   const int cur = u < n ? rank(dmin + u) : R;
   const int prev = u > 0 ? rank(dmin + u - 1) : -1;
-  int* beg = bp.seg + (2 * t) * R;
+  int* beg = bp.rowseg + (2 * t) * R;
   int* end = beg + R;
   for (int q = prev + 1; q <= min(cur, R - 1); ++q) beg[t ? R - 1 - q : q] = dmin + u;
   for (int q = max(prev, 0); q < min(cur, R); ++q) end[t ? R - 1 - q : q] = dmin + u;
 }
 
+// cinfo[b][c] = (lo, hi, all, 0) for the 32-token chunk c of batch row b
+// under a key-padding or segment mask: the range of its nonzero segment
+// ids (lo > hi if none) and whether every token of the chunk is active
+// (tokens past L are inactive).  One thread per chunk.
+DSA_DEV void prep_chunks(const BwdParams& bp, int blk) {
+  const FwdParams& p = bp.f;
+  const int nch = p.LqP / 32;
+  const int64_t idx = (int64_t)blk * 256 + threadIdx.x;
+  if (idx >= (int64_t)p.B * nch) return;
+  const int b = (int)(idx / nch), c = (int)(idx % nch);
+  int lo = 0x7fffffff, hi = (int)0x80000000, all = 1;
+  for (int u = 0; u < 32; ++u) {
+    const int i = 32 * c + u;
+    const int s = i < p.Lq ? seg_at(p, b, i) : 0;
+    if (s != 0) {
+      lo = min(lo, s);
+      hi = max(hi, s);
+    } else {
+      all = 0;
+    }
+  }
+  bp.cinfo[idx] = int4{lo, hi, all, 0};
+}
+
 // The preparation stage in one launch: blocks [0, nb_gather) gather the
-// tables, the next nb_seg blocks find the row segments, the rest compute
-// rowinfo.  The short gather and segment blocks go first and run beside
-// the rowinfo blocks.
+// tables, the next nb_seg blocks find the row segments, the next nb_chunk
+// blocks summarise the mask's chunks, the rest compute rowinfo.  The short
+// blocks go first and run beside the rowinfo blocks.
 struct PrepBlocks {
-  int gather, seg, delta;
+  int gather, seg, chunk, delta;
 };
 template <typename T, int D>
 __global__ __launch_bounds__(256) void dsa_bwd_prep_kernel(BwdParams bp, PrepBlocks nb) {
@@ -145,8 +169,10 @@ __global__ __launch_bounds__(256) void dsa_bwd_prep_kernel(BwdParams bp, PrepBlo
     prep_gather<T, D>(bp, blk);
   } else if (blk < nb.gather + nb.seg) {
     prep_segments(bp, blk - nb.gather);
+  } else if (blk < nb.gather + nb.seg + nb.chunk) {
+    prep_chunks(bp, blk - nb.gather - nb.seg);
   } else {
-    prep_delta<T, D>(bp, blk - nb.gather - nb.seg);
+    prep_delta<T, D>(bp, blk - nb.gather - nb.seg - nb.chunk);
   }
 }
 

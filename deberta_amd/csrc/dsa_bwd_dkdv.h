@@ -75,6 +75,12 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
   __shared__ __align__(16) float Rs0[2 * BQ], Rs1[2 * BQ];  // per query: lse*log2e (inf: no probabilities), Delta
   __shared__ __align__(16) T Ring[NRB * RBE];     // qrgt window (p2c)
   __shared__ __align__(16) T Stg[NW * SW];        // each wave's dS^T tile
+  constexpr bool SEGM = seg_mode(MASK);
+  constexpr int MAXQT = 1024;  // query tiles (Lq <= 32768)
+  // segment masks: per query tile, bit 0 = active (dS computed and
+  // written), bit 1 = no masking needed; query segments of MASK_SEG tiles
+  __shared__ unsigned char qflag[SEGM ? MAXQT : 1];
+  __shared__ __align__(16) int qsg[MASK == MASK_SEG ? 2 : 1][MASK == MASK_SEG ? BQ : 1];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = tid >> 6, g = (tid & 63) >> 4, c16 = tid & 15;
@@ -94,8 +100,8 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
   const T* dobase = (const T*)bp.dout + (int64_t)b * bp.dos[0] + (int64_t)h * bp.dos[2];
   const BT* biasb = (const BT*)p.bias;
   const float* rib = bp.rowinfo + (int64_t)(b * p.H + h) * p.LqP * 2;
-  const uint8_t* kkb = (MASK == MASK_KEY) ? p.kk + (int64_t)b * p.kkb : nullptr;
   const uint8_t* pkb = (MASK == MASK_PAIR) ? p.pk + (int64_t)b * p.pkb : nullptr;
+  const SegView<MASK> sv(p, b);
   T* dsw = (T*)bp.ds + (int64_t)(b * p.H + h) * p.LqP * p.LkP + jw;  // dS column jw, row 0
   const T* qrg = p2c ? (const T*)bp.qrgt + (int64_t)h * D * bp.TGP : nullptr;
   // qrgt column of the workgroup window's first offset at query tile 0
@@ -103,20 +109,31 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
   const int tw0 = -j0 - (BKW - 1) + bp.OFF;
   T* stg = Stg + w * SW;
 
-  int jcol[2];
+  int jcol[2], jseg[2] = {0, 0};
   bool jkeep[2];
 #pragma unroll
   for (int jb = 0; jb < 2; ++jb) {
     const int j = jw + 16 * jb + c16;
     jcol[jb] = j;
-    jkeep[jb] = j < Lk && (MASK != MASK_KEY || kkb[j] != 0);
+    if (SEGM && j < Lk) jseg[jb] = sv(j);
+    jkeep[jb] = j < Lk && (!SEGM || jseg[jb] != 0);
   }
-  int wg_keep = 0;
-  if (tid < BKW) {
-    const int j = j0 + tid;
-    if (j < Lk) wg_keep = (MASK == MASK_KEY) ? kkb[j] != 0 : 1;
+  // Segment masks: which query tiles meet this key tile (ChunkRange); the
+  // others are neither computed nor written.
+  bool any_key;
+  if constexpr (SEGM) {
+    const ChunkRange kr = key_tile_range(bp.cinfo + (int64_t)b * nqt, kt, nqt);
+    for (int c = tid; c < nqt; c += 256) {
+      const ChunkRange x = chunk_range(bp.cinfo + (int64_t)b * nqt, c);
+      const bool act = x.meets(kr);
+      const bool full = act && x.all && kr.all && x.lo == x.hi && kr.lo == kr.hi && x.lo == kr.lo;
+      qflag[c] = (act ? 1 : 0) | (full ? 2 : 0);
+    }
+    any_key = kr.lo <= kr.hi;
+    __syncthreads();
+  } else {
+    any_key = __syncthreads_or(tid < BKW && j0 + tid < Lk);
   }
-  const bool any_key = __syncthreads_or(wg_keep);
 
   f32x4 dka[ND][2], dva[ND][2];
 #pragma unroll
@@ -141,8 +158,14 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
   // order = physical chunk order; Q and dO rows are clamped to Lq - 1, where
   // probabilities are zero anyway), and its qrgt block (whose ring slot was
   // last read two tiles earlier).
+  int qseg_next = 0;  // MASK_SEG: query segment of lane (w = 1, lane < 32) in the next tile
   auto issue = [&](int qi, T* Qd, T* dOd, BT* Bd, float* Rd) {
     const int i0 = qi * BQ;
+    if (SEGM && !(qflag[qi] & 1)) {  // inactive tile: only the ring advances
+      if (p2c) issue_ring(tw0 / 32 + qi + 4);
+      return;
+    }
+    if (MASK == MASK_SEG && w == 1 && lane < BQ) qseg_next = (i0 + lane < Lq) ? sv(i0 + lane) : 0;
 #pragma unroll
     for (int k = 0; k < (QCW + 63) / 64; ++k) {
       const int pc = w * QCW + 64 * k + lane;  // physical chunk
@@ -177,7 +200,8 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
     *reinterpret_cast<vec4*>(dsw + (int64_t)(i0 + 16 * mi + c16) * p.LkP + 16 * kk + 4 * g) = v;
   };
   if (!any_key) {
-    for (int qi = 0; qi < nqt; ++qi)
+    if (!SEGM)
+      for (int qi = 0; qi < nqt; ++qi)
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
@@ -212,17 +236,21 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
       const int i0 = qi * BQ;
       // This wave's copies of tile qi have landed: they were issued before
       // the previous tile's four dS stores, its last vector-memory
-      // instructions (tile 0 was waited for before the loop).
-      vm_wait<4>();
+      // instructions (tile 0 was waited for before the loop).  Under a
+      // segment mask an inactive previous tile stored nothing.
+      const int fl = SEGM ? qflag[qi] : 1;
+      if (SEGM && qi > 0 && !(qflag[qi - 1] & 1)) vm_wait<0>();
+      else vm_wait<4>();
+      if (MASK == MASK_SEG && w == 1 && lane < BQ) qsg[qi & 1][lane] = qseg_next;
       __syncthreads();  // ... every wave's, and tile qi - 1 is no longer read
       if (qi + 1 < nqt) issue(qi + 1, nQ, ndO, nBt, nR);
-      // Tiles without a kept (query, key) pair store zeros.
-      bool skip = i0 >= Lq;
-      if (!skip && MASK == MASK_KEY) {
-        int live = 0;
-        if (tid < BQ) live = (i0 + tid < Lq) && kkb[i0 + tid];
-        skip = !__syncthreads_or(live);
-      } else if (!skip && MASK == MASK_PAIR) {
+      if (SEGM && !(fl & 1)) return;  // no pair of one segment: nothing computed or written
+      // With segments, a tile whose queries all share the workgroup's single
+      // key segment needs no masking beyond the dead-row test.  Other modes:
+      // tiles without a kept (query, key) pair store zeros.
+      const bool full = SEGM && (fl & 2);
+      bool skip = !SEGM && i0 >= Lq;
+      if (!skip && MASK == MASK_PAIR) {
         int keep = 0;
         const int r = tid >> 3, part = tid & 7;
         const int i = i0 + r;
@@ -296,6 +324,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
             // rows without probabilities (dead, padding) have lr = inf and may hold an
             // unwritten saved term: they are never exponentiated
             bool keep = jkeep[jb] && lr != INFINITY;
+            if (MASK == MASK_SEG && !full) keep = keep && qsg[qi & 1][il] == jseg[jb];
             if (MASK == MASK_PAIR) keep = keep && pkb[(int64_t)min(i0 + il, Lq - 1) * p.pkq + jcol[jb]] != 0;
             const float pe = keep ? __builtin_amdgcn_exp2f(__builtin_fmaf(sc[jb][ib][e], sl2, -lr)) : 0.f;
             pp[jb][ib][e] = pe;

@@ -24,6 +24,7 @@ namespace dsa {
 
 namespace dqcfg {
 constexpr int NW = 4, WQ = 32, BQ = 128, BK = 64;
+constexpr int MAX_KT = 1024;  // key tiles (Lk <= 65536)
 constexpr int XW = 96;   // offset rows per wave (95 used)
 constexpr int ZC = 32;   // zero columns before each staged dS row
 }  // namespace dqcfg
@@ -53,6 +54,8 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dq_kernel(BwdParams bp) {
   __shared__ __align__(16) T Ss[(BQ + 1) * SSTR];
   __shared__ __align__(16) T Ks[BK * KSTR];
   __shared__ __align__(16) T KG[D * GSTR];
+  __shared__ short klist[MAX_KT];  // key tiles that can hold nonzero dS
+  __shared__ int segred[1];
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, g = (tid & 63) >> 4, c16 = tid & 15;
@@ -85,16 +88,20 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dq_kernel(BwdParams bp) {
     vecT s[SCH], k[KCH], g[GCH];
   };
   Regs ra, rb;
-  auto fetch = [&](int kt, Regs& r) {
+  auto fetch = [&](int entry, Regs& r) {
     vecT(&sr)[SCH] = r.s;
     vecT(&kr)[KCH] = r.k;
     vecT(&gr)[GCH] = r.g;
+    const int kt = entry & 1023, cmask = entry >> 10;
     const int j0 = kt * BK;
 #pragma unroll
     for (int k = 0; k < SCH; ++k) {
       const int c = tid + 256 * k;
-      if (c < SV)
-        sr[k] = *reinterpret_cast<const vecT*>(dsb + (int64_t)(c / (BK / VEC)) * bp.f.LkP + j0 + (c % (BK / VEC)) * VEC);
+      const int row = c / (BK / VEC);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) sr[k][e] = (T)0.0f;
+      if (c < SV && ((cmask >> (row / 32)) & 1))
+        sr[k] = *reinterpret_cast<const vecT*>(dsb + (int64_t)row * bp.f.LkP + j0 + (c % (BK / VEC)) * VEC);
     }
 #pragma unroll
     for (int k = 0; k < KCH; ++k) {
@@ -114,8 +121,35 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dq_kernel(BwdParams bp) {
     }
   };
 
-  const int nkt = bp.f.LkP / BK;
-  auto tile = [&](int kt, Regs& r) {
+  // With a key-padding or segment mask, dS was computed only for the tiles
+  // of 32 queries x 128 keys whose segments can meet (ChunkRange): a key
+  // tile is visited if one of its 4 query chunks is active, and the rows of
+  // inactive chunks are read as zeros.  klist holds kt | (chunk mask << 10).
+  int nkt = bp.f.LkP / BK;
+  if (bp.cinfo) {
+    const int nch = bp.f.LqP / 32;
+    const int4* ci = bp.cinfo + (int64_t)b * nch;
+    for (int kt = tid; kt < nkt; kt += 256) {
+      const ChunkRange kr = key_tile_range(ci, kt / 2, nch);
+      int mask = 0;
+#pragma unroll
+      for (int u = 0; u < BQ / 32; ++u) mask |= chunk_range(ci, i0 / 32 + u).meets(kr) ? (1 << u) : 0;
+      klist[kt] = (short)(mask ? (kt | (mask << 10)) : -1);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      int n = 0;
+      for (int kt = 0; kt < nkt; ++kt)
+        if (klist[kt] >= 0) klist[n++] = klist[kt];  // n <= kt: compaction in place
+      segred[0] = n;
+    }
+    __syncthreads();
+    nkt = segred[0];
+  } else {
+    for (int t = tid; t < nkt; t += 256) klist[t] = (short)(t | (0xf << 10));
+    __syncthreads();
+  }
+  auto tile = [&](int n, Regs& r) {
     __syncthreads();  // previous tile's readers are done
 #pragma unroll
     for (int k = 0; k < SCH; ++k) {
@@ -135,7 +169,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dq_kernel(BwdParams bp) {
       }
     }
     __syncthreads();
-    if (kt + 2 < nkt) fetch(kt + 2, r);
+    if (n + 2 < nkt) fetch(klist[n + 2], r);
 
     // ---- dQ^T += K^T dS^T: B = dS row i, keys KSTEP*s + FE*g + [0, FE) -----------------------
 #pragma unroll
@@ -177,11 +211,11 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dq_kernel(BwdParams bp) {
       }
     }
   };
-  fetch(0, ra);
-  if (nkt > 1) fetch(1, rb);
-  for (int kt = 0; kt < nkt; kt += 2) {
-    tile(kt, ra);
-    if (kt + 1 < nkt) tile(kt + 1, rb);
+  if (nkt > 0) fetch(klist[0], ra);
+  if (nkt > 1) fetch(klist[1], rb);
+  for (int n = 0; n < nkt; n += 2) {
+    tile(n, ra);
+    if (n + 1 < nkt) tile(n + 1, rb);
   }
 
   // ---- dQ ---------------------------------------------------------------------------------

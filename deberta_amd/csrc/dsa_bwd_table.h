@@ -178,19 +178,52 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
     auto bload = [&](__amdgpu_buffer_rsrc_t rs, unsigned off) {
       return __builtin_bit_cast(vecT, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, 0));
     };
+    // Under a segment mask, dS exists only in the active tiles of 32 queries
+    // x 128 keys (ChunkRange).  Bit u of an item's mask: Gc, key tile
+    // kA + u of the region's columns (kA = the first); Gp, query chunk
+    // cA + u of the region's rows.  Inactive parts are read as zeros and an
+    // item without active parts is skipped.
+    const int nqc = p.LqP / 32, nkt128 = p.LkP / 128;
+    auto item_mask = [&](int b, int r0) -> int {
+      if (!bp.cinfo) return 0xff;
+      const int4* ci = bp.cinfo + (int64_t)b * nqc;
+      int m = 0;
+      if constexpr (!P) {
+        const int jc0 = r0 - d0 - DBW, kA = (jc0 >= 0 ? jc0 : jc0 - 127) / 128;
+        const ChunkRange qc = chunk_range(ci, r0 / 32);
+#pragma unroll
+        for (int u = 0; u < 3; ++u) {
+          const int k = kA + u;
+          if (k >= 0 && k < nkt128 && 128 * k < jc0 + DBW + CH && qc.meets(key_tile_range(ci, k, nqc))) m |= 1 << u;
+        }
+      } else {
+        const ChunkRange kr = key_tile_range(ci, r0 / 128, nqc);
+        const int cA = (r0 + d0) / 32;  // r0 + d0 is a multiple of 32 (may be negative)
+#pragma unroll
+        for (int u = 0; u < PR / 32; ++u) {
+          const int c = cA + u;
+          if (c >= 0 && c < nqc && chunk_range(ci, c).meets(kr)) m |= 1 << u;
+        }
+      }
+      return m;
+    };
     // buffer resources and pass-0 byte offsets of item it
     struct ItemSrc {
       __amdgpu_buffer_rsrc_t xs, rs;
       unsigned xoff, roff;
+      int mask;
     };
     auto item_src = [&](int it) {
       const int b = b_lo + it / nch, r0 = rstart + (it % nch) * CH;
       ItemSrc o;
+      o.mask = item_mask(b, r0);
       const T* dsb = (const T*)bp.ds + (int64_t)(b * p.H + h) * p.LqP * p.LkP;
       o.xs = __builtin_amdgcn_make_buffer_rsrc((void*)dsb, 0, p.LqP * p.LkP * (int)sizeof(T), 0x00020000);
       if constexpr (!P) {
-        const int j = r0 - d0 - DBW + lc * VEC;  // a multiple of VEC: chunks lie wholly in or out
-        const bool ok = lr < RPI && j >= 0 && j < p.LkP;
+        const int jc0 = r0 - d0 - DBW, kA = (jc0 >= 0 ? jc0 : jc0 - 127) / 128;
+        const int j = jc0 + lc * VEC;  // a multiple of VEC: chunks lie wholly in or out
+        const int kb = (j >= 0 ? j / 128 : 0) - kA;
+        const bool ok = lr < RPI && j >= 0 && j < p.LkP && ((o.mask >> kb) & 1);
         o.xoff = ok ? (unsigned)(((r0 + lr) * p.LkP + j) * (int)sizeof(T)) : OOB;
       } else {
         o.xoff = (unsigned)(((r0 + d0 + lr) * p.LkP + r0 + lc * VEC) * (int)sizeof(T));
@@ -206,13 +239,22 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
     auto xok = [&](int t) { return lr < RPI && lr + RPI * t < NXR; };
     auto rok = [&](int t) { return rr + RPI_R * t < CH; };
 
+    // region offset of pass t (Gp: a pass's rows may fall in an inactive chunk)
+    auto xoff_t = [&](const ItemSrc& o, int t) -> unsigned {
+      if constexpr (P) {
+        if (!((o.mask >> ((lr + RPI * t) >> 5)) & 1)) return OOB;
+      }
+      return o.xoff + t * xstride;
+    };
     vecT pre[PREFETCH ? NSLOT : 1];
-    auto fetch = [&](int it) {
+    auto fetch = [&](int it) -> int {
       const ItemSrc o = item_src(it);
+      if (!o.mask) return 0;
 #pragma unroll
-      for (int t = 0; t < NP_X; ++t) pre[t] = bload(o.xs, o.xoff + t * xstride);
+      for (int t = 0; t < NP_X; ++t) pre[t] = bload(o.xs, xoff_t(o, t));
 #pragma unroll
       for (int t = 0; t < NP_R; ++t) pre[NP_X + t] = bload(o.rs, o.roff + t * rstride);
+      return o.mask;
     };
     auto commit = [&]() {
 #pragma unroll
@@ -222,12 +264,14 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
       for (int t = 0; t < NP_R; ++t)
         if (rok(t)) *reinterpret_cast<vecT*>(rd + t * RPI_R * KSTR) = pre[NP_X + t];
     };
-    auto stage_direct = [&](int it) {
+    auto stage_direct = [&](int it) -> int {
       const ItemSrc o = item_src(it);
+      if (!o.mask) return 0;
       for (int t = 0; t < NP_X; ++t)
-        if (xok(t)) *reinterpret_cast<vecT*>(xd + t * RPI * XS) = bload(o.xs, o.xoff + t * xstride);
+        if (xok(t)) *reinterpret_cast<vecT*>(xd + t * RPI * XS) = bload(o.xs, xoff_t(o, t));
       for (int t = 0; t < NP_R; ++t)
         if (rok(t)) *reinterpret_cast<vecT*>(rd + t * RPI_R * KSTR) = bload(o.rs, o.roff + t * rstride);
+      return o.mask;
     };
 
     // B fragment of 16-offset block eb, k-step s: Gc reads X[k][k + e + 1],
@@ -242,17 +286,20 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
       return f;
     };
 
-    int it = sub;
+    int it = sub, mnext = 0;
     if constexpr (PREFETCH) {
-      if (it < nitems) fetch(it);
+      if (it < nitems) mnext = fetch(it);
     }
     for (; it < nitems; it += 2) {
+      int mcur;
       if constexpr (PREFETCH) {
-        commit();
-        if (it + 2 < nitems) fetch(it + 2);
+        mcur = mnext;
+        if (mcur) commit();
+        mnext = (it + 2 < nitems) ? fetch(it + 2) : 0;
       } else {
-        stage_direct(it);
+        mcur = stage_direct(it);
       }
+      if (!mcur) continue;  // no active part: only zeros
       wave_lds_sync();
       frag af[NS][ND];
 #pragma unroll
@@ -316,32 +363,53 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
 
 // tab[h][r][:] (+)= s * sum over batch groups and offsets d with row(d) = r
 // of the partials (accumulated into fp32, or written in fp32 or bf16).  One
-// wave per (table, h, r): 64 / (D/4) parts split the (offset, batch group)
-// pairs of the row's offset range [begin, end) (from prep_segments) and are
-// summed with lane shuffles; lanes of a part hold 4 columns each.
-template <int D>
-__global__ __launch_bounds__(64) void dsa_bwd_fold_kernel(BwdParams bp) {
+// workgroup of NT threads per (table, h, r): NT / (D/4) parts split the
+// (offset, batch group) pairs of the row's offset range [begin, end) (from
+// prep_segments), each part with four independent sums so that four loads
+// are in flight; lanes of a part hold 4 columns each.  The parts are summed
+// with lane shuffles and, across waves, through LDS in a fixed order.  Long
+// sequences use NT = 256: the rows where the relative position saturates
+// then hold thousands of offsets.
+template <int D, int NT>
+__global__ __launch_bounds__(NT) void dsa_bwd_fold_kernel(BwdParams bp) {
   using namespace tbcfg;
   const FwdParams& p = bp.f;
   const int R = 2 * p.A;
-  constexpr int Q4 = D / 4, NP = 64 / Q4;
+  constexpr int Q4 = D / 4, NP = NT / Q4, NWV = NT / 64;
   const int t = blockIdx.x / (p.H * R), h = (blockIdx.x / R) % p.H, r = blockIdx.x % R;
   if (!(p.flags & (1 << t))) return;
   const bool q = t == 1;  // false: dKr (c2p), true: dQr (p2c)
   const int c4 = threadIdx.x % Q4, part = threadIdx.x / Q4;
-  const int beg = bp.seg[(2 * t) * R + r], end = bp.seg[(2 * t + 1) * R + r];
-  f32x4 acc = zero4();
+  const int beg = bp.rowseg[(2 * t) * R + r], end = bp.rowseg[(2 * t + 1) * R + r];
   const int npairs = (end - beg) * bp.NBG;
-  for (int it = part; it < npairs; it += NP) {
+  auto pair_src = [&](int it) {
     const int d = beg + it / bp.NBG, k = it % bp.NBG;
     const int dblk = (d + bp.f.LkP) / DBW, dd = (d + bp.f.LkP) % DBW;
-    acc += *reinterpret_cast<const f32x4*>(bp.gpart + ((int64_t)(h * bp.NDB + dblk) * bp.NBG + k) * 2 * DBW * D +
-                                           (int64_t)((q ? DBW : 0) + dd) * D + 4 * c4);
+    return reinterpret_cast<const f32x4*>(bp.gpart + ((int64_t)(h * bp.NDB + dblk) * bp.NBG + k) * 2 * DBW * D +
+                                          (int64_t)((q ? DBW : 0) + dd) * D + 4 * c4);
+  };
+  f32x4 a4[4] = {zero4(), zero4(), zero4(), zero4()};
+  int it = part;
+  for (; it + 3 * NP < npairs; it += 4 * NP) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) a4[u] += *pair_src(it + u * NP);
   }
+  for (; it < npairs; it += NP) a4[0] += *pair_src(it);
+  f32x4 acc = (a4[0] + a4[1]) + (a4[2] + a4[3]);
 #pragma unroll
   for (int m = Q4; m < 64; m <<= 1)
 #pragma unroll
     for (int e = 0; e < 4; ++e) acc[e] += __shfl_xor(acc[e], m);
+  if constexpr (NWV > 1) {
+    __shared__ f32x4 wsum[NWV][Q4];
+    const int w = threadIdx.x / 64, lane = threadIdx.x % 64;
+    if (lane < Q4) wsum[w][lane] = acc;
+    __syncthreads();
+    if (w != 0) return;
+    acc = wsum[0][c4];
+#pragma unroll
+    for (int k = 1; k < NWV; ++k) acc += wsum[k][c4];
+  }
   if (part != 0) return;
   const int64_t o = ((int64_t)h * R + r) * D + 4 * c4;
   void* tab = q ? bp.dqr : bp.dkr;

@@ -87,8 +87,9 @@ int check_fwd(const dsa_fwd_args* a) {
   }
   if ((a->flags & DSA_C2P) && !a->kr) return fail("dsa: c2p needs the pos-key table kr");
   if ((a->flags & DSA_P2C) && !a->qr) return fail("dsa: p2c needs the pos-query table qr");
-  if (a->key_keep && a->pair_keep) return fail("dsa: give at most one of key_keep and pair_keep");
-  if ((a->key_keep || a->pair_keep) && a->Lq != a->Lk)
+  if ((a->key_keep ? 1 : 0) + (a->pair_keep ? 1 : 0) + (a->seg ? 1 : 0) > 1)
+    return fail("dsa: give at most one of key_keep, pair_keep and seg");
+  if ((a->key_keep || a->pair_keep || a->seg) && a->Lq != a->Lk)
     return fail("dsa: masks need Lq == Lk (query liveness is read from the key mask)");
   const int vec = 16 / elem_bytes(a->dtype);
   const void* ptrs[] = {a->q, a->k, a->v, a->out};
@@ -131,6 +132,8 @@ dsa::FwdParams to_params(const dsa_fwd_args* a) {
   p.kkb = a->key_keep_stride_b;
   p.pkb = a->pair_keep_strides[0];
   p.pkq = a->pair_keep_strides[1];
+  p.seg = a->seg;
+  p.segb = a->seg_stride_b;
   p.B = a->B;
   p.H = a->H;
   p.Lq = a->Lq;
@@ -144,7 +147,7 @@ dsa::FwdParams to_params(const dsa_fwd_args* a) {
 }
 
 int mask_mode(const dsa_fwd_args* a) {
-  return a->pair_keep ? dsa::MASK_PAIR : (a->key_keep ? dsa::MASK_KEY : dsa::MASK_NONE);
+  return a->pair_keep ? dsa::MASK_PAIR : a->key_keep ? dsa::MASK_KEY : a->seg ? dsa::MASK_SEG : dsa::MASK_NONE;
 }
 
 int launch_check(const char* what) {
@@ -165,6 +168,7 @@ int fwd_mask(const dsa::FwdParams& p, int mode, hipStream_t st) {
   switch (mode) {
     case dsa::MASK_KEY: return launch_fwd<T, D, dsa::MASK_KEY>(p, st);
     case dsa::MASK_PAIR: return launch_fwd<T, D, dsa::MASK_PAIR>(p, st);
+    case dsa::MASK_SEG: return launch_fwd<T, D, dsa::MASK_SEG>(p, st);
     default: return launch_fwd<T, D, dsa::MASK_NONE>(p, st);
   }
 }
@@ -180,7 +184,7 @@ int device_cus() {
 // extents the kernels share.
 struct WsLayout {
   int LqP, LkP, TGP, OFF, NDB, NBG, BPG;
-  size_t rowinfo, krgt, qrgt, ds, gpart, seg, total;
+  size_t rowinfo, krgt, qrgt, ds, gpart, seg, cinfo, total;
 };
 
 WsLayout ws_layout(const dsa_bwd_args* a) {
@@ -212,6 +216,8 @@ WsLayout ws_layout(const dsa_bwd_args* a) {
   if (f.flags) off = align_up(off + (size_t)f.H * w.NDB * w.NBG * 2 * dsa::tbcfg::DBW * f.D * sizeof(float), 256);
   w.seg = off;
   if (f.flags) off = align_up(off + (size_t)2 * 2 * (2 * f.att_span) * sizeof(int), 256);
+  w.cinfo = off;
+  if (f.key_keep || f.seg) off = align_up(off + (size_t)f.B * (w.LqP / 32) * 4 * sizeof(int), 256);
   w.total = off;
   return w;
 }
@@ -241,7 +247,8 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
   bp.qrgt = base + ws.qrgt;
   bp.ds = base + ws.ds;
   bp.gpart = reinterpret_cast<float*>(base + ws.gpart);
-  bp.seg = reinterpret_cast<int*>(base + ws.seg);
+  bp.rowseg = reinterpret_cast<int*>(base + ws.seg);
+  bp.cinfo = (f.key_keep || f.seg) ? reinterpret_cast<int4*>(base + ws.cinfo) : nullptr;
   bp.TGP = ws.TGP;
   bp.OFF = ws.OFF;
   bp.NDB = ws.NDB;
@@ -254,14 +261,15 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
     dsa::PrepBlocks nb;
     const int64_t n = (int64_t)f.B * f.H * ws.LqP * (D / (16 / (int)sizeof(T)));
     nb.delta = (int)((n + 255) / 256);
-    nb.gather = nb.seg = 0;
+    nb.gather = nb.seg = nb.chunk = 0;
+    if (f.key_keep || f.seg) nb.chunk = (int)(((int64_t)f.B * (ws.LqP / 32) + 255) / 256);
     if (f.flags) {
       const int64_t m = 2 * (int64_t)f.H * D * (ws.TGP / (16 / (int)sizeof(T)));
       nb.gather = (int)((m + 255) / 256);
       const int64_t ns = 2 * (int64_t)(f.Lq + f.Lk);
       nb.seg = (int)((ns + 255) / 256);
     }
-    hipLaunchKernelGGL((dsa::dsa_bwd_prep_kernel<T, D>), dim3((unsigned)(nb.gather + nb.seg + nb.delta)), dim3(256), 0,
+    hipLaunchKernelGGL((dsa::dsa_bwd_prep_kernel<T, D>), dim3((unsigned)(nb.gather + nb.seg + nb.chunk + nb.delta)), dim3(256), 0,
                        st, bp, nb);
     if (launch_check("dsa_bwd_prep_kernel")) return 1;
   }
@@ -273,6 +281,9 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
         break;
       case dsa::MASK_PAIR:
         hipLaunchKernelGGL((dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_PAIR>), grid, dim3(256), 0, st, bp);
+        break;
+      case dsa::MASK_SEG:
+        hipLaunchKernelGGL((dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_SEG>), grid, dim3(256), 0, st, bp);
         break;
       default:
         hipLaunchKernelGGL((dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_NONE>), grid, dim3(256), 0, st, bp);
@@ -299,7 +310,11 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
     if (side && hipEventRecord(side->join, sq) != hipSuccess) return fail("dsa: side stream join failed");
   }
   if (fold) {
-    hipLaunchKernelGGL((dsa::dsa_bwd_fold_kernel<D>), dim3((unsigned)(2 * f.H * (2 * f.att_span))), dim3(64), 0, st, bp);
+    const dim3 fg((unsigned)(2 * f.H * (2 * f.att_span)));
+    if (f.Lq + f.Lk > 2048)  // long rows of saturated relative positions: four waves a row
+      hipLaunchKernelGGL((dsa::dsa_bwd_fold_kernel<D, 256>), fg, dim3(256), 0, st, bp);
+    else
+      hipLaunchKernelGGL((dsa::dsa_bwd_fold_kernel<D, 64>), fg, dim3(64), 0, st, bp);
     if (launch_check("dsa_bwd_fold_kernel")) return 1;
   }
   if (side && hipStreamWaitEvent(st, side->join, 0) != hipSuccess) return fail("dsa: side stream join failed");
@@ -310,7 +325,7 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
 
 extern "C" {
 
-int dsa_version(void) { return 3; }
+int dsa_version(void) { return 4; }
 
 const char* dsa_last_error(void) { return g_err.c_str(); }
 

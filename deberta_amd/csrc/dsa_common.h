@@ -141,6 +141,11 @@ DSA_DEV int wave_max(int x) {
   for (int o = 1; o < 64; o <<= 1) x = max(x, __shfl_xor(x, o));
   return x;
 }
+DSA_DEV int wave_and(int x) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) x = x & __shfl_xor(x, o);
+  return x;
+}
 
 // Orders LDS traffic between lanes of one wave (write by one lane, read by
 // another).  DS instructions of a wave complete in order; this keeps the
@@ -330,6 +335,6 @@ DSA_DEV float opaque_one() {
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
-enum MaskMode { MASK_NONE = 0, MASK_KEY = 1, MASK_PAIR = 2 };
+enum MaskMode { MASK_NONE = 0, MASK_KEY = 1, MASK_PAIR = 2, MASK_SEG = 3 };
 
 }  // namespace dsa

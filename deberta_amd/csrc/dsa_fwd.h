@@ -44,6 +44,9 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
   __shared__ short crow[XG], prow[XG];
   __shared__ __align__(16) BT cb_all[NW * CB_ELEMS];
   __shared__ __align__(16) BT pb[PB_ELEMS];
+  constexpr bool SEGM = seg_mode(MASK);
+  __shared__ int segred[SEGM ? 3 * NW : 1];
+  __shared__ __align__(16) int ksg[SEGM ? 2 : 1][SEGM ? BK : 1];  // key segments, by tile parity
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, g = (tid & 63) >> 4, c16 = tid & 15;
@@ -60,18 +63,21 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
   const T* vbase = (const T*)p.v + (int64_t)b * p.vs[0] + (int64_t)h * p.vs[2];
   const T* krh = (p.flags & 1) ? (const T*)p.kr + (int64_t)h * p.krs[0] : nullptr;
   const T* qrh = (p.flags & 2) ? (const T*)p.qr + (int64_t)h * p.qrs[0] : nullptr;
-  const uint8_t* kkb = (MASK == MASK_KEY) ? p.kk + (int64_t)b * p.kkb : nullptr;
   const uint8_t* pkb = (MASK == MASK_PAIR) ? p.pk + (int64_t)b * p.pkb : nullptr;
+  const SegView<MASK> sv(p, b);
 
-  // Per-lane query columns (two 16-wide tiles per wave).
-  int irow[2];
+  // Per-lane query columns (two 16-wide tiles per wave) and their segments.
+  int irow[2], sq[2] = {0, 0};
   bool ilive[2];
 #pragma unroll
   for (int ib = 0; ib < 2; ++ib) {
     irow[ib] = iw + 16 * ib + c16;
     bool valid = irow[ib] < Lq;
     bool live = valid;
-    if (MASK == MASK_KEY && valid) live = kkb[irow[ib]] != 0;
+    if (SEGM && valid) {
+      sq[ib] = sv(irow[ib]);
+      live = sq[ib] != 0;
+    }
     if (MASK == MASK_PAIR && valid) live = pkb[(int64_t)irow[ib] * p.pkq + irow[ib]] != 0;
     ilive[ib] = live;
   }
@@ -99,16 +105,22 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
                                   : nullptr;
 
   // Is any query row of this workgroup live?  If not, nothing to compute.
-  int wg_live = 0;
-  if (tid < BQ) {
-    int i = i0 + tid;
-    if (i < Lq) {
-      if (MASK == MASK_NONE) wg_live = 1;
-      else if (MASK == MASK_KEY) wg_live = kkb[i] != 0;
-      else wg_live = pkb[(int64_t)i * p.pkq + i] != 0;
+  // Segment masks: the range of the workgroup's query segments decides
+  // which key tiles can hold kept pairs.
+  SegRange qsr{0, -1, false};
+  bool any_live;
+  if constexpr (SEGM) {
+    const int i = i0 + tid;
+    qsr = wg_seg_range((tid < BQ && i < Lq) ? sv(i) : 0, tid < BQ, segred);
+    any_live = qsr.any();
+  } else {
+    int wg_live = 0;
+    if (tid < BQ) {
+      int i = i0 + tid;
+      if (i < Lq) wg_live = (MASK == MASK_NONE) ? 1 : pkb[(int64_t)i * p.pkq + i] != 0;
     }
+    any_live = __syncthreads_or(wg_live);
   }
-  const bool any_live = __syncthreads_or(wg_live);
 
   // The next key tile (K and V rows) is fetched into registers while the
   // current one is computed.
@@ -136,11 +148,15 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
   for (int kt = 0; any_live && kt < nkt; ++kt) {
     const int j0 = kt * BK;
     // Skip key tiles that every query row of the workgroup masks out: their
-    // probabilities are exactly zero.
-    if (MASK == MASK_KEY) {
-      int keep = 0;
-      if (tid < BK) keep = (j0 + tid < Lk) && kkb[j0 + tid];
-      if (!__syncthreads_or(keep)) continue;
+    // probabilities are exactly zero.  With segments, a tile whose keys all
+    // share the workgroup's single query segment needs no masking at all.
+    bool full = false;
+    if constexpr (SEGM) {
+      const int j = j0 + tid;
+      const int sk = (tid < BK && j < Lk) ? sv(j) : 0;
+      if (tid < BK) ksg[kt & 1][tid] = sk;
+      if (!__syncthreads_or(qsr.meets(sk))) continue;
+      full = qsr.all && qsr.lo == qsr.hi && __syncthreads_and(tid >= BK || sk == qsr.lo);
     } else if (MASK == MASK_PAIR) {
       int keep = 0;
       const int r = tid >> 1, half = tid & 1;
@@ -189,12 +205,14 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
                               biasl ? biasl + (int64_t)kt * 8192 : nullptr);
 
     // ---- mask: only where a key or query of the tile can be masked out ------
-    if (MASK != MASK_NONE || j0 + BK > Lk) {
+    if (MASK == MASK_PAIR || (SEGM && !full) || j0 + BK > Lk) {
 #pragma unroll
       for (int ib = 0; ib < 2; ++ib) {
         const int i = irow[ib];
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb) {
+          int4 ks4 = {0, 0, 0, 0};
+          if constexpr (SEGM) ks4 = *reinterpret_cast<const int4*>(&ksg[kt & 1][16 * jb + 4 * g]);
           uint32_t pk4 = 0;
           if (MASK == MASK_PAIR && ilive[ib]) {
             const uint8_t* row = pkb + (int64_t)i * p.pkq;
@@ -208,7 +226,7 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
           for (int e = 0; e < 4; ++e) {
             const int j = j0 + 16 * jb + 4 * g + e;
             bool keep = ilive[ib] && j < Lk;
-            if (MASK == MASK_KEY) keep = keep && kkb[j] != 0;
+            if constexpr (SEGM) keep = keep && sq[ib] == (e == 0 ? ks4.x : e == 1 ? ks4.y : e == 2 ? ks4.z : ks4.w);
             if (MASK == MASK_PAIR) keep = keep && ((pk4 >> e) & 1u);
             if (!keep) st[ib][jb][e] = -INFINITY;
           }

@@ -20,12 +20,13 @@ struct FwdParams {
   const int32_t* rel;
   const uint8_t* kk;
   const uint8_t* pk;
+  const int32_t* seg;   // segment ids [B, L] (0: inactive token) or null
   void* out;
   float* lse;
   void* bias;       // saved relative term [B, H, LqP, LkP] or null
   int64_t qs[3], ks[3], vs[3], os[3];
   int64_t krs[2], qrs[2];
-  int64_t kkb, pkb, pkq;
+  int64_t kkb, pkb, pkq, segb;
   int B, H, Lq, Lk, A, flags;
   int LqP, LkP;     // Lq, Lk rounded up to 128 (extents of bias and dS^T)
   float scale;
@@ -48,10 +49,107 @@ struct BwdParams {
   void* krgt;       // [H, D, TGP]: krgt[h][d][t] = Kr[h][c(t - OFF)][d]
   void* qrgt;       // [H, D, TGP]: qrgt[h][d][t] = Qr[h][p(t - OFF)][d]
   float* gpart;     // table-gradient partials [H][NDB][NBG][2][128][D]
-  int* seg;         // [2][2][R]: offsets [begin, end) of each table row (c2p, p2c)
+  int* rowseg;      // [2][2][R]: offsets [begin, end) of each table row (c2p, p2c)
+  int4* cinfo;      // segment masks: [B][LqP / 32] per 32-token chunk (lo, hi, all active, 0)
   int TGP, OFF;     // row length and offset origin of krgt / qrgt
   int NDB, NBG, BPG;  // offset blocks, batch groups, batches per group
 };
+
+// Segment view of the key-padding (MASK_KEY) and segment-id (MASK_SEG)
+// masks: token i of batch row b belongs to segment seg(i), 0 meaning an
+// inactive token.  Pair (i, j) is kept iff seg(i) != 0 and seg(i) ==
+// seg(j), and a query with seg 0 is a dead row.  A key-padding mask is the
+// case seg = (keep ? 1 : 0): a live query keeps exactly the kept keys.  The
+// reference's document-block mask (training/compile.py:310-349) is the case
+// seg = document id: its pad queries are dead rows, whose single kept key
+// (the CLS edge) never reaches an output.
+constexpr bool seg_mode(int mask) { return mask == MASK_KEY || mask == MASK_SEG; }
+
+template <int MASK>
+struct SegView {
+  const uint8_t* kk;
+  const int32_t* sg;
+  DSA_DEV SegView(const FwdParams& p, int b)
+      : kk(MASK == MASK_KEY ? p.kk + (int64_t)b * p.kkb : nullptr),
+        sg(MASK == MASK_SEG ? p.seg + (int64_t)b * p.segb : nullptr) {}
+  DSA_DEV int operator()(int i) const {
+    if constexpr (MASK == MASK_KEY) return kk[i] != 0;
+    else return sg[i];
+  }
+};
+
+// The same view chosen at run time (kernels not specialised on the mask).
+DSA_DEV int seg_at(const FwdParams& p, int b, int i) {
+  return p.seg ? p.seg[(int64_t)b * p.segb + i] : (p.kk[(int64_t)b * p.kkb + i] != 0);
+}
+
+// Backward tile activity under a segment mask, from the per-chunk summaries
+// (dsa_bwd_prep_kernel): the dkdv kernel computes the dS tile of query chunk
+// c (32 queries) and key tile k (128 keys) iff the chunk's segment range
+// meets the union of the key tile's four chunk ranges, and writes nothing
+// for other tiles; the dq and table kernels read dS only where this
+// predicate holds (zeros elsewhere), so all three agree on every element.
+// The dS of a pair outside an active tile is zero: the tile holds no pair of
+// one segment.
+struct ChunkRange {
+  int lo, hi, all;
+  DSA_DEV bool meets(const ChunkRange& o) const { return lo <= hi && o.lo <= o.hi && lo <= o.hi && o.lo <= hi; }
+};
+DSA_DEV ChunkRange chunk_range(const int4* ci, int c) {
+  const int4 v = ci[c];
+  return ChunkRange{v.x, v.y, v.z};
+}
+// union of the ranges of key tile k's four chunks (chunks past nchunks are
+// empty)
+DSA_DEV ChunkRange key_tile_range(const int4* ci, int k, int nchunks) {
+  ChunkRange r{0x7fffffff, (int)0x80000000, 1};
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int c = 4 * k + u;
+    if (c < nchunks) {
+      const ChunkRange x = chunk_range(ci, c);
+      r.lo = min(r.lo, x.lo);
+      r.hi = max(r.hi, x.hi);
+      r.all = r.all && x.all;
+    } else {
+      r.all = 0;
+    }
+  }
+  return r;
+}
+
+// Range [lo, hi] of the nonzero segments among a set of tokens (lo > hi if
+// none) and whether every token of the set is active.  Every thread of the
+// workgroup calls it (it holds two barriers); threads with has = false
+// contribute nothing.  red: NW * 3 ints of LDS.
+struct SegRange {
+  int lo, hi;
+  bool all;
+  DSA_DEV bool any() const { return lo <= hi; }
+  DSA_DEV bool meets(int s) const { return s != 0 && s >= lo && s <= hi; }
+};
+DSA_DEV SegRange wg_seg_range(int s, bool has, int* red) {
+  constexpr int NWG = 4;
+  const bool act = has && s != 0;
+  int lo = wave_min(act ? s : 0x7fffffff), hi = wave_max(act ? s : (int)0x80000000);
+  const int all = wave_and((!has || s != 0) ? 1 : 0);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();  // red may still be read by an earlier call
+  if ((threadIdx.x & 63) == 0) {
+    red[3 * w] = lo;
+    red[3 * w + 1] = hi;
+    red[3 * w + 2] = all;
+  }
+  __syncthreads();
+  SegRange r{0x7fffffff, (int)0x80000000, true};
+#pragma unroll
+  for (int k = 0; k < NWG; ++k) {
+    r.lo = min(r.lo, red[3 * k]);
+    r.hi = max(r.hi, red[3 * k + 1]);
+    r.all = r.all && red[3 * k + 2] != 0;
+  }
+  return r;
+}
 
 template <typename T>
 struct Pad {

@@ -63,17 +63,72 @@ def build_doc_block_mask(doc_ids: torch.Tensor) -> torch.Tensor:
     return keep
 
 
+class SegmentMask:
+    """Compact form of the packed-document keep mask: the ``(B, S)`` document
+    id of every token (0 for padding) in place of the ``(B, 1, S, S)``
+    boolean tensor ``_build_doc_block_mask`` builds (training/compile.py:
+    310-349; ``build_doc_block_mask`` here).
+
+    Accepted as ``attention_mask`` by ``DisentangledSelfAttention`` and
+    ``disentangled_attention``: the kernels read the ids (4 bytes a token
+    instead of S bytes) and skip the key tiles of other documents.  The
+    results are those of ``dense()``, the reference's boolean mask: its pad
+    queries are dead rows (their one kept key, the CLS edge, never reaches
+    an output), so a pair is kept iff both tokens carry the same nonzero id.
+    """
+
+    def __init__(self, doc_ids: torch.Tensor):
+        if not isinstance(doc_ids, torch.Tensor):
+            raise TypeError(f"doc_ids must be a torch.Tensor, got {type(doc_ids)!r}.")
+        if doc_ids.ndim != 2:
+            raise ValueError(f"doc_ids must be rank-2 (B,S); got shape={tuple(doc_ids.shape)}")
+        if doc_ids.dtype == torch.bool or torch.is_floating_point(doc_ids):
+            raise ValueError(f"doc_ids must be an integer tensor; got {doc_ids.dtype}")
+        self.doc_ids = doc_ids
+
+    @property
+    def shape(self) -> tuple[int, int, int, int]:
+        b, s = self.doc_ids.shape
+        return (b, 1, s, s)
+
+    def dense(self) -> torch.Tensor:
+        """The reference's ``(B, 1, S, S)`` boolean keep mask."""
+        return build_doc_block_mask(self.doc_ids)[:, None]
+
+    def segment_ids(self, device: torch.device) -> torch.Tensor:
+        """``int32 [B, S]`` ids on ``device`` (the kernels' ``seg``)."""
+        ids = self.doc_ids
+        if ids.dtype != torch.int32:
+            if ids.numel() and (int(ids.max()) > 2**31 - 1 or int(ids.min()) < -(2**31)):
+                raise ValueError("doc_ids must fit in int32")
+            ids = ids.to(torch.int32)
+        return ids.to(device).contiguous()
+
+
 def kernel_masks(
-    attention_mask: Optional[torch.Tensor], batch: int, query_len: int, key_len: int
+    attention_mask: "Optional[torch.Tensor | SegmentMask]",
+    batch: int,
+    query_len: int,
+    key_len: int,
+    device: Optional[torch.device] = None,
 ) -> tuple[Optional[torch.Tensor], Optional[torch.Tensor]]:
     """Split a rank-4 keep mask into the kernels' ``(key_keep, pair_keep)``.
 
     ``(B|1, 1, 1, K)`` becomes a ``[B, K]`` byte view (``key_keep``),
     ``(B|1, 1, Q, K)`` a ``[B, Q, K]`` byte view (``pair_keep``).  A batch
-    dimension of 1 is broadcast with stride 0.  ``None`` means no mask.
+    dimension of 1 is broadcast with stride 0.  A ``SegmentMask`` becomes
+    ``int32 [B, S]`` segment ids in the ``key_keep`` slot, on ``device``
+    (default: the ids' own).  ``None`` means no mask.
     """
     if attention_mask is None:
         return None, None
+    if isinstance(attention_mask, SegmentMask):
+        ids = attention_mask.doc_ids
+        if ids.shape[0] != batch or ids.shape[1] != key_len or query_len != key_len:
+            raise ValueError(
+                f"SegmentMask of shape {tuple(ids.shape)} does not match (B={batch}, Q={query_len}, K={key_len})"
+            )
+        return attention_mask.segment_ids(device if device is not None else ids.device), None
     keep = normalize_keep_mask(attention_mask)
     if keep.ndim != 4:
         raise ValueError(f"attention_mask must be rank-4 [B,1,Q,K]; got shape={tuple(keep.shape)}")

@@ -11,7 +11,9 @@ Tensor layouts (see include/dsa.h):
   kr, qr            [H, 2A, D] views (projected relative tables) or None
   rel_table         int32 [Lq + Lk - 1]: relative position of offset i - j at
                     index (i - j) + (Lk - 1)
-  key_keep          uint8 [B, Lk] or None  (broadcast keep mask)
+  key_keep          uint8 [B, Lk] (broadcast keep mask), or int32 [B, L]
+                    segment ids (0: inactive token; pair (i, j) kept iff
+                    both ids are equal and nonzero), or None
   pair_keep         uint8 [B, Lq, Lk] or None (pairwise keep mask)
   out               [B, Lq, H, D] contiguous, dtype of q
   lse               float32 [B, H, Lq]
@@ -92,6 +94,9 @@ def _fill_fwd_args(
     a.q, a.k, a.v = q.data_ptr(), k.data_ptr(), v.data_ptr()
     a.kr, a.qr = _ptr(kr), _ptr(qr)
     a.rel_table = _ptr(rel_table)
+    if key_keep is not None and key_keep.dtype == torch.int32:
+        a.seg, a.seg_stride_b = key_keep.data_ptr(), key_keep.stride(0)
+        key_keep = None
     a.key_keep, a.pair_keep = _ptr(key_keep), _ptr(pair_keep)
     a.out, a.lse = out.data_ptr(), lse.data_ptr()
     a.bias = _ptr(bias) if bias is not None and bias.numel() else None

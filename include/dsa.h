@@ -40,6 +40,14 @@
  *     follows the reference (deberta_v2_native.py:625-639): key_keep[b,i]
  *     for the broadcast form, pair_keep[b,i,i] for the pairwise form; dead
  *     query rows produce exactly zero output and zero gradient.
+ *     seg is a compact form of block-diagonal masks: an int32 [B, L]
+ *     segment id per token (Lq == Lk), 0 for an inactive token.  Pair
+ *     (i, j) is kept iff seg[b,i] != 0 and seg[b,i] == seg[b,j]; a query
+ *     with seg 0 is a dead row.  With seg = document ids this is the
+ *     reference's packed-document mask (training/compile.py:310-349, whose
+ *     pad queries are dead rows); key_keep is the case seg = keep ? 1 : 0.
+ *     The kernels skip tiles whose query and key segments cannot meet.
+ *     At most one of key_keep, pair_keep and seg may be given.
  */
 #ifndef DSA_H_
 #define DSA_H_
@@ -95,6 +103,8 @@ typedef struct dsa_fwd_args {
   int32_t dtype;          /* DSA_F32 or DSA_BF16 */
   int32_t flags;          /* DSA_C2P | DSA_P2C */
   float scale;            /* 1/sqrt(D * scale_factor) */
+  const int32_t* seg;     /* [B, L] segment ids or NULL (see Masks above) */
+  int64_t seg_stride_b;
 } dsa_fwd_args;
 
 typedef struct dsa_bwd_args {

@@ -22,7 +22,7 @@ class Case:
     buckets: int = 256
     max_pos: int = 512
     types: str = "c2p|p2c"
-    mask: str = "none"  # none | key | pair | dead
+    mask: str = "none"  # none | key | pair | seg | seg_mixed | dead
     seed: int = 0
     Lk: Optional[int] = None
     std: float = 1.0
@@ -50,12 +50,13 @@ def make_inputs(c: Case) -> dict:
     dout = torch.randn(c.B, c.L, c.H, c.D, generator=g)
     if c.ramp:
         k = k * (1 + c.ramp * torch.arange(Lk, dtype=torch.float32) / Lk)[None, :, None, None]
-    mask = None
+    mask = seg = None
     if c.mask == "key":
         lens = torch.randint(max(1, c.L // 8), c.L + 1, (c.B,), generator=g)
         lens[0] = c.L
         mask = (torch.arange(c.L)[None, :] < lens[:, None])[:, None, None, :]
-    elif c.mask == "pair":
+    elif c.mask in ("pair", "seg"):
+        # packed documents: contiguous runs of ids 1, 2, ..., a padded tail (id 0)
         ids = torch.zeros(c.B, c.L, dtype=torch.long)
         for b in range(c.B):
             pos, doc = 0, 1
@@ -68,13 +69,22 @@ def make_inputs(c: Case) -> dict:
             if pad:
                 ids[b, c.L - pad :] = 0
         mask = eager.doc_block_mask(ids)[:, None]
+        if c.mask == "seg":
+            seg = ids
+    elif c.mask == "seg_mixed":
+        # interleaved segments (ids repeat out of order) and scattered
+        # inactive tokens: every tile's segment range overlaps
+        ids = (torch.arange(c.L)[None, :] // 7 + torch.arange(c.B)[:, None]) % 3 + 1
+        ids = ids * (torch.rand(c.B, c.L, generator=g) > 0.1)
+        mask = eager.doc_block_mask(ids)[:, None]
+        seg = ids
     elif c.mask == "dead":
         keep = torch.rand(c.B, c.L, c.L, generator=g) < 0.5
         live = torch.rand(c.B, c.L, generator=g) < 0.7
         eye = torch.eye(c.L, dtype=torch.bool)
         keep = (keep & ~eye) | (eye & live[:, :, None])
         mask = keep[:, None]
-    return dict(q=q, k=k, v=v, kr=kr, qr=qr, dout=dout, mask=mask)
+    return dict(q=q, k=k, v=v, kr=kr, qr=qr, dout=dout, mask=mask, seg=seg)
 
 
 def oracle_run(c: Case, x: dict, dtype: torch.dtype, grads: bool = True) -> dict:
@@ -117,8 +127,13 @@ def hip_run(c: Case, x: dict, dtype: torch.dtype, device, grads: bool = True) ->
     table = None
     if kr is not None or qr is not None:
         table = relative_offset_table(c.L, Lk, bucket_size=c.buckets, max_position=c.max_pos, device=device)
-    mask = x["mask"].to(device) if x["mask"] is not None else None
-    kk, pk = kernel_masks(mask, c.B, c.L, Lk)
+    if x.get("seg") is not None:
+        from deberta_amd.masks import SegmentMask
+
+        mask = SegmentMask(x["seg"])
+    else:
+        mask = x["mask"].to(device) if x["mask"] is not None else None
+    kk, pk = kernel_masks(mask, c.B, c.L, Lk, device)
     sf = 1 + sum(t in types for t in ("c2p", "p2c", "p2p"))
     scale = 1.0 / math.sqrt(c.D * sf)
     out, lse, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, kk, pk, c.A, scale)

@@ -105,18 +105,20 @@ def test_growing_scores(mask, dtype, gpu):
     [
         (Case(B=1, H=2, L=4096, D=64, mask="pair", seed=51), torch.bfloat16),
         (Case(B=1, H=2, L=4096, D=64, mask="pair", seed=52), torch.float32),
+        (Case(B=1, H=2, L=4096, D=64, mask="seg", seed=51), torch.bfloat16),
+        (Case(B=1, H=2, L=4096, D=64, mask="seg", seed=52), torch.float32),
         (Case(B=1, H=2, L=4096, D=64, seed=53), torch.bfloat16),
         (Case(B=2, H=2, L=2048, D=64, mask="key", seed=54), torch.float32),
         (Case(B=2, H=16, L=512, D=64, seed=55), torch.bfloat16),
     ],
-    ids=["L4096-doc-bf16", "L4096-doc-fp32", "L4096-bf16", "L2048-key-fp32", "H16-bf16"],
+    ids=["L4096-doc-bf16", "L4096-doc-fp32", "L4096-seg-bf16", "L4096-seg-fp32", "L4096-bf16", "L2048-key-fp32", "H16-bf16"],
 )
 def test_long_sequences(c, dtype, gpu):
     _check(c, dtype, gpu)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
-@pytest.mark.parametrize("mask", ["key", "pair", "dead"])
+@pytest.mark.parametrize("mask", ["key", "pair", "seg", "seg_mixed", "dead"])
 def test_masks(mask, dtype, gpu):
     c = Case(B=3, H=2, L=260, D=64, mask=mask, seed=11)
     got = _check(c, dtype, gpu)
