@@ -36,6 +36,17 @@ B, L, H, D, BUCKETS, MAX_POS = 32, 512, 12, 64, 256, 512
 A = BUCKETS
 R = 2 * A
 
+# --workload: the headline (default) and the other BASELINE shapes that fit
+# one GPU, for reference figures; only the headline's line is the metric.
+#   name: (batch, seq_len, heads, mask kind, description)
+WORKLOADS = {
+    "headline": (32, 512, 12, None, "BASELINE configs[1] shape, all-ones mask"),
+    "C2pad": (32, 512, 12, "key", "configs[1] shape, per-row valid length ~U{64..512} as a (B,1,1,L) key mask"),
+    "C5": (64, 512, 16, None, "B=64 L=512 H=16, no mask"),
+    "C4": (4, 4096, 12, "doc", "B=4 L=4096 H=12, packed documents (lengths ~Geometric(mean 600)) as the dense (B,1,L,L) doc-block mask"),
+    "C4seg": (4, 4096, 12, "seg", "as C4, the same documents given as segment ids (SegmentMask)"),
+}
+
 
 # HBM bytes per launch at this workload, from two rocprofv3 --pmc passes over
 # `bench.py --kernels-only` (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch),
@@ -63,6 +74,36 @@ def hbm_bytes(stage: str):
 
 def flops_fwd(b: int, l: int, h: int, d: int, r: int) -> float:
     return 4.0 * b * h * d * l * l + 4.0 * b * h * d * l * r
+
+
+def workload_mask(kind, b: int, l: int, g, dev):
+    """Synthetic mask of a workload, drawn from the generator g.
+
+    Returns (attention_mask, kept pairs, live query rows)."""
+    import torch
+
+    from deberta_amd.masks import SegmentMask, build_doc_block_mask
+
+    if kind is None:
+        return None, b * l * l, b * l
+    if kind == "key":
+        lens = torch.randint(64, l + 1, (b,), generator=g)
+        keep = torch.arange(l)[None, :] < lens[:, None]
+        return keep[:, None, None, :].to(dev), int((lens.double() ** 2).sum()), int(lens.sum())
+    ids = torch.zeros(b, l, dtype=torch.int64)
+    for r in range(b):  # document lengths 1 + Geometric(p = 1/600) by inversion, cut at the row's end
+        pos, doc = 0, 1
+        while pos < l:
+            u = float(torch.rand((), generator=g, dtype=torch.float64))
+            n = 1 + int(math.floor(math.log1p(-u) / math.log1p(-1.0 / 600.0)))
+            n = min(n, l - pos)
+            ids[r, pos : pos + n] = doc
+            pos, doc = pos + n, doc + 1
+    dense = build_doc_block_mask(ids)
+    kept = int(dense.sum())
+    if kind == "doc":
+        return dense[:, None].to(dev), kept, b * l
+    return SegmentMask(ids.to(dev)), kept, b * l
 
 
 def cpu_model() -> str:
@@ -126,6 +167,12 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument(
+        "--workload",
+        choices=sorted(WORKLOADS),
+        default="headline",
+        help="shape and mask; the headline is the metric, the others print reference figures",
+    )
+    ap.add_argument(
         "--kernels-only",
         action="store_true",
         help="only run each kernel --steps times (for rocprofv3 counter passes); prints per-kernel times",
@@ -149,10 +196,13 @@ def main() -> None:
 
     import deberta_amd  # noqa: F401
     from deberta_amd import _lib, ops
+    from deberta_amd.masks import kernel_masks
     from deberta_amd.relpos import relative_offset_table
 
     lib = _lib.load()
     dev = torch.device("cuda:0")
+    B, L, H, mask_kind, wl_desc = WORKLOADS[args.workload]
+    headline = args.workload == "headline"
     g = torch.Generator(device="cpu").manual_seed(0)
     mk = lambda *s: torch.randn(*s, generator=g).to(device=dev, dtype=torch.bfloat16)
     q, k, v = mk(B, L, H, D), mk(B, L, H, D), mk(B, L, H, D)
@@ -163,9 +213,11 @@ def main() -> None:
     table = relative_offset_table(L, L, bucket_size=BUCKETS, max_position=MAX_POS, device=dev)
     scale = 1.0 / math.sqrt(D * 3)
     leaves = (q, k, v, kr, qr)
+    mask, kept_pairs, live_rows = workload_mask(mask_kind, B, L, g, dev)
+    kk, pk = kernel_masks(mask, B, L, L, dev)
 
     def step():
-        out, _, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, A, scale)
+        out, _, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, kk, pk, A, scale)
         return torch.autograd.grad(out, leaves, dout)
 
     if args.copy_probe_mib:
@@ -200,14 +252,17 @@ def main() -> None:
     f_fwd = flops_fwd(B, L, H, D, R)
     f_step = 3 * f_fwd
     tflops = f_step / (ms_step * 1e-3) / 1e12
+    # masked work counted over kept pairs and live rows only (the skipped
+    # pairs are not work): 3 x (4 H D kept + 4 H D R live)
+    f_kept = 3.0 * H * D * (4.0 * kept_pairs + 4.0 * R * live_rows)
 
     # ---- per-kernel times: each launch timed on the stream it runs on ------------
     stream = torch.cuda.current_stream(dev)
-    out, lse, bias = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, A, scale)
+    out, lse, bias = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, kk, pk, A, scale)
     f32 = dict(dtype=torch.float32, device=dev)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     dkr, dqr = torch.zeros((H, R, D), **f32), torch.zeros((H, R, D), **f32)
-    bargs = ops.fill_bwd_args(dout, q, k, v, kr, qr, table, None, None, out, lse, bias, A, scale, dq, dk, dv, dkr, dqr)
+    bargs = ops.fill_bwd_args(dout, q, k, v, kr, qr, table, kk, pk, out, lse, bias, A, scale, dq, dk, dv, dkr, dqr)
     ws = torch.empty((ops.bwd_workspace_bytes(bargs),), dtype=torch.uint8, device=dev)
     bargs.workspace, bargs.workspace_bytes = ws.data_ptr(), ws.numel()
     fargs = bargs.fwd
@@ -252,6 +307,25 @@ def main() -> None:
     achieved = kernels[dom][1] / (dom_ms * 1e-3) / 1e12
     if args.kernels_only:
         print(json.dumps({"per_kernel": per_kernel}), flush=True)
+        return
+    if not headline:
+        # reference figures of another shape: not the metric (no roofline or
+        # CPU leg; per-kernel TFLOP/s use the dense counts)
+        print(
+            json.dumps(
+                {
+                    "workload": args.workload,
+                    "description": wl_desc,
+                    "ms_per_step": round(ms_step, 4),
+                    "tflops_dense_count": round(tflops, 2),
+                    "kept_pair_fraction": round(kept_pairs / (B * L * L), 4),
+                    "tflops_kept_pairs": round(f_kept / (ms_step * 1e-3) / 1e12, 2),
+                    "steps": args.steps,
+                    "per_kernel": per_kernel,
+                }
+            ),
+            flush=True,
+        )
         return
 
     res = {

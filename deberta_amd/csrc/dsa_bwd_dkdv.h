@@ -77,9 +77,10 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
   __shared__ __align__(16) T Stg[NW * SW];        // each wave's dS^T tile
   constexpr bool SEGM = seg_mode(MASK);
   constexpr int MAXQT = 1024;  // query tiles (Lq <= 32768)
-  // segment masks: per query tile, bit 0 = active (dS computed and
-  // written), bit 1 = no masking needed; query segments of MASK_SEG tiles
-  __shared__ unsigned char qflag[SEGM ? MAXQT : 1];
+  // segment masks: the active query tiles in order (tile | 0x4000 if it
+  // needs no masking); query segments of MASK_SEG tiles
+  __shared__ short qlist[SEGM ? MAXQT : 1];
+  __shared__ int qlen;
   __shared__ __align__(16) int qsg[MASK == MASK_SEG ? 2 : 1][MASK == MASK_SEG ? BQ : 1];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -118,19 +119,30 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
     if (SEGM && j < Lk) jseg[jb] = sv(j);
     jkeep[jb] = j < Lk && (!SEGM || jseg[jb] != 0);
   }
-  // Segment masks: which query tiles meet this key tile (ChunkRange); the
-  // others are neither computed nor written.
+  // Segment masks: the query tiles that meet this key tile (ChunkRange),
+  // listed by wave 0 (one chunk per lane); the others are neither computed
+  // nor written.
   bool any_key;
+  int nlist = nqt;
   if constexpr (SEGM) {
     const ChunkRange kr = key_tile_range(bp.cinfo + (int64_t)b * nqt, kt, nqt);
-    for (int c = tid; c < nqt; c += 256) {
-      const ChunkRange x = chunk_range(bp.cinfo + (int64_t)b * nqt, c);
-      const bool act = x.meets(kr);
-      const bool full = act && x.all && kr.all && x.lo == x.hi && kr.lo == kr.hi && x.lo == kr.lo;
-      qflag[c] = (act ? 1 : 0) | (full ? 2 : 0);
+    if (w == 0) {
+      int n = 0;
+      for (int c0 = 0; c0 < nqt; c0 += 64) {
+        const int c = c0 + lane;
+        bool act = false, full = false;
+        if (c < nqt) {
+          const ChunkRange x = chunk_range(bp.cinfo + (int64_t)b * nqt, c);
+          act = x.meets(kr);
+          full = act && x.all && kr.all && x.lo == x.hi && kr.lo == kr.hi && x.lo == kr.lo;
+        }
+        n = wave_append(act, (short)(c | (full ? 0x4000 : 0)), qlist, n);
+      }
+      if (lane == 0) qlen = n;
     }
-    any_key = kr.lo <= kr.hi;
     __syncthreads();
+    nlist = __builtin_amdgcn_readfirstlane(qlen);
+    any_key = nlist > 0;
   } else {
     any_key = __syncthreads_or(tid < BKW && j0 + tid < Lk);
   }
@@ -156,15 +168,11 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
 
   // Issues the LDS copies of query tile qi into the given buffers (lane
   // order = physical chunk order; Q and dO rows are clamped to Lq - 1, where
-  // probabilities are zero anyway), and its qrgt block (whose ring slot was
-  // last read two tiles earlier).
+  // probabilities are zero anyway), and, with ring set, its qrgt block
+  // (whose ring slot was last read two tiles earlier).
   int qseg_next = 0;  // MASK_SEG: query segment of lane (w = 1, lane < 32) in the next tile
-  auto issue = [&](int qi, T* Qd, T* dOd, BT* Bd, float* Rd) {
+  auto issue = [&](int qi, bool ring, T* Qd, T* dOd, BT* Bd, float* Rd) {
     const int i0 = qi * BQ;
-    if (SEGM && !(qflag[qi] & 1)) {  // inactive tile: only the ring advances
-      if (p2c) issue_ring(tw0 / 32 + qi + 4);
-      return;
-    }
     if (MASK == MASK_SEG && w == 1 && lane < BQ) qseg_next = (i0 + lane < Lq) ? sv(i0 + lane) : 0;
 #pragma unroll
     for (int k = 0; k < (QCW + 63) / 64; ++k) {
@@ -190,7 +198,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
       }
     }
     if (w == 0 && lane < 2 * BQ * 4 / 16) lds_dma16(rib + 2 * i0 + 4 * lane, (char*)Rd);
-    if (p2c) issue_ring(tw0 / 32 + qi + 4);
+    if (p2c && ring) issue_ring(tw0 / 32 + qi + 4);
   };
 
   // dS rows i of the wave's 32 keys: lane (g, c16) writes keys jw + 16 kk +
@@ -226,29 +234,42 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
       static_assert(SW % VEC == 0, "whole chunks");
       for (int c = lane; c < SW / VEC; c += 64) reinterpret_cast<vecT*>(stg)[c] = z;
     }
-    // the ring's first window, older blocks
+    // The qrgt ring holds blocks [qi, qi + 4] of the window (relative to
+    // tw0 / 32) while tile qi is computed; block qi + 5 lands in the sixth
+    // slot meanwhile when the next tile is qi + 1.  The first window:
+    const int qfirst = SEGM ? (__builtin_amdgcn_readfirstlane(qlist[0]) & 0x3ff) : 0;
     if (p2c)
-      for (int r = 0; r < 4; ++r) issue_ring(tw0 / 32 + r);
-    issue(0, Qs0, dOs0, Bs0, Rs0);
+      for (int r = 0; r < 4; ++r) issue_ring(tw0 / 32 + qfirst + r);
+    issue(qfirst, true, Qs0, dOs0, Bs0, Rs0);
     lds_dma_wait();
-    auto tile = [&](int qi, const T* Q, const T* dO, const BT* Bt, const float* R, T* nQ, T* ndO, BT* nBt,
+    auto tile = [&](int n, const T* Q, const T* dO, const BT* Bt, const float* R, T* nQ, T* ndO, BT* nBt,
                     float* nR) {
-      const int i0 = qi * BQ;
+      const int ent = SEGM ? __builtin_amdgcn_readfirstlane(qlist[n]) : n;
+      const int qi = ent & 0x3ff, i0 = qi * BQ;
       // This wave's copies of tile qi have landed: they were issued before
       // the previous tile's four dS stores, its last vector-memory
-      // instructions (tile 0 was waited for before the loop).  Under a
-      // segment mask an inactive previous tile stored nothing.
-      const int fl = SEGM ? qflag[qi] : 1;
-      if (SEGM && qi > 0 && !(qflag[qi - 1] & 1)) vm_wait<0>();
-      else vm_wait<4>();
-      if (MASK == MASK_SEG && w == 1 && lane < BQ) qsg[qi & 1][lane] = qseg_next;
-      __syncthreads();  // ... every wave's, and tile qi - 1 is no longer read
-      if (qi + 1 < nqt) issue(qi + 1, nQ, ndO, nBt, nR);
-      if (SEGM && !(fl & 1)) return;  // no pair of one segment: nothing computed or written
+      // instructions (tile 0 was waited for before the loop).
+      vm_wait<4>();
+      if (MASK == MASK_SEG && w == 1 && lane < BQ) qsg[n & 1][lane] = qseg_next;
+      __syncthreads();  // ... every wave's, and the previous tile is no longer read
+      if (SEGM && p2c && n > 0) {
+        // after skipped tiles: the blocks of this tile's window not in the
+        // ring yet (their slots hold blocks no longer needed)
+        const int pv = __builtin_amdgcn_readfirstlane(qlist[n - 1]) & 0x3ff;
+        if (qi > pv + 1) {
+          for (int x = max(qi, pv + 5); x <= qi + 4; ++x) issue_ring(tw0 / 32 + x);
+          vm_wait<0>();
+          __syncthreads();
+        }
+      }
+      if (n + 1 < nlist) {
+        const int qn = SEGM ? (__builtin_amdgcn_readfirstlane(qlist[n + 1]) & 0x3ff) : n + 1;
+        issue(qn, qn == qi + 1, nQ, ndO, nBt, nR);
+      }
       // With segments, a tile whose queries all share the workgroup's single
       // key segment needs no masking beyond the dead-row test.  Other modes:
       // tiles without a kept (query, key) pair store zeros.
-      const bool full = SEGM && (fl & 2);
+      const bool full = SEGM && (ent & 0x4000);
       bool skip = !SEGM && i0 >= Lq;
       if (!skip && MASK == MASK_PAIR) {
         int keep = 0;
@@ -324,7 +345,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
             // rows without probabilities (dead, padding) have lr = inf and may hold an
             // unwritten saved term: they are never exponentiated
             bool keep = jkeep[jb] && lr != INFINITY;
-            if (MASK == MASK_SEG && !full) keep = keep && qsg[qi & 1][il] == jseg[jb];
+            if (MASK == MASK_SEG && !full) keep = keep && qsg[n & 1][il] == jseg[jb];
             if (MASK == MASK_PAIR) keep = keep && pkb[(int64_t)min(i0 + il, Lq - 1) * p.pkq + jcol[jb]] != 0;
             const float pe = keep ? __builtin_amdgcn_exp2f(__builtin_fmaf(sc[jb][ib][e], sl2, -lr)) : 0.f;
             pp[jb][ib][e] = pe;
@@ -395,9 +416,9 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
         }
       }
     };
-    for (int qi = 0; qi < nqt; qi += 2) {
-      tile(qi, Qs0, dOs0, Bs0, Rs0, Qs1, dOs1, Bs1, Rs1);
-      if (qi + 1 < nqt) tile(qi + 1, Qs1, dOs1, Bs1, Rs1, Qs0, dOs0, Bs0, Rs0);
+    for (int n = 0; n < nlist; n += 2) {
+      tile(n, Qs0, dOs0, Bs0, Rs0, Qs1, dOs1, Bs1, Rs1);
+      if (n + 1 < nlist) tile(n + 1, Qs1, dOs1, Bs1, Rs1, Qs0, dOs0, Bs0, Rs0);
     }
   }
 

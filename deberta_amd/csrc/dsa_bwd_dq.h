@@ -127,24 +127,25 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dq_kernel(BwdParams bp) {
   // inactive chunks are read as zeros.  klist holds kt | (chunk mask << 10).
   int nkt = bp.f.LkP / BK;
   if (bp.cinfo) {
-    const int nch = bp.f.LqP / 32;
-    const int4* ci = bp.cinfo + (int64_t)b * nch;
-    for (int kt = tid; kt < nkt; kt += 256) {
-      const ChunkRange kr = key_tile_range(ci, kt / 2, nch);
-      int mask = 0;
-#pragma unroll
-      for (int u = 0; u < BQ / 32; ++u) mask |= chunk_range(ci, i0 / 32 + u).meets(kr) ? (1 << u) : 0;
-      klist[kt] = (short)(mask ? (kt | (mask << 10)) : -1);
-    }
-    __syncthreads();
-    if (tid == 0) {
+    // listed by wave 0, one key tile per lane
+    if (tid < 64) {
+      const int nch = bp.f.LqP / 32;
+      const int4* ci = bp.cinfo + (int64_t)b * nch;
       int n = 0;
-      for (int kt = 0; kt < nkt; ++kt)
-        if (klist[kt] >= 0) klist[n++] = klist[kt];  // n <= kt: compaction in place
-      segred[0] = n;
+      for (int k0 = 0; k0 < nkt; k0 += 64) {
+        const int kt = k0 + tid;
+        int mask = 0;
+        if (kt < nkt) {
+          const ChunkRange kr = key_tile_range(ci, kt / 2, nch);
+#pragma unroll
+          for (int u = 0; u < BQ / 32; ++u) mask |= chunk_range(ci, i0 / 32 + u).meets(kr) ? (1 << u) : 0;
+        }
+        n = wave_append(mask != 0, (short)(kt | (mask << 10)), klist, n);
+      }
+      if (tid == 0) segred[0] = n;
     }
     __syncthreads();
-    nkt = segred[0];
+    nkt = __builtin_amdgcn_readfirstlane(segred[0]);
   } else {
     for (int t = tid; t < nkt; t += 256) klist[t] = (short)(t | (0xf << 10));
     __syncthreads();

@@ -9,9 +9,10 @@
 // (prep_segments in dsa_bwd_prep_kernel finds them).
 //
 // dsa_bwd_table_kernel: one workgroup = (128-offset block [d0, d0+128),
-// head h, batch group).  Waves 0 and 1 compute Gc, waves 2 and 3 Gp, each
-// wave on its own items, staged into its own part of LDS (no workgroup
-// barrier until the end).  An item is one batch and 32 rows:
+// head h, partial group: a range of the block's items).  Waves 0 and 1
+// compute Gc, waves 2 and 3 Gp, each wave on its own items, staged into its
+// own part of LDS (no workgroup barrier until the end).  An item is one
+// batch and 32 rows:
 //   Gc item: queries [i0, i0+32); region X[r][c] = dS(i0 + r, i0 - d0 - 128 + c)
 //            (32 x 168); the pair (r, r + e + 1) has offset d0 + 127 - e, so
 //            Gc^T[:, e] += sum_r Q^T[:, i0 + r] X[r][r + e + 1]
@@ -27,8 +28,9 @@
 // offsets x D in registers (fp32) and prefetches its next item's global
 // data into registers while it computes.  The two waves of a kind sum their
 // accumulators through LDS and write one fp32 partial per (block, head,
-// batch group, kind).  The Gc and Gp waves of a workgroup sweep the same
-// batch's band of dS together, so the second reader of each dS line
+// partial group, kind), with a flag; a partial whose items are all inactive
+// under a mask is not written.  The Gc and Gp waves of a workgroup sweep the
+// same batch's band of dS together, so the second reader of each dS line
 // finds it in L2.
 #pragma once
 
@@ -95,7 +97,9 @@ DSA_DEV void block_items(int dblk, int LkP, int Lq, int Lk, bool p2c, int* start
   *n = e > s ? (e - s + CH - 1) / CH : 0;
 }
 
-template <typename T, int D>
+// LISTED: a key-padding or segment mask is given (bp.cinfo): items without
+// an active part are skipped and partials carry flags.
+template <typename T, int D, bool LISTED>
 __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
   using namespace tbcfg;
   using M = Mfma<T>;
@@ -116,6 +120,8 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
   const FwdParams& p = bp.f;
 
   __shared__ __align__(16) T lds[NW * WELEMS];
+  __shared__ int ilist[NW][64];  // per wave: the active items of a window of 64 candidates
+  __shared__ int nact_sh[NW];
 
   const int tid = threadIdx.x;
   // the wave index, known to the compiler as uniform (the item loop's
@@ -123,20 +129,34 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 4, c16 = lane & 15;
   const bool p2c = w >= 2;  // wave kind: 0, 1 -> Gc; 2, 3 -> Gp
   const int sub = w & 1;
-  // Work order: blockIdx.x enumerates (offset block, head, batch group) with
-  // the offset blocks that have the most items first, so the shortest
+  // Work order: blockIdx.x enumerates (offset block, head, partial group)
+  // with the offset blocks that have the most items first, so the shortest
   // workgroups fill in at the end of the launch.
-  const int per_blk = p.H * bp.NBG;
+  const int per_blk = p.H * bp.NPG;
   const int rank = blockIdx.x / per_blk, rem = blockIdx.x % per_blk;
-  const int h = rem / bp.NBG, bg = rem % bp.NBG;
+  const int h = rem / bp.NPG, pg = rem % bp.NPG;
   const int mid = (bp.NDB - 1) / 2;  // central blocks hold the most pairs
   const int dblk = (rank & 1) ? mid + 1 + (rank >> 1) : mid - (rank >> 1);
   const int d0 = -p.LkP + DBW * dblk;
   const bool active = (p.flags & (p2c ? 2 : 1)) != 0;
-  const int b_lo = bg * bp.BPG, b_hi = min(p.B, b_lo + bp.BPG);
   int rstart, nch;
   block_items(dblk, p.LkP, p.Lq, p.Lk, p2c, &rstart, &nch);
-  const int nitems = (active && b_hi > b_lo) ? (b_hi - b_lo) * nch : 0;
+  // The block's items of one kind, (batch, 32-row chunk) batch-major, are
+  // split into NPG contiguous ranges; partial group pg takes range pg.
+  const int total = active ? p.B * nch : 0;
+  const int per = (total + bp.NPG - 1) / bp.NPG;
+  const int it_lo = min(total, pg * per), nitems = min(total, it_lo + per) - it_lo;
+  // A block whose offsets all lie in the offset range of one table row of
+  // its kind (where the relative position saturates, or in a wide log
+  // bucket) is stored summed over its offsets, in row 0 of its partial
+  // (flag 2): the fold reads one row of it instead of 128.  The fold finds
+  // the same blocks from the same ranges.
+  bool collapse = false;
+  if (active && d0 >= -(p.Lk - 1) && d0 + DBW <= p.Lq) {
+    const int R = 2 * p.A, t = p2c ? 1 : 0;
+    const int r = offset_row(p.rel, d0, p.Lq, p.Lk, p.A, p2c);
+    collapse = bp.rowseg[(2 * t) * R + r] <= d0 && bp.rowseg[(2 * t + 1) * R + r] >= d0 + DBW;
+  }
 
   T* X = lds + w * WELEMS;  // this wave's region
   T* Rw = X + XELEMS;       // and its item rows (Q for Gc, K for Gp)
@@ -157,6 +177,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
   // slice of dS (rows before 0 or past LqP: negative offsets are huge as
   // unsigned), for Gc chunks whose columns lie outside [0, LkP) (their
   // offset is pushed past the range), and for item rows past Lq / Lk.
+  int nact = 0;  // items with an active part, this wave
   auto run = [&](auto kind) {
     constexpr bool P = decltype(kind)::value;
     constexpr int CPR = P ? CH / VEC : (DBW + CH) / VEC;  // Gc region: 160 columns read per row
@@ -185,7 +206,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
     // item without active parts is skipped.
     const int nqc = p.LqP / 32, nkt128 = p.LkP / 128;
     auto item_mask = [&](int b, int r0) -> int {
-      if (!bp.cinfo) return 0xff;
+      if (!LISTED) return 0xff;
       const int4* ci = bp.cinfo + (int64_t)b * nqc;
       int m = 0;
       if constexpr (!P) {
@@ -213,10 +234,10 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
       unsigned xoff, roff;
       int mask;
     };
-    auto item_src = [&](int it) {
-      const int b = b_lo + it / nch, r0 = rstart + (it % nch) * CH;
+    auto item_src = [&](int it, int mask) {
+      const int a = it_lo + it, b = a / nch, r0 = rstart + (a % nch) * CH;
       ItemSrc o;
-      o.mask = item_mask(b, r0);
+      o.mask = mask;
       const T* dsb = (const T*)bp.ds + (int64_t)(b * p.H + h) * p.LqP * p.LkP;
       o.xs = __builtin_amdgcn_make_buffer_rsrc((void*)dsb, 0, p.LqP * p.LkP * (int)sizeof(T), 0x00020000);
       if constexpr (!P) {
@@ -246,15 +267,14 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
       }
       return o.xoff + t * xstride;
     };
+    // list entries: item index << 8 | mask
     vecT pre[PREFETCH ? NSLOT : 1];
-    auto fetch = [&](int it) -> int {
-      const ItemSrc o = item_src(it);
-      if (!o.mask) return 0;
+    auto fetch = [&](int e) {
+      const ItemSrc o = item_src(e >> 8, e & 0xff);
 #pragma unroll
       for (int t = 0; t < NP_X; ++t) pre[t] = bload(o.xs, xoff_t(o, t));
 #pragma unroll
       for (int t = 0; t < NP_R; ++t) pre[NP_X + t] = bload(o.rs, o.roff + t * rstride);
-      return o.mask;
     };
     auto commit = [&]() {
 #pragma unroll
@@ -264,14 +284,12 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
       for (int t = 0; t < NP_R; ++t)
         if (rok(t)) *reinterpret_cast<vecT*>(rd + t * RPI_R * KSTR) = pre[NP_X + t];
     };
-    auto stage_direct = [&](int it) -> int {
-      const ItemSrc o = item_src(it);
-      if (!o.mask) return 0;
+    auto stage_direct = [&](int e) {
+      const ItemSrc o = item_src(e >> 8, e & 0xff);
       for (int t = 0; t < NP_X; ++t)
         if (xok(t)) *reinterpret_cast<vecT*>(xd + t * RPI * XS) = bload(o.xs, xoff_t(o, t));
       for (int t = 0; t < NP_R; ++t)
         if (rok(t)) *reinterpret_cast<vecT*>(rd + t * RPI_R * KSTR) = bload(o.rs, o.roff + t * rstride);
-      return o.mask;
     };
 
     // B fragment of 16-offset block eb, k-step s: Gc reads X[k][k + e + 1],
@@ -286,20 +304,38 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
       return f;
     };
 
-    int it = sub, mnext = 0;
-    if constexpr (PREFETCH) {
-      if (it < nitems) mnext = fetch(it);
-    }
-    for (; it < nitems; it += 2) {
-      int mcur;
-      if constexpr (PREFETCH) {
-        mcur = mnext;
-        if (mcur) commit();
-        mnext = (it + 2 < nitems) ? fetch(it + 2) : 0;
-      } else {
-        mcur = stage_direct(it);
+    // The wave's items are sub, sub + 2, ...; they are taken in windows of
+    // 64.  Under a mask, the items of a window with an active part are
+    // listed first, each lane testing one (so the chunk summaries of a
+    // window are read in one round trip).
+    int* const lst = ilist[w];
+    const int ncand = nitems > sub ? (nitems - sub + 1) / 2 : 0;
+    for (int base = 0; base < ncand; base += 64) {
+      int cnt = min(64, ncand - base);
+      if (LISTED) {
+        const int c = base + lane, it = sub + 2 * c;
+        int m = 0;
+        if (c < ncand) {
+          const int a = it_lo + it;
+          m = item_mask(a / nch, rstart + (a % nch) * CH);
+        }
+        cnt = wave_append(m != 0, (it << 8) | m, lst, 0);
+        wave_lds_sync();
       }
-      if (!mcur) continue;  // no active part: only zeros
+      nact += cnt;
+      auto entry = [&](int n) {
+        return LISTED ? __builtin_amdgcn_readfirstlane(lst[n]) : ((sub + 2 * (base + n)) << 8) | 0xff;
+      };
+      if constexpr (PREFETCH) {
+        if (cnt > 0) fetch(entry(0));
+      }
+    for (int n = 0; n < cnt; ++n) {
+      if constexpr (PREFETCH) {
+        commit();
+        if (n + 1 < cnt) fetch(entry(n + 1));
+      } else {
+        stage_direct(entry(n));
+      }
       wave_lds_sync();
       frag af[NS][ND];
 #pragma unroll
@@ -331,15 +367,24 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
       }
       wave_lds_sync();  // the region is rewritten by the next item
     }
+    }
   };
   if (p2c) run(std::true_type{});
   else run(std::false_type{});
 
   // Sum the two waves of each kind (1 into 0, 3 into 2) through LDS, then
-  // store the partial of this (block, head, batch group): [kind][dd][d], fp32.
+  // store the partial of this (block, head, partial group): [kind][dd][d],
+  // fp32, and its flag.  A partial without an active item is not written
+  // (its flag says so).
+  if (lane == 0) nact_sh[w] = nact;
   __syncthreads();
   float* red = reinterpret_cast<float*>(lds);
-  if (sub == 1) {
+  // without a mask every partial is written (zeros if it has no items) and
+  // the flags are not used
+  const bool any = nact + nact_sh[w ^ 1] > 0 || !LISTED;
+  if (LISTED && sub == 0 && active && lane == 0)
+    bp.gflag[((int64_t)(h * bp.NDB + dblk) * bp.NPG + pg) * 2 + (p2c ? 1 : 0)] = any ? (collapse ? 2 : 1) : 0;
+  if (sub == 1 && any) {
     f32x4* dst = reinterpret_cast<f32x4*>(red) + (w >> 1) * (NEB * ND * 64) + lane;
 #pragma unroll
     for (int eb = 0; eb < NEB; ++eb)
@@ -347,24 +392,43 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
       for (int db = 0; db < ND; ++db) dst[(eb * ND + db) * 64] = acc[eb][db];
   }
   __syncthreads();
-  if (sub == 0 && active) {
+  if (sub == 0 && active && any) {
     const f32x4* src = reinterpret_cast<const f32x4*>(red) + (w >> 1) * (NEB * ND * 64) + lane;
-    float* out = bp.gpart + ((int64_t)(h * bp.NDB + dblk) * bp.NBG + bg) * 2 * DBW * D + (p2c ? DBW * D : 0);
+    float* out = bp.gpart + ((int64_t)(h * bp.NDB + dblk) * bp.NPG + pg) * 2 * DBW * D + (p2c ? DBW * D : 0);
+    if (collapse) {
+      // sum over the offsets: the 8 blocks of 16 in registers, then the 16
+      // lanes of a lane group
+      f32x4 sum[ND];
 #pragma unroll
-    for (int eb = 0; eb < NEB; ++eb) {
-      const int e = 16 * eb + c16;
-      const int dd = p2c ? e : DBW - 1 - e;  // offset d0 + dd
+      for (int db = 0; db < ND; ++db) {
+        sum[db] = zero4();
 #pragma unroll
-      for (int db = 0; db < ND; ++db)
-        *reinterpret_cast<f32x4*>(out + (int64_t)dd * D + 16 * db + 4 * g) = acc[eb][db] + src[(eb * ND + db) * 64];
+        for (int eb = 0; eb < NEB; ++eb) sum[db] += acc[eb][db] + src[(eb * ND + db) * 64];
+#pragma unroll
+        for (int m = 1; m < 16; m <<= 1)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sum[db][e] += __shfl_xor(sum[db][e], m);
+      }
+      if (c16 == 0)
+#pragma unroll
+        for (int db = 0; db < ND; ++db) *reinterpret_cast<f32x4*>(out + 16 * db + 4 * g) = sum[db];
+    } else {
+#pragma unroll
+      for (int eb = 0; eb < NEB; ++eb) {
+        const int e = 16 * eb + c16;
+        const int dd = p2c ? e : DBW - 1 - e;  // offset d0 + dd
+#pragma unroll
+        for (int db = 0; db < ND; ++db)
+          *reinterpret_cast<f32x4*>(out + (int64_t)dd * D + 16 * db + 4 * g) = acc[eb][db] + src[(eb * ND + db) * 64];
+      }
     }
   }
 }
 
-// tab[h][r][:] (+)= s * sum over batch groups and offsets d with row(d) = r
+// tab[h][r][:] (+)= s * sum over partial groups and offsets d with row(d) = r
 // of the partials (accumulated into fp32, or written in fp32 or bf16).  One
 // workgroup of NT threads per (table, h, r): NT / (D/4) parts split the
-// (offset, batch group) pairs of the row's offset range [begin, end) (from
+// (offset, partial group) pairs of the row's offset range [begin, end) (from
 // prep_segments), each part with four independent sums so that four loads
 // are in flight; lanes of a part hold 4 columns each.  The parts are summed
 // with lane shuffles and, across waves, through LDS in a fixed order.  Long
@@ -381,20 +445,37 @@ __global__ __launch_bounds__(NT) void dsa_bwd_fold_kernel(BwdParams bp) {
   const bool q = t == 1;  // false: dKr (c2p), true: dQr (p2c)
   const int c4 = threadIdx.x % Q4, part = threadIdx.x / Q4;
   const int beg = bp.rowseg[(2 * t) * R + r], end = bp.rowseg[(2 * t + 1) * R + r];
-  const int npairs = (end - beg) * bp.NBG;
-  auto pair_src = [&](int it) {
-    const int d = beg + it / bp.NBG, k = it % bp.NBG;
-    const int dblk = (d + bp.f.LkP) / DBW, dd = (d + bp.f.LkP) % DBW;
-    return reinterpret_cast<const f32x4*>(bp.gpart + ((int64_t)(h * bp.NDB + dblk) * bp.NBG + k) * 2 * DBW * D +
-                                          (int64_t)((q ? DBW : 0) + dd) * D + 4 * c4);
+  // The range splits into single offsets at its ends and whole offset
+  // blocks between them (stored summed by the table kernel, row 0).
+  const int LkP = p.LkP;
+  const int b1 = beg + (DBW - (beg + LkP) % DBW) % DBW, b2 = end - (end + LkP) % DBW;  // beg + LkP > 0
+  int nl = end - beg, nf = 0, nr = 0;
+  if (b2 - b1 >= DBW) {
+    nl = b1 - beg;
+    nf = (b2 - b1) / DBW;
+    nr = end - b2;
+  }
+  const int npairs = (nl + nf + nr) * bp.NPG;
+  const bool flagged = bp.cinfo != nullptr;  // masks: partials without items were not written
+  // partial of (unit, group) pair it; zero where none was written
+  auto pair_val = [&](int it) {
+    const int u = it / bp.NPG, k = it % bp.NPG;
+    const bool whole = u >= nl && u < nl + nf;
+    const int d = u < nl ? beg + u : whole ? b1 + (u - nl) * DBW : b2 + (u - nl - nf);
+    const int dblk = (d + LkP) / DBW, dd = whole ? 0 : (d + LkP) % DBW;
+    const int64_t pi = (int64_t)(h * bp.NDB + dblk) * bp.NPG + k;
+    const f32x4* src =
+        reinterpret_cast<const f32x4*>(bp.gpart + pi * 2 * DBW * D + (int64_t)((q ? DBW : 0) + dd) * D + 4 * c4);
+    const f32x4 v = *src;  // read in any case (inside the workspace), so both loads are in flight together
+    return (!flagged || bp.gflag[pi * 2 + t]) ? v : zero4();
   };
   f32x4 a4[4] = {zero4(), zero4(), zero4(), zero4()};
   int it = part;
   for (; it + 3 * NP < npairs; it += 4 * NP) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) a4[u] += *pair_src(it + u * NP);
+    for (int u = 0; u < 4; ++u) a4[u] += pair_val(it + u * NP);
   }
-  for (; it < npairs; it += NP) a4[0] += *pair_src(it);
+  for (; it < npairs; it += NP) a4[0] += pair_val(it);
   f32x4 acc = (a4[0] + a4[1]) + (a4[2] + a4[3]);
 #pragma unroll
   for (int m = Q4; m < 64; m <<= 1)

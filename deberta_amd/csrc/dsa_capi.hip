@@ -3,6 +3,7 @@
 // attention.  Every launch goes on the caller's stream.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -91,6 +92,8 @@ int check_fwd(const dsa_fwd_args* a) {
     return fail("dsa: give at most one of key_keep, pair_keep and seg");
   if ((a->key_keep || a->pair_keep || a->seg) && a->Lq != a->Lk)
     return fail("dsa: masks need Lq == Lk (query liveness is read from the key mask)");
+  if ((a->key_keep || a->seg) && a->Lk > 32768)  // per-tile lists in LDS
+    return fail("dsa: key-padding and segment masks support sequences of at most 32768 tokens, got %d", a->Lk);
   const int vec = 16 / elem_bytes(a->dtype);
   const void* ptrs[] = {a->q, a->k, a->v, a->out};
   const int64_t* strides[] = {a->q_strides, a->k_strides, a->v_strides, a->o_strides};
@@ -183,8 +186,8 @@ int device_cus() {
 // Workspace of the backward (offsets 256-byte aligned) and the padded
 // extents the kernels share.
 struct WsLayout {
-  int LqP, LkP, TGP, OFF, NDB, NBG, BPG;
-  size_t rowinfo, krgt, qrgt, ds, gpart, seg, cinfo, total;
+  int LqP, LkP, TGP, OFF, NDB, NPG;
+  size_t rowinfo, krgt, qrgt, ds, gpart, gflag, seg, cinfo, total;
 };
 
 WsLayout ws_layout(const dsa_bwd_args* a) {
@@ -196,13 +199,17 @@ WsLayout ws_layout(const dsa_bwd_args* a) {
   w.OFF = w.LkP - 1;            // offset origin: t = d + OFF, 32-aligned tile starts
   w.TGP = w.LqP + w.LkP;        // offsets [-(LkP - 1), LqP] of every band window
   w.NDB = (w.LqP + w.LkP) / dsa::tbcfg::DBW;
-  // batch groups of the table kernel: about three workgroups per CU (two
-  // run at a time; the workgroups of the outer offset blocks are short)
+  // Partial groups of the table kernel (ranges of an offset block's items
+  // of one kind; a central block has about B * L / 32): about three
+  // workgroups per CU (two run at a time; the workgroups of the outer
+  // offset blocks are short).  Long sequences and masks concentrate the
+  // work in the central blocks, whose workgroups then bound the launch:
+  // those get at most 64 items of a kind each.
   const int per = f.H * w.NDB;
-  int groups = (3 * device_cus() + per - 1) / per;
-  groups = groups < 1 ? 1 : (groups > f.B ? f.B : groups);
-  w.BPG = (f.B + groups - 1) / groups;
-  w.NBG = (f.B + w.BPG - 1) / w.BPG;
+  const int64_t items = (int64_t)f.B * ((w.LqP > w.LkP ? w.LqP : w.LkP) / 32);
+  int64_t groups = (3 * device_cus() + per - 1) / per;
+  if (w.NDB > 16 || f.key_keep || f.seg) groups = std::max<int64_t>(groups, (items + 63) / 64);
+  w.NPG = (int)std::min<int64_t>(std::max<int64_t>(groups, 1), items);
   size_t off = 0;
   w.rowinfo = off;
   off = align_up(off + (size_t)f.B * f.H * w.LqP * 2 * sizeof(float), 256);
@@ -213,7 +220,9 @@ WsLayout ws_layout(const dsa_bwd_args* a) {
   w.ds = off;
   off = align_up(off + (size_t)f.B * f.H * w.LkP * w.LqP * es, 256);
   w.gpart = off;
-  if (f.flags) off = align_up(off + (size_t)f.H * w.NDB * w.NBG * 2 * dsa::tbcfg::DBW * f.D * sizeof(float), 256);
+  if (f.flags) off = align_up(off + (size_t)f.H * w.NDB * w.NPG * 2 * dsa::tbcfg::DBW * f.D * sizeof(float), 256);
+  w.gflag = off;
+  if (f.flags) off = align_up(off + (size_t)f.H * w.NDB * w.NPG * 2, 256);
   w.seg = off;
   if (f.flags) off = align_up(off + (size_t)2 * 2 * (2 * f.att_span) * sizeof(int), 256);
   w.cinfo = off;
@@ -247,13 +256,13 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
   bp.qrgt = base + ws.qrgt;
   bp.ds = base + ws.ds;
   bp.gpart = reinterpret_cast<float*>(base + ws.gpart);
+  bp.gflag = reinterpret_cast<uint8_t*>(base + ws.gflag);
   bp.rowseg = reinterpret_cast<int*>(base + ws.seg);
   bp.cinfo = (f.key_keep || f.seg) ? reinterpret_cast<int4*>(base + ws.cinfo) : nullptr;
   bp.TGP = ws.TGP;
   bp.OFF = ws.OFF;
   bp.NDB = ws.NDB;
-  bp.NBG = ws.NBG;
-  bp.BPG = ws.BPG;
+  bp.NPG = ws.NPG;
   const int stages =
       a->stages ? a->stages : (DSA_STAGE_PREP | DSA_STAGE_DQ | DSA_STAGE_DKDV | DSA_STAGE_FOLD);
 
@@ -299,7 +308,10 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
   if (side && (hipEventRecord(side->fork, st) != hipSuccess || hipStreamWaitEvent(side->stream, side->fork, 0) != hipSuccess))
     return fail("dsa: side stream fork failed");
   if (fold) {
-    hipLaunchKernelGGL((dsa::dsa_bwd_table_kernel<T, D>), dim3(ws.NDB * f.H * ws.NBG), dim3(256), 0, st, bp);
+    if (bp.cinfo)
+      hipLaunchKernelGGL((dsa::dsa_bwd_table_kernel<T, D, true>), dim3(ws.NDB * f.H * ws.NPG), dim3(256), 0, st, bp);
+    else
+      hipLaunchKernelGGL((dsa::dsa_bwd_table_kernel<T, D, false>), dim3(ws.NDB * f.H * ws.NPG), dim3(256), 0, st, bp);
     if (launch_check("dsa_bwd_table_kernel")) return 1;
   }
   if (stages & DSA_STAGE_DQ) {

@@ -147,6 +147,18 @@ DSA_DEV int wave_and(int x) {
   return x;
 }
 
+// Stream compaction within a wave: the lanes with keep set store value at
+// list[n + (their rank among those lanes)], in lane order; returns the new
+// count, the same in every lane.  Callers order the LDS writes against
+// later reads themselves.
+template <typename V>
+DSA_DEV int wave_append(bool keep, V value, V* list, int n) {
+  const unsigned long long m = __ballot(keep);
+  const int lane = __lane_id();
+  if (keep) list[n + __popcll(m & ((1ull << lane) - 1ull))] = value;
+  return n + __popcll(m);
+}
+
 // Orders LDS traffic between lanes of one wave (write by one lane, read by
 // another).  DS instructions of a wave complete in order; this keeps the
 // compiler from moving loads across the point.

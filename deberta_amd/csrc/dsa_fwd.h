@@ -45,8 +45,14 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
   __shared__ __align__(16) BT cb_all[NW * CB_ELEMS];
   __shared__ __align__(16) BT pb[PB_ELEMS];
   constexpr bool SEGM = seg_mode(MASK);
+  constexpr int MAXKT = 512;  // key tiles (Lk <= 32768)
   __shared__ int segred[SEGM ? 3 * NW : 1];
-  __shared__ __align__(16) int ksg[SEGM ? 2 : 1][SEGM ? BK : 1];  // key segments, by tile parity
+  __shared__ __align__(16) int ksg[SEGM ? BK : 1];  // key segments of the current tile
+  // segment masks: per key tile, bit 0 = some pair of one segment, bit 1 =
+  // no masking needed; the list of the active tiles in order
+  __shared__ unsigned char kflag[SEGM ? MAXKT : 1];
+  __shared__ short klist[SEGM ? MAXKT : 1];
+  __shared__ int klen;
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, g = (tid & 63) >> 4, c16 = tid & 15;
@@ -122,14 +128,56 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
     any_live = __syncthreads_or(wg_live);
   }
 
+  // Segment masks: the key tiles with a kept pair (a key whose segment is
+  // one of the workgroup's query segments), found once from the key
+  // segments (wave w tests tiles w, w + 4, ..., eight at a time), and
+  // listed in order; the loop visits only those.
+  int nlist = nkt;
+  if constexpr (SEGM) {
+    static_assert(BK == 64, "one key of a tile per lane");
+    if (any_live) {
+      const bool one = qsr.all && qsr.lo == qsr.hi;  // every query in one segment
+      const int lane = tid & 63;
+      for (int u0 = 0; u0 < nkt; u0 += 4 * 8) {
+        int s8[8];
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          const int j = (u0 + 4 * v + w) * BK + lane;
+          s8[v] = j < Lk ? sv(j) : 0;
+        }
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          const int kt = u0 + 4 * v + w;
+          const bool act = __ballot(qsr.meets(s8[v])) != 0;
+          const bool full = one && __ballot(s8[v] != qsr.lo) == 0;
+          if (lane == 0 && kt < nkt) kflag[kt] = (act ? 1 : 0) | (act && full ? 2 : 0);
+        }
+      }
+    }
+    __syncthreads();
+    if (w == 0) {
+      const int lane = tid & 63;
+      int n = 0;
+      for (int c0 = 0; any_live && c0 < nkt; c0 += 64) {
+        const int c = c0 + lane;
+        n = wave_append(c < nkt && (kflag[c] & 1), (short)c, klist, n);
+      }
+      if (lane == 0) klen = n;
+    }
+    __syncthreads();
+    nlist = __builtin_amdgcn_readfirstlane(klen);
+  }
+
   // The next key tile (K and V rows) is fetched into registers while the
   // current one is computed.
   vecT kr[KCH], vr[KCH];
   int relv = 0;  // this thread's relative position of the fetched tile (tid < XG)
+  int ksn = 0;   // segment masks: this thread's key segment of the fetched tile (tid < BK)
   int kfetched = -1;
   auto fetch = [&](int kt) {
     const int j0 = kt * BK;
     if (p.flags && tid < XG) relv = rel_of_tile(p.rel, i0, j0, Lq, Lk, tid);
+    if (SEGM && tid < BK) ksn = j0 + tid < Lk ? sv(j0 + tid) : 0;
 #pragma unroll
     for (int k = 0; k < KCH; ++k) {
       const int c = tid + 256 * k;
@@ -143,20 +191,18 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
     }
     kfetched = kt;
   };
-  if (any_live) fetch(0);
+  if (any_live && nlist > 0) fetch(SEGM ? __builtin_amdgcn_readfirstlane(klist[0]) : 0);
 
-  for (int kt = 0; any_live && kt < nkt; ++kt) {
+  for (int n = 0; any_live && n < nlist; ++n) {
+    const int kt = SEGM ? __builtin_amdgcn_readfirstlane(klist[n]) : n;
     const int j0 = kt * BK;
     // Skip key tiles that every query row of the workgroup masks out: their
-    // probabilities are exactly zero.  With segments, a tile whose keys all
-    // share the workgroup's single query segment needs no masking at all.
+    // probabilities are exactly zero (segment masks: the list holds the
+    // others).  With segments, a tile whose keys all share the workgroup's
+    // single query segment needs no masking at all.
     bool full = false;
     if constexpr (SEGM) {
-      const int j = j0 + tid;
-      const int sk = (tid < BK && j < Lk) ? sv(j) : 0;
-      if (tid < BK) ksg[kt & 1][tid] = sk;
-      if (!__syncthreads_or(qsr.meets(sk))) continue;
-      full = qsr.all && qsr.lo == qsr.hi && __syncthreads_and(tid >= BK || sk == qsr.lo);
+      full = (kflag[kt] & 2) != 0;
     } else if (MASK == MASK_PAIR) {
       int keep = 0;
       const int r = tid >> 1, half = tid & 1;
@@ -180,9 +226,10 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
         *reinterpret_cast<vecT*>(Vs + r * KSTR + c0) = vr[k];
       }
     }
+    if (SEGM && tid < BK) ksg[tid] = ksn;
     if (p.flags) store_row_tables(crow, prow, relv, A, tid);
     __syncthreads();
-    if (kt + 1 < nkt) fetch(kt + 1);
+    if (n + 1 < nlist) fetch(SEGM ? __builtin_amdgcn_readfirstlane(klist[n + 1]) : n + 1);
 
     // ---- y = K Q^T + c2p + p2c (unscaled) -------------------------------------
     frag kf[4][NS];
@@ -212,7 +259,7 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb) {
           int4 ks4 = {0, 0, 0, 0};
-          if constexpr (SEGM) ks4 = *reinterpret_cast<const int4*>(&ksg[kt & 1][16 * jb + 4 * g]);
+          if constexpr (SEGM) ks4 = *reinterpret_cast<const int4*>(&ksg[16 * jb + 4 * g]);
           uint32_t pk4 = 0;
           if (MASK == MASK_PAIR && ilive[ib]) {
             const uint8_t* row = pkb + (int64_t)i * p.pkq;

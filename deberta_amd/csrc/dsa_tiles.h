@@ -48,11 +48,13 @@ struct BwdParams {
   void* ds;         // dS [B, H, f.LqP, f.LkP] (rows = queries), zero outside [0, Lq) x [0, Lk)
   void* krgt;       // [H, D, TGP]: krgt[h][d][t] = Kr[h][c(t - OFF)][d]
   void* qrgt;       // [H, D, TGP]: qrgt[h][d][t] = Qr[h][p(t - OFF)][d]
-  float* gpart;     // table-gradient partials [H][NDB][NBG][2][128][D]
+  float* gpart;     // table-gradient partials [H][NDB][NPG][2][128][D]
+  uint8_t* gflag;   // masks: [H][NDB][NPG][2], 0 = partial not written (no active item), 1 = written
+                    // per offset, 2 = written summed over its block (row 0)
   int* rowseg;      // [2][2][R]: offsets [begin, end) of each table row (c2p, p2c)
   int4* cinfo;      // segment masks: [B][LqP / 32] per 32-token chunk (lo, hi, all active, 0)
   int TGP, OFF;     // row length and offset origin of krgt / qrgt
-  int NDB, NBG, BPG;  // offset blocks, batch groups, batches per group
+  int NDB, NPG;     // offset blocks, partial groups per block (item ranges)
 };
 
 // Segment view of the key-padding (MASK_KEY) and segment-id (MASK_SEG)
