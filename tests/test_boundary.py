@@ -19,7 +19,7 @@ import deberta_amd
 from deberta_amd import _lib, ops
 from deberta_amd.attention import DisentangledSelfAttention
 from deberta_amd.config import normalize_attention_kernel, normalize_pos_att_type
-from deberta_amd.masks import get_attention_mask, kernel_masks, normalize_keep_mask
+from deberta_amd.masks import SegmentMask, build_doc_block_mask, get_attention_mask, kernel_masks, normalize_keep_mask
 from oracle import eager
 
 ROOT = Path(__file__).resolve().parents[1]
@@ -224,6 +224,50 @@ def test_kernel_masks():
     assert kernel_masks(None, 2, 4, 4) == (None, None)
     with pytest.raises(ValueError, match="rank-4"):
         kernel_masks(torch.ones(2, 4, dtype=torch.bool), 2, 4, 4)
+
+
+def test_segment_mask_host_side():
+    """SegmentMask is the ids form of the reference's packed-document mask:
+    dense() is that mask, and the kernels get the ids as int32 [B, S]."""
+    ids = torch.tensor([[1, 1, 2, 2, 2, 0], [5, 5, 5, 5, 0, 0]])
+    m = SegmentMask(ids)
+    assert m.shape == (2, 1, 6, 6)
+    assert torch.equal(m.dense(), build_doc_block_mask(ids)[:, None])
+    seg, pk = kernel_masks(m, 2, 6, 6)
+    assert pk is None and seg.dtype == torch.int32 and seg.is_contiguous() and seg.tolist() == ids.tolist()
+    # the kernels' rule (both ids equal and nonzero) gives the dense mask on
+    # every live query row; pad rows are dead in both (the reference zeroes
+    # their output), and only their CLS edge differs
+    live = ids != 0
+    rule = (ids[:, :, None] == ids[:, None, :]) & live[:, :, None]
+    dense = m.dense()[:, 0]
+    assert torch.equal(rule[live], dense[live])
+    with pytest.raises(ValueError, match="does not match"):
+        kernel_masks(m, 2, 6, 5)
+    with pytest.raises(ValueError, match="rank-2"):
+        SegmentMask(ids[0])
+    with pytest.raises(ValueError, match="integer"):
+        SegmentMask(ids.float())
+    with pytest.raises(TypeError):
+        SegmentMask([[1, 2]])
+
+
+def test_mask_argument_errors(lib):
+    a = _lib.DsaFwdArgs()
+    a.B, a.H, a.Lq, a.Lk, a.D, a.dtype = 1, 1, 40000, 40000, 64, _lib.DSA_BF16
+    buf = (ctypes.c_uint8 * 64)()
+    p = ctypes.cast(buf, ctypes.c_void_p).value
+    for f in ("q", "k", "v", "out", "lse"):
+        setattr(a, f, p)
+    a.seg = p
+    assert lib.dsa_fwd(ctypes.byref(a), None) != 0
+    assert "at most 32768 tokens" in _lib.last_error()
+    a.key_keep = p
+    assert lib.dsa_fwd(ctypes.byref(a), None) != 0
+    assert "at most one of key_keep, pair_keep and seg" in _lib.last_error()
+    a.key_keep, a.Lk = None, 100
+    assert lib.dsa_fwd(ctypes.byref(a), None) != 0
+    assert "Lq == Lk" in _lib.last_error()
 
 
 @pytest.mark.parametrize("share", [False, True])
