@@ -6,6 +6,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 
@@ -87,6 +88,11 @@ int check_fwd(const dsa_fwd_args* a) {
     if (!a->rel_table) return fail("dsa: rel_table is required when c2p/p2c is enabled");
   }
   if ((a->flags & DSA_C2P) && !a->kr) return fail("dsa: c2p needs the pos-key table kr");
+  // the forward addresses table rows with 32-bit element offsets
+  if ((a->flags & DSA_C2P) && (int64_t)(2 * a->att_span - 1) * llabs(a->kr_strides[1]) + a->D > 0x7fffffffLL)
+    return fail("dsa: kr row stride too large (rows of one head over 2^31 elements)");
+  if ((a->flags & DSA_P2C) && (int64_t)(2 * a->att_span - 1) * llabs(a->qr_strides[1]) + a->D > 0x7fffffffLL)
+    return fail("dsa: qr row stride too large (rows of one head over 2^31 elements)");
   if ((a->flags & DSA_P2C) && !a->qr) return fail("dsa: p2c needs the pos-query table qr");
   if ((a->key_keep ? 1 : 0) + (a->pair_keep ? 1 : 0) + (a->seg ? 1 : 0) > 1)
     return fail("dsa: give at most one of key_keep, pair_keep and seg");

@@ -41,7 +41,7 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
 
   __shared__ __align__(16) T Ks[BK * KSTR];
   __shared__ __align__(16) T Vs[BK * KSTR];
-  __shared__ short crow[XG], prow[XG];
+  __shared__ int crow[XG], prow[XG];
   __shared__ __align__(16) BT cb_all[NW * CB_ELEMS];
   __shared__ __align__(16) BT pb[PB_ELEMS];
   constexpr bool SEGM = seg_mode(MASK);
@@ -227,7 +227,7 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
       }
     }
     if (SEGM && tid < BK) ksg[tid] = ksn;
-    if (p.flags) store_row_tables(crow, prow, relv, A, tid);
+    if (p.flags) store_row_tables(crow, prow, relv, A, (int)p.krs[1], (int)p.qrs[1], tid);
     __syncthreads();
     if (n + 1 < nlist) fetch(SEGM ? __builtin_amdgcn_readfirstlane(klist[n + 1]) : n + 1);
 
@@ -248,7 +248,7 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
         st[ib][jb] = acc;
       }
     if (p.flags)
-      add_delta_bands_T<T, D>(st, kf, qf, cb, pb, crow, prow, w, g, c16, krh, p.krs[1], qrh, p.qrs[1], p.flags,
+      add_delta_bands_T<T, D, MASK == MASK_PAIR ? 3 : 6>(st, kf, qf, cb, pb, crow, prow, w, g, c16, krh, qrh, p.flags,
                               biasl ? biasl + (int64_t)kt * 8192 : nullptr);
 
     // ---- mask: only where a key or query of the tile can be masked out ------

@@ -231,22 +231,23 @@ constexpr int CB_ELEMS = WQ * CTS;
 constexpr int PB_ELEMS = XG * PBT;
 }  // namespace dcfg
 
-// Row tables of one tile: crow[x] / prow[x] are the c2p / p2c table rows of
-// offset x (x = (i - i0) - (j - j0) + 63, i0 / j0 the tile's first query /
-// key), for x in [0, 192).
+// Row tables of one tile: crow[x] / prow[x] are the element offsets (row *
+// row stride) of the c2p / p2c table rows of offset x (x = (i - i0) - (j -
+// j0) + 63, i0 / j0 the tile's first query / key), for x in [0, 192); the
+// host checks that they fit in 32 bits.
 // rel_of_tile reads thread tid's relative position (tid < XG), store_row_tables
-// turns it into the two table rows.
+// turns it into the two row offsets.
 DSA_DEV int rel_of_tile(const int32_t* rel, int i0, int j0, int Lq, int Lk, int tid) {
   int d = i0 - j0 - (dcfg::BK - 1) + tid;
   d = min(max(d, -(Lk - 1)), Lq - 1);
   return rel[d + Lk - 1];
 }
 
-DSA_DEV void store_row_tables(short* crow, short* prow, int t, int A, int tid) {
+DSA_DEV void store_row_tables(int* crow, int* prow, int t, int A, int krs, int qrs, int tid) {
   if (tid < dcfg::XG) {
     t = min(max(t, -A), A);
-    crow[tid] = (short)c2p_row(t, A);
-    prow[tid] = (short)p2c_row(t, A);
+    crow[tid] = c2p_row(t, A) * krs;
+    prow[tid] = p2c_row(t, A) * qrs;
   }
 }
 
@@ -299,46 +300,57 @@ DSA_DEV void store4_contig(B* p, const f32x4& v) {
 // on return.
 //   kf: A fragments of the 64 key rows, qf: B fragments of the wave's queries
 //   cb: this wave's c2p band (WQ * CTS), pb: the shared p2c band (XG * PBT)
+//   crow, prow: the tile's table row offsets (store_row_tables)
+//   GR: c2p row blocks whose table rows are loaded before their products
+//       (all six: one L2 round trip per tile instead of six)
 //   bias: if not null, where this lane's part of the tile's saved relative
 //         term goes (see bias_tile_offset): the unscaled c2p + p2c values,
 //         stored for the backward
 // Contains one __syncthreads (the p2c band is shared): call it from every
 // thread of the workgroup.
-template <typename T, int D>
+template <typename T, int D, int GR>
 DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&kf)[4][D / Mfma<T>::KSTEP],
                                const typename Mfma<T>::frag (&qf)[2][D / Mfma<T>::KSTEP],
-                               typename BandType<T>::type* cb, typename BandType<T>::type* pb, const short* crow,
-                               const short* prow, int w, int g, int c16, const T* krh, int64_t krs, const T* qrh,
-                               int64_t qrs, int flags, typename BandType<T>::type* bias = nullptr) {
+                               typename BandType<T>::type* cb, typename BandType<T>::type* pb, const int* crow,
+                               const int* prow, int w, int g, int c16, const T* krh, const T* qrh, int flags,
+                               typename BandType<T>::type* bias = nullptr) {
   using M = Mfma<T>;
   typedef typename M::frag frag;
   typedef typename BandType<T>::type BT;
   using namespace dcfg;
   constexpr int NS = D / M::KSTEP;
   if (flags & 1) {
+    // GR row blocks have their table rows requested together (one L2
+    // round trip per group)
+    static_assert((XW / 16) % GR == 0, "whole groups");
 #pragma unroll
-    for (int rb = 0; rb < XW / 16; ++rb) {
-      const int row = crow[WQ * w + 16 * rb + c16];
-      frag af[NS];
+    for (int rb0 = 0; rb0 < XW / 16; rb0 += GR) {
+      frag af[GR][NS];
 #pragma unroll
-      for (int s = 0; s < NS; ++s) af[s] = M::load_contig(krh + (int64_t)row * krs, s, g);
+      for (int u = 0; u < GR; ++u) {
+        const T* rowp = krh + crow[WQ * w + 16 * (rb0 + u) + c16];
 #pragma unroll
-      for (int ib = 0; ib < 2; ++ib) {
-        f32x4 acc = zero4();
-#pragma unroll
-        for (int s = 0; s < NS; ++s) acc = M::mma(af[s], qf[ib][s], acc);
-        store4_contig<BT>(cb + (16 * ib + c16) * CTS + 16 * rb + 4 * g, acc);
+        for (int s = 0; s < NS; ++s) af[u][s] = M::load_contig(rowp, s, g);
       }
+#pragma unroll
+      for (int u = 0; u < GR; ++u)
+#pragma unroll
+        for (int ib = 0; ib < 2; ++ib) {
+          f32x4 acc = zero4();
+#pragma unroll
+          for (int s = 0; s < NS; ++s) acc = M::mma(af[u][s], qf[ib][s], acc);
+          store4_contig<BT>(cb + (16 * ib + c16) * CTS + 16 * (rb0 + u) + 4 * g, acc);
+        }
     }
   }
   if (flags & 2) {
 #pragma unroll
     for (int t = 0; t < XG / 16 / NW; ++t) {
       const int xb = w + NW * t;
-      const int row = prow[16 * xb + c16];
+      const T* rowp = qrh + prow[16 * xb + c16];
       frag bf[NS];
 #pragma unroll
-      for (int s = 0; s < NS; ++s) bf[s] = M::load_contig(qrh + (int64_t)row * qrs, s, g);
+      for (int s = 0; s < NS; ++s) bf[s] = M::load_contig(rowp, s, g);
 #pragma unroll
       for (int jb = 0; jb < 4; ++jb) {
         f32x4 acc = zero4();
