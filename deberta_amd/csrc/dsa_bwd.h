@@ -61,8 +61,7 @@ DSA_DEV void prep_delta(const BwdParams& bp, int blk) {
   for (int m = LPR / 2; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);
   if (row < n && part == 0) {
     const float lse2 = (i < p.Lq) ? p.lse[((int64_t)b * p.H + h) * p.Lq + i] * kLog2e : INFINITY;
-    bp.rowinfo[2 * row] = lse2;
-    bp.rowinfo[2 * row + 1] = acc;
+    *reinterpret_cast<float2*>(bp.rowinfo + 2 * row) = make_float2(lse2, acc);
   }
 }
 
@@ -76,8 +75,10 @@ DSA_DEV int offset_row(const int32_t* rel, int d, int Lq, int Lk, int A, bool p2
 // krgt[h][d][t] = Kr[h][c(t' - OFF)][d] with t' = t ^ (VEC - 1) (each
 // aligned group of VEC = 16 / sizeof(T) offsets reversed: the dq kernel's
 // operand order), qrgt[h][d][t] = Qr[h][p(t - OFF)][d], for t in [0, TGP).
-// One thread per (table, h, d, group of VEC consecutive t): VEC gathered
-// elements, one 16-byte store.  Block blk of 256 threads.
+// One thread per (table, h, group of VEC consecutive t, d), d fastest: the
+// lanes of a wave read one table row (coalesced) per element, and each
+// thread stores its VEC gathered elements in one 16-byte store.  Block blk
+// of 256 threads.
 template <typename T, int D>
 DSA_DEV void prep_gather(const BwdParams& bp, int blk) {
   constexpr int VEC = 16 / sizeof(T);
@@ -90,8 +91,8 @@ DSA_DEV void prep_gather(const BwdParams& bp, int blk) {
   const bool q = idx >= per;
   if (q ? !(p.flags & 2) : !(p.flags & 1)) return;
   const int64_t r = q ? idx - per : idx;
-  const int t0 = (int)(r % NG) * VEC;
-  const int d = (int)((r / NG) % D);
+  const int d = (int)(r % D);
+  const int t0 = (int)((r / D) % NG) * VEC;
   const int h = (int)(r / ((int64_t)NG * D));
   const T* src = q ? (const T*)p.qr + (int64_t)h * p.qrs[0] : (const T*)p.kr + (int64_t)h * p.krs[0];
   const int64_t rs = q ? p.qrs[1] : p.krs[1];

@@ -305,8 +305,11 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
 #pragma unroll
           for (int s = 0; s < NS; ++s)
             acc = M::mma(qa[s], kf[jb][s], acc);
-          if (p.flags) {
-            // rows 16*ib + 4*g + e of key column 32w + 16*jb + c16 (forward tile order)
+          {
+            // rows 16*ib + 4*g + e of key column 32w + 16*jb + c16 (forward
+            // tile order).  The LDS read is issued whatever the flags (the
+            // buffer is in bounds; without relative terms it is not added),
+            // so it is not held behind a branch.
             const int jl = WK * w + 16 * jb;
             const int o = (jl / 64) * 2048 + ib * 1024 + ((jl % 64) / 16) * 256;
             if constexpr (sizeof(BT) == 2) {
@@ -314,11 +317,16 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
               typedef _Float16 h4 __attribute__((ext_vector_type(4)));
               const h4 v = __builtin_bit_cast(
                   h4, tr4_at(reinterpret_cast<const bf16*>(Bt) + o + (4 * g + (c16 >> 2)) * 16 + (c16 & 3) * 4));
+              if (p.flags)
 #pragma unroll
-              for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf((float)v[e], one, acc[e]);
+                for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf((float)v[e], one, acc[e]);
             } else {
+              float v[4];
 #pragma unroll
-              for (int e = 0; e < 4; ++e) acc[e] += Bt[o + (4 * g + e) * 16 + c16];
+              for (int e = 0; e < 4; ++e) v[e] = Bt[o + (4 * g + e) * 16 + c16];
+              if (p.flags)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[e] += v[e];
             }
           }
           sc[jb][ib] = acc;
