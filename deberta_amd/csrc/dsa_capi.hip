@@ -237,6 +237,22 @@ WsLayout ws_layout(const dsa_bwd_args* a) {
   return w;
 }
 
+// Dynamic LDS that takes a table-kernel workgroup just past half of a CU's
+// 160 KB (queried once per instantiation; 0 if the query fails).
+template <typename T, int D, bool LISTED>
+unsigned half_cu_lds_pad() {
+  static const unsigned pad = [] {
+    hipFuncAttributes fa;
+    if (hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(&dsa::dsa_bwd_table_kernel<T, D, LISTED>)) !=
+        hipSuccess) {
+      (void)hipGetLastError();
+      return 0u;
+    }
+    return fa.sharedSizeBytes < 81920 + 256 ? (unsigned)(81920 + 256 - fa.sharedSizeBytes) : 0u;
+  }();
+  return pad;
+}
+
 template <typename T, int D>
 int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t st) {
   const dsa_fwd_args& f = a->fwd;
@@ -314,10 +330,18 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
   if (side && (hipEventRecord(side->fork, st) != hipSuccess || hipStreamWaitEvent(side->stream, side->fork, 0) != hipSuccess))
     return fail("dsa: side stream fork failed");
   if (fold) {
+    // With DQ beside it and no mask, the table kernel (bound by memory
+    // throughput, as fast at one workgroup per CU as at two) asks for unused
+    // dynamic LDS that takes it just past half a CU's 160 KB, so that each
+    // CU keeps room for a dq workgroup next to one table workgroup (backward
+    // 344 -> 339 us at B=32, L=512).  Under a mask the table kernel's work
+    // sits in few workgroups that need the second slot (C4 segments: 962 ->
+    // 987 us with the pad), so it is not padded.
+    const unsigned dyn = (side && !bp.cinfo) ? half_cu_lds_pad<T, D, false>() : 0u;
     if (bp.cinfo)
-      hipLaunchKernelGGL((dsa::dsa_bwd_table_kernel<T, D, true>), dim3(ws.NDB * f.H * ws.NPG), dim3(256), 0, st, bp);
+      hipLaunchKernelGGL((dsa::dsa_bwd_table_kernel<T, D, true>), dim3(ws.NDB * f.H * ws.NPG), dim3(256), dyn, st, bp);
     else
-      hipLaunchKernelGGL((dsa::dsa_bwd_table_kernel<T, D, false>), dim3(ws.NDB * f.H * ws.NPG), dim3(256), 0, st, bp);
+      hipLaunchKernelGGL((dsa::dsa_bwd_table_kernel<T, D, false>), dim3(ws.NDB * f.H * ws.NPG), dim3(256), dyn, st, bp);
     if (launch_check("dsa_bwd_table_kernel")) return 1;
   }
   if (stages & DSA_STAGE_DQ) {
