@@ -43,6 +43,8 @@ WORKLOADS = {
     "headline": (32, 512, 12, None, "BASELINE configs[1] shape, all-ones mask"),
     "C2pad": (32, 512, 12, "key", "configs[1] shape, per-row valid length ~U{64..512} as a (B,1,1,L) key mask"),
     "C5": (64, 512, 16, None, "B=64 L=512 H=16, no mask"),
+    "C3": (16, 512, 12, None, "12-layer DeBERTa-v3-base-shaped encoder fwd+bwd under an RTD loss, bf16 autocast"),
+    "C5layer": (64, 512, 16, None, "DeBERTa-v3-large-shaped attention layer (hidden 1024, projections included) fwd+bwd, bf16, inside torch.compile"),
     "C4": (4, 4096, 12, "doc", "B=4 L=4096 H=12, packed documents (lengths ~Geometric(mean 600)) as the dense (B,1,L,L) doc-block mask"),
     "C4seg": (4, 4096, 12, "seg", "as C4, the same documents given as segment ids (SegmentMask)"),
 }
@@ -104,6 +106,187 @@ def workload_mask(kind, b: int, l: int, g, dev):
     if kind == "doc":
         return dense[:, None].to(dev), kept, b * l
     return SegmentMask(ids.to(dev)), kept, b * l
+
+
+def run_encoder(args) -> None:
+    """C3: a 12-layer DeBERTa-v3-base-shaped encoder (hidden 768, 12 heads,
+    FFN 3072, vocab 128100, relative embeddings shared by the layers with a
+    LayerNorm, keys shared with the relative projections) with the fused
+    attention module in every layer, fwd+bwd of an RTD-style discriminator
+    loss (BCE over a Bernoulli(0.15) replaced-token label per token) under
+    bf16 autocast, on synthetic token ids, random init N(0, 0.02).  This is
+    a measurement harness around the attention path, not a model of this
+    package.  Prints step time, tokens/s and the attention share (the fused
+    op's fwd+bwd at the same shape, times 12, over the step)."""
+    import torch
+    from torch import nn
+
+    import deberta_amd
+    from deberta_amd.relpos import relative_offset_table
+
+    dev = torch.device("cuda:0")
+    Bc, Lc, Hc, hid, ffn, vocab = 16, 512, 12, 768, 3072, 128100
+    cfg = type("Cfg", (), dict(hidden_size=hid, num_attention_heads=Hc, share_att_key=True,
+                               pos_att_type="p2c|c2p", relative_attention=True, position_buckets=BUCKETS,
+                               max_relative_positions=-1, max_position_embeddings=MAX_POS,
+                               hidden_dropout_prob=0.0, attention_probs_dropout_prob=0.0))()
+
+    class Layer(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.attn = deberta_amd.DisentangledSelfAttention(cfg)
+            self.out = nn.Linear(hid, hid)
+            self.ln1 = nn.LayerNorm(hid, eps=1e-7)
+            self.up, self.down = nn.Linear(hid, ffn), nn.Linear(ffn, hid)
+            self.ln2 = nn.LayerNorm(hid, eps=1e-7)
+
+        def forward(self, x, mask, rel_pos, rel):
+            a, _ = self.attn(x, mask, relative_pos=rel_pos, rel_embeddings=rel)
+            x = self.ln1(self.out(a) + x)
+            return self.ln2(self.down(nn.functional.gelu(self.up(x))) + x)
+
+    class Encoder(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.emb = nn.Embedding(vocab, hid)
+            self.emb_ln = nn.LayerNorm(hid, eps=1e-7)
+            self.rel = nn.Parameter(torch.empty(2 * BUCKETS, hid))
+            self.rel_ln = nn.LayerNorm(hid, eps=1e-7)
+            self.layers = nn.ModuleList(Layer() for _ in range(12))
+            self.head = nn.Sequential(nn.Linear(hid, hid), nn.GELU(), nn.LayerNorm(hid, eps=1e-7), nn.Linear(hid, 1))
+
+        def forward(self, ids, mask, rel_pos):
+            x = self.emb_ln(self.emb(ids))
+            rel = self.rel_ln(self.rel)
+            for layer in self.layers:
+                x = layer(x, mask, rel_pos, rel)
+            return self.head(x).squeeze(-1)
+
+    torch.manual_seed(0)
+    model = Encoder().to(dev)
+    for n_, prm in model.named_parameters():
+        if prm.dim() > 1:
+            nn.init.normal_(prm, 0.0, 0.02)
+        elif "ln" not in n_ and "head.2" not in n_:
+            nn.init.zeros_(prm)
+    g = torch.Generator().manual_seed(0)
+    ids = torch.randint(0, vocab, (Bc, Lc), generator=g).to(dev)
+    labels = (torch.rand(Bc, Lc, generator=g) < 0.15).float().to(dev)
+    mask = torch.ones(Bc, 1, 1, Lc, dtype=torch.bool, device=dev)
+    rel_pos = deberta_amd.build_relative_position(Lc, Lc, bucket_size=BUCKETS, max_position=MAX_POS, device=dev)
+    params = [p_ for p_ in model.parameters()]
+
+    def step():
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            logits = model(ids, mask, rel_pos)
+        loss = nn.functional.binary_cross_entropy_with_logits(logits.float(), labels)
+        torch.autograd.grad(loss, params)
+
+    def timed(fn, n):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    n = max(3, args.steps)
+    ms = timed(step, n)
+    # the fused op alone at one layer's shape (q, k, v, kr, qr leaves, bf16)
+    gq = torch.Generator().manual_seed(1)
+    mk = lambda *sh: torch.randn(*sh, generator=gq).to(device=dev, dtype=torch.bfloat16).requires_grad_(True)
+    q, k, v = mk(Bc, Lc, Hc, D), mk(Bc, Lc, Hc, D), mk(Bc, Lc, Hc, D)
+    kr, qr = mk(Hc, R, D), mk(Hc, R, D)
+    dout = torch.randn(Bc, Lc, Hc, D, generator=gq).to(device=dev, dtype=torch.bfloat16)
+    table = relative_offset_table(Lc, Lc, bucket_size=BUCKETS, max_position=MAX_POS, device=dev)
+    scale = 1.0 / math.sqrt(D * 3)
+
+    def attn_step():
+        out, _, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, A, scale)
+        torch.autograd.grad(out, (q, k, v, kr, qr), dout)
+
+    ms_attn = timed(attn_step, 10)
+    print(
+        json.dumps(
+            {
+                "workload": "C3",
+                "description": WORKLOADS["C3"][4],
+                "ms_per_step": round(ms, 3),
+                "tokens_per_s": round(Bc * Lc / (ms * 1e-3), 1),
+                "attention_ms_per_layer": round(ms_attn, 4),
+                "attention_share": round(12 * ms_attn / ms, 4),
+                "steps": n,
+                "data": "synthetic token ids and labels, random init",
+            }
+        ),
+        flush=True,
+    )
+
+
+def run_compiled_layer(args) -> None:
+    """C5 as BASELINE states it: one DeBERTa-v3-large-shaped attention
+    layer (hidden 1024, 16 heads x 64, relative projections shared with the
+    keys, c2p|p2c, full mask) fwd+bwd in bf16 inside torch.compile
+    (inductor), so the op runs through its fake implementations.  Prints the
+    step time and TFLOP/s of the op's algorithmic count; the projections
+    (four 1024 x 1024 Linear layers on 32768 tokens, and the two on the
+    relative table) run in hipBLASLt inside the same step."""
+    import torch
+
+    import deberta_amd
+
+    dev = torch.device("cuda:0")
+    Bc, Lc, Hc, hid = 64, 512, 16, 1024
+    cfg = type("Cfg", (), dict(hidden_size=hid, num_attention_heads=Hc, share_att_key=True,
+                               pos_att_type="p2c|c2p", relative_attention=True, position_buckets=BUCKETS,
+                               max_relative_positions=-1, max_position_embeddings=MAX_POS,
+                               hidden_dropout_prob=0.0, attention_probs_dropout_prob=0.0))()
+    torch.manual_seed(0)
+    layer = deberta_amd.DisentangledSelfAttention(cfg).to(dev, torch.bfloat16)
+    for prm in layer.parameters():
+        torch.nn.init.normal_(prm, 0.0, 0.02) if prm.dim() > 1 else torch.nn.init.zeros_(prm)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(Bc, Lc, hid, generator=g).to(dev, torch.bfloat16).requires_grad_(True)
+    rel = (torch.randn(2 * BUCKETS, hid, generator=g) * 0.02).to(dev, torch.bfloat16).requires_grad_(True)
+    dout = torch.randn(Bc, Lc, hid, generator=g).to(dev, torch.bfloat16)
+    rel_pos = deberta_amd.build_relative_position(Lc, Lc, bucket_size=BUCKETS, max_position=MAX_POS, device=dev)
+    compiled = torch.compile(layer)
+
+    def step():
+        out, _ = compiled(x, None, relative_pos=rel_pos, rel_embeddings=rel)
+        out.backward(dout)
+
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    n = max(3, args.steps)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(n):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / n
+    f_op = 3 * flops_fwd(Bc, Lc, Hc, D, R)
+    f_proj = 3 * (2.0 * 3 * Bc * Lc * hid * hid + 2.0 * 2 * (2 * BUCKETS) * hid * hid)
+    print(
+        json.dumps(
+            {
+                "workload": "C5layer",
+                "description": WORKLOADS["C5layer"][4],
+                "ms_per_step": round(ms, 4),
+                "tflops_op_count": round(f_op / (ms * 1e-3) / 1e12, 2),
+                "tflops_with_projections": round((f_op + f_proj) / (ms * 1e-3) / 1e12, 2),
+                "steps": n,
+                "data": "synthetic hidden states, random init",
+            }
+        ),
+        flush=True,
+    )
 
 
 def cpu_model() -> str:
@@ -191,6 +374,13 @@ def main() -> None:
             file=sys.stderr,
         )
         sys.exit(2)
+
+    if args.workload == "C3":
+        run_encoder(args)
+        return
+    if args.workload == "C5layer":
+        run_compiled_layer(args)
+        return
 
     import torch
 
