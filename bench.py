@@ -456,6 +456,10 @@ def main() -> None:
     ws = torch.empty((ops.bwd_workspace_bytes(bargs),), dtype=torch.uint8, device=dev)
     bargs.workspace, bargs.workspace_bytes = ws.data_ptr(), ws.numel()
     fargs = bargs.fwd
+    nfws = lib.dsa_fwd_workspace_bytes(ctypes.byref(fargs))  # launch-order scratch under masks
+    fws = torch.empty((max(nfws, 16),), dtype=torch.uint8, device=dev)
+    if nfws:
+        fargs.workspace, fargs.workspace_bytes = fws.data_ptr(), nfws
     sptr = ctypes.c_void_p(stream.cuda_stream)
 
     def run_fwd():

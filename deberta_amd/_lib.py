@@ -22,7 +22,7 @@ DSA_STAGE_DQ = 2
 DSA_STAGE_DKDV = 4
 DSA_STAGE_FOLD = 8
 
-EXPECTED_VERSION = 4
+EXPECTED_VERSION = 5
 
 _i64x3 = ctypes.c_int64 * 3
 _i64x2 = ctypes.c_int64 * 2
@@ -60,6 +60,8 @@ class DsaFwdArgs(ctypes.Structure):
         ("scale", ctypes.c_float),
         ("seg", ctypes.c_void_p),
         ("seg_stride_b", ctypes.c_int64),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
     ]
 
 
@@ -90,6 +92,7 @@ EXPORTS = (
     "dsa_bwd",
     "dsa_bwd_workspace_bytes",
     "dsa_fwd_bias_bytes",
+    "dsa_fwd_workspace_bytes",
     "dsa_last_error",
     "dsa_version",
 )
@@ -124,6 +127,8 @@ def load() -> ctypes.CDLL:
         lib.dsa_bwd_workspace_bytes.restype = ctypes.c_size_t
         lib.dsa_fwd_bias_bytes.argtypes = [ctypes.POINTER(DsaFwdArgs)]
         lib.dsa_fwd_bias_bytes.restype = ctypes.c_size_t
+        lib.dsa_fwd_workspace_bytes.argtypes = [ctypes.POINTER(DsaFwdArgs)]
+        lib.dsa_fwd_workspace_bytes.restype = ctypes.c_size_t
         lib.dsa_last_error.argtypes = []
         lib.dsa_last_error.restype = ctypes.c_char_p
         lib.dsa_version.argtypes = []

@@ -87,8 +87,16 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
   const int w = tid >> 6, g = (tid & 63) >> 4, c16 = tid & 15;
   const int Lq = p.Lq, Lk = p.Lk;
   const int NKT = p.LkP / BKW;
-  const int m = xcd_remap(blockIdx.x, gridDim.x);  // (b, h, kt), kt fastest
-  const int kt = m % NKT, h = (m / NKT) % p.H, b = m / (NKT * p.H);
+  // (b, h, kt), kt fastest; with an order (masks), item order[r / H] and
+  // head r % H, heaviest first
+  int kt, h, b;
+  if (bp.korder) {
+    const int it = bp.korder[blockIdx.x / p.H];
+    h = blockIdx.x % p.H, kt = it % NKT, b = it / NKT;
+  } else {
+    const int m = xcd_remap(blockIdx.x, gridDim.x);
+    kt = m % NKT, h = (m / NKT) % p.H, b = m / (NKT * p.H);
+  }
   const bool p2c = (p.flags & 2) != 0;
   const float sl2 = p.scale * kLog2e;
   const int nqt = p.LqP / BQ;

@@ -15,6 +15,7 @@
 #include "dsa_bwd_dkdv.h"
 #include "dsa_bwd_dq.h"
 #include "dsa_bwd_table.h"
+#include "dsa_order.h"
 #include "dsa_fwd.h"
 
 namespace {
@@ -143,6 +144,7 @@ dsa::FwdParams to_params(const dsa_fwd_args* a) {
   p.pkq = a->pair_keep_strides[1];
   p.seg = a->seg;
   p.segb = a->seg_stride_b;
+  p.order = nullptr;
   p.B = a->B;
   p.H = a->H;
   p.Lq = a->Lq;
@@ -164,6 +166,32 @@ int launch_check(const char* what) {
   if (e != hipSuccess) return fail("dsa: %s launch failed: %s", what, hipGetErrorString(e));
   return 0;
 }
+
+// Heaviest-first order (dsa_order.h) of B * ntiles items: cost and order
+// arrays of that many ints each.  Used under key_keep / seg masks only, and
+// for at most this many items (one block sorts them).
+constexpr int64_t kMaxOrderItems = 65536;
+
+size_t order_bytes(const dsa_fwd_args* a, int ntiles) {
+  const int64_t n = (int64_t)a->B * ntiles;
+  if (!(a->key_keep || a->seg) || n > kMaxOrderItems) return 0;
+  return align_up((size_t)2 * n * sizeof(int), 256);
+}
+
+int launch_order(const dsa::FwdParams& p, int* buf, int ntiles, bool fwd, hipStream_t st) {
+  dsa::OrderParams op;
+  op.f = p;
+  op.cost = buf;
+  op.order = buf + (int64_t)p.B * ntiles;
+  op.ntiles = ntiles;
+  op.fwd = fwd ? 1 : 0;
+  hipLaunchKernelGGL(dsa::dsa_order_cost_kernel, dim3((unsigned)p.B), dim3(256), 0, st, op);
+  if (launch_check("dsa_order_cost_kernel")) return 1;
+  hipLaunchKernelGGL(dsa::dsa_order_sort_kernel, dim3(1), dim3(1024), 0, st, op);
+  return launch_check("dsa_order_sort_kernel");
+}
+
+int fwd_tiles(const dsa_fwd_args* a) { return (a->Lq + dsa::dcfg::BQ - 1) / dsa::dcfg::BQ; }
 
 template <typename T, int D, int MASK>
 int launch_fwd(const dsa::FwdParams& p, hipStream_t st) {
@@ -193,7 +221,7 @@ int device_cus() {
 // extents the kernels share.
 struct WsLayout {
   int LqP, LkP, TGP, OFF, NDB, NPG;
-  size_t rowinfo, krgt, qrgt, ds, gpart, gflag, seg, cinfo, total;
+  size_t rowinfo, krgt, qrgt, ds, gpart, gflag, seg, cinfo, korder, total;
 };
 
 WsLayout ws_layout(const dsa_bwd_args* a) {
@@ -233,6 +261,8 @@ WsLayout ws_layout(const dsa_bwd_args* a) {
   if (f.flags) off = align_up(off + (size_t)2 * 2 * (2 * f.att_span) * sizeof(int), 256);
   w.cinfo = off;
   if (f.key_keep || f.seg) off = align_up(off + (size_t)f.B * (w.LqP / 32) * 4 * sizeof(int), 256);
+  w.korder = off;  // dkdv launch order (cost, order), under key_keep / seg
+  off += order_bytes(&f, w.LkP / dsa::kvcfg::BKW);
   w.total = off;
   return w;
 }
@@ -281,6 +311,9 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
   bp.gflag = reinterpret_cast<uint8_t*>(base + ws.gflag);
   bp.rowseg = reinterpret_cast<int*>(base + ws.seg);
   bp.cinfo = (f.key_keep || f.seg) ? reinterpret_cast<int4*>(base + ws.cinfo) : nullptr;
+  const int nkt = ws.LkP / dsa::kvcfg::BKW;
+  int* kbuf = order_bytes(&f, nkt) ? reinterpret_cast<int*>(base + ws.korder) : nullptr;
+  bp.korder = kbuf ? kbuf + (int64_t)f.B * nkt : nullptr;
   bp.TGP = ws.TGP;
   bp.OFF = ws.OFF;
   bp.NDB = ws.NDB;
@@ -303,6 +336,7 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
     hipLaunchKernelGGL((dsa::dsa_bwd_prep_kernel<T, D>), dim3((unsigned)(nb.gather + nb.seg + nb.chunk + nb.delta)), dim3(256), 0,
                        st, bp, nb);
     if (launch_check("dsa_bwd_prep_kernel")) return 1;
+    if (kbuf && launch_order(bp.f, kbuf, nkt, false, st)) return 1;
   }
   if (stages & DSA_STAGE_DKDV) {
     dim3 grid((unsigned)(ws.LkP / dsa::kvcfg::BKW * f.H * f.B));
@@ -367,16 +401,24 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
 
 extern "C" {
 
-int dsa_version(void) { return 4; }
+int dsa_version(void) { return 5; }
 
 const char* dsa_last_error(void) { return g_err.c_str(); }
 
 int dsa_fwd(const dsa_fwd_args* a, void* stream) {
   g_err.clear();
   if (check_fwd(a)) return 1;
-  const dsa::FwdParams p = to_params(a);
+  dsa::FwdParams p = to_params(a);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int mode = mask_mode(a);
+  const size_t ob = order_bytes(a, fwd_tiles(a));
+  if (ob && a->workspace) {
+    if (a->workspace_bytes < ob) return fail("dsa: forward workspace of %zu bytes required, got %zu", ob, a->workspace_bytes);
+    if (!aligned16(a->workspace)) return fail("dsa: forward workspace must be 16-byte aligned");
+    int* buf = static_cast<int*>(a->workspace);
+    if (launch_order(p, buf, fwd_tiles(a), true, st)) return 1;
+    p.order = buf + (int64_t)a->B * fwd_tiles(a);
+  }
   if (a->dtype == DSA_BF16) {
     return a->D == 64 ? fwd_mask<dsa::bf16, 64>(p, mode, st) : fwd_mask<dsa::bf16, 32>(p, mode, st);
   }
@@ -386,6 +428,11 @@ int dsa_fwd(const dsa_fwd_args* a, void* stream) {
 size_t dsa_fwd_bias_bytes(const dsa_fwd_args* a) {
   if (!a || !a->flags) return 0;
   return (size_t)a->B * a->H * round_up(a->Lq, 128) * round_up(a->Lk, 128) * (a->dtype == DSA_BF16 ? 2 : 4);
+}
+
+size_t dsa_fwd_workspace_bytes(const dsa_fwd_args* a) {
+  if (!a || a->B < 1 || a->Lq < 1) return 0;
+  return order_bytes(a, fwd_tiles(a));
 }
 
 size_t dsa_bwd_workspace_bytes(const dsa_bwd_args* a) {

@@ -57,8 +57,16 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
   const int tid = threadIdx.x;
   const int w = tid >> 6, g = (tid & 63) >> 4, c16 = tid & 15;
   const int NQT = (p.Lq + BQ - 1) / BQ;
-  const int m = xcd_remap(blockIdx.x, gridDim.x);  // (b, h, qt), qt fastest
-  const int qt = m % NQT, h = (m / NQT) % p.H, b = m / (NQT * p.H);
+  // (b, h, qt), qt fastest; with an order (masks), item order[r / H] and
+  // head r % H, heaviest first
+  int qt, h, b;
+  if (p.order) {
+    const int it = p.order[blockIdx.x / p.H];
+    h = blockIdx.x % p.H, qt = it % NQT, b = it / NQT;
+  } else {
+    const int m = xcd_remap(blockIdx.x, gridDim.x);
+    qt = m % NQT, h = (m / NQT) % p.H, b = m / (NQT * p.H);
+  }
   const int Lq = p.Lq, Lk = p.Lk, A = p.A;
   const int i0 = qt * BQ;
   const int iw = i0 + w * WQ;

@@ -24,6 +24,7 @@ struct FwdParams {
   void* out;
   float* lse;
   void* bias;       // saved relative term [B, H, LqP, LkP] or null
+  const int* order; // launch order of the (batch row, tile) items, heaviest first, or null (dsa_order.h)
   int64_t qs[3], ks[3], vs[3], os[3];
   int64_t krs[2], qrs[2];
   int64_t kkb, pkb, pkq, segb;
@@ -53,6 +54,7 @@ struct BwdParams {
                     // per offset, 2 = written summed over its block (row 0)
   int* rowseg;      // [2][2][R]: offsets [begin, end) of each table row (c2p, p2c)
   int4* cinfo;      // segment masks: [B][LqP / 32] per 32-token chunk (lo, hi, all active, 0)
+  const int* korder;  // dkdv launch order of the (batch row, key tile) items, or null (dsa_order.h)
   int TGP, OFF;     // row length and offset origin of krgt / qrgt
   int NDB, NPG;     // offset blocks, partial groups per block (item ranges)
 };

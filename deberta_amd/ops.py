@@ -183,6 +183,11 @@ def dsa_fwd(
         bias = torch.empty((0,), dtype=bias_dtype(q.dtype), device=q.device)
     args = _fill_fwd_args(q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, att_span, scale, bias)
     lib = _lib.load()
+    # scratch for the heaviest-first launch order under key / segment masks
+    nws = lib.dsa_fwd_workspace_bytes(ctypes.byref(args))
+    ws = torch.empty((nws,), dtype=torch.uint8, device=q.device) if nws else None
+    if ws is not None:
+        args.workspace, args.workspace_bytes = ws.data_ptr(), nws
     stream = torch.cuda.current_stream(q.device).cuda_stream
     _lib.check(lib.dsa_fwd(ctypes.byref(args), ctypes.c_void_p(stream)), "dsa_fwd")
     return out, lse, bias

@@ -105,6 +105,13 @@ typedef struct dsa_fwd_args {
   float scale;            /* 1/sqrt(D * scale_factor) */
   const int32_t* seg;     /* [B, L] segment ids or NULL (see Masks above) */
   int64_t seg_stride_b;
+  /* Optional scratch of dsa_fwd_workspace_bytes(args) bytes (16-byte
+     aligned), used only under key_keep or seg: the forward then launches
+     its workgroups heaviest first (a small cost and sort pass before the
+     kernel).  NULL: the default order, same results.  Ignored by dsa_bwd,
+     which has its own workspace. */
+  void* workspace;
+  size_t workspace_bytes;
 } dsa_fwd_args;
 
 typedef struct dsa_bwd_args {
@@ -148,6 +155,11 @@ size_t dsa_bwd_workspace_bytes(const dsa_bwd_args* args);
  * No counterpart in the reference, which keeps its (B, H, L, L) relative
  * terms alive for autograd instead. */
 size_t dsa_fwd_bias_bytes(const dsa_fwd_args* args);
+
+/* Bytes of dsa_fwd_args.workspace for these arguments: nonzero only under
+ * key_keep or seg (the heaviest-first launch order).  No counterpart in the
+ * reference, whose eager path has no launch order to choose. */
+size_t dsa_fwd_workspace_bytes(const dsa_fwd_args* args);
 
 /* Thread-local description of the last error (empty string if none). */
 const char* dsa_last_error(void);
