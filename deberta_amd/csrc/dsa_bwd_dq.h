@@ -60,8 +60,16 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dq_kernel(BwdParams bp) {
   const int tid = threadIdx.x;
   const int w = tid >> 6, g = (tid & 63) >> 4, c16 = tid & 15;
   const int NQT = bp.f.LqP / BQ;
-  const int m = xcd_remap(blockIdx.x, gridDim.x);  // (b, h, qt), qt fastest
-  const int qt = m % NQT, h = (m / NQT) % p.H, b = m / (NQT * p.H);
+  // (b, h, qt), qt fastest; with an order (masks), item order[r / H] and
+  // head r % H, heaviest first
+  int qt, h, b;
+  if (bp.qorder) {
+    const int it = bp.qorder[blockIdx.x / p.H];
+    h = blockIdx.x % p.H, qt = it % NQT, b = it / NQT;
+  } else {
+    const int m = xcd_remap(blockIdx.x, gridDim.x);
+    qt = m % NQT, h = (m / NQT) % p.H, b = m / (NQT * p.H);
+  }
   const int i0 = qt * BQ, iw = i0 + w * WQ;
   const bool c2p = (p.flags & 1) != 0;
   const T* kbase = (const T*)p.k + (int64_t)b * p.ks[0] + (int64_t)h * p.ks[2];

@@ -221,7 +221,7 @@ int device_cus() {
 // extents the kernels share.
 struct WsLayout {
   int LqP, LkP, TGP, OFF, NDB, NPG;
-  size_t rowinfo, krgt, qrgt, ds, gpart, gflag, seg, cinfo, korder, total;
+  size_t rowinfo, krgt, qrgt, ds, gpart, gflag, seg, cinfo, korder, qorder, total;
 };
 
 WsLayout ws_layout(const dsa_bwd_args* a) {
@@ -263,6 +263,8 @@ WsLayout ws_layout(const dsa_bwd_args* a) {
   if (f.key_keep || f.seg) off = align_up(off + (size_t)f.B * (w.LqP / 32) * 4 * sizeof(int), 256);
   w.korder = off;  // dkdv launch order (cost, order), under key_keep / seg
   off += order_bytes(&f, w.LkP / dsa::kvcfg::BKW);
+  w.qorder = off;  // dq launch order
+  off += order_bytes(&f, w.LqP / dsa::dqcfg::BQ);
   w.total = off;
   return w;
 }
@@ -314,6 +316,9 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
   const int nkt = ws.LkP / dsa::kvcfg::BKW;
   int* kbuf = order_bytes(&f, nkt) ? reinterpret_cast<int*>(base + ws.korder) : nullptr;
   bp.korder = kbuf ? kbuf + (int64_t)f.B * nkt : nullptr;
+  const int nqt = ws.LqP / dsa::dqcfg::BQ;
+  int* qbuf = order_bytes(&f, nqt) ? reinterpret_cast<int*>(base + ws.qorder) : nullptr;
+  bp.qorder = qbuf ? qbuf + (int64_t)f.B * nqt : nullptr;
   bp.TGP = ws.TGP;
   bp.OFF = ws.OFF;
   bp.NDB = ws.NDB;
@@ -337,6 +342,8 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
                        st, bp, nb);
     if (launch_check("dsa_bwd_prep_kernel")) return 1;
     if (kbuf && launch_order(bp.f, kbuf, nkt, false, st)) return 1;
+    // dq's tiles (128 queries against 64-key tiles) weigh as the forward's
+    if (qbuf && launch_order(bp.f, qbuf, nqt, true, st)) return 1;
   }
   if (stages & DSA_STAGE_DKDV) {
     dim3 grid((unsigned)(ws.LkP / dsa::kvcfg::BKW * f.H * f.B));

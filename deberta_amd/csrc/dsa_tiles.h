@@ -55,6 +55,7 @@ struct BwdParams {
   int* rowseg;      // [2][2][R]: offsets [begin, end) of each table row (c2p, p2c)
   int4* cinfo;      // segment masks: [B][LqP / 32] per 32-token chunk (lo, hi, all active, 0)
   const int* korder;  // dkdv launch order of the (batch row, key tile) items, or null (dsa_order.h)
+  const int* qorder;  // dq launch order of the (batch row, query tile) items, or null
   int TGP, OFF;     // row length and offset origin of krgt / qrgt
   int NDB, NPG;     // offset blocks, partial groups per block (item ranges)
 };
