@@ -160,8 +160,16 @@ DSA_DEV void prep_chunks(const BwdParams& bp, int blk) {
 // tables, the next nb_seg blocks find the row segments, the next nb_chunk
 // blocks summarise the mask's chunks, the rest compute rowinfo.  The short
 // blocks go first and run beside the rowinfo blocks.
+// Zeroes the table kernel's block accumulators (gacc_floats floats, a
+// multiple of 4): one 16-byte store a thread.
+DSA_DEV void prep_zero(const BwdParams& bp, int64_t gacc_floats, int blk) {
+  const int64_t i = ((int64_t)blk * 256 + threadIdx.x) * 4;
+  if (i < gacc_floats) *reinterpret_cast<f32x4*>(bp.gpart + i) = zero4();
+}
+
 struct PrepBlocks {
-  int gather, seg, chunk, delta;
+  int gather, seg, chunk, zero, delta;
+  int64_t gacc_floats;
 };
 template <typename T, int D>
 __global__ __launch_bounds__(256) void dsa_bwd_prep_kernel(BwdParams bp, PrepBlocks nb) {
@@ -172,8 +180,10 @@ __global__ __launch_bounds__(256) void dsa_bwd_prep_kernel(BwdParams bp, PrepBlo
     prep_segments(bp, blk - nb.gather);
   } else if (blk < nb.gather + nb.seg + nb.chunk) {
     prep_chunks(bp, blk - nb.gather - nb.seg);
+  } else if (blk < nb.gather + nb.seg + nb.chunk + nb.zero) {
+    prep_zero(bp, nb.gacc_floats, blk - nb.gather - nb.seg - nb.chunk);
   } else {
-    prep_delta<T, D>(bp, blk - nb.gather - nb.seg - nb.chunk);
+    prep_delta<T, D>(bp, blk - nb.gather - nb.seg - nb.chunk - nb.zero);
   }
 }
 

@@ -372,63 +372,59 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
   if (p2c) run(std::true_type{});
   else run(std::false_type{});
 
-  // Sum the two waves of each kind (1 into 0, 3 into 2) through LDS, then
-  // store the partial of this (block, head, partial group): [kind][dd][d],
-  // fp32, and its flag.  A partial without an active item is not written
-  // (its flag says so).
+  // Sum the two waves of each kind (1 into 0, 3 into 2) through LDS, in
+  // row-major [kind][dd][d] order, then add the sums to the block's
+  // accumulator (zeroed by the prep kernel) with fp32 atomics, one row of D
+  // consecutive floats per wave instruction.  The workgroups of one block
+  // and head meet there, so the fold reads one accumulator per block; the
+  // order of the additions, and so the last bits of dKr and dQr, varies
+  // from run to run.  A kind whose workgroup had no active item adds
+  // nothing.  A collapsed block adds only row 0, the sum over its offsets.
+  constexpr int RS = D + 4;  // fp32 row stride of the sums in LDS
+  static_assert(NW * WELEMS * sizeof(T) >= 2 * DBW * RS * sizeof(float), "LDS holds both kinds' sums");
   if (lane == 0) nact_sh[w] = nact;
-  __syncthreads();
-  float* red = reinterpret_cast<float*>(lds);
-  // without a mask every partial is written (zeros if it has no items) and
-  // the flags are not used
-  const bool any = nact + nact_sh[w ^ 1] > 0 || !LISTED;
-  if (LISTED && sub == 0 && active && lane == 0)
-    bp.gflag[((int64_t)(h * bp.NDB + dblk) * bp.NPG + pg) * 2 + (p2c ? 1 : 0)] = any ? (collapse ? 2 : 1) : 0;
-  if (sub == 1 && any) {
-    f32x4* dst = reinterpret_cast<f32x4*>(red) + (w >> 1) * (NEB * ND * 64) + lane;
+  __syncthreads();  // every wave is done with its region
+  const bool any = nact + nact_sh[w ^ 1] > 0;
+  float* red = reinterpret_cast<float*>(lds) + (p2c ? DBW * RS : 0);
+  auto put = [&](bool add) {
 #pragma unroll
-    for (int eb = 0; eb < NEB; ++eb)
-#pragma unroll
-      for (int db = 0; db < ND; ++db) dst[(eb * ND + db) * 64] = acc[eb][db];
-  }
-  __syncthreads();
-  if (sub == 0 && active && any) {
-    const f32x4* src = reinterpret_cast<const f32x4*>(red) + (w >> 1) * (NEB * ND * 64) + lane;
-    float* out = bp.gpart + ((int64_t)(h * bp.NDB + dblk) * bp.NPG + pg) * 2 * DBW * D + (p2c ? DBW * D : 0);
-    if (collapse) {
-      // sum over the offsets: the 8 blocks of 16 in registers, then the 16
-      // lanes of a lane group
-      f32x4 sum[ND];
+    for (int eb = 0; eb < NEB; ++eb) {
+      const int e = 16 * eb + c16;
+      const int dd = p2c ? e : DBW - 1 - e;  // offset d0 + dd
 #pragma unroll
       for (int db = 0; db < ND; ++db) {
-        sum[db] = zero4();
-#pragma unroll
-        for (int eb = 0; eb < NEB; ++eb) sum[db] += acc[eb][db] + src[(eb * ND + db) * 64];
-#pragma unroll
-        for (int m = 1; m < 16; m <<= 1)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) sum[db][e] += __shfl_xor(sum[db][e], m);
+        f32x4* r = reinterpret_cast<f32x4*>(red + dd * RS + 16 * db + 4 * g);
+        *r = add ? *r + acc[eb][db] : acc[eb][db];
       }
-      if (c16 == 0)
-#pragma unroll
-        for (int db = 0; db < ND; ++db) *reinterpret_cast<f32x4*>(out + 16 * db + 4 * g) = sum[db];
+    }
+  };
+  if (sub == 1) put(false);
+  __syncthreads();
+  if (sub == 0) put(true);
+  __syncthreads();
+  if (active && any) {
+    float* out = bp.gpart + ((int64_t)(h * bp.NDB + dblk) * 2 + (p2c ? 1 : 0)) * DBW * D;
+    const int tt = sub * 64 + lane;  // 128 threads of this kind
+    if (collapse) {
+      if (tt < D) {
+        float sum = 0.f;
+        for (int dd = 0; dd < DBW; ++dd) sum += red[dd * RS + tt];
+        unsafeAtomicAdd(out + tt, sum);
+      }
     } else {
-#pragma unroll
-      for (int eb = 0; eb < NEB; ++eb) {
-        const int e = 16 * eb + c16;
-        const int dd = p2c ? e : DBW - 1 - e;  // offset d0 + dd
-#pragma unroll
-        for (int db = 0; db < ND; ++db)
-          *reinterpret_cast<f32x4*>(out + (int64_t)dd * D + 16 * db + 4 * g) = acc[eb][db] + src[(eb * ND + db) * 64];
+#pragma unroll 8
+      for (int i = 0; i < DBW * D / 128; ++i) {
+        const int f = 128 * i + tt, dd = f / D, d = f % D;
+        unsafeAtomicAdd(out + f, red[dd * RS + d]);
       }
     }
   }
 }
 
-// tab[h][r][:] (+)= s * sum over partial groups and offsets d with row(d) = r
-// of the partials (accumulated into fp32, or written in fp32 or bf16).  One
+// tab[h][r][:] (+)= s * sum over offsets d with row(d) = r of the block
+// accumulators (accumulated into fp32, or written in fp32 or bf16).  One
 // workgroup of NT threads per (table, h, r): NT / (D/4) parts split the
-// (offset, partial group) pairs of the row's offset range [begin, end) (from
+// units of the row's offset range [begin, end) (from
 // prep_segments), each part with four independent sums so that four loads
 // are in flight; lanes of a part hold 4 columns each.  The parts are summed
 // with lane shuffles and, across waves, through LDS in a fixed order.  Long
@@ -455,19 +451,14 @@ __global__ __launch_bounds__(NT) void dsa_bwd_fold_kernel(BwdParams bp) {
     nf = (b2 - b1) / DBW;
     nr = end - b2;
   }
-  const int npairs = (nl + nf + nr) * bp.NPG;
-  const bool flagged = bp.cinfo != nullptr;  // masks: partials without items were not written
-  // partial of (unit, group) pair it; zero where none was written
+  const int npairs = nl + nf + nr;
+  // accumulator row of unit it (a single offset, or a whole block's row 0)
   auto pair_val = [&](int it) {
-    const int u = it / bp.NPG, k = it % bp.NPG;
-    const bool whole = u >= nl && u < nl + nf;
-    const int d = u < nl ? beg + u : whole ? b1 + (u - nl) * DBW : b2 + (u - nl - nf);
+    const bool whole = it >= nl && it < nl + nf;
+    const int d = it < nl ? beg + it : whole ? b1 + (it - nl) * DBW : b2 + (it - nl - nf);
     const int dblk = (d + LkP) / DBW, dd = whole ? 0 : (d + LkP) % DBW;
-    const int64_t pi = (int64_t)(h * bp.NDB + dblk) * bp.NPG + k;
-    const f32x4* src =
-        reinterpret_cast<const f32x4*>(bp.gpart + pi * 2 * DBW * D + (int64_t)((q ? DBW : 0) + dd) * D + 4 * c4);
-    const f32x4 v = *src;  // read in any case (inside the workspace), so both loads are in flight together
-    return (!flagged || bp.gflag[pi * 2 + t]) ? v : zero4();
+    return *reinterpret_cast<const f32x4*>(bp.gpart + ((int64_t)(h * bp.NDB + dblk) * 2 + t) * DBW * D +
+                                           (int64_t)dd * D + 4 * c4);
   };
   f32x4 a4[4] = {zero4(), zero4(), zero4(), zero4()};
   int it = part;

@@ -221,7 +221,7 @@ int device_cus() {
 // extents the kernels share.
 struct WsLayout {
   int LqP, LkP, TGP, OFF, NDB, NPG;
-  size_t rowinfo, krgt, qrgt, ds, gpart, gflag, seg, cinfo, korder, qorder, total;
+  size_t rowinfo, krgt, qrgt, ds, gpart, seg, cinfo, korder, qorder, total;
 };
 
 WsLayout ws_layout(const dsa_bwd_args* a) {
@@ -234,14 +234,16 @@ WsLayout ws_layout(const dsa_bwd_args* a) {
   w.TGP = w.LqP + w.LkP;        // offsets [-(LkP - 1), LqP] of every band window
   w.NDB = (w.LqP + w.LkP) / dsa::tbcfg::DBW;
   // Partial groups of the table kernel (ranges of an offset block's items
-  // of one kind; a central block has about B * L / 32): about three
-  // workgroups per CU (two run at a time; the workgroups of the outer
-  // offset blocks are short).  Long sequences and masks concentrate the
-  // work in the central blocks, whose workgroups then bound the launch:
-  // those get at most 64 items of a kind each.
+  // of one kind; a central block has about B * L / 32): about one and a
+  // half workgroups per CU, whose fp32 atomics into the block accumulators
+  // stay few and which leave room for dq beside them (B=32, L=512: DQ and
+  // FOLD 166 us with three workgroups per CU, 157 with one and a half, 200
+  // with six).  Long sequences and masks concentrate the work in the
+  // central blocks, whose workgroups then bound the launch: those get at
+  // most 64 items of a kind each.
   const int per = f.H * w.NDB;
   const int64_t items = (int64_t)f.B * ((w.LqP > w.LkP ? w.LqP : w.LkP) / 32);
-  int64_t groups = (3 * device_cus() + per - 1) / per;
+  int64_t groups = (3 * device_cus() / 2 + per - 1) / per;
   if (w.NDB > 16 || f.key_keep || f.seg) groups = std::max<int64_t>(groups, (items + 63) / 64);
   w.NPG = (int)std::min<int64_t>(std::max<int64_t>(groups, 1), items);
   size_t off = 0;
@@ -254,9 +256,7 @@ WsLayout ws_layout(const dsa_bwd_args* a) {
   w.ds = off;
   off = align_up(off + (size_t)f.B * f.H * w.LkP * w.LqP * es, 256);
   w.gpart = off;
-  if (f.flags) off = align_up(off + (size_t)f.H * w.NDB * w.NPG * 2 * dsa::tbcfg::DBW * f.D * sizeof(float), 256);
-  w.gflag = off;
-  if (f.flags) off = align_up(off + (size_t)f.H * w.NDB * w.NPG * 2, 256);
+  if (f.flags) off = align_up(off + (size_t)f.H * w.NDB * 2 * dsa::tbcfg::DBW * f.D * sizeof(float), 256);
   w.seg = off;
   if (f.flags) off = align_up(off + (size_t)2 * 2 * (2 * f.att_span) * sizeof(int), 256);
   w.cinfo = off;
@@ -310,7 +310,6 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
   bp.qrgt = base + ws.qrgt;
   bp.ds = base + ws.ds;
   bp.gpart = reinterpret_cast<float*>(base + ws.gpart);
-  bp.gflag = reinterpret_cast<uint8_t*>(base + ws.gflag);
   bp.rowseg = reinterpret_cast<int*>(base + ws.seg);
   bp.cinfo = (f.key_keep || f.seg) ? reinterpret_cast<int4*>(base + ws.cinfo) : nullptr;
   const int nkt = ws.LkP / dsa::kvcfg::BKW;
@@ -330,16 +329,20 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
     dsa::PrepBlocks nb;
     const int64_t n = (int64_t)f.B * f.H * ws.LqP * (D / (16 / (int)sizeof(T)));
     nb.delta = (int)((n + 255) / 256);
-    nb.gather = nb.seg = nb.chunk = 0;
+    nb.gather = nb.seg = nb.chunk = nb.zero = 0;
+    nb.gacc_floats = 0;
     if (f.key_keep || f.seg) nb.chunk = (int)(((int64_t)f.B * (ws.LqP / 32) + 255) / 256);
     if (f.flags) {
       const int64_t m = 2 * (int64_t)f.H * D * (ws.TGP / (16 / (int)sizeof(T)));
       nb.gather = (int)((m + 255) / 256);
       const int64_t ns = 2 * (int64_t)(f.Lq + f.Lk);
       nb.seg = (int)((ns + 255) / 256);
+      // the table kernel's block accumulators, added to in FOLD
+      nb.gacc_floats = (int64_t)f.H * ws.NDB * 2 * dsa::tbcfg::DBW * D;
+      nb.zero = (int)((nb.gacc_floats / 4 + 255) / 256);
     }
-    hipLaunchKernelGGL((dsa::dsa_bwd_prep_kernel<T, D>), dim3((unsigned)(nb.gather + nb.seg + nb.chunk + nb.delta)), dim3(256), 0,
-                       st, bp, nb);
+    hipLaunchKernelGGL((dsa::dsa_bwd_prep_kernel<T, D>),
+                       dim3((unsigned)(nb.gather + nb.seg + nb.chunk + nb.zero + nb.delta)), dim3(256), 0, st, bp, nb);
     if (launch_check("dsa_bwd_prep_kernel")) return 1;
     if (kbuf && launch_order(bp.f, kbuf, nkt, false, st)) return 1;
     // dq's tiles (128 queries against 64-key tiles) weigh as the forward's

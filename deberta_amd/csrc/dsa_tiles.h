@@ -49,9 +49,8 @@ struct BwdParams {
   void* ds;         // dS [B, H, f.LqP, f.LkP] (rows = queries), zero outside [0, Lq) x [0, Lk)
   void* krgt;       // [H, D, TGP]: krgt[h][d][t] = Kr[h][c(t - OFF)][d]
   void* qrgt;       // [H, D, TGP]: qrgt[h][d][t] = Qr[h][p(t - OFF)][d]
-  float* gpart;     // table-gradient partials [H][NDB][NPG][2][128][D]
-  uint8_t* gflag;   // masks: [H][NDB][NPG][2], 0 = partial not written (no active item), 1 = written
-                    // per offset, 2 = written summed over its block (row 0)
+  float* gpart;     // table-gradient block accumulators [H][NDB][2][128][D], fp32: zeroed by the prep
+                    // kernel, added to by the table kernel (a block summed over its offsets: row 0)
   int* rowseg;      // [2][2][R]: offsets [begin, end) of each table row (c2p, p2c)
   int4* cinfo;      // segment masks: [B][LqP / 32] per 32-token chunk (lo, hi, all active, 0)
   const int* korder;  // dkdv launch order of the (batch row, key tile) items, or null (dsa_order.h)
