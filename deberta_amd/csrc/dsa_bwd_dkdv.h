@@ -82,6 +82,9 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
   __shared__ short qlist[SEGM ? MAXQT : 1];
   __shared__ int qlen;
   __shared__ __align__(16) int qsg[MASK == MASK_SEG ? 2 : 1][MASK == MASK_SEG ? BQ : 1];
+  // dense pair masks: the current tile's mask, one bit per (query, key),
+  // 16 keys a word (read once per tile with 16-byte loads)
+  __shared__ uint16_t pmask[MASK == MASK_PAIR ? BQ : 1][MASK == MASK_PAIR ? BKW / 16 : 1];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = tid >> 6, g = (tid & 63) >> 4, c16 = tid & 15;
@@ -283,12 +286,21 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
         int keep = 0;
         const int r = tid >> 3, part = tid & 7;
         const int i = i0 + r;
+        uint32_t bits = 0;
         if (i < Lq && pkb[(int64_t)i * p.pkq + i]) {
-          const uint8_t* row = pkb + (int64_t)i * p.pkq;
+          // one 16-byte read of the mask row (rows 16-byte aligned,
+          // host-checked; a 16-key chunk that starts below Lk lies in the
+          // row's allocation), kept as 16 bits in LDS for the tile
           const int jb0 = j0 + part * (BKW / 8);
-          const int jend = min(jb0 + BKW / 8, Lk);
-          for (int j = jb0; j < jend; ++j) keep |= row[j];
+          if (jb0 < Lk) {
+            const uint4 v = *reinterpret_cast<const uint4*>(pkb + (int64_t)i * p.pkq + jb0);
+            const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int q = 0; q < 16; ++q) bits |= ((wv[q >> 2] >> (8 * (q & 3))) & 0xffu) ? (1u << q) : 0u;
+          }
         }
+        pmask[r][part] = (uint16_t)bits;
+        keep = bits != 0;
         skip = !__syncthreads_or(keep);
       }
       if (skip) {
@@ -362,7 +374,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
             // unwritten saved term: they are never exponentiated
             bool keep = jkeep[jb] && lr != INFINITY;
             if (MASK == MASK_SEG && !full) keep = keep && qsg[n & 1][il] == jseg[jb];
-            if (MASK == MASK_PAIR) keep = keep && pkb[(int64_t)min(i0 + il, Lq - 1) * p.pkq + jcol[jb]] != 0;
+            if (MASK == MASK_PAIR) keep = keep && ((pmask[il][2 * w + jb] >> c16) & 1u);
             const float pe = keep ? __builtin_amdgcn_exp2f(__builtin_fmaf(sc[jb][ib][e], sl2, -lr)) : 0.f;
             pp[jb][ib][e] = pe;
             dsh[jb][ib][e] = pe * (dp[e] - R[2 * il + 1]);

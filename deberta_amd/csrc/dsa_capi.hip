@@ -99,6 +99,13 @@ int check_fwd(const dsa_fwd_args* a) {
     return fail("dsa: give at most one of key_keep, pair_keep and seg");
   if ((a->key_keep || a->pair_keep || a->seg) && a->Lq != a->Lk)
     return fail("dsa: masks need Lq == Lk (query liveness is read from the key mask)");
+  if (a->pair_keep) {  // the kernels read 16-byte chunks of the mask rows
+    const int64_t k16 = (a->Lk + 15) / 16 * 16;
+    if (!aligned16(a->pair_keep) || a->pair_keep_strides[0] % 16 || a->pair_keep_strides[1] % 16 ||
+        (a->pair_keep_strides[1] != 0 ? a->pair_keep_strides[1] < k16 : a->Lk % 16 != 0))
+      return fail("dsa: pair_keep must be 16-byte aligned, with batch and row strides multiples of 16 bytes "
+                  "and each row's allocation reaching a multiple of 16 bytes past Lk");
+  }
   if ((a->key_keep || a->seg) && a->Lk > 32768)  // per-tile lists in LDS
     return fail("dsa: key-padding and segment masks support sequences of at most 32768 tokens, got %d", a->Lk);
   const int vec = 16 / elem_bytes(a->dtype);

@@ -212,16 +212,23 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
     if constexpr (SEGM) {
       full = (kflag[kt] & 2) != 0;
     } else if (MASK == MASK_PAIR) {
-      int keep = 0;
+      // 16-byte reads of the mask rows (rows 16-byte aligned, host-checked;
+      // a 16-key chunk that starts below Lk lies in the row's allocation)
+      uint32_t keep = 0;
       const int r = tid >> 1, half = tid & 1;
       const int i = i0 + r;
       if (i < Lq) {
         const uint8_t* row = pkb + (int64_t)i * p.pkq;
-        const int jb0 = j0 + half * (BK / 2);
-        const int jend = min(jb0 + BK / 2, Lk);
-        for (int j = jb0; j < jend; ++j) keep |= row[j];
+#pragma unroll
+        for (int c = 0; c < BK / 32; ++c) {
+          const int jc = j0 + half * (BK / 2) + 16 * c;
+          if (jc < Lk) {
+            const uint4 v = *reinterpret_cast<const uint4*>(row + jc);
+            keep |= v.x | v.y | v.z | v.w;
+          }
+        }
       }
-      if (!__syncthreads_or(keep)) continue;
+      if (!__syncthreads_or(keep != 0)) continue;
     }
     __syncthreads();  // previous tile's LDS reads are done
     if (kt != kfetched) fetch(kt);  // a tile after skipped ones was not prefetched
@@ -270,11 +277,11 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
           if constexpr (SEGM) ks4 = *reinterpret_cast<const int4*>(&ksg[16 * jb + 4 * g]);
           uint32_t pk4 = 0;
           if (MASK == MASK_PAIR && ilive[ib]) {
-            const uint8_t* row = pkb + (int64_t)i * p.pkq;
+            const int j = j0 + 16 * jb + 4 * g;
+            if (j < Lk) {  // one 4-byte read: keys j .. j + 3 (j < Lk covers them, as above)
+              const uint32_t v = *reinterpret_cast<const uint32_t*>(pkb + (int64_t)i * p.pkq + j);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int j = j0 + 16 * jb + 4 * g + e;
-              pk4 |= (j < Lk && row[j]) ? (1u << e) : 0u;
+              for (int e = 0; e < 4; ++e) pk4 |= ((v >> (8 * e)) & 0xffu) ? (1u << e) : 0u;
             }
           }
 #pragma unroll

@@ -147,6 +147,18 @@ def kernel_masks(
             kk = kk.contiguous()
         return kk.expand(batch, key_len), None
     pk = bytes_[:, 0, :, :]
-    if pk.stride(-1) != 1:
-        pk = pk.contiguous()
+    # the kernels read 16-byte chunks of the rows: rows 16-byte aligned,
+    # row and batch strides multiples of 16 bytes, each row's allocation
+    # reaching the next multiple of 16 past key_len (zero padding)
+    k16 = (key_len + 15) // 16 * 16
+    if (
+        pk.stride(-1) != 1
+        or pk.data_ptr() % 16
+        or pk.stride(-2) % 16
+        or pk.stride(-2) < k16
+        or (pk.shape[0] > 1 and pk.stride(0) % 16)
+    ):
+        padded = torch.zeros(pk.shape[0], pk.shape[1], k16, dtype=torch.uint8, device=pk.device)
+        padded[:, :, :key_len] = pk
+        pk = padded[:, :, :key_len]
     return None, pk.expand(batch, query_len, key_len)

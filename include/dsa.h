@@ -97,7 +97,10 @@ typedef struct dsa_fwd_args {
   int64_t kr_strides[2];  /* element strides of h, r */
   int64_t qr_strides[2];
   int64_t key_keep_stride_b;
-  int64_t pair_keep_strides[2]; /* b, q (k contiguous) */
+  int64_t pair_keep_strides[2]; /* b, q (k contiguous); pair_keep 16-byte aligned,
+                                   both strides multiples of 16, each row's
+                                   allocation reaching round_up(Lk, 16) bytes
+                                   (read in 16-byte chunks) */
   int32_t B, H, Lq, Lk, D;
   int32_t att_span;       /* A; R = 2A rows in kr/qr */
   int32_t dtype;          /* DSA_F32 or DSA_BF16 */
