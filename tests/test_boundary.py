@@ -226,6 +226,22 @@ def test_kernel_masks():
         kernel_masks(torch.ones(2, 4, dtype=torch.bool), 2, 4, 4)
 
 
+def test_pair_mask_rows_are_16_byte_aligned():
+    """The kernels read pair-mask rows in 16-byte chunks: kernel_masks hands
+    them rows whose stride is a multiple of 16 reaching round_up(L, 16),
+    padding a copy with zeros when the input's rows do not."""
+    g = torch.Generator().manual_seed(3)
+    for L in (64, 700):
+        dense = torch.rand(2, 1, L, L, generator=g) > 0.5
+        kk, pk = kernel_masks(dense, 2, L, L)
+        assert kk is None and pk.shape == (2, L, L) and pk.stride(-1) == 1
+        assert pk.stride(-2) % 16 == 0 and pk.stride(-2) >= (L + 15) // 16 * 16 and pk.data_ptr() % 16 == 0
+        assert torch.equal(pk.bool(), dense[:, 0])
+        if L % 16:
+            base = pk.as_strided((2, L, pk.stride(-2)), (pk.stride(0), pk.stride(1), 1))
+            assert not base[:, :, L:].any()  # zero padding
+
+
 def test_segment_mask_host_side():
     """SegmentMask is the ids form of the reference's packed-document mask:
     dense() is that mask, and the kernels get the ids as int32 [B, S]."""
