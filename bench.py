@@ -45,7 +45,7 @@ WORKLOADS = {
     "C5": (64, 512, 16, None, "B=64 L=512 H=16, no mask"),
     "C3": (16, 512, 12, None, "12-layer DeBERTa-v3-base-shaped encoder fwd+bwd under an RTD loss, bf16 autocast"),
     "C5layer": (64, 512, 16, None, "DeBERTa-v3-large-shaped attention layer (hidden 1024, projections included) fwd+bwd, bf16, inside torch.compile"),
-    "C4": (4, 4096, 12, "doc", "B=4 L=4096 H=12, packed documents (lengths ~Geometric(mean 600)) as the dense (B,1,L,L) doc-block mask"),
+    "C4": (4, 4096, 12, "doc", "B=4 L=4096 H=12, packed documents (lengths ~Geometric(mean 600)) as the dense (B,1,L,L) doc-block mask (recognised once and run as segment ids)"),
     "C4seg": (4, 4096, 12, "seg", "as C4, the same documents given as segment ids (SegmentMask)"),
 }
 

@@ -8,6 +8,7 @@ document mask ``_build_doc_block_mask`` (training/compile.py:310-349).
 
 from __future__ import annotations
 
+import weakref
 from typing import Optional
 
 import torch
@@ -105,17 +106,63 @@ class SegmentMask:
         return ids.to(device).contiguous()
 
 
+def dense_as_segments(pair_keep: torch.Tensor) -> Optional[torch.Tensor]:
+    """Segment ids with the same meaning as a dense ``[B, L, L]`` keep mask,
+    or None if there are none.
+
+    The kernels' segment rule keeps (i, j) iff seg_i != 0 and seg_i ==
+    seg_j, and a query with seg 0 is a dead row; the dense rule keeps (i, j)
+    per element, a query whose diagonal is unset being a dead row.  Take
+    seg_i = 1 + (the first key row i keeps) for live rows, 0 for dead ones:
+    the two rules agree iff every live row keeps exactly the keys with its
+    own id (dead rows' contents never reach an output).  The packed-document
+    masks of the reference (``_build_doc_block_mask``, training/compile.py:
+    310-349) have this form.  One pass over the mask on its device, and one
+    host synchronisation for the answer."""
+    keep = pair_keep.bool()
+    b, lq, lk = keep.shape
+    if lq != lk or lk > 32768:
+        return None
+    live = keep.diagonal(dim1=1, dim2=2)
+    first = keep.to(torch.uint8).argmax(dim=-1)  # first kept key (argmax: first of the maxima)
+    ids = torch.where(live, first + 1, torch.zeros_like(first)).to(torch.int32)
+    expect = ids[:, :, None] == ids[:, None, :]
+    agree = (keep == expect) | ~live[:, :, None]
+    if not bool(agree.all()):
+        return None
+    return ids.contiguous()
+
+
+# dense mask -> (its version, segment ids or None), per mask tensor object
+_SEGMENTS_OF: "weakref.WeakKeyDictionary[torch.Tensor, tuple[int, Optional[torch.Tensor]]]" = (
+    weakref.WeakKeyDictionary()
+)
+
+
+def _segments_cached(mask: torch.Tensor, pair_keep: torch.Tensor) -> Optional[torch.Tensor]:
+    hit = _SEGMENTS_OF.get(mask)
+    if hit is not None and hit[0] == mask._version:
+        return hit[1]
+    ids = dense_as_segments(pair_keep)
+    _SEGMENTS_OF[mask] = (mask._version, ids)
+    return ids
+
+
 def kernel_masks(
     attention_mask: "Optional[torch.Tensor | SegmentMask]",
     batch: int,
     query_len: int,
     key_len: int,
     device: Optional[torch.device] = None,
+    segments_from_dense: bool = True,
 ) -> tuple[Optional[torch.Tensor], Optional[torch.Tensor]]:
     """Split a rank-4 keep mask into the kernels' ``(key_keep, pair_keep)``.
 
     ``(B|1, 1, 1, K)`` becomes a ``[B, K]`` byte view (``key_keep``),
-    ``(B|1, 1, Q, K)`` a ``[B, Q, K]`` byte view (``pair_keep``).  A batch
+    ``(B|1, 1, Q, K)`` a ``[B, Q, K]`` byte view (``pair_keep``), or, for a
+    dense mask of the packed-document form on the GPU in eager mode, the
+    equivalent int32 segment ids (``dense_as_segments``; off with
+    ``segments_from_dense=False``).  A batch
     dimension of 1 is broadcast with stride 0.  A ``SegmentMask`` becomes
     ``int32 [B, S]`` segment ids in the ``key_keep`` slot, on ``device``
     (default: the ids' own).  ``None`` means no mask.
@@ -147,6 +194,13 @@ def kernel_masks(
             kk = kk.contiguous()
         return kk.expand(batch, key_len), None
     pk = bytes_[:, 0, :, :]
+    # A dense mask of the packed-document form runs as segment ids (the
+    # kernels then skip the tiles between documents); checked once per mask
+    # tensor and version, in eager mode on the GPU only.
+    if segments_from_dense and pk.is_cuda and not torch.compiler.is_compiling():
+        ids = _segments_cached(attention_mask, pk.expand(batch, query_len, key_len))
+        if ids is not None:
+            return (ids.to(device) if device is not None else ids), None
     # the kernels read 16-byte chunks of the rows: rows 16-byte aligned,
     # row and batch strides multiples of 16 bytes, each row's allocation
     # reaching the next multiple of 16 past key_len (zero padding)

@@ -22,7 +22,7 @@ class Case:
     buckets: int = 256
     max_pos: int = 512
     types: str = "c2p|p2c"
-    mask: str = "none"  # none | key | pair | seg | seg_mixed | dead
+    mask: str = "none"  # none | key | pair | pair_auto | seg | seg_mixed | dead
     seed: int = 0
     Lk: Optional[int] = None
     std: float = 1.0
@@ -55,7 +55,7 @@ def make_inputs(c: Case) -> dict:
         lens = torch.randint(max(1, c.L // 8), c.L + 1, (c.B,), generator=g)
         lens[0] = c.L
         mask = (torch.arange(c.L)[None, :] < lens[:, None])[:, None, None, :]
-    elif c.mask in ("pair", "seg"):
+    elif c.mask in ("pair", "pair_auto", "seg"):
         # packed documents: contiguous runs of ids 1, 2, ..., a padded tail (id 0)
         ids = torch.zeros(c.B, c.L, dtype=torch.long)
         for b in range(c.B):
@@ -133,7 +133,11 @@ def hip_run(c: Case, x: dict, dtype: torch.dtype, device, grads: bool = True) ->
         mask = SegmentMask(x["seg"])
     else:
         mask = x["mask"].to(device) if x["mask"] is not None else None
-    kk, pk = kernel_masks(mask, c.B, c.L, Lk, device)
+    # "pair" keeps the dense document mask on the pair-mask kernels;
+    # "pair_auto" lets kernel_masks turn it into segment ids
+    kk, pk = kernel_masks(mask, c.B, c.L, Lk, device, segments_from_dense=c.mask != "pair")
+    if c.mask == "pair_auto":
+        assert pk is None and kk is not None and kk.dtype == torch.int32, "document mask not recognised"
     sf = 1 + sum(t in types for t in ("c2p", "p2c", "p2p"))
     scale = 1.0 / math.sqrt(c.D * sf)
     out, lse, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, kk, pk, c.A, scale)

@@ -242,6 +242,27 @@ def test_pair_mask_rows_are_16_byte_aligned():
             assert not base[:, :, L:].any()  # zero padding
 
 
+def test_dense_document_masks_are_recognised():
+    """dense_as_segments: a packed-document mask (reference form, pad rows
+    keeping only their CLS edge) has segment ids with the kernels' rule,
+    which then agrees with it on every live row; other masks have none."""
+    from deberta_amd.masks import dense_as_segments
+
+    ids = torch.tensor([[1, 1, 2, 2, 2, 3, 0, 0], [4, 4, 4, 4, 5, 5, 5, 0]])
+    dense = build_doc_block_mask(ids)
+    seg = dense_as_segments(dense)
+    assert seg is not None and seg.dtype == torch.int32
+    live = ids != 0
+    rule = (seg[:, :, None] == seg[:, None, :]) & (seg[:, :, None] != 0)
+    assert torch.equal(rule[live], dense[live]) and torch.equal(seg != 0, live)
+    # interleaved segments are an equivalence too
+    ids2 = torch.tensor([[1, 2, 1, 2, 3, 3, 1, 0]])
+    assert dense_as_segments(build_doc_block_mask(ids2)) is not None
+    # a causal mask is not one
+    causal = torch.tril(torch.ones(8, 8, dtype=torch.bool))[None]
+    assert dense_as_segments(causal) is None
+
+
 def test_segment_mask_host_side():
     """SegmentMask is the ids form of the reference's packed-document mask:
     dense() is that mask, and the kernels get the ids as int32 [B, S]."""

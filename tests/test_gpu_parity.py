@@ -118,7 +118,7 @@ def test_long_sequences(c, dtype, gpu):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
-@pytest.mark.parametrize("mask", ["key", "pair", "seg", "seg_mixed", "dead"])
+@pytest.mark.parametrize("mask", ["key", "pair", "pair_auto", "seg", "seg_mixed", "dead"])
 def test_masks(mask, dtype, gpu):
     c = Case(B=3, H=2, L=260, D=64, mask=mask, seed=11)
     got = _check(c, dtype, gpu)
@@ -130,6 +130,24 @@ def test_masks(mask, dtype, gpu):
         # dead query rows: output exactly zero, no gradient into q
         assert float(got["out"][dead].abs().max()) == 0.0
         assert float(got["dq"][dead].abs().max()) == 0.0
+
+
+def test_document_mask_runs_as_segments(gpu):
+    """A dense packed-document mask is recognised and run as segment ids:
+    the results equal those of the dense pair-mask kernels bit for bit
+    (skipped tiles only ever add exact zeros), dKr / dQr up to the order of
+    their fp32 atomic additions."""
+    import dataclasses
+
+    c = Case(B=2, H=2, L=384, D=64, mask="pair", seed=61)
+    x = make_inputs(c)
+    dense = hip_run(c, x, torch.bfloat16, gpu)
+    auto = hip_run(dataclasses.replace(c, mask="pair_auto"), x, torch.bfloat16, gpu)
+    print(f"[doc mask as segments] keys {sorted(dense)}", file=sys.stderr, flush=True)
+    for name in ("out", "lse", "dq", "dk", "dv"):
+        assert torch.equal(dense[name], auto[name]), name
+    for name in ("dkr", "dqr"):
+        assert max_rel(auto[name], dense[name]) <= 1e-2, name
 
 
 # --- relative-position configurations --------------------------------------------
