@@ -312,6 +312,10 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
       }
 
       // ---- scores (queries down, keys across): Q K^T + saved bias (unscaled) --------------------
+      // The products run at a raised wave priority and the P / dS arithmetic
+      // at the normal one, so that the SIMD's other wave fills in (dkdv
+      // 158.2 -> 156.8 us in one process).
+      __builtin_amdgcn_s_setprio(1);
       const float one = opaque_one();
       f32x4 sc[2][BQ / 16];
 #pragma unroll
@@ -353,6 +357,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
         }
       }
 
+      __builtin_amdgcn_s_setprio(0);
       // ---- P, dP, dS -----------------------------------------------------------------------------
       f32x4 pp[2][BQ / 16], dsh[2][BQ / 16];
 #pragma unroll
@@ -399,6 +404,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
           store_ds(i0, kk, mi, __builtin_bit_cast(vec4, tr4(stg + ZL, SROW, 16 * kk + 4 * g, 16 * mi, c16)));
 
       // ---- dV^T += dO^T P,  dK^T += Q^T dS (dO^T, Q^T read transposed) -----------------------
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int s = 0; s < BQ / M::KSTEP; ++s) {
         frag pf[2], df[2];
@@ -443,6 +449,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
           }
         }
       }
+      __builtin_amdgcn_s_setprio(0);
     };
     for (int n = 0; n < nlist; n += 2) {
       tile(n, Qs0, dOs0, Bs0, Rs0, Qs1, dOs1, Bs1, Rs1);
