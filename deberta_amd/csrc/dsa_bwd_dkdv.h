@@ -215,16 +215,19 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
   // dS rows i of the wave's 32 keys: lane (g, c16) writes keys jw + 16 kk +
   // 4g + [0, 4) of query i0 + 16 mi + c16.
   typedef T vec4 __attribute__((ext_vector_type(4)));
-  auto store_ds = [&](int i0, int kk, int mi, const vec4& v) {
-    *reinterpret_cast<vec4*>(dsw + (int64_t)(i0 + 16 * mi + c16) * p.LkP + 16 * kk + 4 * g) = v;
+  // dS rows i of the wave's 32 keys: lane (g, c16) writes keys jw + 8g +
+  // [0, 8) of query i0 + 16 mi + c16, one 16-byte store (bf16; two for
+  // fp32): NST store instructions per tile.
+  typedef T vec8 __attribute__((ext_vector_type(8)));
+  constexpr int NST = (BQ / 16) * (int)(sizeof(vec8) / 16);
+  auto store_ds = [&](int i0, int mi, const vec8& v) {
+    *reinterpret_cast<vec8*>(dsw + (int64_t)(i0 + 16 * mi + c16) * p.LkP + 8 * g) = v;
   };
   if (!any_key) {
     if (!SEGM)
       for (int qi = 0; qi < nqt; ++qi)
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int mi = 0; mi < BQ / 16; ++mi) store_ds(qi * BQ, kk, mi, vec4{});
+        for (int mi = 0; mi < BQ / 16; ++mi) store_ds(qi * BQ, mi, vec8{});
   } else {
     // K and V rows of the wave's keys stay in registers (B operands)
     frag kf[2][NS], vf[2][NS];
@@ -258,9 +261,9 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
       const int ent = SEGM ? __builtin_amdgcn_readfirstlane(qlist[n]) : n;
       const int qi = ent & 0x3ff, i0 = qi * BQ;
       // This wave's copies of tile qi have landed: they were issued before
-      // the previous tile's four dS stores, its last vector-memory
+      // the previous tile's NST dS stores, its last vector-memory
       // instructions (tile 0 was waited for before the loop).
-      vm_wait<4>();
+      vm_wait<NST>();
       if (MASK == MASK_SEG && w == 1 && lane < BQ) qsg[n & 1][lane] = qseg_next;
       __syncthreads();  // ... every wave's, and the previous tile is no longer read
       if (SEGM && p2c && n > 0) {
@@ -305,9 +308,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
       }
       if (skip) {
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-          for (int mi = 0; mi < BQ / 16; ++mi) store_ds(i0, kk, mi, vec4{});
+          for (int mi = 0; mi < BQ / 16; ++mi) store_ds(i0, mi, vec8{});
         return;
       }
 
@@ -398,10 +399,8 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
           *reinterpret_cast<vec4*>(stg + (16 * jb + c16) * SROW + ZL + 16 * ib + 4 * g) = v;
         }
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int mi = 0; mi < BQ / 16; ++mi)
-          store_ds(i0, kk, mi, __builtin_bit_cast(vec4, tr4(stg + ZL, SROW, 16 * kk + 4 * g, 16 * mi, c16)));
+      for (int mi = 0; mi < BQ / 16; ++mi)
+        store_ds(i0, mi, join_halves<T>(tr4(stg + ZL, SROW, 8 * g, 16 * mi, c16), tr4(stg + ZL, SROW, 8 * g + 4, 16 * mi, c16)));
 
       // ---- dV^T += dO^T P,  dK^T += Q^T dS (dO^T, Q^T read transposed) -----------------------
       __builtin_amdgcn_s_setprio(1);

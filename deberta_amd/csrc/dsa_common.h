@@ -190,6 +190,19 @@ DSA_DEV f32x4 tr4(const float* X, int str, int k0, int m0, int c16) {
                X[(k0 + 3) * str + m0 + c16]};
 }
 
+// Eight elements of type T from two four-element vectors (a, then b).
+template <typename T, typename V4>
+DSA_DEV auto join_halves(const V4& a, const V4& b) {
+  typedef T v8 __attribute__((ext_vector_type(8)));
+  v8 r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    r[e] = a[e];
+    r[4 + e] = b[e];
+  }
+  return r;
+}
+
 DSA_DEV bf16x8 join8(bf16x4 a, bf16x4 b) {
   bf16x8 f;
 #pragma unroll
