@@ -57,11 +57,11 @@ WORKLOADS = {
 # (x1.0).  Commands and raw figures: profiles/hbm_traffic_headline.md.
 FETCH_SCALE, WRITE_SCALE = 2.0, 1.0
 TRAFFIC_KIB = {  # kernel: (FETCH_SIZE, WRITE_SIZE) as read
-    "dsa_fwd_kernel": (55296, 225024),
-    "dsa_bwd_dkdv_kernel": (179816, 245836),
-    "dsa_bwd_dq_kernel": (127051, 24576),
-    "dsa_bwd_table_kernel": (207371, 24576),
-    "dsa_bwd_fold_kernel": (4081, 2458),
+    "dsa_fwd_kernel": (55304, 225024),
+    "dsa_bwd_dkdv_kernel": (178632, 245781),
+    "dsa_bwd_dq_kernel": (127075, 24576),
+    "dsa_bwd_table_kernel": (208256, 24576),
+    "dsa_bwd_fold_kernel": (4082, 2458),
     "dsa_bwd_prep_kernel": (25834, 10760),
 }
 
