@@ -129,7 +129,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 4, c16 = lane & 15;
   const bool p2c = w >= 2;  // wave kind: 0, 1 -> Gc; 2, 3 -> Gp
   const int sub = w & 1;
-  // Work order.  Short sequences (fewer than 16 offset blocks, a grid of
+  // Work order.  Short sequences (fewer than 32 offset blocks, a grid of
   // a few workgroups per CU): blockIdx.x enumerates (offset block, head,
   // partial group) with the offset blocks that have the most items first,
   // so the shortest workgroups fill in at the end of the launch.  Longer
@@ -137,9 +137,10 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
   // enumerates (head, partial group, offset block), so the offset blocks of
   // one head and group, which stage the same Q and K item rows, run on one
   // XCD side by side and share its L2 (the balance at the end matters less
-  // there: 10% less time at L = 4096, 25% more at L = 512).
+  // there: 3% less time at L = 2048, 7% less at L = 4096 with documents;
+  // 33% more at L = 1024 and 25% more at L = 512).
   int rank, rem;
-  if (bp.NDB >= 16) {
+  if (bp.NDB >= 32) {
     const int m = xcd_remap(blockIdx.x, gridDim.x);
     rank = m % bp.NDB, rem = m / bp.NDB;
   } else {
