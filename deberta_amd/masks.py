@@ -8,10 +8,10 @@ document mask ``_build_doc_block_mask`` (training/compile.py:310-349).
 
 from __future__ import annotations
 
-import weakref
 from typing import Optional
 
 import torch
+from torch.utils.weak import WeakIdKeyDictionary
 
 
 def normalize_keep_mask(mask: torch.Tensor, *, name: str = "attention_mask") -> torch.Tensor:
@@ -133,13 +133,16 @@ def dense_as_segments(pair_keep: torch.Tensor) -> Optional[torch.Tensor]:
     return ids.contiguous()
 
 
-# dense mask -> (its version, segment ids or None), per mask tensor object
-_SEGMENTS_OF: "weakref.WeakKeyDictionary[torch.Tensor, tuple[int, Optional[torch.Tensor]]]" = (
-    weakref.WeakKeyDictionary()
-)
+# dense mask -> (its version, segment ids or None), per mask tensor object.
+# Keyed by object identity: a plain WeakKeyDictionary compares tensor keys
+# with Tensor.__eq__ (elementwise), which cannot decide a lookup.
+_SEGMENTS_OF: WeakIdKeyDictionary = WeakIdKeyDictionary()
 
 
 def _segments_cached(mask: torch.Tensor, pair_keep: torch.Tensor) -> Optional[torch.Tensor]:
+    """Segment ids of ``pair_keep`` (a ``[B or 1, L, L]`` view of ``mask``,
+    not expanded over the batch), cached per mask object and version.  The
+    ids keep the mask's own batch extent; callers expand them."""
     hit = _SEGMENTS_OF.get(mask)
     if hit is not None and hit[0] == mask._version:
         return hit[1]
@@ -198,9 +201,12 @@ def kernel_masks(
     # kernels then skip the tiles between documents); checked once per mask
     # tensor and version, in eager mode on the GPU only.
     if segments_from_dense and pk.is_cuda and not torch.compiler.is_compiling():
-        ids = _segments_cached(attention_mask, pk.expand(batch, query_len, key_len))
+        ids = _segments_cached(attention_mask, pk)
         if ids is not None:
-            return (ids.to(device) if device is not None else ids), None
+            ids = ids.to(device) if device is not None else ids
+            # a broadcast (1, 1, S, S) mask gives one row of ids, read with
+            # batch stride 0
+            return ids.expand(batch, key_len), None
     # the kernels read 16-byte chunks of the rows: rows 16-byte aligned,
     # row and batch strides multiples of 16 bytes, each row's allocation
     # reaching the next multiple of 16 past key_len (zero padding)

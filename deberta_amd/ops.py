@@ -25,6 +25,7 @@ Tensor layouts (see include/dsa.h):
 from __future__ import annotations
 
 import ctypes
+import warnings
 from typing import Optional
 
 import torch
@@ -151,6 +152,25 @@ def _validate(
         raise ValueError("dsa: rel_table of Lq + Lk - 1 entries is required with relative tables")
     if key_keep is not None and pair_keep is not None:
         raise ValueError("dsa: give at most one of key_keep and pair_keep")
+    # The kernels index the masks by (b, i) / (b, i, j) over the full batch:
+    # a mask of another extent would be read out of bounds.
+    Lk = k.shape[1]
+    if key_keep is not None:
+        if key_keep.dtype not in (torch.uint8, torch.int32):
+            raise TypeError(f"dsa: key_keep must be uint8 (keep bytes) or int32 (segment ids), got {key_keep.dtype}")
+        if key_keep.dim() != 2 or tuple(key_keep.shape) != (B, Lk) or key_keep.stride(-1) != 1:
+            raise ValueError(f"dsa: key_keep / segment ids must be [B={B}, Lk={Lk}] with unit key stride, "
+                             f"got {tuple(key_keep.shape)} strides {key_keep.stride()}")
+        if key_keep.device != q.device:
+            raise ValueError("dsa: key_keep must be on q's device")
+    if pair_keep is not None:
+        if pair_keep.dtype != torch.uint8:
+            raise TypeError(f"dsa: pair_keep must be uint8, got {pair_keep.dtype}")
+        if pair_keep.dim() != 3 or tuple(pair_keep.shape) != (B, Lq, Lk) or pair_keep.stride(-1) != 1:
+            raise ValueError(f"dsa: pair_keep must be [B={B}, Lq={Lq}, Lk={Lk}] with unit key stride, "
+                             f"got {tuple(pair_keep.shape)} strides {pair_keep.stride()}")
+        if pair_keep.device != q.device:
+            raise ValueError("dsa: pair_keep must be on q's device")
 
 
 @torch.library.custom_op("deberta_amd::dsa_fwd", mutates_args=(), device_types="cuda")
@@ -249,6 +269,25 @@ def fill_bwd_args(
     return a
 
 
+def _alert_nondeterministic_tables() -> None:
+    """torch's deterministic-algorithms contract: the relative-table
+    gradients are summed with fp32 atomics, so their last bits vary from run
+    to run (every other output is bitwise reproducible).  Raises under
+    ``torch.use_deterministic_algorithms(True)``, warns under
+    ``warn_only=True``."""
+    if not torch.are_deterministic_algorithms_enabled():
+        return
+    msg = (
+        "deberta_amd::dsa_bwd does not have a deterministic implementation of the relative-table "
+        "gradients (dkr / dqr are accumulated with fp32 atomics), but you set "
+        "'torch.use_deterministic_algorithms(True)'."
+    )
+    if torch.is_deterministic_algorithms_warn_only_enabled():
+        warnings.warn(msg)
+    else:
+        raise RuntimeError(msg)
+
+
 @torch.library.custom_op("deberta_amd::dsa_bwd", mutates_args=(), device_types="cuda")
 def dsa_bwd(
     dout: Tensor,
@@ -269,6 +308,8 @@ def dsa_bwd(
     """Gradients (dq, dk, dv, dkr, dqr).  dkr/dqr are [H, 2A, D] in the
     tables' dtype (empty when the matching table is None).  ``bias`` is the relative term
     dsa_fwd saved (required with c2p/p2c)."""
+    if kr is not None or qr is not None:
+        _alert_nondeterministic_tables()
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
     kr = None if kr is None else _kernel_ready(kr)
     qr = None if qr is None else _kernel_ready(qr)

@@ -9,10 +9,16 @@ clamped to [-A, A], c = clamp(t + A, 0, 2A-1), p = clamp(A - t, 0, 2A-1)
   S_ij  = -inf if the pair is masked;  row i is dead if not live_i
   P     = softmax_j(S) on live rows, 0 on dead rows;   O_i = sum_j P_ij v_j
 
+With the position-to-position term (p2p, deberta_v2_native.py:298-347) the
+score also holds s * Qr[A + min(i, A-1)].Kr[c]: the query's position row
+from the positive half of Qr, clamped to its A rows, against the same c2p
+row of Kr.
+
 Backward (Delta_i = dO_i.O_i, dS_ij = P_ij (dO_i.v_j - Delta_i)):
   dv_j  += P_ij dO_i
   dq_i  += s dS_ij (k_j + Kr[c])       dk_j += s dS_ij (q_i + Qr[p])
   dKr[c] += s dS_ij q_i                 dQr[p] += s dS_ij k_j
+  p2p:  dKr[c] += s dS_ij Qr[r_i],      dQr[r_i] += s dS_ij Kr[c],  r_i = A + min(i, A-1)
 Small shapes only (pure Python loops over (b, h, i, j)).
 """
 
@@ -51,9 +57,14 @@ def forward(
     pairwise: bool,
     scale: float,
     A: int,
+    p2p: bool = False,
+    c2p: bool = True,
+    p2c: bool = True,
 ) -> tuple[np.ndarray, np.ndarray]:
     """q, k, v: (B, H, L, D) fp64; kr, qr: (H, 2A, D) or None; rel (Lq, Lk).
-    Returns (O (B, H, Lq, D), P (B, H, Lq, Lk))."""
+    c2p / p2c use kr / qr when given (``c2p`` / ``p2c`` False leave a table
+    given for p2p out of those terms); ``p2p`` adds the position-to-position
+    term (needs both tables).  Returns (O (B, H, Lq, D), P (B, H, Lq, Lk))."""
     B, H, Lq, D = q.shape
     Lk = k.shape[2]
     pk, live = _liveness(keep, B, Lq, Lk, pairwise)
@@ -72,10 +83,12 @@ def forward(
                     if not pk[b, i, j]:
                         continue
                     acc = float(q[b, h, i] @ k[b, h, j])
-                    if kr is not None:
+                    if kr is not None and c2p:
                         acc += float(q[b, h, i] @ kr[h, c[i, j]])
-                    if qr is not None:
+                    if qr is not None and p2c:
                         acc += float(k[b, h, j] @ qr[h, p[i, j]])
+                    if p2p:
+                        acc += float(qr[h, A + min(i, A - 1)] @ kr[h, c[i, j]])
                     s_row[j] = scale * acc
                 m = np.max(s_row)
                 e = np.exp(s_row - m)
@@ -96,11 +109,14 @@ def backward(
     pairwise: bool,
     scale: float,
     A: int,
+    p2p: bool = False,
+    c2p: bool = True,
+    p2c: bool = True,
 ) -> dict[str, np.ndarray]:
     """Analytic gradients from the formulas in the module docstring."""
     B, H, Lq, D = q.shape
     Lk = k.shape[2]
-    O, P = forward(q, k, v, kr, qr, rel, keep, pairwise, scale, A)
+    O, P = forward(q, k, v, kr, qr, rel, keep, pairwise, scale, A, p2p=p2p, c2p=c2p, p2c=p2c)
     pk, live = _liveness(keep, B, Lq, Lk, pairwise)
     c = p = None
     if rel is not None:
@@ -126,12 +142,16 @@ def backward(
                     ds = pij * (float(dO[b, h, i] @ v[b, h, j]) - delta)
                     g["q"][b, h, i] += scale * ds * k[b, h, j]
                     g["k"][b, h, j] += scale * ds * q[b, h, i]
-                    if kr is not None:
+                    if kr is not None and c2p:
                         g["q"][b, h, i] += scale * ds * kr[h, c[i, j]]
                         g["kr"][h, c[i, j]] += scale * ds * q[b, h, i]
-                    if qr is not None:
+                    if qr is not None and p2c:
                         g["k"][b, h, j] += scale * ds * qr[h, p[i, j]]
                         g["qr"][h, p[i, j]] += scale * ds * k[b, h, j]
+                    if p2p:
+                        r = A + min(i, A - 1)
+                        g["kr"][h, c[i, j]] += scale * ds * qr[h, r]
+                        g["qr"][h, r] += scale * ds * kr[h, c[i, j]]
     return g
 
 

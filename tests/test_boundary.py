@@ -335,3 +335,58 @@ def test_module_rejects_bad_config_and_cpu():
 def test_package_surface():
     for name in deberta_amd.__all__:
         assert hasattr(deberta_amd, name), name
+
+
+def test_segment_cache_is_keyed_by_identity_and_keeps_the_mask_batch():
+    """The dense-mask recognition cache is looked up twice with the same mask
+    object (layer 2 of an encoder, the next step): identity-keyed, so the
+    lookup never compares tensors elementwise.  A broadcast (1, 1, S, S)
+    mask keeps one row of ids, expanded to each call's batch."""
+    from deberta_amd.masks import _SEGMENTS_OF, _segments_cached
+
+    ids = torch.tensor([[1, 1, 2, 2, 2, 3, 0, 0]])
+    mask = build_doc_block_mask(ids)[:, None]
+    pk = mask.view(torch.uint8)[:, 0]
+    first = _segments_cached(mask, pk)
+    second = _segments_cached(mask, pk)
+    assert first is second and first.shape == (1, 8)
+    other = mask.clone()
+    assert _segments_cached(other, other.view(torch.uint8)[:, 0]) is not first
+    other[0, 0, 0, 0] = False  # a new version is checked again
+    assert _segments_cached(other, other.view(torch.uint8)[:, 0]) is None
+    assert mask in _SEGMENTS_OF and other in _SEGMENTS_OF
+
+
+def test_mask_shapes_are_checked_before_launch():
+    """ops._validate refuses masks whose extent differs from (B, Lk) /
+    (B, Lq, Lk): the kernels would read them out of bounds."""
+    q, k, v, kr, qr, table = _inputs(B=2, L=64)
+    good = torch.ones(2, 64, dtype=torch.uint8)
+    ops._validate(q, k, v, kr, qr, table, good, None, 16)
+    ops._validate(q, k, v, kr, qr, table, good[:1].expand(2, 64), None, 16)  # batch stride 0
+    with pytest.raises(ValueError, match=r"key_keep / segment ids must be \[B=2, Lk=64\]"):
+        ops._validate(q, k, v, kr, qr, table, good[:1], None, 16)
+    with pytest.raises(ValueError, match="key_keep / segment ids"):
+        ops._validate(q, k, v, kr, qr, table, torch.ones(2, 63, dtype=torch.int32), None, 16)
+    with pytest.raises(TypeError, match="key_keep must be uint8"):
+        ops._validate(q, k, v, kr, qr, table, good.float(), None, 16)
+    with pytest.raises(ValueError, match=r"pair_keep must be \[B=2, Lq=64, Lk=64\]"):
+        ops._validate(q, k, v, kr, qr, table, None, torch.ones(1, 64, 64, dtype=torch.uint8), 16)
+
+
+def test_deterministic_mode_alerts_on_table_gradients():
+    """torch.use_deterministic_algorithms(True) refuses the backward with
+    relative tables (dkr / dqr are summed with fp32 atomics); warn_only
+    warns.  Checked before any device work."""
+    prev, prev_warn = torch.are_deterministic_algorithms_enabled(), torch.is_deterministic_algorithms_warn_only_enabled()
+    try:
+        torch.use_deterministic_algorithms(True)
+        with pytest.raises(RuntimeError, match="deterministic implementation"):
+            ops._alert_nondeterministic_tables()
+        torch.use_deterministic_algorithms(True, warn_only=True)
+        with pytest.warns(UserWarning, match="deterministic implementation"):
+            ops._alert_nondeterministic_tables()
+        torch.use_deterministic_algorithms(False)
+        ops._alert_nondeterministic_tables()
+    finally:
+        torch.use_deterministic_algorithms(prev, warn_only=prev_warn)
