@@ -50,28 +50,76 @@ WORKLOADS = {
 }
 
 
-# HBM bytes per launch at this workload, from two rocprofv3 --pmc passes over
-# `bench.py --kernels-only` (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch),
-# each scaled by what the same counter reads for a plain 256 MiB device copy
-# in the same run: FETCH_SIZE reads 128 MiB for it (x2.0), WRITE_SIZE 256 MiB
-# (x1.0).  Commands and raw figures: profiles/hbm_traffic_headline.md.
-FETCH_SCALE, WRITE_SCALE = 2.0, 1.0
-TRAFFIC_KIB = {  # kernel: (FETCH_SIZE, WRITE_SIZE) as read
-    "dsa_fwd_kernel": (55304, 225024),
-    "dsa_bwd_dkdv_kernel": (178632, 245781),
-    "dsa_bwd_dq_kernel": (127075, 24576),
-    "dsa_bwd_table_kernel": (208256, 24576),
-    "dsa_bwd_fold_kernel": (4082, 2458),
-    "dsa_bwd_prep_kernel": (25834, 10760),
-}
+# HBM bytes per launch at this workload come from the committed rocprofv3
+# summary of this build's kernels (two --pmc passes over `bench.py
+# --kernels-only`, FETCH_SIZE then WRITE_SIZE in KiB per dispatch, each
+# scaled by what the counter reads for a plain device copy of known size in
+# the same run; commands, raw figures and factors in the file).
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "hbm_traffic_headline.md")
+
+
+def traffic_table(path: str = TRAFFIC_PROFILE):
+    """{kernel: (FETCH_SIZE KiB, WRITE_SIZE KiB)} and the two scale factors,
+    parsed from the profile summary's table and its calibration sentence
+    ("FETCH_SIZE is scaled by F and WRITE_SIZE by W")."""
+    import re
+
+    try:
+        with open(path) as f:
+            text = f.read()
+    except OSError:
+        return {}, None, None
+    rows = {}
+    for m in re.finditer(r"^\| (dsa_\w+) \| (\d+) \| (\d+) \|", text, re.M):
+        rows[m.group(1)] = (int(m.group(2)), int(m.group(3)))
+    m = re.search(r"FETCH_SIZE is scaled by ([0-9.]+) and WRITE_SIZE by ([0-9.]+)", text)
+    if not m:
+        return rows, None, None
+    return rows, float(m.group(1)), float(m.group(2))
 
 
 def hbm_bytes(stage: str):
-    """HBM bytes per launch of a bench stage (the sum over its kernels)."""
-    names = [k for k in TRAFFIC_KIB if k in stage]
-    if not names:
+    """HBM bytes per launch of a bench stage (the sum over its kernels), or
+    None when the profile does not cover them."""
+    rows, fs, ws = traffic_table()
+    names = [k for k in rows if k in stage]
+    if not names or fs is None:
         return None
-    return int(round(sum(TRAFFIC_KIB[k][0] * FETCH_SCALE + TRAFFIC_KIB[k][1] * WRITE_SCALE for k in names) * 1024))
+    return int(round(sum(rows[k][0] * fs + rows[k][1] * ws for k in names) * 1024))
+
+
+def mfma_peak_probe(dev) -> dict:
+    """Measured bf16 dense MFMA throughput of this GPU (libdsa_probe.so:
+    four independent v_mfma_f32_32x32x16_bf16 chains per wave, eight
+    workgroups of four waves per CU), timed with HIP events on its stream:
+    the measured figure beside the published 2.5 PFLOP/s."""
+    import ctypes
+
+    import torch
+
+    from deberta_amd._build import PROBE_PATH
+
+    lib = ctypes.CDLL(str(PROBE_PATH))
+    lib.dsa_probe_mfma_bf16.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    lib.dsa_probe_mfma_bf16.restype = ctypes.c_int
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    wgs, iters = 8 * cus, 2048
+    sink = torch.empty(wgs * 256, dtype=torch.float32, device=dev)
+    st = torch.cuda.current_stream(dev)
+    run = lambda: lib.dsa_probe_mfma_bf16(wgs, iters, ctypes.c_void_p(sink.data_ptr()), ctypes.c_void_p(st.cuda_stream))
+    for _ in range(3):
+        if run():
+            raise RuntimeError("MFMA probe launch failed")
+    best = float("inf")
+    for _ in range(5):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(st)
+        run()
+        b.record(st)
+        torch.cuda.synchronize(dev)
+        best = min(best, a.elapsed_time(b))
+    flops = wgs * 4.0 * iters * 4 * 32768
+    return {"tflops": round(flops / (best * 1e-3) / 1e12, 1), "cus": cus, "workgroups": wgs, "ms": round(best, 4)}
 
 
 def flops_fwd(b: int, l: int, h: int, d: int, r: int) -> float:
@@ -119,59 +167,18 @@ def run_encoder(args) -> None:
     package.  Prints step time, tokens/s and the attention share (the fused
     op's fwd+bwd at the same shape, times 12, over the step)."""
     import torch
-    from torch import nn
 
     import deberta_amd
     from deberta_amd.relpos import relative_offset_table
+    from tests._encoder import Encoder, init_weights, rtd_loss, synthetic_batch
 
     dev = torch.device("cuda:0")
-    Bc, Lc, Hc, hid, ffn, vocab = 16, 512, 12, 768, 3072, 128100
-    cfg = type("Cfg", (), dict(hidden_size=hid, num_attention_heads=Hc, share_att_key=True,
-                               pos_att_type="p2c|c2p", relative_attention=True, position_buckets=BUCKETS,
-                               max_relative_positions=-1, max_position_embeddings=MAX_POS,
-                               hidden_dropout_prob=0.0, attention_probs_dropout_prob=0.0))()
-
-    class Layer(nn.Module):
-        def __init__(self):
-            super().__init__()
-            self.attn = deberta_amd.DisentangledSelfAttention(cfg)
-            self.out = nn.Linear(hid, hid)
-            self.ln1 = nn.LayerNorm(hid, eps=1e-7)
-            self.up, self.down = nn.Linear(hid, ffn), nn.Linear(ffn, hid)
-            self.ln2 = nn.LayerNorm(hid, eps=1e-7)
-
-        def forward(self, x, mask, rel_pos, rel):
-            a, _ = self.attn(x, mask, relative_pos=rel_pos, rel_embeddings=rel)
-            x = self.ln1(self.out(a) + x)
-            return self.ln2(self.down(nn.functional.gelu(self.up(x))) + x)
-
-    class Encoder(nn.Module):
-        def __init__(self):
-            super().__init__()
-            self.emb = nn.Embedding(vocab, hid)
-            self.emb_ln = nn.LayerNorm(hid, eps=1e-7)
-            self.rel = nn.Parameter(torch.empty(2 * BUCKETS, hid))
-            self.rel_ln = nn.LayerNorm(hid, eps=1e-7)
-            self.layers = nn.ModuleList(Layer() for _ in range(12))
-            self.head = nn.Sequential(nn.Linear(hid, hid), nn.GELU(), nn.LayerNorm(hid, eps=1e-7), nn.Linear(hid, 1))
-
-        def forward(self, ids, mask, rel_pos):
-            x = self.emb_ln(self.emb(ids))
-            rel = self.rel_ln(self.rel)
-            for layer in self.layers:
-                x = layer(x, mask, rel_pos, rel)
-            return self.head(x).squeeze(-1)
-
-    torch.manual_seed(0)
-    model = Encoder().to(dev)
-    for n_, prm in model.named_parameters():
-        if prm.dim() > 1:
-            nn.init.normal_(prm, 0.0, 0.02)
-        elif "ln" not in n_ and "head.2" not in n_:
-            nn.init.zeros_(prm)
-    g = torch.Generator().manual_seed(0)
-    ids = torch.randint(0, vocab, (Bc, Lc), generator=g).to(dev)
-    labels = (torch.rand(Bc, Lc, generator=g) < 0.15).float().to(dev)
+    Bc, Lc, Hc = 16, 512, 12
+    model = Encoder(deberta_amd.DisentangledSelfAttention)
+    init_weights(model, seed=0)
+    model = model.to(dev)
+    ids, labels = synthetic_batch(Bc, Lc, seed=0)
+    ids, labels = ids.to(dev), labels.to(dev)
     mask = torch.ones(Bc, 1, 1, Lc, dtype=torch.bool, device=dev)
     rel_pos = deberta_amd.build_relative_position(Lc, Lc, bucket_size=BUCKETS, max_position=MAX_POS, device=dev)
     params = [p_ for p_ in model.parameters()]
@@ -179,8 +186,7 @@ def run_encoder(args) -> None:
     def step():
         with torch.autocast("cuda", dtype=torch.bfloat16):
             logits = model(ids, mask, rel_pos)
-        loss = nn.functional.binary_cross_entropy_with_logits(logits.float(), labels)
-        torch.autograd.grad(loss, params)
+        torch.autograd.grad(rtd_loss(logits, labels), params)
 
     def timed(fn, n):
         for _ in range(3):
@@ -332,6 +338,7 @@ def cpu_baseline(budget_s: float = 15.0) -> dict:
         if total >= budget_s:
             break
     tflops = runs * 3 * flops_fwd(b, L, H, D, R) / total / 1e12
+    c1 = c1_cpu_forward()
     return {
         "value": round(tflops, 4),
         "unit": "TFLOP/s",
@@ -340,7 +347,41 @@ def cpu_baseline(budget_s: float = 15.0) -> dict:
         "sample": f"fp32 eager oracle fwd+bwd on {runs} x {b} batch rows of B={B} L={L} H={H} D={D} R={R} "
         f"(no mask) = {runs * b / B:.1f} steps' worth in {total:.1f} s ({total / runs * 1e3:.1f} ms per run); "
         f"CPU: {cpu_model()}",
+        "c1_forward": c1,
     }
+
+
+def c1_cpu_forward(runs: int = 20) -> dict:
+    """BASELINE configs[0] on the host: the oracle's restatement of the
+    reference module, forward only, fp32, B=2, L=128, hidden 128, 4 heads x
+    32, buckets 256, max relative positions 512, relative embeddings
+    [512, 128]; hidden states N(0, 1), weights N(0, 0.02) from seed 0,
+    all-ones mask.  Median wall time over `runs` forwards."""
+    import torch
+
+    from oracle import eager
+
+    cfg = eager.make_config(hidden_size=128, num_attention_heads=4, position_buckets=256, max_relative_positions=512)
+    torch.manual_seed(0)
+    m = eager.EagerDisentangledSelfAttention(cfg).eval()
+    g = torch.Generator().manual_seed(0)
+    with torch.no_grad():
+        for n_, p_ in m.named_parameters():
+            p_.copy_(torch.randn(p_.shape, generator=g) * 0.02 if n_.endswith("weight") else torch.zeros_like(p_))
+    x = torch.randn(2, 128, 128, generator=g)
+    rel = torch.randn(512, 128, generator=g) * 0.02
+    mask = torch.ones(2, 1, 1, 128, dtype=torch.bool)
+    ts = []
+    with torch.no_grad():
+        m(x, mask, rel_embeddings=rel)
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            m(x, mask, rel_embeddings=rel)
+            ts.append(time.perf_counter() - t0)
+    ms = sorted(ts)[len(ts) // 2] * 1e3
+    f = flops_fwd(2, 128, 4, 32, 512)
+    return {"ms": round(ms, 3), "gflops": round(f / (ms * 1e-3) / 1e9, 2), "flop": f,
+            "sample": "BASELINE configs[0]: oracle module forward, fp32, B=2 L=128 H=4 D=32, median of 20"}
 
 
 def main() -> None:
@@ -419,7 +460,7 @@ def main() -> None:
         torch.cuda.synchronize()
         del src_t, dst_t
 
-    ms_step = wall = float("nan")
+    ms_step = wall = ms_median = ms_p10 = ms_p90 = float("nan")
     if args.kernels_only:
         # the same sustained load before the per-kernel timing as in a full
         # run (the GPU's clocks settle under it)
@@ -431,14 +472,19 @@ def main() -> None:
             step()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(args.steps):
+        # an event between consecutive steps: per-step times for the median
+        # and p10 / p90, and their span for the mean over exactly K steps
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+        evs[0].record()
+        for n_ in range(args.steps):
             step()
-        e1.record()
+            evs[n_ + 1].record()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        ms_step = e0.elapsed_time(e1) / args.steps
+        ms_step = evs[0].elapsed_time(evs[-1]) / args.steps
+        per_step = sorted(evs[n_].elapsed_time(evs[n_ + 1]) for n_ in range(args.steps))
+        pct = lambda f: per_step[min(len(per_step) - 1, int(round(f * (len(per_step) - 1))))]
+        ms_median, ms_p10, ms_p90 = pct(0.5), pct(0.1), pct(0.9)
     f_fwd = flops_fwd(B, L, H, D, R)
     f_step = 3 * f_fwd
     tflops = f_step / (ms_step * 1e-3) / 1e12
@@ -547,6 +593,9 @@ def main() -> None:
             "flop_per_step": f_step,
         },
         "pct_bf16_peak": round(100.0 * tflops / PEAK_BF16_TFLOPS, 2),
+        "step_ms_median_p10_p90": [round(ms_median, 4), round(ms_p10, 4), round(ms_p90, 4)],
+        "tflops_at_median_step": round(f_step / (ms_median * 1e-3) / 1e12, 2),
+        "mfma_peak_measured": mfma_peak_probe(dev),
         "per_kernel": per_kernel,
         "roofline": {
             "kernel": dom,

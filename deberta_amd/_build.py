@@ -11,6 +11,9 @@ PKG_DIR = Path(__file__).resolve().parent
 CSRC_DIR = PKG_DIR / "csrc"
 LIB_PATH = PKG_DIR / "libdsa.so"
 SOURCES = ("dsa_capi.hip",)
+# bench.py's MFMA throughput probe (include/dsa_probe.h), a library of its own
+PROBE_PATH = PKG_DIR / "libdsa_probe.so"
+PROBE_SOURCES = ("dsa_probe.hip",)
 ARCH = "gfx950"
 
 # Packed fp32 VALU ops are kept out of the generated code: hipcc otherwise
@@ -40,23 +43,29 @@ def hipcc_path() -> str:
     raise RuntimeError("hipcc not found: libdsa.so cannot be built without the ROCm toolchain")
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every HIP source into ``deberta_amd/libdsa.so``.
-
-    Always recompiles.  The library is written to a temporary name first and
-    renamed into place, so a process that already loaded the old file keeps a
-    consistent image.
-    """
-    srcs = [str(CSRC_DIR / s) for s in SOURCES]
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+def _compile(sources, out: Path, verbose: bool) -> Path:
+    srcs = [str(CSRC_DIR / s) for s in sources]
+    tmp = out.with_suffix(".so.tmp")
     cmd = [hipcc_path(), *HIPCC_FLAGS, *srcs, "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{' '.join(cmd)}\n{proc.stdout}\n{proc.stderr}")
     if verbose:
         print(" ".join(cmd))
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, out)
+    return out
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every HIP source: ``deberta_amd/libdsa.so`` (the kernels and
+    their C ABI) and ``deberta_amd/libdsa_probe.so`` (the MFMA probe).
+
+    Always recompiles.  Each library is written to a temporary name first and
+    renamed into place, so a process that already loaded the old file keeps a
+    consistent image.
+    """
+    _compile(PROBE_SOURCES, PROBE_PATH, verbose)
+    return _compile(SOURCES, LIB_PATH, verbose)
 
 
 if __name__ == "__main__":

@@ -22,7 +22,7 @@ DSA_STAGE_DQ = 2
 DSA_STAGE_DKDV = 4
 DSA_STAGE_FOLD = 8
 
-EXPECTED_VERSION = 5
+EXPECTED_VERSION = 6
 
 _i64x3 = ctypes.c_int64 * 3
 _i64x2 = ctypes.c_int64 * 2
@@ -62,6 +62,8 @@ class DsaFwdArgs(ctypes.Structure):
         ("seg_stride_b", ctypes.c_int64),
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_size_t),
+        ("qc", ctypes.c_void_p),
+        ("qc_strides", _i64x3),
     ]
 
 
@@ -83,6 +85,8 @@ class DsaBwdArgs(ctypes.Structure):
         ("stages", ctypes.c_int32),
         ("dtab_dtype", ctypes.c_int32),
         ("dtab_overwrite", ctypes.c_int32),
+        ("dqc", ctypes.c_void_p),
+        ("dqc_strides", _i64x3),
     ]
 
 
@@ -90,6 +94,7 @@ class DsaBwdArgs(ctypes.Structure):
 EXPORTS = (
     "dsa_fwd",
     "dsa_bwd",
+    "dsa_bias",
     "dsa_bwd_workspace_bytes",
     "dsa_fwd_bias_bytes",
     "dsa_fwd_workspace_bytes",
@@ -123,6 +128,8 @@ def load() -> ctypes.CDLL:
         lib.dsa_fwd.restype = ctypes.c_int
         lib.dsa_bwd.argtypes = [ctypes.POINTER(DsaBwdArgs), ctypes.c_void_p]
         lib.dsa_bwd.restype = ctypes.c_int
+        lib.dsa_bias.argtypes = [ctypes.POINTER(DsaFwdArgs), ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64), ctypes.c_void_p]
+        lib.dsa_bias.restype = ctypes.c_int
         lib.dsa_bwd_workspace_bytes.argtypes = [ctypes.POINTER(DsaBwdArgs)]
         lib.dsa_bwd_workspace_bytes.restype = ctypes.c_size_t
         lib.dsa_fwd_bias_bytes.argtypes = [ctypes.POINTER(DsaFwdArgs)]

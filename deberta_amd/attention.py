@@ -18,6 +18,7 @@ from typing import Any, Optional
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 from deberta_amd import ops  # noqa: F401  (registers the custom ops)
 from deberta_amd.config import normalize_attention_kernel, normalize_pos_att_type
@@ -89,6 +90,46 @@ def _require_gpu(t: torch.Tensor) -> None:
         )
 
 
+def position_query_rows(qr: torch.Tensor, query_len: int, att_span: int) -> torch.Tensor:
+    """The p2p term's query rows ``Qr[:, A + min(i, A - 1)]`` for i <
+    query_len, as a ``[1, Lq, H, D]`` view (deberta_v2_native.py:330-342:
+    the positive half of the pos-query table, indexed by the clamped query
+    position)."""
+    A = int(att_span)
+    rows = torch.arange(query_len, device=qr.device).clamp(max=A - 1) + A
+    return qr.index_select(1, rows).permute(1, 0, 2).unsqueeze(0)
+
+
+def relative_operands(
+    types: list[str],
+    q: torch.Tensor,
+    kr: Optional[torch.Tensor],
+    qr: Optional[torch.Tensor],
+    att_span: int,
+) -> tuple[Optional[torch.Tensor], Optional[torch.Tensor], Optional[torch.Tensor]]:
+    """The kernels' relative operands ``(kr, qr, qc)`` for the score terms in
+    ``types`` (q ``[B, L, H, D]``; kr / qr the projected ``(H, 2A, D)``
+    tables in q's dtype).
+
+    The p2p term, ``Qr[A + min(i, A - 1)] . Kr[c(i - j)]``, reads the same
+    Kr rows as c2p, so it is carried by the c2p term's query rows:
+    ``qc = q + Qr[A + min(i, A - 1)]`` with c2p, ``qc = Qr[A + min(i, A - 1)]``
+    alone without it (the kernels then run their c2p term on qc).  Autograd
+    returns qc's gradient to q and to Qr."""
+    c2p, p2c, p2p = ("c2p" in types), ("p2c" in types), ("p2p" in types)
+    if (c2p or p2p) and kr is None:
+        raise RuntimeError("p2p/c2p path requires pos_key projection.")
+    if (p2c or p2p) and qr is None:
+        raise RuntimeError("p2p/p2c path requires pos_query projection.")
+    if p2p and (kr is None or qr is None):
+        raise RuntimeError("p2p path requires both pos_key and pos_query projections.")
+    qc = None
+    if p2p:
+        pq = position_query_rows(qr, q.shape[1], att_span)
+        qc = q + pq if c2p else pq.expand(q.shape[0], -1, -1, -1)
+    return (kr if (c2p or p2p) else None), (qr if p2c else None), qc
+
+
 def fused_attention(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -99,8 +140,11 @@ def fused_attention(
     attention_mask: Optional[torch.Tensor],
     att_span: int,
     scale: float,
+    qc: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
-    """Core call on ``[B, L, H, D]`` layers; returns ``[B, Lq, H, D]``."""
+    """Core call on ``[B, L, H, D]`` layers; returns ``[B, Lq, H, D]``.
+    ``kr`` / ``qr`` are the c2p / p2c tables (None: term off); ``qc`` the
+    c2p term's query rows (None: q)."""
     _require_gpu(q)
     B, Lq = q.shape[0], q.shape[1]
     Lk = k.shape[1]
@@ -109,14 +153,16 @@ def fused_attention(
         kr = kr.to(q.dtype)
     if qr is not None:
         qr = qr.to(q.dtype)
+    if qc is not None:
+        qc = qc.to(q.dtype)
     if kr is None and qr is None:
         table = None
     # The relative term is saved only when a backward can follow.
     save_bias = torch.is_grad_enabled() and any(
-        t is not None and t.requires_grad for t in (q, k, v, kr, qr)
+        t is not None and t.requires_grad for t in (q, k, v, kr, qr, qc)
     )
     out, _, _ = torch.ops.deberta_amd.dsa_fwd(
-        q, k, v, kr, qr, table, key_keep, pair_keep, int(att_span), float(scale), save_bias
+        q, k, v, kr, qr, table, key_keep, pair_keep, int(att_span), float(scale), save_bias, qc
     )
     return out
 
@@ -142,14 +188,12 @@ def disentangled_attention(
     reference's ``_shape`` output) or ``(B, L, H, D)`` (``layout="blhd"``, the
     Linear output viewed per head, read in place).  ``pos_key_layer`` /
     ``pos_query_layer`` are the projected relative tables ``(H, 2A, D)``
-    (``_project_rel``); the c2p / p2c terms are used when ``att_type`` names
-    them.  ``relative_pos`` and ``attention_mask`` follow the module's
+    (``_project_rel``); the c2p / p2c / p2p terms are used when ``att_type``
+    names them.  ``relative_pos`` and ``attention_mask`` follow the module's
     contract.  ``scale_factor`` defaults to ``1 + #att_type terms``.  The
     result has the layout of ``query_layer``.
     """
     types = normalize_pos_att_type(att_type)
-    if "p2p" in types:
-        raise NotImplementedError("p2p is not supported by the fused disentangled-attention kernels")
     if layout not in ("bhld", "blhd"):
         raise ValueError(f"layout must be 'bhld' or 'blhd', got {layout!r}")
     if layout == "bhld":
@@ -160,25 +204,24 @@ def disentangled_attention(
         scale_factor = 1 + sum(t in types for t in ("c2p", "p2c", "p2p"))
     D = q.shape[-1]
     scale = 1.0 / math.sqrt(float(D * scale_factor))
-    kr = pos_key_layer if "c2p" in types else None
-    qr = pos_query_layer if "p2c" in types else None
-    if "c2p" in types and kr is None:
-        raise RuntimeError("p2p/c2p path requires pos_key projection.")
-    if "p2c" in types and qr is None:
-        raise RuntimeError("p2p/p2c path requires pos_query projection.")
+    tables = [t for t in (pos_key_layer, pos_query_layer) if t is not None]
+    att_span = tables[0].shape[1] // 2 if tables else 1
+    kr, qr, qc = relative_operands(
+        types, q,
+        None if pos_key_layer is None else pos_key_layer.to(q.dtype),
+        None if pos_query_layer is None else pos_query_layer.to(q.dtype),
+        att_span,
+    )
+    table = None
     if kr is not None or qr is not None:
-        rows = (kr if kr is not None else qr).shape[1]
-        att_span = rows // 2
         table = table_for(relative_pos, q.shape[1], k.shape[1], position_buckets, max_relative_positions, q.device)
-    else:
-        att_span, table = 1, None
     if attention_mask is not None and not isinstance(attention_mask, SegmentMask):
         attention_mask = normalize_keep_mask(attention_mask)
         if attention_mask.ndim != 4:
             raise ValueError(
                 f"attention_mask must be rank-4 [B,1,Q,K]; got shape={tuple(attention_mask.shape)}"
             )
-    out = fused_attention(q, k, v, kr, qr, table, attention_mask, att_span, scale)
+    out = fused_attention(q, k, v, kr, qr, table, attention_mask, att_span, scale, qc)
     return out.transpose(1, 2) if layout == "bhld" else out
 
 
@@ -241,6 +284,28 @@ class DisentangledSelfAttention(nn.Module):
         bsz, seq_len, _ = x.shape
         return x.view(bsz, seq_len, self.num_attention_heads, self.attention_head_size)
 
+    def _project_qkv(
+        self, hidden_states: torch.Tensor, query_states: Optional[torch.Tensor]
+    ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """q, k, v as ``(B, L, H, D)`` views of one fused projection
+        (deberta_v2_native.py:587-589 as a single GEMM): the three weights
+        are concatenated at call time, so the parameters (and the state-dict
+        keys query_proj / key_proj / value_proj) stay the reference's.  With
+        separate ``query_states`` only the key and value projections are
+        fused."""
+        H, D = self.num_attention_heads, self.attention_head_size
+        bsz, seq_len, _ = hidden_states.shape
+        if query_states is None:
+            w = torch.cat([self.query_proj.weight, self.key_proj.weight, self.value_proj.weight])
+            bias = torch.cat([self.query_proj.bias, self.key_proj.bias, self.value_proj.bias])
+            qkv = F.linear(hidden_states, w, bias).view(bsz, seq_len, 3, H, D)
+            return qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2]
+        q = self._heads(self.query_proj(query_states))
+        w = torch.cat([self.key_proj.weight, self.value_proj.weight])
+        bias = torch.cat([self.key_proj.bias, self.value_proj.bias])
+        kv = F.linear(hidden_states, w, bias).view(bsz, seq_len, 2, H, D)
+        return q, kv[:, :, 0], kv[:, :, 1]
+
     def _project_rel(self, rel_embeddings: torch.Tensor, *, use_query: bool) -> torch.Tensor:
         """Projected relative table ``(H, 2A, D)`` as a view of the Linear
         output (deberta_v2_native.py:273-296 without the permute copy)."""
@@ -256,6 +321,48 @@ class DisentangledSelfAttention(nn.Module):
         projected = projected.view(2 * att_span, self.num_attention_heads, self.attention_head_size)
         return projected.permute(1, 0, 2)
 
+    def _relative_tables(
+        self, rel_embeddings: torch.Tensor, dtype: torch.dtype
+    ) -> tuple[Optional[torch.Tensor], Optional[torch.Tensor]]:
+        """(Kr, Qr) projected for the configured terms (None where unused),
+        in ``dtype`` (deberta_v2_native.py:372-375)."""
+        types = self.pos_att_type
+        kr = qr = None
+        if ("c2p" in types) or ("p2p" in types):
+            kr = self._project_rel(rel_embeddings, use_query=False).to(dtype)
+        if ("p2c" in types) or ("p2p" in types):
+            qr = self._project_rel(rel_embeddings, use_query=True).to(dtype)
+        return kr, qr
+
+    def disentangled_attention_bias(
+        self,
+        query_layer: torch.Tensor,
+        key_layer: torch.Tensor,
+        relative_pos: Optional[torch.Tensor],
+        rel_embeddings: torch.Tensor,
+        scale_factor: int,
+    ) -> torch.Tensor:
+        """The relative score term ``(c2p + p2c + p2p) / sqrt(D * scale_factor)``
+        of ``(B, H, Q, D)`` query and key layers, as ``(B, H, Q, K)`` in the
+        query's dtype (deberta_v2_native.py:530-562; every kernel choice
+        computes the same function).  Computed by the fused kernels' band
+        code (``deberta_amd::dsa_bias``), unmasked; forward only (training
+        differentiates through ``forward``)."""
+        _require_gpu(query_layer)
+        if query_layer.dtype not in (torch.float32, torch.bfloat16):
+            raise TypeError(f"disentangled_attention_bias: query dtype must be float32 or bfloat16, got {query_layer.dtype}")
+        q = query_layer.transpose(1, 2)
+        k = key_layer.to(q.dtype).transpose(1, 2)
+        Lq, Lk = q.shape[1], k.shape[1]
+        att_span = int(self.pos_ebd_size)
+        kr_full, qr_full = self._relative_tables(rel_embeddings, q.dtype)
+        kr, qr, qc = relative_operands(self.pos_att_type, q, kr_full, qr_full, att_span)
+        table = None
+        if kr is not None or qr is not None:
+            table = table_for(relative_pos, Lq, Lk, self.position_buckets, self.max_relative_positions, q.device)
+        scale = 1.0 / math.sqrt(float(self.attention_head_size * int(scale_factor)))
+        return torch.ops.deberta_amd.dsa_bias(q, k, kr, qr, table, att_span, scale, qc)
+
     def forward(
         self,
         hidden_states: torch.Tensor,
@@ -268,36 +375,28 @@ class DisentangledSelfAttention(nn.Module):
         """Same contract as the reference forward (deberta_v2_native.py:564-652).
 
         Not provided by the fused kernels (raise ``NotImplementedError``):
-        ``output_attentions=True`` (probabilities are never materialised),
-        ``p2p`` terms, and attention dropout ``p > 0`` in training mode.
+        ``output_attentions=True`` (probabilities are never materialised) and
+        attention dropout ``p > 0`` in training mode.
         """
         if output_attentions:
             raise NotImplementedError("output_attentions=True: the fused kernels never materialise probabilities")
         if self.training and self.dropout.p > 0.0:
             raise NotImplementedError("attention dropout p > 0 is not supported by the fused kernels")
-        if query_states is None:
-            query_states = hidden_states
         _require_gpu(hidden_states)
 
-        q = self._heads(self.query_proj(query_states))
-        k = self._heads(self.key_proj(hidden_states))
-        v = self._heads(self.value_proj(hidden_states))
+        q, k, v = self._project_qkv(hidden_states, query_states)
         model_dtype = hidden_states.dtype
 
         scale_factor = 1 + sum(t in self.pos_att_type for t in ("c2p", "p2c", "p2p"))
         scale = 1.0 / math.sqrt(float(self.attention_head_size * scale_factor))
 
-        kr = qr = table = None
+        kr = qr = qc = table = None
         att_span = 1
         if self.relative_attention and rel_embeddings is not None:
-            if "p2p" in self.pos_att_type:
-                raise NotImplementedError("p2p is not supported by the fused disentangled-attention kernels")
             rel_embeddings = self.pos_dropout(rel_embeddings)
             att_span = int(self.pos_ebd_size)
-            if "c2p" in self.pos_att_type:
-                kr = self._project_rel(rel_embeddings, use_query=False)
-            if "p2c" in self.pos_att_type:
-                qr = self._project_rel(rel_embeddings, use_query=True)
+            kr_full, qr_full = self._relative_tables(rel_embeddings, q.dtype)
+            kr, qr, qc = relative_operands(self.pos_att_type, q, kr_full, qr_full, att_span)
             if kr is not None or qr is not None:
                 table = table_for(
                     relative_pos,
@@ -315,7 +414,7 @@ class DisentangledSelfAttention(nn.Module):
                     f"attention_mask must be rank-4 [B,1,Q,K]; got shape={tuple(attention_mask.shape)}"
                 )
 
-        ctx = fused_attention(q, k, v, kr, qr, table, attention_mask, att_span, scale)
+        ctx = fused_attention(q, k, v, kr, qr, table, attention_mask, att_span, scale, qc)
         bsz, seq_len = ctx.shape[0], ctx.shape[1]
         context_layer = ctx.reshape(bsz, seq_len, self.all_head_size).to(dtype=model_dtype)
         return context_layer, None

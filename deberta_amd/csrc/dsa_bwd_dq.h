@@ -29,7 +29,9 @@ constexpr int XW = 96;   // offset rows per wave (95 used)
 constexpr int ZC = 32;   // zero columns before each staged dS row
 }  // namespace dqcfg
 
-template <typename T, int D>
+// QC: the c2p part (the gradient of the c2p term's query rows qc) is
+// accumulated apart and written to dqc; dq then holds the content part.
+template <typename T, int D, bool QC = false>
 __global__ __launch_bounds__(256, 2) void dsa_bwd_dq_kernel(BwdParams bp) {
   using namespace dqcfg;
   using M = Mfma<T>;
@@ -88,6 +90,9 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dq_kernel(BwdParams bp) {
   f32x4 dqa[ND][2];
 #pragma unroll
   for (int db = 0; db < ND; ++db) dqa[db][0] = dqa[db][1] = zero4();
+  f32x4 dqca[QC ? ND : 1][2];  // QC: the c2p part
+#pragma unroll
+  for (int db = 0; db < (QC ? ND : 1); ++db) dqca[db][0] = dqca[db][1] = zero4();
 
   // Key tiles (dS columns, K rows, krgt window) are fetched into registers
   // two tiles ahead, into two register sets used in turn (a tile's compute
@@ -215,7 +220,10 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dq_kernel(BwdParams bp) {
         for (int db = 0; db < ND; ++db) {
           const frag af = *reinterpret_cast<const frag*>(KG + (16 * db + c16) * GSTR + WQ * w + xb);
 #pragma unroll
-          for (int ib = 0; ib < 2; ++ib) dqa[db][ib] = M::mma(af, bfr[ib], dqa[db][ib]);
+          for (int ib = 0; ib < 2; ++ib) {
+            if constexpr (QC) dqca[db][ib] = M::mma(af, bfr[ib], dqca[db][ib]);
+            else dqa[db][ib] = M::mma(af, bfr[ib], dqa[db][ib]);
+          }
         }
       }
     }
@@ -241,6 +249,17 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dq_kernel(BwdParams bp) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = (T)(dqa[db][ib][e] * p.scale);
         *reinterpret_cast<vec4*>(row + 16 * db + 4 * g) = v;
+      }
+      if constexpr (QC) {
+        T* crow = (T*)bp.dqc + (int64_t)b * bp.dqcs[0] + (int64_t)h * bp.dqcs[2] + (int64_t)i * bp.dqcs[1];
+#pragma unroll
+        for (int db = 0; db < ND; ++db) {
+          typedef T vec4 __attribute__((ext_vector_type(4)));
+          vec4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = (T)(dqca[db][ib][e] * p.scale);
+          *reinterpret_cast<vec4*>(crow + 16 * db + 4 * g) = v;
+        }
       }
     }
   }

@@ -11,6 +11,7 @@
 #include <string>
 
 #include "../../include/dsa.h"
+#include "dsa_bias.h"
 #include "dsa_bwd.h"
 #include "dsa_bwd_dkdv.h"
 #include "dsa_bwd_dq.h"
@@ -70,6 +71,17 @@ int round_up(int x, int a) { return (x + a - 1) / a * a; }
 
 int elem_bytes(int dtype) { return dtype == DSA_BF16 ? 2 : 4; }
 
+// The c2p term's query rows (qc, optional): c2p on, aligned like q.
+int check_qc(const dsa_fwd_args* a) {
+  if (!a->qc) return 0;
+  if (!(a->flags & DSA_C2P)) return fail("dsa: qc (the c2p term's query rows) needs DSA_C2P and kr");
+  const int vec = 16 / elem_bytes(a->dtype);
+  if (!aligned16(a->qc)) return fail("dsa: qc must be 16-byte aligned");
+  for (int s = 0; s < 3; ++s)
+    if (a->qc_strides[s] % vec != 0) return fail("dsa: qc strides must be multiples of %d elements", vec);
+  return 0;
+}
+
 // Checks shared by forward and backward.  Shapes are validated on the host
 // so every access the kernels make stays inside the caller's buffers.
 int check_fwd(const dsa_fwd_args* a) {
@@ -120,7 +132,7 @@ int check_fwd(const dsa_fwd_args* a) {
     return fail("dsa: kr must be 16-byte aligned with strides that are multiples of %d", vec);
   if ((a->flags & DSA_P2C) && (!aligned16(a->qr) || a->qr_strides[0] % vec || a->qr_strides[1] % vec))
     return fail("dsa: qr must be 16-byte aligned with strides that are multiples of %d", vec);
-  return 0;
+  return check_qc(a);
 }
 
 dsa::FwdParams to_params(const dsa_fwd_args* a) {
@@ -152,6 +164,8 @@ dsa::FwdParams to_params(const dsa_fwd_args* a) {
   p.seg = a->seg;
   p.segb = a->seg_stride_b;
   p.order = nullptr;
+  p.qc = a->qc;
+  for (int s = 0; s < 3; ++s) p.qcs[s] = a->qc ? a->qc_strides[s] : 0;
   p.B = a->B;
   p.H = a->H;
   p.Lq = a->Lq;
@@ -200,10 +214,14 @@ int launch_order(const dsa::FwdParams& p, int* buf, int ntiles, bool fwd, hipStr
 
 int fwd_tiles(const dsa_fwd_args* a) { return (a->Lq + dsa::dcfg::BQ - 1) / dsa::dcfg::BQ; }
 
+
 template <typename T, int D, int MASK>
 int launch_fwd(const dsa::FwdParams& p, hipStream_t st) {
   dim3 grid((unsigned)((p.Lq + dsa::dcfg::BQ - 1) / dsa::dcfg::BQ * p.H * p.B));
-  hipLaunchKernelGGL((dsa::dsa_fwd_kernel<T, D, MASK>), grid, dim3(256), 0, st, p);
+  if (p.qc)
+    hipLaunchKernelGGL((dsa::dsa_fwd_kernel<T, D, MASK, true>), grid, dim3(256), 0, st, p);
+  else
+    hipLaunchKernelGGL((dsa::dsa_fwd_kernel<T, D, MASK, false>), grid, dim3(256), 0, st, p);
   return launch_check("dsa_fwd_kernel");
 }
 
@@ -307,6 +325,8 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
   bp.dq = a->dq;
   bp.dk = a->dk;
   bp.dv = a->dv;
+  bp.dqc = f.qc ? a->dqc : nullptr;
+  for (int s = 0; s < 3; ++s) bp.dqcs[s] = f.qc ? a->dqc_strides[s] : 0;
   bp.dkr = a->dkr;
   bp.dqr = a->dqr;
   bp.dtab_bf16 = a->dtab_dtype == DSA_BF16;
@@ -389,16 +409,25 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
     // sits in few workgroups that need the second slot (C4 segments: 962 ->
     // 987 us with the pad), so it is not padded.
     const unsigned dyn = (side && !bp.cinfo) ? half_cu_lds_pad<T, D, false>() : 0u;
+    // dKr sums dS_ij times the c2p term's query rows: qc when it is given
+    dsa::BwdParams tp = bp;
+    if (f.qc) {
+      tp.f.q = f.qc;
+      for (int s = 0; s < 3; ++s) tp.f.qs[s] = f.qc_strides[s];
+    }
     if (bp.cinfo)
-      hipLaunchKernelGGL((dsa::dsa_bwd_table_kernel<T, D, true>), dim3(ws.NDB * f.H * ws.NPG), dim3(256), dyn, st, bp);
+      hipLaunchKernelGGL((dsa::dsa_bwd_table_kernel<T, D, true>), dim3(ws.NDB * f.H * ws.NPG), dim3(256), dyn, st, tp);
     else
-      hipLaunchKernelGGL((dsa::dsa_bwd_table_kernel<T, D, false>), dim3(ws.NDB * f.H * ws.NPG), dim3(256), dyn, st, bp);
+      hipLaunchKernelGGL((dsa::dsa_bwd_table_kernel<T, D, false>), dim3(ws.NDB * f.H * ws.NPG), dim3(256), dyn, st, tp);
     if (launch_check("dsa_bwd_table_kernel")) return 1;
   }
   if (stages & DSA_STAGE_DQ) {
     hipStream_t sq = side ? side->stream : st;
     dim3 grid((unsigned)(ws.LqP / dsa::dqcfg::BQ * f.H * f.B));
-    hipLaunchKernelGGL((dsa::dsa_bwd_dq_kernel<T, D>), grid, dim3(256), 0, sq, bp);
+    if (f.qc)
+      hipLaunchKernelGGL((dsa::dsa_bwd_dq_kernel<T, D, true>), grid, dim3(256), 0, sq, bp);
+    else
+      hipLaunchKernelGGL((dsa::dsa_bwd_dq_kernel<T, D, false>), grid, dim3(256), 0, sq, bp);
     if (launch_check("dsa_bwd_dq_kernel")) return 1;
     if (side && hipEventRecord(side->join, sq) != hipSuccess) return fail("dsa: side stream join failed");
   }
@@ -414,32 +443,101 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
   return 0;
 }
 
+// The forward with the launch-order scratch `order_buf` (NULL: no
+// heaviest-first order).  Arguments already checked.
+int run_fwd(const dsa_fwd_args* a, int* order_buf, hipStream_t st) {
+  dsa::FwdParams p = to_params(a);
+  const int mode = mask_mode(a);
+  if (order_buf) {
+    if (launch_order(p, order_buf, fwd_tiles(a), true, st)) return 1;
+    p.order = order_buf + (int64_t)a->B * fwd_tiles(a);
+  }
+  if (a->dtype == DSA_BF16) {
+    return a->D == 64 ? fwd_mask<dsa::bf16, 64>(p, mode, st) : fwd_mask<dsa::bf16, 32>(p, mode, st);
+  }
+  return a->D == 64 ? fwd_mask<float, 64>(p, mode, st) : fwd_mask<float, 32>(p, mode, st);
+}
+
 }  // namespace
 
 extern "C" {
 
-int dsa_version(void) { return 5; }
+int dsa_version(void) { return 6; }
 
 const char* dsa_last_error(void) { return g_err.c_str(); }
 
 int dsa_fwd(const dsa_fwd_args* a, void* stream) {
   g_err.clear();
   if (check_fwd(a)) return 1;
-  dsa::FwdParams p = to_params(a);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int mode = mask_mode(a);
   const size_t ob = order_bytes(a, fwd_tiles(a));
+  int* buf = nullptr;
   if (ob && a->workspace) {
     if (a->workspace_bytes < ob) return fail("dsa: forward workspace of %zu bytes required, got %zu", ob, a->workspace_bytes);
     if (!aligned16(a->workspace)) return fail("dsa: forward workspace must be 16-byte aligned");
-    int* buf = static_cast<int*>(a->workspace);
-    if (launch_order(p, buf, fwd_tiles(a), true, st)) return 1;
-    p.order = buf + (int64_t)a->B * fwd_tiles(a);
+    buf = static_cast<int*>(a->workspace);
   }
+  return run_fwd(a, buf, st);
+}
+
+int dsa_bias(const dsa_fwd_args* a, void* out, const int64_t* out_strides, void* stream) {
+  g_err.clear();
+  if (!a) return fail("dsa: null arguments");
+  if (a->dtype != DSA_BF16 && a->dtype != DSA_F32) return fail("dsa: unsupported dtype %d", a->dtype);
+  if (a->D != 32 && a->D != 64) return fail("dsa: head dim must be 32 or 64, got %d", a->D);
+  if (a->B < 1 || a->H < 1 || a->Lq < 1 || a->Lk < 1)
+    return fail("dsa: empty shape B=%d H=%d Lq=%d Lk=%d", a->B, a->H, a->Lq, a->Lk);
+  if (a->B > 65535 || a->H > 65535) return fail("dsa: B and H must be <= 65535");
+  const int64_t nqt = (a->Lq + dsa::dcfg::BQ - 1) / dsa::dcfg::BQ, nkt = (a->Lk + dsa::dcfg::BK - 1) / dsa::dcfg::BK;
+  if ((int64_t)a->B * a->H * nqt * nkt > 0x7fffffff) return fail("dsa: B * H * tiles exceeds the 1-D grid range");
+  if (!a->q || !a->k || !out || !out_strides) return fail("dsa: q, k, out and out_strides are required");
+  if ((a->flags & ~(DSA_C2P | DSA_P2C)) != 0) return fail("dsa: unknown flags 0x%x", a->flags);
+  if (a->flags) {
+    if (a->att_span < 1 || a->att_span > 16383) return fail("dsa: att_span must be in [1, 16383], got %d", a->att_span);
+    if (!a->rel_table) return fail("dsa: rel_table is required when c2p/p2c is enabled");
+  }
+  if ((a->flags & DSA_C2P) && !a->kr) return fail("dsa: c2p needs the pos-key table kr");
+  if ((a->flags & DSA_P2C) && !a->qr) return fail("dsa: p2c needs the pos-query table qr");
+  if ((a->flags & DSA_C2P) && (int64_t)(2 * a->att_span - 1) * llabs(a->kr_strides[1]) + a->D > 0x7fffffffLL)
+    return fail("dsa: kr row stride too large (rows of one head over 2^31 elements)");
+  if ((a->flags & DSA_P2C) && (int64_t)(2 * a->att_span - 1) * llabs(a->qr_strides[1]) + a->D > 0x7fffffffLL)
+    return fail("dsa: qr row stride too large (rows of one head over 2^31 elements)");
+  const int vec = 16 / elem_bytes(a->dtype);
+  if (!aligned16(a->q) || !aligned16(a->k)) return fail("dsa: q and k must be 16-byte aligned");
+  for (int s = 0; s < 3; ++s)
+    if (a->q_strides[s] % vec || a->k_strides[s] % vec)
+      return fail("dsa: q / k strides must be multiples of %d elements", vec);
+  if ((a->flags & DSA_C2P) && (!aligned16(a->kr) || a->kr_strides[0] % vec || a->kr_strides[1] % vec))
+    return fail("dsa: kr must be 16-byte aligned with strides that are multiples of %d", vec);
+  if ((a->flags & DSA_P2C) && (!aligned16(a->qr) || a->qr_strides[0] % vec || a->qr_strides[1] % vec))
+    return fail("dsa: qr must be 16-byte aligned with strides that are multiples of %d", vec);
+  if (check_qc(a)) return 1;
+  if ((reinterpret_cast<uintptr_t>(out) % elem_bytes(a->dtype)) != 0) return fail("dsa: out must be aligned to its element size");
+  dsa::BiasParams bp;
+  bp.f = to_params(a);
+  bp.out = out;
+  for (int s = 0; s < 3; ++s) bp.obs[s] = out_strides[s];
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)(a->B * (int64_t)a->H * nqt * nkt));
+  const bool qc = a->qc != nullptr;
   if (a->dtype == DSA_BF16) {
-    return a->D == 64 ? fwd_mask<dsa::bf16, 64>(p, mode, st) : fwd_mask<dsa::bf16, 32>(p, mode, st);
+    if (a->D == 64) {
+      if (qc) hipLaunchKernelGGL((dsa::dsa_bias_kernel<dsa::bf16, 64, true>), grid, dim3(256), 0, st, bp);
+      else hipLaunchKernelGGL((dsa::dsa_bias_kernel<dsa::bf16, 64, false>), grid, dim3(256), 0, st, bp);
+    } else {
+      if (qc) hipLaunchKernelGGL((dsa::dsa_bias_kernel<dsa::bf16, 32, true>), grid, dim3(256), 0, st, bp);
+      else hipLaunchKernelGGL((dsa::dsa_bias_kernel<dsa::bf16, 32, false>), grid, dim3(256), 0, st, bp);
+    }
+  } else {
+    if (a->D == 64) {
+      if (qc) hipLaunchKernelGGL((dsa::dsa_bias_kernel<float, 64, true>), grid, dim3(256), 0, st, bp);
+      else hipLaunchKernelGGL((dsa::dsa_bias_kernel<float, 64, false>), grid, dim3(256), 0, st, bp);
+    } else {
+      if (qc) hipLaunchKernelGGL((dsa::dsa_bias_kernel<float, 32, true>), grid, dim3(256), 0, st, bp);
+      else hipLaunchKernelGGL((dsa::dsa_bias_kernel<float, 32, false>), grid, dim3(256), 0, st, bp);
+    }
   }
-  return a->D == 64 ? fwd_mask<float, 64>(p, mode, st) : fwd_mask<float, 32>(p, mode, st);
+  return launch_check("dsa_bias_kernel");
 }
 
 size_t dsa_fwd_bias_bytes(const dsa_fwd_args* a) {
@@ -469,6 +567,12 @@ int dsa_bwd(const dsa_bwd_args* a, void* stream) {
   if (a->dtab_dtype == DSA_BF16 && !a->dtab_overwrite)
     return fail("dsa: bf16 table gradients are written, not accumulated (set dtab_overwrite)");
   if (f.flags && !f.bias) return fail("dsa: the backward needs the relative term saved by dsa_fwd (fwd.bias)");
+  if (f.qc) {
+    const int v = 16 / elem_bytes(f.dtype);
+    if (!a->dqc || !aligned16(a->dqc)) return fail("dsa: with fwd.qc the backward needs dqc (16-byte aligned)");
+    for (int s = 0; s < 3; ++s)
+      if (a->dqc_strides[s] % v != 0) return fail("dsa: dqc strides must be multiples of %d elements", v);
+  }
   if (f.flags && !aligned16(f.bias)) return fail("dsa: fwd.bias must be 16-byte aligned");
   const int vec = 16 / elem_bytes(f.dtype);
   const void* ptrs[] = {a->dout, a->dq, a->dk, a->dv};

@@ -357,6 +357,13 @@ DSA_DEV float opaque_one() {
   return one;
 }
 
+// a if C else b, for arrays and other objects a ternary cannot pick
+template <bool C, typename X>
+DSA_DEV const X& pick(const X& a, const X& b) {
+  if constexpr (C) return a;
+  else return b;
+}
+
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 

@@ -24,7 +24,9 @@
 
 namespace dsa {
 
-template <typename T, int D, int MASK>
+// QC: the c2p term reads the query rows p.qc (which carry the p2p term)
+// instead of q.
+template <typename T, int D, int MASK, bool QC = false>
 __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
   using namespace dcfg;
   using M = Mfma<T>;
@@ -103,6 +105,16 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
 #pragma unroll
     for (int s = 0; s < NS; ++s)
       qf[ib][s] = (irow[ib] < Lq) ? M::load_contig(qbase + (int64_t)irow[ib] * p.qs[1], s, g) : M::zero();
+  // the c2p term's query rows (QC: qc, else the same Q^T fragments)
+  frag qcf[2][NS];
+  if constexpr (QC) {
+    const T* qcbase = (const T*)p.qc + (int64_t)b * p.qcs[0] + (int64_t)h * p.qcs[2];
+#pragma unroll
+    for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+      for (int s = 0; s < NS; ++s)
+        qcf[ib][s] = (irow[ib] < Lq) ? M::load_contig(qcbase + (int64_t)irow[ib] * p.qcs[1], s, g) : M::zero();
+  }
 
   float mref[2] = {-INFINITY, -INFINITY};  // reference max of the unscaled scores
   float lrow[2] = {0.f, 0.f};
@@ -267,7 +279,7 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
         st[ib][jb] = acc;
       }
     if (p.flags)
-      add_delta_bands_T<T, D, MASK == MASK_PAIR ? 3 : 6>(st, kf, qf, cb, pb, crow, prow, w, g, c16, krh, qrh, p.flags,
+      add_delta_bands_T<T, D, MASK == MASK_PAIR ? 3 : 6>(st, kf, pick<QC>(qcf, qf), cb, pb, crow, prow, w, g, c16, krh, qrh, p.flags,
                               biasl ? biasl + (int64_t)kt * 8192 : nullptr);
     __builtin_amdgcn_s_setprio(0);
 

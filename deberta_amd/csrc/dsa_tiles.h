@@ -25,7 +25,8 @@ struct FwdParams {
   float* lse;
   void* bias;       // saved relative term [B, H, LqP, LkP] or null
   const int* order; // launch order of the (batch row, tile) items, heaviest first, or null (dsa_order.h)
-  int64_t qs[3], ks[3], vs[3], os[3];
+  const void* qc;   // query rows of the c2p term [B, Lq, H, D] (carries p2p), or null: q
+  int64_t qs[3], ks[3], vs[3], os[3], qcs[3];
   int64_t krs[2], qrs[2];
   int64_t kkb, pkb, pkq, segb;
   int B, H, Lq, Lk, A, flags;
@@ -41,6 +42,8 @@ struct BwdParams {
   void* dk;
   void* dv;
   int64_t dqs[3], dks[3], dvs[3];
+  void* dqc;        // with f.qc: the c2p part of dq, written here instead of into dq
+  int64_t dqcs[3];
   void* dkr;        // table gradients: fp32 accumulated, or fp32 / bf16 overwritten
   void* dqr;
   int dtab_bf16, dtab_overwrite;
@@ -301,6 +304,7 @@ DSA_DEV void store4_contig(B* p, const f32x4& v) {
 // c16 of the tile).  y holds q.k on entry and q.k + c2p + p2c (unscaled)
 // on return.
 //   kf: A fragments of the 64 key rows, qf: B fragments of the wave's queries
+//   (the c2p term's query rows: q, or qc when it is given)
 //   cb: this wave's c2p band (WQ * CTS), pb: the shared p2c band (XG * PBT)
 //   crow, prow: the tile's table row offsets (store_row_tables)
 //   GR: c2p row blocks whose table rows are loaded before their products

@@ -20,6 +20,8 @@ Tensor layouts (see include/dsa.h):
   bias              [B, H, pad128(Lq), pad128(Lk)] the relative score term
                     c2p + p2c saved for the backward (float16 for bfloat16
                     inputs, float32 for float32); empty when not saved
+  qc                [B, Lq, H, D] or None: the query rows of the c2p term
+                    (q when None); the p2p term rides on it (attention.py)
 """
 
 from __future__ import annotations
@@ -88,6 +90,7 @@ def _fill_fwd_args(
     att_span: int,
     scale: float,
     bias: Optional[Tensor] = None,
+    qc: Optional[Tensor] = None,
 ) -> _lib.DsaFwdArgs:
     B, Lq, H, D = q.shape
     Lk = k.shape[1]
@@ -118,6 +121,9 @@ def _fill_fwd_args(
     a.dtype = _DTYPES[q.dtype]
     a.flags = _flags(kr, qr)
     a.scale = float(scale)
+    if qc is not None:
+        a.qc = qc.data_ptr()
+        a.qc_strides[:] = _strides3(qc)
     return a
 
 
@@ -131,6 +137,7 @@ def _validate(
     key_keep: Optional[Tensor],
     pair_keep: Optional[Tensor],
     att_span: int,
+    qc: Optional[Tensor] = None,
 ) -> None:
     if q.dtype not in _DTYPES:
         raise TypeError(f"dsa: q dtype must be float32 or bfloat16, got {q.dtype}")
@@ -171,6 +178,11 @@ def _validate(
                              f"got {tuple(pair_keep.shape)} strides {pair_keep.stride()}")
         if pair_keep.device != q.device:
             raise ValueError("dsa: pair_keep must be on q's device")
+    if qc is not None:
+        if kr is None:
+            raise ValueError("dsa: qc (the c2p term's query rows) needs the pos-key table kr")
+        if qc.shape != q.shape or qc.dtype != q.dtype:
+            raise ValueError(f"dsa: qc must match q ({tuple(q.shape)}, {q.dtype}), got {tuple(qc.shape)}, {qc.dtype}")
 
 
 @torch.library.custom_op("deberta_amd::dsa_fwd", mutates_args=(), device_types="cuda")
@@ -186,14 +198,16 @@ def dsa_fwd(
     att_span: int,
     scale: float,
     save_bias: bool = True,
+    qc: Optional[Tensor] = None,
 ) -> tuple[Tensor, Tensor, Tensor]:
     """(out, lse, bias).  With c2p/p2c and ``save_bias`` the relative score
     term is written to ``bias`` for the backward (which needs it); else
-    ``bias`` is empty."""
-    _validate(q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span)
+    ``bias`` is empty.  ``qc``: the c2p term's query rows (q when None)."""
+    _validate(q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, qc)
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
     kr = None if kr is None else _kernel_ready(kr)
     qr = None if qr is None else _kernel_ready(qr)
+    qc = None if qc is None else _kernel_ready(qc)
     B, Lq, H, D = q.shape
     out = torch.empty((B, Lq, H, D), dtype=q.dtype, device=q.device)
     lse = torch.empty((B, H, Lq), dtype=torch.float32, device=q.device)
@@ -201,7 +215,7 @@ def dsa_fwd(
         bias = torch.empty(bias_shape(q, k), dtype=bias_dtype(q.dtype), device=q.device)
     else:
         bias = torch.empty((0,), dtype=bias_dtype(q.dtype), device=q.device)
-    args = _fill_fwd_args(q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, att_span, scale, bias)
+    args = _fill_fwd_args(q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, att_span, scale, bias, qc)
     lib = _lib.load()
     # scratch for the heaviest-first launch order under key / segment masks
     nws = lib.dsa_fwd_workspace_bytes(ctypes.byref(args))
@@ -214,7 +228,7 @@ def dsa_fwd(
 
 
 @dsa_fwd.register_fake
-def _dsa_fwd_fake(q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias=True):
+def _dsa_fwd_fake(q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias=True, qc=None):
     B, Lq, H, D = q.shape
     out = q.new_empty((B, Lq, H, D))
     lse = q.new_empty((B, H, Lq), dtype=torch.float32)
@@ -250,11 +264,17 @@ def fill_bwd_args(
     dkr: Optional[Tensor],
     dqr: Optional[Tensor],
     dtab_overwrite: bool = False,
+    qc: Optional[Tensor] = None,
+    dqc: Optional[Tensor] = None,
 ) -> _lib.DsaBwdArgs:
     """Backward arguments.  dkr / dqr are fp32 and accumulated into, or, with
-    ``dtab_overwrite``, written (fp32 or bf16, their dtype)."""
+    ``dtab_overwrite``, written (fp32 or bf16, their dtype).  With ``qc``,
+    ``dqc`` receives its gradient (the c2p part of dq)."""
     a = _lib.DsaBwdArgs()
-    a.fwd = _fill_fwd_args(q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, att_span, scale, bias)
+    a.fwd = _fill_fwd_args(q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, att_span, scale, bias, qc)
+    if dqc is not None:
+        a.dqc = dqc.data_ptr()
+        a.dqc_strides[:] = _strides3(dqc)
     a.dout = dout.data_ptr()
     a.do_strides[:] = _strides3(dout)
     a.dq, a.dk, a.dv = dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
@@ -304,15 +324,19 @@ def dsa_bwd(
     bias: Tensor,
     att_span: int,
     scale: float,
-) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
-    """Gradients (dq, dk, dv, dkr, dqr).  dkr/dqr are [H, 2A, D] in the
-    tables' dtype (empty when the matching table is None).  ``bias`` is the relative term
-    dsa_fwd saved (required with c2p/p2c)."""
+    qc: Optional[Tensor] = None,
+) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Gradients (dq, dk, dv, dkr, dqr, dqc).  dkr/dqr are [H, 2A, D] in the
+    tables' dtype (empty when the matching table is None).  ``bias`` is the
+    relative term dsa_fwd saved (required with c2p/p2c).  With ``qc`` (the
+    c2p term's query rows), dqc is its gradient and dq the content part;
+    else dqc is empty."""
     if kr is not None or qr is not None:
         _alert_nondeterministic_tables()
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
     kr = None if kr is None else _kernel_ready(kr)
     qr = None if qr is None else _kernel_ready(qr)
+    qc = None if qc is None else _kernel_ready(qc)
     if (kr is not None or qr is not None) and tuple(bias.shape) != bias_shape(q, k):
         raise RuntimeError("dsa_bwd: the relative term saved by dsa_fwd (save_bias=True) is required")
     dout = _kernel_ready(dout.to(q.dtype))
@@ -326,9 +350,11 @@ def dsa_bwd(
     tab = dict(dtype=q.dtype, device=q.device)
     dkr = torch.empty((H, R, D), **tab) if kr is not None else torch.empty((0,), **tab)
     dqr = torch.empty((H, R, D), **tab) if qr is not None else torch.empty((0,), **tab)
+    dqc = torch.empty_like(q, memory_format=torch.contiguous_format) if qc is not None else torch.empty((0,), **tab)
     args = fill_bwd_args(
         dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, att_span, scale,
         dq, dk, dv, dkr if kr is not None else None, dqr if qr is not None else None, dtab_overwrite=True,
+        qc=qc, dqc=dqc if qc is not None else None,
     )
     ws = torch.empty((max(bwd_workspace_bytes(args), 16),), dtype=torch.uint8, device=q.device)
     args.workspace = ws.data_ptr()
@@ -336,44 +362,87 @@ def dsa_bwd(
     lib = _lib.load()
     stream = torch.cuda.current_stream(q.device).cuda_stream
     _lib.check(lib.dsa_bwd(ctypes.byref(args), ctypes.c_void_p(stream)), "dsa_bwd")
-    return dq, dk, dv, dkr, dqr
+    return dq, dk, dv, dkr, dqr, dqc
 
 
 @dsa_bwd.register_fake
-def _dsa_bwd_fake(dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, att_span, scale):
+def _dsa_bwd_fake(dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, att_span, scale, qc=None):
     H, D = q.shape[2], q.shape[3]
     R = 2 * int(att_span)
     dkr = q.new_empty((H, R, D)) if kr is not None else q.new_empty((0,))
     dqr = q.new_empty((H, R, D)) if qr is not None else q.new_empty((0,))
+    dqc = q.new_empty(q.shape) if qc is not None else q.new_empty((0,))
     return (
         q.new_empty(q.shape),
         k.new_empty(k.shape),
         v.new_empty(v.shape),
         dkr,
         dqr,
+        dqc,
     )
 
 
 def _setup_context(ctx, inputs, output):
-    q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias = inputs
+    q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias, qc = inputs
     out, lse, bias = output
     ctx.mark_non_differentiable(lse, bias)
     # lse and the saved term get no gradient: do not materialise zeros for
     # them (the saved term is (B, H, L, L)-sized)
     ctx.set_materialize_grads(False)
-    ctx.save_for_backward(q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias)
+    ctx.save_for_backward(q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, qc)
     ctx.att_span = att_span
     ctx.scale = scale
 
 
 def _backward(ctx, dout, dlse, dbias):
-    q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias = ctx.saved_tensors
+    q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, qc = ctx.saved_tensors
     if dout is None:  # the output itself received no gradient
-        return (None,) * 11
-    dq, dk, dv, dkr, dqr = dsa_bwd(
-        dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, ctx.att_span, ctx.scale
+        return (None,) * 12
+    dq, dk, dv, dkr, dqr, dqc = dsa_bwd(
+        dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, ctx.att_span, ctx.scale, qc
     )
-    return dq, dk, dv, (dkr if kr is not None else None), (dqr if qr is not None else None), None, None, None, None, None, None
+    return (
+        dq, dk, dv, (dkr if kr is not None else None), (dqr if qr is not None else None),
+        None, None, None, None, None, None, (dqc if qc is not None else None),
+    )
 
 
 torch.library.register_autograd("deberta_amd::dsa_fwd", _backward, setup_context=_setup_context)
+
+
+@torch.library.custom_op("deberta_amd::dsa_bias", mutates_args=(), device_types="cuda")
+def dsa_bias(
+    q: Tensor,
+    k: Tensor,
+    kr: Optional[Tensor],
+    qr: Optional[Tensor],
+    rel_table: Optional[Tensor],
+    att_span: int,
+    scale: float,
+    qc: Optional[Tensor] = None,
+) -> Tensor:
+    """The relative score term ``scale * (c2p + p2c)`` as ``(B, H, Lq, Lk)``
+    in q's dtype (the reference's ``disentangled_attention_bias``,
+    deberta_v2_native.py:530-562), unmasked; zeros without tables.  q, k are
+    ``[B, L, H, D]`` views; ``qc`` the c2p term's query rows (q when None)."""
+    _validate(q, k, k, kr, qr, rel_table, None, None, att_span, qc)
+    q, k = _kernel_ready(q), _kernel_ready(k)
+    kr = None if kr is None else _kernel_ready(kr)
+    qr = None if qr is None else _kernel_ready(qr)
+    qc = None if qc is None else _kernel_ready(qc)
+    B, Lq, H, _ = q.shape
+    Lk = k.shape[1]
+    out = torch.empty((B, H, Lq, Lk), dtype=q.dtype, device=q.device)
+    dummy = torch.empty((0,), dtype=torch.float32, device=q.device)
+    args = _fill_fwd_args(q, k, k, kr, qr, rel_table, None, None, q, dummy, att_span, scale, None, qc)
+    strides = (ctypes.c_int64 * 3)(*out.stride()[:3])
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(q.device).cuda_stream
+    _lib.check(lib.dsa_bias(ctypes.byref(args), ctypes.c_void_p(out.data_ptr()), strides, ctypes.c_void_p(stream)), "dsa_bias")
+    return out
+
+
+@dsa_bias.register_fake
+def _dsa_bias_fake(q, k, kr, qr, rel_table, att_span, scale, qc=None):
+    B, Lq, H, _ = q.shape
+    return q.new_empty((B, H, Lq, k.shape[1]))

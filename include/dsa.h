@@ -115,6 +115,15 @@ typedef struct dsa_fwd_args {
      which has its own workspace. */
   void* workspace;
   size_t workspace_bytes;
+  /* Optional [B, Lq, H, D] (element strides qc_strides, D contiguous): the
+     query rows of the c2p term, which then reads qc_i . Kr[c(i-j)] instead
+     of q_i . Kr[c(i-j)]; NULL means q.  The position-to-position term
+     (p2p, deberta_v2_native.py:298-347: Qr[A + min(i, A-1)] . Kr[c(i-j)],
+     the same Kr rows as c2p) is carried this way: qc = q + Qr[A + min(i,
+     A-1)] with c2p and p2p, qc = Qr[A + min(i, A-1)] with p2p alone (flags
+     then hold DSA_C2P).  The saved relative term holds the c2p term of qc. */
+  const void* qc;
+  int64_t qc_strides[3];
 } dsa_fwd_args;
 
 typedef struct dsa_bwd_args {
@@ -138,6 +147,11 @@ typedef struct dsa_bwd_args {
   int32_t dtab_dtype;     /* dtype of dkr / dqr: DSA_F32 (0) or DSA_BF16 */
   int32_t dtab_overwrite; /* 0: dkr / dqr are fp32 and accumulated (+=) into;
                              1: they are overwritten (=), either dtype */
+  /* With fwd.qc: [B, Lq, H, D], dtype of q, the gradient of qc
+     (s sum_j dS_ij Kr[c(i-j)], the c2p part of dq); dq then holds only
+     s sum_j dS_ij k_j.  Unused without fwd.qc. */
+  void* dqc;
+  int64_t dqc_strides[3];
 } dsa_bwd_args;
 
 /* Forward: out = softmax(mask((QK^T + c2p + p2c) * scale)) V and its
@@ -150,6 +164,18 @@ int dsa_fwd(const dsa_fwd_args* args, void* stream);
  * fp32 or bf16, per dtab_dtype / dtab_overwrite).  Replaces ATen autograd through deberta_v2_native.py:592-652 and
  * the einsum/bmm + gather bias path (:349-528). */
 int dsa_bwd(const dsa_bwd_args* args, void* stream);
+
+/* The relative score term alone, the reference's bias API
+ * DisentangledSelfAttention.disentangled_attention_bias
+ * (deberta_v2_native.py:530-562, dispatching to :349-432 / :434-528):
+ *   out[b, h, i, j] = scale * (qc_i . Kr[c(i-j)] + k_j . Qr[p(i-j)])
+ * for the terms in args->flags (qc = q unless args->qc is set; p2p rides
+ * on qc as in dsa_fwd_args), zeros with no flags.  Reads q (or qc), k, kr,
+ * qr, rel_table, B, H, Lq, Lk, D, att_span, dtype, flags and scale from
+ * args (masks, v, out, lse, bias and workspace are ignored: the reference's
+ * bias is unmasked).  out: [B, H, Lq, Lk] in the dtype of q, element
+ * strides out_strides = (b, h, i) and unit stride over j, 16-byte aligned. */
+int dsa_bias(const dsa_fwd_args* args, void* out, const int64_t* out_strides, void* stream);
 
 /* Workspace bytes dsa_bwd needs for these arguments. */
 size_t dsa_bwd_workspace_bytes(const dsa_bwd_args* args);

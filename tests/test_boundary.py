@@ -137,8 +137,13 @@ def test_fake_shapes():
         assert lse.shape == (2, 2, 64) and lse.dtype == torch.float32
         assert bias.shape == (2, 2, 128, 128) and bias.dtype == torch.float16
         g = torch.ops.deberta_amd.dsa_bwd(out, q, k, v, kr, qr, table, None, None, out, lse, bias, 16, 0.1)
-        assert [t.shape for t in g] == [q.shape, k.shape, v.shape, (2, 32, 64), (2, 32, 64)]
+        assert [t.shape for t in g] == [q.shape, k.shape, v.shape, (2, 32, 64), (2, 32, 64), (0,)]
         assert g[3].dtype == q.dtype
+        # with the c2p term's query rows (qc, the carrier of p2p): their gradient
+        g = torch.ops.deberta_amd.dsa_bwd(out, q, k, v, kr, qr, table, None, None, out, lse, bias, 16, 0.1, q)
+        assert g[5].shape == q.shape
+        b = torch.ops.deberta_amd.dsa_bias(q, k, kr, qr, table, 16, 0.1, None)
+        assert b.shape == (2, 2, 64, 64) and b.dtype == q.dtype
 
 
 def test_trace_forward_and_backward_with_fake_tensors():

@@ -1,0 +1,186 @@
+"""GPU tests of the rest of the reference's call surface on the fused
+kernels: the bias API (``disentangled_attention_bias``,
+deberta_v2_native.py:530-562) through ``dsa_bias``, the p2p term
+(``:298-347``) carried by the c2p term's query rows, and the device-side
+relative-position table at the bucket function's saturation edge.
+
+Tolerances: fp32 max|err| / max|ref| <= 1e-4 (the north_star's "max
+relative error" read relative to the tensor's scale, so that entries near
+zero do not dominate); bf16 max|err| <= 2e-2 against the fp32 oracle on the
+same bf16-rounded inputs.
+"""
+
+from __future__ import annotations
+
+import math
+import sys
+
+import pytest
+import torch
+
+from deberta_amd import DisentangledSelfAttention, disentangled_attention
+from deberta_amd.relpos import relative_offset_table
+from oracle import eager
+from tests._cases import max_abs, max_rel
+from tests._modules import _errors, _pair, _run
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def _bias_inputs(B, H, L, D, hidden, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, H, L, D, generator=g)
+    k = torch.randn(B, H, L, D, generator=g)
+    rel = torch.randn(512, hidden, generator=g)
+    return q, k, rel
+
+
+def _oracle_bias(ref, q, k, rel, types, sf, relative_pos=None):
+    A = ref.pos_ebd_size
+    kr = ref.project_rel(rel, use_query=False) if ("c2p" in types or "p2p" in types) else None
+    qr = ref.project_rel(rel, use_query=True) if ("p2c" in types or "p2p" in types) else None
+    rp = eager.canonical_rel(relative_pos, q.shape[2], k.shape[2], ref.position_buckets, ref.max_relative_positions)
+    return eager.relative_bias(q, k, kr, qr, rp, A, types, sf, ref.attention_head_size)
+
+
+@pytest.mark.parametrize("types", ["c2p|p2c", "c2p", "p2c", "p2p", "c2p|p2c|p2p"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+@pytest.mark.parametrize("share", [False, True])
+def test_bias_api_matches_oracle(types, dtype, share, gpu):
+    """disentangled_attention_bias on the GPU against the oracle's bias
+    (einsum + gather) at L = 300 (ragged tiles, log buckets in use)."""
+    cfg = eager.make_config(hidden_size=128, num_attention_heads=4, share_att_key=share, pos_att_type=types)
+    ref, ours = _pair(cfg, seed=11)
+    ours = ours.to(gpu)
+    B, H, L, D = 2, 4, 300, 32
+    q, k, rel = _bias_inputs(B, H, L, D, 128, seed=4)
+    rnd = lambda t: t.to(dtype).float()
+    types_l = eager.pos_att_types(types)
+    sf = 1 + len(types_l)
+    with torch.no_grad():
+        want = _oracle_bias(ref, rnd(q), rnd(k), rel, types_l, sf)
+        if dtype == torch.bfloat16:  # the tables the kernel reads are rounded too
+            kr = ref.project_rel(rel, use_query=False).to(dtype).float() if ("c2p" in types_l or "p2p" in types_l) else None
+            qr = ref.project_rel(rel, use_query=True).to(dtype).float() if ("p2c" in types_l or "p2p" in types_l) else None
+            rp = eager.relative_positions(L, L, 256, 512)
+            want = eager.relative_bias(rnd(q), rnd(k), kr, qr, rp, 256, types_l, sf, D)
+        got = ours.disentangled_attention_bias(q.to(gpu, dtype), k.to(gpu, dtype), None, rel.to(gpu), sf)
+    assert got.shape == (B, H, L, L) and got.dtype == dtype
+    got = got.float().cpu()
+    if dtype == torch.float32:
+        err = max_rel(got, want)
+        _say(f"[bias {types} fp32 share={share}] rel {err:.2e}")
+        assert err <= 1e-4
+    else:
+        err = max_abs(got, want)
+        _say(f"[bias {types} bf16 share={share}] abs {err:.2e} (max |ref| {float(want.abs().max()):.2f})")
+        assert err <= 2e-2
+
+
+def test_bias_api_recomputes_and_respects_scale_factor(gpu):
+    """The reference's assertions on the bias API, restated at head dim 32
+    (the kernels' smallest): tests/test_smoke.py:1853-1900 (a new query/key
+    pair gives a new bias: nothing is cached across calls), :2072-2123 (p2p
+    alone is nonzero and scales as sqrt(8 / 2)) and :2126-2175 (c2p|p2c
+    scales as sqrt(12 / 3))."""
+    cfg = eager.make_config(hidden_size=128, num_attention_heads=4, max_position_embeddings=32,
+                            position_buckets=-1, max_relative_positions=-1, pos_att_type="c2p|p2c")
+    attn = DisentangledSelfAttention(cfg).to(gpu).eval()
+    g = torch.Generator().manual_seed(0)
+    mk = lambda *s: torch.randn(*s, generator=g).to(gpu)
+    qa, ka, qb, kb = mk(2, 4, 8, 32), mk(2, 4, 8, 32), mk(2, 4, 8, 32), mk(2, 4, 8, 32)
+    rel = mk(64, 128)
+    with torch.no_grad():
+        sa = attn.disentangled_attention_bias(query_layer=qa, key_layer=ka, relative_pos=None, rel_embeddings=rel, scale_factor=3)
+        sb = attn.disentangled_attention_bias(query_layer=qb, key_layer=kb, relative_pos=None, rel_embeddings=rel, scale_factor=3)
+        s12 = attn.disentangled_attention_bias(query_layer=qa, key_layer=ka, relative_pos=None, rel_embeddings=rel, scale_factor=12)
+    assert sa.shape == sb.shape == (2, 4, 8, 8)
+    assert not torch.allclose(sa, sb, rtol=0.0, atol=0.0) and float((sa - sb).abs().max()) > 0.0
+    ratio = float(sa.abs().mean()) / float(s12.abs().mean())
+    assert ratio == pytest.approx(math.sqrt(12.0 / 3.0), rel=1e-4, abs=1e-4)
+
+    cfg_p = eager.make_config(hidden_size=128, num_attention_heads=4, max_position_embeddings=32,
+                              position_buckets=-1, max_relative_positions=-1, pos_att_type="p2p")
+    attn_p = DisentangledSelfAttention(cfg_p).to(gpu).eval()
+    with torch.no_grad():
+        p2 = attn_p.disentangled_attention_bias(query_layer=qa, key_layer=ka, relative_pos=None, rel_embeddings=rel, scale_factor=2)
+        p8 = attn_p.disentangled_attention_bias(query_layer=qa, key_layer=ka, relative_pos=None, rel_embeddings=rel, scale_factor=8)
+    assert torch.isfinite(p2).all() and float(p2.abs().sum()) > 0.0
+    assert float(p2.abs().mean()) / float(p8.abs().mean()) == pytest.approx(math.sqrt(8.0 / 2.0), rel=1e-4, abs=1e-4)
+
+
+def _p2p_config(share, types="c2p|p2c|p2p"):
+    return eager.make_config(hidden_size=128, num_attention_heads=4, position_buckets=256, max_relative_positions=512,
+                             share_att_key=share, pos_att_type=types)
+
+
+@pytest.mark.parametrize("types", ["c2p|p2c|p2p", "p2p", "c2p|p2p", "p2c|p2p"])
+@pytest.mark.parametrize("share", [False, True])
+@pytest.mark.parametrize("mask", ["none", "padding"])
+def test_p2p_module_parity_fp32(types, share, mask, gpu):
+    """The module with the p2p term (deberta_v2_native.py:298-347) against the
+    oracle module, fp32, forward and every gradient.  The p2p query rows
+    A + min(i, A - 1) stop moving past i = A - 1 = 255, which L = 300
+    exercises."""
+    cfg = _p2p_config(share, types)
+    ref, ours = _pair(cfg, seed=3)
+    ours = ours.to(gpu)
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(2, 300, 128, generator=g)
+    rel = torch.randn(512, 128, generator=g) * 0.5
+    m = None
+    if mask == "padding":
+        keep = torch.ones(2, 300, dtype=torch.bool)
+        keep[1, 211:] = False
+        m = keep[:, None, None, :]
+    a = _run(ref, x, m, rel, "cpu")
+    b = _run(ours, x, m, rel, gpu)
+    errs = _errors(a, b)
+    _say(f"[p2p module fp32 {types} share={share} mask={mask}] {errs}")
+    assert all(e <= 1e-4 for e in errs.values()), errs
+
+
+def test_p2p_op_bf16(gpu):
+    """The functional op with p2p in bf16 against the fp32 oracle on the
+    same bf16-rounded inputs: max abs error <= 2e-2 on the output and on
+    every gradient (q, k, v and both tables)."""
+    B, H, L, D, A = 2, 4, 300, 64, 256
+    g = torch.Generator().manual_seed(21)
+    q, k, v, dO = (torch.randn(B, H, L, D, generator=g) for _ in range(4))
+    kr, qr = (torch.randn(H, 2 * A, D, generator=g) for _ in range(2))
+    bf = lambda t: t.to(torch.bfloat16)
+    types = ["c2p", "p2c", "p2p"]
+    lc = [bf(t).float().requires_grad_(True) for t in (q, k, v, kr, qr)]
+    rel = eager.relative_positions(L, L, 256, 512)
+    ctx, _ = eager.attend(*lc, rel, None, types=types, att_span=A)
+    gc = torch.autograd.grad(ctx, lc, bf(dO).float())
+    ld = [bf(t).to(gpu).requires_grad_(True) for t in (q, k, v, kr, qr)]
+    out = disentangled_attention(*ld, None, None, position_buckets=256, max_relative_positions=512,
+                                 att_type="c2p|p2c|p2p")
+    gd = torch.autograd.grad(out, ld, bf(dO).to(gpu))
+    errs = {"out": max_abs(out.detach().float().cpu(), ctx.detach())}
+    for n, a_, b_ in zip(("dq", "dk", "dv", "dkr", "dqr"), gd, gc):
+        errs[n] = max_abs(a_.float().cpu(), b_)
+    _say(f"[p2p op bf16] {errs}")
+    assert all(e <= 2e-2 for e in errs.values()), errs
+
+
+@pytest.mark.parametrize("buckets,max_pos", [(256, 512), (128, 512)])
+def test_device_bucket_table_matches_oracle(buckets, max_pos, gpu):
+    """The relative-position table built on the GPU (the kernels' input)
+    equals the CPU oracle's bucket function over |i - j| <= 4095, the
+    saturation edge included: the device's fp32 log / ceil land on the same
+    integers as the CPU's for every offset of a 4096-token sequence."""
+    L = 4096
+    dev = relative_offset_table(L, L, bucket_size=buckets, max_position=max_pos, device=gpu).cpu().long()
+    d = torch.arange(-(L - 1), L)
+    want = eager.log_bucket(d, buckets, max_pos)
+    mid = buckets // 2
+    edge = {int(x): int(dev[x + L - 1]) for x in (mid - 1, mid, max_pos - 2, max_pos - 1, max_pos, L - 1)}
+    _say(f"[bucket table {buckets}/{max_pos}] values at the edges {edge}")
+    assert torch.equal(dev, want)
+    assert edge[L - 1] == edge[max_pos - 1] == -int(dev[0])  # saturated, odd
