@@ -94,6 +94,7 @@ class DsaBwdArgs(ctypes.Structure):
 EXPORTS = (
     "dsa_fwd",
     "dsa_bwd",
+    "dsa_fwd_static",
     "dsa_bias",
     "dsa_bwd_workspace_bytes",
     "dsa_fwd_bias_bytes",
@@ -128,6 +129,8 @@ def load() -> ctypes.CDLL:
         lib.dsa_fwd.restype = ctypes.c_int
         lib.dsa_bwd.argtypes = [ctypes.POINTER(DsaBwdArgs), ctypes.c_void_p]
         lib.dsa_bwd.restype = ctypes.c_int
+        lib.dsa_fwd_static.argtypes = [ctypes.POINTER(DsaFwdArgs), ctypes.c_void_p]
+        lib.dsa_fwd_static.restype = ctypes.c_int
         lib.dsa_bias.argtypes = [ctypes.POINTER(DsaFwdArgs), ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64), ctypes.c_void_p]
         lib.dsa_bias.restype = ctypes.c_int
         lib.dsa_bwd_workspace_bytes.argtypes = [ctypes.POINTER(DsaBwdArgs)]

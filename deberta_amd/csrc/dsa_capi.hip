@@ -8,6 +8,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../../include/dsa.h"
@@ -18,6 +19,15 @@
 #include "dsa_bwd_table.h"
 #include "dsa_order.h"
 #include "dsa_fwd.h"
+
+// Library-owned scratch of dsa_fwd_static: the launch order's cost and
+// order arrays for up to 65536 (batch row, query tile) items, 512 KiB, one
+// copy per GPU for the life of the process.  Host code never uses the
+// array's name as an address: static_scratch() resolves this GPU's copy
+// once per device (hipGetSymbolAddress with that device current) and keeps
+// it.
+constexpr size_t kStaticScratchBytes = 512 * 1024;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
 
 namespace {
 
@@ -443,6 +453,26 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
   return 0;
 }
 
+static_assert(kStaticScratchBytes == 2 * kMaxOrderItems * sizeof(int), "the static scratch holds one launch order");
+
+constexpr int kMaxDevices = 64;
+
+void* static_scratch(int* err_device) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    *err_device = dev;
+    return nullptr;
+  }
+  static std::once_flag once[kMaxDevices];
+  static void* addr[kMaxDevices];
+  std::call_once(once[dev], [dev] {
+    void* ptr = nullptr;
+    addr[dev] = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) == hipSuccess ? ptr : nullptr;
+  });
+  *err_device = dev;
+  return addr[dev];
+}
+
 // The forward with the launch-order scratch `order_buf` (NULL: no
 // heaviest-first order).  Arguments already checked.
 int run_fwd(const dsa_fwd_args* a, int* order_buf, hipStream_t st) {
@@ -478,6 +508,23 @@ int dsa_fwd(const dsa_fwd_args* a, void* stream) {
     buf = static_cast<int*>(a->workspace);
   }
   return run_fwd(a, buf, st);
+}
+
+int dsa_fwd_static(const dsa_fwd_args* a, void* stream) {
+  g_err.clear();
+  if (check_fwd(a)) return 1;
+  int* buf = nullptr;
+  if (a->key_keep || a->seg) {
+    const int64_t n = (int64_t)a->B * fwd_tiles(a);
+    if (n > kMaxOrderItems)
+      return fail("dsa_fwd_static: B * ceil(Lq / 128) = %lld launch-order items exceed the static scratch's "
+                  "%lld (%zu bytes); use dsa_fwd with a caller workspace",
+                  (long long)n, (long long)kMaxOrderItems, kStaticScratchBytes);
+    int dev = -1;
+    buf = static_cast<int*>(static_scratch(&dev));
+    if (!buf) return fail("dsa_fwd_static: no address for the static scratch on device %d", dev);
+  }
+  return run_fwd(a, buf, static_cast<hipStream_t>(stream));
 }
 
 int dsa_bias(const dsa_fwd_args* a, void* out, const int64_t* out_strides, void* stream) {
