@@ -43,7 +43,7 @@ WORKLOADS = {
     "headline": (32, 512, 12, None, "BASELINE configs[1] shape, all-ones mask"),
     "C2pad": (32, 512, 12, "key", "configs[1] shape, per-row valid length ~U{64..512} as a (B,1,1,L) key mask"),
     "C5": (64, 512, 16, None, "B=64 L=512 H=16, no mask"),
-    "C3": (16, 512, 12, None, "12-layer DeBERTa-v3-base-shaped encoder fwd+bwd under an RTD loss, bf16 autocast"),
+    "C3": (16, 512, 12, None, "12-layer DeBERTa-v3-base-shaped encoder fwd+bwd under an RTD loss, bf16 autocast, fused attention and fused row kernels around it (step time with plain torch blocks beside it)"),
     "C5layer": (64, 512, 16, None, "DeBERTa-v3-large-shaped attention layer (hidden 1024, projections included) fwd+bwd, bf16, inside torch.compile"),
     "C4": (4, 4096, 12, "doc", "B=4 L=4096 H=12, packed documents (lengths ~Geometric(mean 600)) as the dense (B,1,L,L) doc-block mask (recognised once and run as segment ids)"),
     "C4seg": (4, 4096, 12, "seg", "as C4, the same documents given as segment ids (SegmentMask)"),
@@ -170,23 +170,27 @@ def run_encoder(args) -> None:
 
     import deberta_amd
     from deberta_amd.relpos import relative_offset_table
-    from tests._encoder import Encoder, init_weights, rtd_loss, synthetic_batch
+    from tests._encoder import Encoder, init_weights, synthetic_batch
 
     dev = torch.device("cuda:0")
     Bc, Lc, Hc = 16, 512, 12
-    model = Encoder(deberta_amd.DisentangledSelfAttention)
-    init_weights(model, seed=0)
-    model = model.to(dev)
     ids, labels = synthetic_batch(Bc, Lc, seed=0)
     ids, labels = ids.to(dev), labels.to(dev)
     mask = torch.ones(Bc, 1, 1, Lc, dtype=torch.bool, device=dev)
     rel_pos = deberta_amd.build_relative_position(Lc, Lc, bucket_size=BUCKETS, max_position=MAX_POS, device=dev)
-    params = [p_ for p_ in model.parameters()]
 
-    def step():
-        with torch.autocast("cuda", dtype=torch.bfloat16):
-            logits = model(ids, mask, rel_pos)
-        torch.autograd.grad(rtd_loss(logits, labels), params)
+    def make_step(fused_blocks):
+        model = Encoder(deberta_amd.DisentangledSelfAttention, fused_blocks=fused_blocks)
+        init_weights(model, seed=0)
+        model = model.to(dev)
+        params = [p_ for p_ in model.parameters()]
+
+        def step():
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                loss, _ = model.loss(ids, mask, rel_pos, labels)
+            torch.autograd.grad(loss, params)
+
+        return step
 
     def timed(fn, n):
         for _ in range(3):
@@ -200,8 +204,29 @@ def run_encoder(args) -> None:
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / n
 
+    def timed_pair(fa, fb, n):
+        """Median step times of two step functions run alternately (one
+        step of each per round, each bracketed by events), so that clock
+        and thermal drift fall on both alike."""
+        for _ in range(3):
+            fa()
+            fb()
+        torch.cuda.synchronize()
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(n)]
+        for e in ev:
+            e[0].record()
+            fa()
+            e[1].record()
+            e[2].record()
+            fb()
+            e[3].record()
+        torch.cuda.synchronize()
+        ta = sorted(e[0].elapsed_time(e[1]) for e in ev)
+        tb = sorted(e[2].elapsed_time(e[3]) for e in ev)
+        return ta[n // 2], tb[n // 2]
+
     n = max(3, args.steps)
-    ms = timed(step, n)
+    ms, ms_plain = timed_pair(make_step(True), make_step(False), n)
     # the fused op alone at one layer's shape (q, k, v, kr, qr leaves, bf16)
     gq = torch.Generator().manual_seed(1)
     mk = lambda *sh: torch.randn(*sh, generator=gq).to(device=dev, dtype=torch.bfloat16).requires_grad_(True)
@@ -223,6 +248,8 @@ def run_encoder(args) -> None:
                 "description": WORKLOADS["C3"][4],
                 "ms_per_step": round(ms, 3),
                 "tokens_per_s": round(Bc * Lc / (ms * 1e-3), 1),
+                "ms_per_step_plain_torch_blocks": round(ms_plain, 3),
+                "timing": "median step of each, the two encoders stepped alternately",
                 "attention_ms_per_layer": round(ms_attn, 4),
                 "attention_share": round(12 * ms_attn / ms, 4),
                 "steps": n,

@@ -6,12 +6,24 @@ Public surface:
   build_relative_position, make_log_bucket_position, relative_offset_table
   normalize_keep_mask, build_doc_block_mask, get_attention_mask
   SegmentMask                 packed-document ids in place of the dense mask
+  FusedSelfOutput, FusedOutput, FusedIntermediate, FusedRTDHead,
+  RelativeEmbeddings          the blocks around the attention on fused row
+                              kernels (residual + LayerNorm, bias + GELU,
+                              classifier + BCE loss)
   normalize_attention_kernel  the attention-kernel selector
 The compute runs in libdsa.so (hand-written HIP for gfx950) through the
 torch.library ops ``deberta_amd::dsa_fwd`` / ``deberta_amd::dsa_bwd``.
 """
 
 from deberta_amd.attention import DisentangledSelfAttention, disentangled_attention, fused_attention
+from deberta_amd.blocks import (
+    FusedIntermediate,
+    FusedOutput,
+    FusedRTDHead,
+    FusedSelfOutput,
+    RelativeEmbeddings,
+    fused_add_layer_norm,
+)
 from deberta_amd.config import normalize_attention_kernel, normalize_pos_att_type
 from deberta_amd.masks import SegmentMask, build_doc_block_mask, get_attention_mask, normalize_keep_mask
 from deberta_amd.relpos import build_relative_position, make_log_bucket_position, relative_offset_table
@@ -29,4 +41,10 @@ __all__ = [
     "build_relative_position",
     "make_log_bucket_position",
     "relative_offset_table",
+    "FusedSelfOutput",
+    "FusedOutput",
+    "FusedIntermediate",
+    "FusedRTDHead",
+    "RelativeEmbeddings",
+    "fused_add_layer_norm",
 ]

@@ -90,6 +90,113 @@ class DsaBwdArgs(ctypes.Structure):
     ]
 
 
+DSA_BLOCK_LN = 0
+DSA_BLOCK_GELU = 1
+DSA_BLOCK_RTD = 2
+
+
+class DsaLnArgs(ctypes.Structure):
+    """dsa_ln_args (include/dsa_block.h)."""
+
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("bias", ctypes.c_void_p),
+        ("res", ctypes.c_void_p),
+        ("gamma", ctypes.c_void_p),
+        ("beta", ctypes.c_void_p),
+        ("x_stride", ctypes.c_int64),
+        ("res_strides", _i64x2),
+        ("rows_per_group", ctypes.c_int64),
+        ("y", ctypes.c_void_p),
+        ("y_stride", ctypes.c_int64),
+        ("mean", ctypes.c_void_p),
+        ("rstd", ctypes.c_void_p),
+        ("dy", ctypes.c_void_p),
+        ("dy_stride", ctypes.c_int64),
+        ("dz", ctypes.c_void_p),
+        ("dz_stride", ctypes.c_int64),
+        ("dgamma", ctypes.c_void_p),
+        ("dbeta", ctypes.c_void_p),
+        ("dbias", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+        ("N", ctypes.c_int64),
+        ("C", ctypes.c_int32),
+        ("x_dtype", ctypes.c_int32),
+        ("res_dtype", ctypes.c_int32),
+        ("y_dtype", ctypes.c_int32),
+        ("dy_dtype", ctypes.c_int32),
+        ("dz_dtype", ctypes.c_int32),
+        ("param_dtype", ctypes.c_int32),
+        ("eps", ctypes.c_float),
+    ]
+
+
+class DsaGeluArgs(ctypes.Structure):
+    """dsa_gelu_args (include/dsa_block.h)."""
+
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("bias", ctypes.c_void_p),
+        ("y", ctypes.c_void_p),
+        ("dy", ctypes.c_void_p),
+        ("dz", ctypes.c_void_p),
+        ("dbias", ctypes.c_void_p),
+        ("x_stride", ctypes.c_int64),
+        ("y_stride", ctypes.c_int64),
+        ("dy_stride", ctypes.c_int64),
+        ("dz_stride", ctypes.c_int64),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+        ("N", ctypes.c_int64),
+        ("C", ctypes.c_int32),
+        ("x_dtype", ctypes.c_int32),
+        ("y_dtype", ctypes.c_int32),
+        ("dy_dtype", ctypes.c_int32),
+        ("dz_dtype", ctypes.c_int32),
+        ("param_dtype", ctypes.c_int32),
+    ]
+
+
+class DsaRtdArgs(ctypes.Structure):
+    """dsa_rtd_args (include/dsa_block.h)."""
+
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("w", ctypes.c_void_p),
+        ("b", ctypes.c_void_p),
+        ("labels", ctypes.c_void_p),
+        ("active", ctypes.c_void_p),
+        ("x_stride", ctypes.c_int64),
+        ("logits", ctypes.c_void_p),
+        ("loss", ctypes.c_void_p),
+        ("denom", ctypes.c_void_p),
+        ("dloss", ctypes.c_void_p),
+        ("dx", ctypes.c_void_p),
+        ("dx_stride", ctypes.c_int64),
+        ("dw", ctypes.c_void_p),
+        ("db", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+        ("N", ctypes.c_int64),
+        ("C", ctypes.c_int32),
+        ("x_dtype", ctypes.c_int32),
+        ("dx_dtype", ctypes.c_int32),
+        ("param_dtype", ctypes.c_int32),
+    ]
+
+
+# Entry points of include/dsa_block.h (the fused row kernels).
+BLOCK_EXPORTS = (
+    "dsa_block_workspace_bytes",
+    "dsa_add_ln_fwd",
+    "dsa_add_ln_bwd",
+    "dsa_bias_gelu_fwd",
+    "dsa_bias_gelu_bwd",
+    "dsa_rtd_loss_fwd",
+    "dsa_rtd_loss_bwd",
+)
+
 # Every entry point include/dsa.h declares.
 EXPORTS = (
     "dsa_fwd",
@@ -143,6 +250,19 @@ def load() -> ctypes.CDLL:
         lib.dsa_last_error.restype = ctypes.c_char_p
         lib.dsa_version.argtypes = []
         lib.dsa_version.restype = ctypes.c_int
+        lib.dsa_block_workspace_bytes.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int32]
+        lib.dsa_block_workspace_bytes.restype = ctypes.c_size_t
+        for name, st in (
+            ("dsa_add_ln_fwd", DsaLnArgs),
+            ("dsa_add_ln_bwd", DsaLnArgs),
+            ("dsa_bias_gelu_fwd", DsaGeluArgs),
+            ("dsa_bias_gelu_bwd", DsaGeluArgs),
+            ("dsa_rtd_loss_fwd", DsaRtdArgs),
+            ("dsa_rtd_loss_bwd", DsaRtdArgs),
+        ):
+            fn = getattr(lib, name)
+            fn.argtypes = [ctypes.POINTER(st), ctypes.c_void_p]
+            fn.restype = ctypes.c_int
         ver = lib.dsa_version()
         if ver != EXPECTED_VERSION:
             raise RuntimeError(f"{LIB_PATH} has ABI version {ver}, expected {EXPECTED_VERSION}; rebuild it")

@@ -325,13 +325,25 @@ class DisentangledSelfAttention(nn.Module):
         self, rel_embeddings: torch.Tensor, dtype: torch.dtype
     ) -> tuple[Optional[torch.Tensor], Optional[torch.Tensor]]:
         """(Kr, Qr) projected for the configured terms (None where unused),
-        in ``dtype`` (deberta_v2_native.py:372-375)."""
+        in ``dtype`` (deberta_v2_native.py:372-375).  When both are needed
+        they come from one GEMM through the two weight matrices
+        concatenated at call time (the parameters stay the reference's), as
+        ``(H, 2A, D)`` views of its output."""
         types = self.pos_att_type
-        kr = qr = None
-        if ("c2p" in types) or ("p2p" in types):
-            kr = self._project_rel(rel_embeddings, use_query=False).to(dtype)
-        if ("p2c" in types) or ("p2p" in types):
-            qr = self._project_rel(rel_embeddings, use_query=True).to(dtype)
+        need_k = ("c2p" in types) or ("p2p" in types)
+        need_q = ("p2c" in types) or ("p2p" in types)
+        if need_k and need_q:
+            kl = self.key_proj if self.share_att_key else self.pos_key_proj
+            ql = self.query_proj if self.share_att_key else self.pos_query_proj
+            if kl is None or ql is None:
+                raise RuntimeError("Requested relative projection is not configured for this attention module.")
+            A, H, D = int(self.pos_ebd_size), self.num_attention_heads, self.attention_head_size
+            w = torch.cat([kl.weight, ql.weight])
+            b = torch.cat([kl.bias, ql.bias])
+            both = F.linear(rel_embeddings[: 2 * A, :], w, b).to(dtype).view(2 * A, 2, H, D)
+            return both[:, 0].permute(1, 0, 2), both[:, 1].permute(1, 0, 2)
+        kr = self._project_rel(rel_embeddings, use_query=False).to(dtype) if need_k else None
+        qr = self._project_rel(rel_embeddings, use_query=True).to(dtype) if need_q else None
         return kr, qr
 
     def disentangled_attention_bias(

@@ -9,9 +9,11 @@
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
+#include <type_traits>
 #include <string>
 
 #include "../../include/dsa.h"
+#include "../../include/dsa_block.h"
 #include "dsa_bias.h"
 #include "dsa_bwd.h"
 #include "dsa_bwd_dkdv.h"
@@ -19,6 +21,7 @@
 #include "dsa_bwd_table.h"
 #include "dsa_order.h"
 #include "dsa_fwd.h"
+#include "dsa_rows.h"
 
 // Library-owned scratch of dsa_fwd_static: the launch order's cost and
 // order arrays for up to 65536 (batch row, query tile) items, 512 KiB, one
@@ -488,6 +491,164 @@ int run_fwd(const dsa_fwd_args* a, int* order_buf, hipStream_t st) {
   return a->D == 64 ? fwd_mask<float, 64>(p, mode, st) : fwd_mask<float, 32>(p, mode, st);
 }
 
+// ---- fused row kernels (include/dsa_block.h) ------------------------------------------------
+bool dtype_ok(int dt) { return dt == DSA_F32 || dt == DSA_BF16; }
+
+// a tensor read or written in 4-element vectors along rows: base aligned to
+// four elements, row stride a multiple of four
+bool rows_ok(const void* p, int64_t stride, int dt) {
+  const uintptr_t a = 4u * (uintptr_t)elem_bytes(dt);
+  return p && (reinterpret_cast<uintptr_t>(p) % a) == 0 && stride % 4 == 0;
+}
+bool vec_ok(const void* p, int dt) { return !p || (reinterpret_cast<uintptr_t>(p) % (4u * (uintptr_t)elem_bytes(dt))) == 0; }
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+int reduce_cols(const float* part, int64_t nparts, int64_t stride, int K, int nout, const int64_t* off, void* const* out,
+                int dt, hipStream_t st) {
+  dsa::rows::ReduceCols rc;
+  rc.part = part;
+  rc.nparts = nparts;
+  rc.stride = stride;
+  rc.K = K;
+  rc.nout = nout;
+  for (int j = 0; j < 3; ++j) {
+    rc.off[j] = j < nout ? off[j] : 0;
+    rc.out[j] = j < nout ? out[j] : nullptr;
+  }
+  rc.dt = dt;
+  hipLaunchKernelGGL(dsa::rows::reduce_cols_kernel, dim3((unsigned)cdiv(K, 64), (unsigned)nout), dim3(64 * dsa::rows::RED_W), 0,
+                     st, rc);
+  return launch_check("reduce_cols_kernel");
+}
+
+int check_ln(const dsa_ln_args* a, bool bwd) {
+  if (!a) return fail("dsa: null arguments");
+  if (a->N < 1 || a->C < 4 || a->C % 4 || a->C > 2048)
+    return fail("dsa_add_ln: N >= 1 and C a multiple of 4 in [4, 2048] required, got N=%lld C=%d", (long long)a->N, a->C);
+  if (!dtype_ok(a->x_dtype) || !dtype_ok(a->param_dtype) || (a->res && !dtype_ok(a->res_dtype)))
+    return fail("dsa_add_ln: unsupported dtype");
+  if (!rows_ok(a->x, a->x_stride, a->x_dtype)) return fail("dsa_add_ln: x must be aligned to 4 elements with a row stride a multiple of 4");
+  if (!a->gamma || !a->beta || !vec_ok(a->gamma, a->param_dtype) || !vec_ok(a->beta, a->param_dtype) || !vec_ok(a->bias, a->param_dtype))
+    return fail("dsa_add_ln: gamma and beta (and bias) must be given and aligned to 4 elements");
+  if (a->res && (a->rows_per_group < 1 || !vec_ok(a->res, a->res_dtype) || a->res_strides[0] % 4 || a->res_strides[1] % 4))
+    return fail("dsa_add_ln: res needs rows_per_group >= 1, 4-element alignment and strides multiples of 4");
+  if (!a->mean || !a->rstd) return fail("dsa_add_ln: mean and rstd are required");
+  if (!bwd) {
+    if (!dtype_ok(a->y_dtype) || !rows_ok(a->y, a->y_stride, a->y_dtype)) return fail("dsa_add_ln: bad y");
+    return 0;
+  }
+  if (!dtype_ok(a->dy_dtype) || !rows_ok(a->dy, a->dy_stride, a->dy_dtype)) return fail("dsa_add_ln: bad dy");
+  if (a->dz_dtype != a->x_dtype || !rows_ok(a->dz, a->dz_stride, a->dz_dtype)) return fail("dsa_add_ln: bad dz (x's dtype)");
+  const size_t need = dsa_block_workspace_bytes(DSA_BLOCK_LN, a->N, a->C);
+  if (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace))
+    return fail("dsa_add_ln: workspace of %zu bytes (16-byte aligned) required", need);
+  return 0;
+}
+
+dsa::rows::LnParams ln_params(const dsa_ln_args* a) {
+  dsa::rows::LnParams p;
+  p.x = a->x;
+  p.bias = a->bias;
+  p.res = a->res;
+  p.gamma = a->gamma;
+  p.beta = a->beta;
+  p.dy = a->dy;
+  p.y = a->y;
+  p.dz = a->dz;
+  p.dgamma = a->dgamma;
+  p.dbeta = a->dbeta;
+  p.dbias = a->dbias;
+  p.mean = a->mean;
+  p.rstd = a->rstd;
+  p.part = static_cast<float*>(a->workspace);
+  p.xs = a->x_stride;
+  p.rs0 = a->res_strides[0];
+  p.rs1 = a->res_strides[1];
+  p.rpg = a->res ? a->rows_per_group : 1;
+  p.ys = a->y_stride;
+  p.dys = a->dy_stride;
+  p.dzs = a->dz_stride;
+  p.N = a->N;
+  p.C = a->C;
+  p.pdt = a->param_dtype;
+  p.eps = a->eps;
+  return p;
+}
+
+int check_gelu(const dsa_gelu_args* a, bool bwd) {
+  if (!a) return fail("dsa: null arguments");
+  if (a->N < 1 || a->C < 4 || a->C % 4) return fail("dsa_bias_gelu: N >= 1 and C a multiple of 4 required");
+  if (!dtype_ok(a->x_dtype) || !dtype_ok(a->param_dtype)) return fail("dsa_bias_gelu: unsupported dtype");
+  if (!rows_ok(a->x, a->x_stride, a->x_dtype) || !vec_ok(a->bias, a->param_dtype)) return fail("dsa_bias_gelu: bad x or bias");
+  if (!bwd) return (!dtype_ok(a->y_dtype) || !rows_ok(a->y, a->y_stride, a->y_dtype)) ? fail("dsa_bias_gelu: bad y") : 0;
+  if (!dtype_ok(a->dy_dtype) || !rows_ok(a->dy, a->dy_stride, a->dy_dtype)) return fail("dsa_bias_gelu: bad dy");
+  if (a->dz_dtype != a->x_dtype || !rows_ok(a->dz, a->dz_stride, a->dz_dtype)) return fail("dsa_bias_gelu: bad dz (x's dtype)");
+  const size_t need = dsa_block_workspace_bytes(DSA_BLOCK_GELU, a->N, a->C);
+  if (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace))
+    return fail("dsa_bias_gelu: workspace of %zu bytes (16-byte aligned) required", need);
+  return 0;
+}
+
+dsa::rows::GeluParams gelu_params(const dsa_gelu_args* a) {
+  dsa::rows::GeluParams p;
+  p.x = a->x;
+  p.bias = a->bias;
+  p.dy = a->dy;
+  p.y = a->y;
+  p.dz = a->dz;
+  p.dbias = a->dbias;
+  p.part = static_cast<float*>(a->workspace);
+  p.xs = a->x_stride;
+  p.ys = a->y_stride;
+  p.dys = a->dy_stride;
+  p.dzs = a->dz_stride;
+  p.N = a->N;
+  p.C = a->C;
+  p.pdt = a->param_dtype;
+  return p;
+}
+
+int check_rtd(const dsa_rtd_args* a, bool bwd) {
+  if (!a) return fail("dsa: null arguments");
+  if (a->N < 1 || a->C < 4 || a->C % 4 || a->C > 2048)
+    return fail("dsa_rtd_loss: N >= 1 and C a multiple of 4 in [4, 2048] required");
+  if (!dtype_ok(a->x_dtype) || !dtype_ok(a->param_dtype)) return fail("dsa_rtd_loss: unsupported dtype");
+  if (!rows_ok(a->x, a->x_stride, a->x_dtype) || !a->w || !vec_ok(a->w, a->param_dtype) || !a->labels)
+    return fail("dsa_rtd_loss: x, w and labels are required (x and w aligned to 4 elements)");
+  if (!a->logits || !a->denom) return fail("dsa_rtd_loss: logits and denom are required");
+  const size_t need = dsa_block_workspace_bytes(DSA_BLOCK_RTD, a->N, a->C);
+  if (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace))
+    return fail("dsa_rtd_loss: workspace of %zu bytes (16-byte aligned) required", need);
+  if (!bwd) return a->loss ? 0 : fail("dsa_rtd_loss: loss is required");
+  if (!a->dloss || !a->dw) return fail("dsa_rtd_loss: dloss and dw are required");
+  if (!dtype_ok(a->dx_dtype) || !rows_ok(a->dx, a->dx_stride, a->dx_dtype)) return fail("dsa_rtd_loss: bad dx");
+  return 0;
+}
+
+dsa::rows::RtdParams rtd_params(const dsa_rtd_args* a) {
+  dsa::rows::RtdParams p;
+  p.x = a->x;
+  p.w = a->w;
+  p.b = a->b;
+  p.labels = a->labels;
+  p.active = a->active;
+  p.logits = a->logits;
+  p.loss = a->loss;
+  p.denom = a->denom;
+  p.part = static_cast<float*>(a->workspace);
+  p.dloss = a->dloss;
+  p.dx = a->dx;
+  p.dw = a->dw;
+  p.db = a->db;
+  p.xs = a->x_stride;
+  p.dxs = a->dx_stride;
+  p.N = a->N;
+  p.C = a->C;
+  p.pdt = a->param_dtype;
+  return p;
+}
+
 }  // namespace
 
 extern "C" {
@@ -647,6 +808,168 @@ int dsa_bwd(const dsa_bwd_args* a, void* stream) {
     return f.D == 64 ? launch_bwd<dsa::bf16, 64>(a, ws, mode, st) : launch_bwd<dsa::bf16, 32>(a, ws, mode, st);
   }
   return f.D == 64 ? launch_bwd<float, 64>(a, ws, mode, st) : launch_bwd<float, 32>(a, ws, mode, st);
+}
+
+}  // extern "C"
+
+namespace {
+// Calls f(std::integral_constant<int, NC>) for NC = ceil(C / 256), the
+// 4-element chunks a lane holds in the row kernels (C <= 2048 is checked
+// before).
+template <typename F>
+void by_chunks(int C, F f) {
+  switch (cdiv(C, 256)) {
+    case 1: f(std::integral_constant<int, 1>{}); break;
+    case 2: f(std::integral_constant<int, 2>{}); break;
+    case 3: f(std::integral_constant<int, 3>{}); break;
+    case 4: f(std::integral_constant<int, 4>{}); break;
+    case 5:
+    case 6: f(std::integral_constant<int, 6>{}); break;
+    default: f(std::integral_constant<int, 8>{}); break;
+  }
+}
+
+template <typename T>
+struct Tag {
+  typedef T type;
+};
+// Calls f(Tag<element type>) for a row tensor's dtype (DSA_BF16 or DSA_F32).
+template <typename F>
+void by_dtype(int dt, F f) {
+  if (dt == DSA_BF16) f(Tag<dsa::bf16>{});
+  else f(Tag<float>{});
+}
+}  // namespace
+
+extern "C" {
+
+size_t dsa_block_workspace_bytes(int kind, int64_t N, int32_t C) {
+  if (N < 1 || C < 1) return 0;
+  switch (kind) {
+    case DSA_BLOCK_LN: return align_up((size_t)cdiv(N, dsa::rows::LN_RB) * 3 * C * sizeof(float), 256);
+    case DSA_BLOCK_GELU: return align_up((size_t)cdiv(N, dsa::rows::GELU_RB) * C * sizeof(float), 256);
+    case DSA_BLOCK_RTD: {
+      const int64_t nb = cdiv(N, dsa::rows::RTD_RB);
+      return align_up((size_t)nb * (size_t)std::max<int64_t>(2, C + 1) * sizeof(float), 256);
+    }
+    default: return 0;
+  }
+}
+
+int dsa_add_ln_fwd(const dsa_ln_args* a, void* stream) {
+  g_err.clear();
+  if (check_ln(a, false)) return 1;
+  const dsa::rows::LnParams p = ln_params(a);
+  by_chunks(a->C, [&](auto nc) {
+    by_dtype(a->x_dtype, [&](auto tx) {
+      by_dtype(a->res ? a->res_dtype : a->x_dtype, [&](auto tr) {
+        by_dtype(a->y_dtype, [&](auto ty) {
+          auto k = dsa::rows::ln_fwd_kernel<decltype(nc)::value, typename decltype(tx)::type, typename decltype(tr)::type,
+                                            typename decltype(ty)::type>;
+          hipLaunchKernelGGL(k, dim3((unsigned)cdiv(a->N, 4)), dim3(256), 0, static_cast<hipStream_t>(stream), p);
+        });
+      });
+    });
+  });
+  return launch_check("ln_fwd_kernel");
+}
+
+int dsa_add_ln_bwd(const dsa_ln_args* a, void* stream) {
+  g_err.clear();
+  if (check_ln(a, true)) return 1;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dsa::rows::LnParams p = ln_params(a);
+  const int64_t nb = cdiv(a->N, dsa::rows::LN_RB);
+  by_chunks(a->C, [&](auto nc) {
+    by_dtype(a->x_dtype, [&](auto tx) {
+      by_dtype(a->res ? a->res_dtype : a->x_dtype, [&](auto tr) {
+        by_dtype(a->dy_dtype, [&](auto tdy) {
+          auto k = dsa::rows::ln_bwd_kernel<decltype(nc)::value, typename decltype(tx)::type, typename decltype(tr)::type,
+                                            typename decltype(tdy)::type>;
+          hipLaunchKernelGGL(k, dim3((unsigned)nb), dim3(256), 0, st, p);
+        });
+      });
+    });
+  });
+  if (launch_check("ln_bwd_kernel")) return 1;
+  const int64_t off[3] = {0, a->C, 2 * (int64_t)a->C};
+  void* const out[3] = {a->dgamma, a->dbeta, a->dbias};
+  return reduce_cols(p.part, nb, 3 * (int64_t)a->C, a->C, 3, off, out, a->param_dtype, st);
+}
+
+int dsa_bias_gelu_fwd(const dsa_gelu_args* a, void* stream) {
+  g_err.clear();
+  if (check_gelu(a, false)) return 1;
+  const dsa::rows::GeluParams p = gelu_params(a);
+  if (cdiv(a->N, dsa::rows::GELU_RB) > 65535)
+    return fail("dsa_bias_gelu: N too large (%lld rows, at most %d)", (long long)a->N, 65535 * dsa::rows::GELU_RB);
+  by_dtype(a->x_dtype, [&](auto tx) {
+    by_dtype(a->y_dtype, [&](auto ty) {
+      auto k = dsa::rows::gelu_fwd_kernel<typename decltype(tx)::type, typename decltype(ty)::type>;
+      hipLaunchKernelGGL(k, dim3((unsigned)cdiv(a->C / 4, 256), (unsigned)cdiv(a->N, dsa::rows::GELU_RB)), dim3(256), 0,
+                         static_cast<hipStream_t>(stream), p);
+    });
+  });
+  return launch_check("gelu_fwd_kernel");
+}
+
+int dsa_bias_gelu_bwd(const dsa_gelu_args* a, void* stream) {
+  g_err.clear();
+  if (check_gelu(a, true)) return 1;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dsa::rows::GeluParams p = gelu_params(a);
+  const int64_t nb = cdiv(a->N, dsa::rows::GELU_RB);
+  if (nb > 65535) return fail("dsa_bias_gelu: N too large (%lld rows, at most %d)", (long long)a->N, 65535 * dsa::rows::GELU_RB);
+  by_dtype(a->x_dtype, [&](auto tx) {
+    by_dtype(a->dy_dtype, [&](auto tdy) {
+      auto k = dsa::rows::gelu_bwd_kernel<typename decltype(tx)::type, typename decltype(tdy)::type>;
+      hipLaunchKernelGGL(k, dim3((unsigned)cdiv(a->C / 4, 256), (unsigned)nb), dim3(256), 0, st, p);
+    });
+  });
+  if (launch_check("gelu_bwd_kernel")) return 1;
+  if (!a->dbias) return 0;
+  const int64_t off[1] = {0};
+  void* const out[1] = {a->dbias};
+  return reduce_cols(p.part, nb, a->C, a->C, 1, off, out, a->param_dtype, st);
+}
+
+int dsa_rtd_loss_fwd(const dsa_rtd_args* a, void* stream) {
+  g_err.clear();
+  if (check_rtd(a, false)) return 1;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dsa::rows::RtdParams p = rtd_params(a);
+  const int64_t nb = cdiv(a->N, dsa::rows::RTD_RB);
+  by_chunks(a->C, [&](auto nc) {
+    by_dtype(a->x_dtype, [&](auto tx) {
+      auto k = dsa::rows::rtd_fwd_kernel<decltype(nc)::value, typename decltype(tx)::type>;
+      hipLaunchKernelGGL(k, dim3((unsigned)nb), dim3(256), 0, st, p);
+    });
+  });
+  if (launch_check("rtd_fwd_kernel")) return 1;
+  hipLaunchKernelGGL(dsa::rows::rtd_loss_kernel, dim3(1), dim3(64), 0, st, p, (int)nb);
+  return launch_check("rtd_loss_kernel");
+}
+
+int dsa_rtd_loss_bwd(const dsa_rtd_args* a, void* stream) {
+  g_err.clear();
+  if (check_rtd(a, true)) return 1;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dsa::rows::RtdParams p = rtd_params(a);
+  const int64_t nb = cdiv(a->N, dsa::rows::RTD_RB);
+  by_chunks(a->C, [&](auto nc) {
+    by_dtype(a->x_dtype, [&](auto tx) {
+      by_dtype(a->dx_dtype, [&](auto tdx) {
+        auto k = dsa::rows::rtd_bwd_kernel<decltype(nc)::value, typename decltype(tx)::type, typename decltype(tdx)::type>;
+        hipLaunchKernelGGL(k, dim3((unsigned)nb), dim3(256), 0, st, p);
+      });
+    });
+  });
+  if (launch_check("rtd_bwd_kernel")) return 1;
+  const int64_t off_w[1] = {0}, off_b[1] = {a->C};
+  void* const out_w[1] = {a->dw};
+  void* const out_b[1] = {a->db};
+  if (reduce_cols(p.part, nb, a->C + 1, a->C, 1, off_w, out_w, a->param_dtype, st)) return 1;
+  return a->db ? reduce_cols(p.part, nb, a->C + 1, 1, 1, off_b, out_b, a->param_dtype, st) : 0;
 }
 
 }  // extern "C"

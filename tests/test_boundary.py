@@ -395,3 +395,90 @@ def test_deterministic_mode_alerts_on_table_gradients():
         ops._alert_nondeterministic_tables()
     finally:
         torch.use_deterministic_algorithms(prev, warn_only=prev_warn)
+
+
+# --- the fused row kernels around the attention (include/dsa_block.h) ---------------------
+BLOCK_HEADER = ROOT / "include" / "dsa_block.h"
+
+
+def test_block_header_matches_the_exports(lib):
+    text = re.sub(r"/\*.*?\*/", "", BLOCK_HEADER.read_text(), flags=re.S)
+    declared = sorted(set(re.findall(r"\b(dsa_[a-z_]+)\s*\([^;{]*\)\s*;", text)))
+    assert declared == sorted(_lib.BLOCK_EXPORTS)
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def test_block_structs_match_the_c_header(tmp_path):
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    structs = (("dsa_ln_args", _lib.DsaLnArgs), ("dsa_gelu_args", _lib.DsaGeluArgs), ("dsa_rtd_args", _lib.DsaRtdArgs))
+    lines = [f'printf("{c} %zu\\n", sizeof({c}));' for c, _ in structs]
+    for cname, st in structs:
+        for fname, _ in st._fields_:
+            lines.append(f"F({cname}, {fname})")
+    src = tmp_path / "probe.c"
+    src.write_text(
+        '#include <stdio.h>\n#include <stddef.h>\n#include "dsa_block.h"\n'
+        '#define F(s, f) printf(#s "." #f " %zu\\n", offsetof(s, f));\n'
+        "int main(void) {\n  " + "\n  ".join(lines) + "\n  return 0;\n}\n"
+    )
+    exe = tmp_path / "probe"
+    subprocess.run([gcc, "-std=c99", "-I", str(BLOCK_HEADER.parent), str(src), "-o", str(exe)], check=True)
+    out = dict(l.rsplit(" ", 1) for l in subprocess.run([str(exe)], capture_output=True, text=True).stdout.splitlines())
+    for cname, st in structs:
+        assert int(out[cname]) == ctypes.sizeof(st), cname
+        for fname, _ in st._fields_:
+            assert int(out[f"{cname}.{fname}"]) == getattr(st, fname).offset, (cname, fname)
+
+
+def test_block_argument_errors(lib):
+    a = _lib.DsaLnArgs()
+    assert lib.dsa_add_ln_fwd(ctypes.byref(a), None) != 0
+    assert "dsa_add_ln" in _lib.last_error()
+    a.N, a.C = 4, 4098
+    assert lib.dsa_add_ln_fwd(ctypes.byref(a), None) != 0
+    assert "multiple of 4 in [4, 2048]" in _lib.last_error()
+    r = _lib.DsaRtdArgs()
+    r.N, r.C = 8, 64
+    assert lib.dsa_rtd_loss_fwd(ctypes.byref(r), None) != 0
+    assert "x, w and labels are required" in _lib.last_error()
+    assert lib.dsa_block_workspace_bytes(_lib.DSA_BLOCK_LN, 8192, 768) >= 256 * 3 * 768 * 4
+
+
+def test_block_ops_fake_shapes_and_cpu_refusal():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    import deberta_amd.blocks  # noqa: F401  (registers the ops)
+
+    with FakeTensorMode():
+        x = torch.randn(2, 8, 64, dtype=torch.bfloat16)
+        w, b = torch.randn(64), torch.randn(64)
+        y, mean, rstd = torch.ops.deberta_amd.add_ln(x, b, x.float(), w, b, 1e-7, torch.float32)
+        assert y.shape == x.shape and y.dtype == torch.float32 and mean.shape == (16,)
+        assert torch.ops.deberta_amd.bias_gelu(x, b.bfloat16()).shape == x.shape
+        loss, logits, denom = torch.ops.deberta_amd.rtd_loss(x, w, b[:1], torch.ones(2, 8), None)
+        assert loss.shape == () and logits.shape == (2, 8)
+    with pytest.raises(NotImplementedError):
+        torch.ops.deberta_amd.bias_gelu(torch.randn(2, 64), None)
+
+
+def test_fused_blocks_take_the_reference_state_dicts():
+    from deberta_amd import FusedIntermediate, FusedOutput, FusedRTDHead, FusedSelfOutput, RelativeEmbeddings
+    from oracle import blocks as ob
+
+    cfg = eager.make_config(hidden_size=64, num_attention_heads=4, intermediate_size=256, layer_norm_eps=1e-7)
+    for ours, ref in (
+        (FusedSelfOutput(cfg), ob.OutputResidualNorm(cfg)),
+        (FusedOutput(cfg), ob.OutputResidualNorm(cfg, in_features=256)),
+        (FusedIntermediate(cfg), ob.Intermediate(cfg)),
+        (FusedRTDHead(cfg), ob.RTDHead(cfg)),
+        (RelativeEmbeddings(cfg), ob.RelativeEmbeddings(cfg)),
+    ):
+        assert {k: v.shape for k, v in ours.state_dict().items()} == {k: v.shape for k, v in ref.state_dict().items()}
+        ours.load_state_dict(ref.state_dict(), strict=True)
+    with pytest.raises(RuntimeError, match="GPU"):
+        FusedSelfOutput(cfg)(torch.randn(1, 4, 64), torch.randn(1, 4, 64))
+    with pytest.raises(NotImplementedError, match="gelu"):
+        FusedIntermediate(eager.make_config(hidden_size=64, intermediate_size=256, hidden_act="relu"))

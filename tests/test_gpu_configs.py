@@ -8,8 +8,9 @@ module; at the full B = 64 the compiled layer is compared with the same
 layer run eagerly.
 
 C3: the 12-layer encoder harness (tests/_encoder.py) with the fused module
-in every layer.  At B = 2 in fp32 it is compared with the same encoder
-built on the oracle module on the CPU (identical weights, ids and labels);
+in every layer and the fused row kernels around it.  At B = 2 in fp32 it is
+compared with the same encoder built on the oracle module and plain torch
+blocks on the CPU (identical weights, ids and labels);
 at the full B = 16 under bf16 autocast, fwd + bwd of the RTD loss must give
 a finite loss and finite gradients.
 
@@ -88,9 +89,11 @@ def test_c5_compiled_full_size_equals_eager(gpu):
 
 
 def _encoder_pair(layers):
+    """The oracle encoder (oracle attention, plain torch blocks) and the
+    fused one (fused attention and fused row kernels), same weights."""
     ref = _encoder.Encoder(eager.EagerDisentangledSelfAttention, layers=layers)
     _encoder.init_weights(ref, seed=3)
-    ours = _encoder.Encoder(DisentangledSelfAttention, layers=layers)
+    ours = _encoder.Encoder(DisentangledSelfAttention, layers=layers, fused_blocks=True)
     ours.load_state_dict(ref.state_dict(), strict=True)
     return ref, ours
 
@@ -98,16 +101,16 @@ def _encoder_pair(layers):
 def _encoder_step(model, ids, labels, rel_pos, mask, autocast=False):
     dev = ids.device
     with torch.autocast(dev.type, dtype=torch.bfloat16, enabled=autocast):
-        logits = model(ids, mask, rel_pos)
-    loss = _encoder.rtd_loss(logits, labels)
+        loss, logits = model.loss(ids, mask, rel_pos, labels)
     names = [n for n, _ in model.named_parameters()]
     grads = torch.autograd.grad(loss, [p for _, p in model.named_parameters()])
     return logits.detach().float().cpu(), loss.detach().float().cpu(), {n: g.float().cpu() for n, g in zip(names, grads)}
 
 
 def test_c3_encoder_fp32_against_oracle(gpu):
-    """C3 encoder (12 layers), B = 2, fp32: the fused module against the
-    oracle module, logits, loss and every parameter gradient."""
+    """C3 encoder (12 layers), B = 2, fp32: the fused attention and fused
+    blocks against the oracle attention and plain torch blocks, logits,
+    loss and every parameter gradient."""
     ref, ours = _encoder_pair(_encoder.LAYERS)
     ours = ours.to(gpu)
     ids, labels = _encoder.synthetic_batch(2, 512, seed=1)
@@ -117,7 +120,7 @@ def test_c3_encoder_fp32_against_oracle(gpu):
     lb, sb, gb = _encoder_step(ours, ids.to(gpu), labels.to(gpu), rp_c.to(gpu), mask.to(gpu))
     errs = {"logits": max_rel(lb, la), "loss": max_rel(sb, sa)}
     for n in ga:
-        if n.endswith("attn.key_proj.bias"):
+        if n.endswith("self.key_proj.bias"):
             # mostly cancelling (a shift of every key is a per-row constant
             # in the content and c2p terms), so compared on the scale of
             # the matching weight gradient
@@ -135,7 +138,7 @@ def test_c3_encoder_full_size_bf16(gpu):
     """C3 at its full size (B = 16, L = 512, bf16 autocast): forward and
     backward of the RTD loss give a finite loss near ln 2 (random init) and
     finite gradients for every parameter."""
-    model = _encoder.Encoder(DisentangledSelfAttention)
+    model = _encoder.Encoder(DisentangledSelfAttention, fused_blocks=True)
     _encoder.init_weights(model, seed=0)
     model = model.to(gpu)
     ids, labels = _encoder.synthetic_batch(16, 512, seed=0)
