@@ -20,7 +20,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from deberta_amd import ops  # noqa: F401  (registers the custom ops)
+from deberta_amd import ops
 from deberta_amd.config import normalize_attention_kernel, normalize_pos_att_type
 from deberta_amd.masks import SegmentMask, kernel_masks, normalize_keep_mask
 from deberta_amd.relpos import (
@@ -161,9 +161,7 @@ def fused_attention(
     save_bias = torch.is_grad_enabled() and any(
         t is not None and t.requires_grad for t in (q, k, v, kr, qr, qc)
     )
-    out, _, _ = torch.ops.deberta_amd.dsa_fwd(
-        q, k, v, kr, qr, table, key_keep, pair_keep, int(att_span), float(scale), save_bias, qc
-    )
+    out, _, _ = ops.attention(q, k, v, kr, qr, table, key_keep, pair_keep, int(att_span), float(scale), save_bias, qc)
     return out
 
 

@@ -35,7 +35,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 from torch import Tensor
 
-from deberta_amd import _lib
+from deberta_amd import _eager, _lib
 
 _DT = {torch.float32: _lib.DSA_F32, torch.bfloat16: _lib.DSA_BF16}
 
@@ -55,7 +55,7 @@ def _rows(t: Tensor) -> Tensor:
 
 
 def _stream(t: Tensor) -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+    return ctypes.c_void_p(_eager.stream_ptr(t))
 
 
 def _ptr(t: Optional[Tensor]) -> Optional[int]:
@@ -88,8 +88,7 @@ def _res_layout(res: Tensor, x: Tensor) -> tuple[Tensor, int, int, int]:
     return res, 0, res.stride(0), res.shape[0]
 
 
-@torch.library.custom_op("deberta_amd::add_ln", mutates_args=(), device_types="cuda")
-def add_ln(
+def _add_ln_impl(
     x: Tensor,
     bias: Optional[Tensor],
     res: Optional[Tensor],
@@ -128,14 +127,16 @@ def add_ln(
     return y, mean, rstd
 
 
+add_ln = torch.library.custom_op("deberta_amd::add_ln", _add_ln_impl, mutates_args=(), device_types="cuda")
+
+
 @add_ln.register_fake
 def _add_ln_fake(x, bias, res, gamma, beta, eps, out_dtype):
     N = x.numel() // x.shape[-1]
     return x.new_empty(x.shape, dtype=out_dtype), x.new_empty((N,), dtype=torch.float32), x.new_empty((N,), dtype=torch.float32)
 
 
-@torch.library.custom_op("deberta_amd::add_ln_bwd", mutates_args=(), device_types="cuda")
-def add_ln_bwd(
+def _add_ln_bwd_impl(
     dy: Tensor,
     x: Tensor,
     bias: Optional[Tensor],
@@ -178,6 +179,9 @@ def add_ln_bwd(
     return dz, dgamma, dbeta, dbias
 
 
+add_ln_bwd = torch.library.custom_op("deberta_amd::add_ln_bwd", _add_ln_bwd_impl, mutates_args=(), device_types="cuda")
+
+
 @add_ln_bwd.register_fake
 def _add_ln_bwd_fake(dy, x, bias, res, gamma, mean, rstd, dz_dtype):
     return (
@@ -198,7 +202,7 @@ def _add_ln_setup(ctx, inputs, output):
 
 def _add_ln_backward(ctx, dy, dmean, drstd):
     x, bias, res, gamma, mean, rstd = ctx.saved_tensors
-    dz, dgamma, dbeta, dbias = add_ln_bwd(dy, x, bias, res, gamma, mean, rstd, x.dtype)
+    dz, dgamma, dbeta, dbias = _eager.on_eager(ctx, add_ln_bwd, _add_ln_bwd_impl)(dy, x, bias, res, gamma, mean, rstd, x.dtype)
     dres = None
     if ctx.has_res:
         dres = dz if res.dtype == dz.dtype else dz.to(res.dtype)
@@ -206,6 +210,15 @@ def _add_ln_backward(ctx, dy, dmean, drstd):
 
 
 torch.library.register_autograd("deberta_amd::add_ln", _add_ln_backward, setup_context=_add_ln_setup)
+_AddLnFunction = _eager.function("_AddLnFunction", _add_ln_impl, _add_ln_setup, _add_ln_backward)
+
+
+def call_add_ln(x, bias, res, gamma, beta, eps: float, out_dtype: torch.dtype):
+    """``deberta_amd::add_ln`` with its autograd (the implementation in a
+    torch.autograd.Function in plain eager mode, the op otherwise)."""
+    if _eager.eager(x):
+        return _AddLnFunction.apply(x, bias, res, gamma, beta, eps, out_dtype)
+    return torch.ops.deberta_amd.add_ln(x, bias, res, gamma, beta, eps, out_dtype)
 
 
 def _ln_out_dtype(x: Tensor, res: Optional[Tensor]) -> torch.dtype:
@@ -223,7 +236,7 @@ def fused_add_layer_norm(
     the last dim, with affine parameters)."""
     if ln.weight is None or ln.bias is None:
         raise ValueError("fused_add_layer_norm needs an affine LayerNorm")
-    y, _, _ = torch.ops.deberta_amd.add_ln(x, bias, res, ln.weight, ln.bias, float(ln.eps), _ln_out_dtype(x, res))
+    y, _, _ = call_add_ln(x, bias, res, ln.weight, ln.bias, float(ln.eps), _ln_out_dtype(x, res))
     return y
 
 
@@ -231,8 +244,7 @@ def fused_add_layer_norm(
 # bias + GELU
 
 
-@torch.library.custom_op("deberta_amd::bias_gelu", mutates_args=(), device_types="cuda")
-def bias_gelu(x: Tensor, bias: Optional[Tensor]) -> Tensor:
+def _bias_gelu_impl(x: Tensor, bias: Optional[Tensor]) -> Tensor:
     """``gelu(x + bias)`` (erf form) in x's dtype."""
     C = x.shape[-1]
     xr = _rows(x)
@@ -248,13 +260,15 @@ def bias_gelu(x: Tensor, bias: Optional[Tensor]) -> Tensor:
     return y
 
 
+bias_gelu = torch.library.custom_op("deberta_amd::bias_gelu", _bias_gelu_impl, mutates_args=(), device_types="cuda")
+
+
 @bias_gelu.register_fake
 def _bias_gelu_fake(x, bias):
     return x.new_empty(x.shape)
 
 
-@torch.library.custom_op("deberta_amd::bias_gelu_bwd", mutates_args=(), device_types="cuda")
-def bias_gelu_bwd(dy: Tensor, x: Tensor, bias: Optional[Tensor]) -> tuple[Tensor, Tensor]:
+def _bias_gelu_bwd_impl(dy: Tensor, x: Tensor, bias: Optional[Tensor]) -> tuple[Tensor, Tensor]:
     """(dz, dbias): the gradient of ``x + bias`` in x's dtype and dbias in
     the bias dtype (empty without a bias)."""
     C = x.shape[-1]
@@ -279,6 +293,9 @@ def bias_gelu_bwd(dy: Tensor, x: Tensor, bias: Optional[Tensor]) -> tuple[Tensor
     return dz, dbias
 
 
+bias_gelu_bwd = torch.library.custom_op("deberta_amd::bias_gelu_bwd", _bias_gelu_bwd_impl, mutates_args=(), device_types="cuda")
+
+
 @bias_gelu_bwd.register_fake
 def _bias_gelu_bwd_fake(dy, x, bias):
     return x.new_empty(x.shape), (bias.new_empty(bias.shape) if bias is not None else x.new_empty((0,)))
@@ -291,19 +308,27 @@ def _bias_gelu_setup(ctx, inputs, output):
 
 def _bias_gelu_backward(ctx, dy):
     x, bias = ctx.saved_tensors
-    dz, dbias = bias_gelu_bwd(dy, x, bias)
+    dz, dbias = _eager.on_eager(ctx, bias_gelu_bwd, _bias_gelu_bwd_impl)(dy, x, bias)
     return dz, (dbias if bias is not None else None)
 
 
 torch.library.register_autograd("deberta_amd::bias_gelu", _bias_gelu_backward, setup_context=_bias_gelu_setup)
+_BiasGeluFunction = _eager.function("_BiasGeluFunction", _bias_gelu_impl, _bias_gelu_setup, _bias_gelu_backward)
+
+
+def call_bias_gelu(x: Tensor, bias: Optional[Tensor]) -> Tensor:
+    """``deberta_amd::bias_gelu`` with its autograd (eager: the
+    implementation in a torch.autograd.Function)."""
+    if _eager.eager(x):
+        return _BiasGeluFunction.apply(x, bias)
+    return torch.ops.deberta_amd.bias_gelu(x, bias)
 
 
 # ---------------------------------------------------------------------------
 # RTD classifier + BCE
 
 
-@torch.library.custom_op("deberta_amd::rtd_loss", mutates_args=(), device_types="cuda")
-def rtd_loss(
+def _rtd_loss_impl(
     x: Tensor, w: Tensor, b: Optional[Tensor], labels: Tensor, active: Optional[Tensor]
 ) -> tuple[Tensor, Tensor, Tensor]:
     """(loss, logits, denom): ``logits = x @ w + b`` per row (float32) and
@@ -332,6 +357,9 @@ def rtd_loss(
     return loss, logits.view(x.shape[:-1]), denom
 
 
+rtd_loss = torch.library.custom_op("deberta_amd::rtd_loss", _rtd_loss_impl, mutates_args=(), device_types="cuda")
+
+
 @rtd_loss.register_fake
 def _rtd_loss_fake(x, w, b, labels, active):
     return (
@@ -341,8 +369,7 @@ def _rtd_loss_fake(x, w, b, labels, active):
     )
 
 
-@torch.library.custom_op("deberta_amd::rtd_loss_bwd", mutates_args=(), device_types="cuda")
-def rtd_loss_bwd(
+def _rtd_loss_bwd_impl(
     dloss: Tensor, x: Tensor, w: Tensor, b: Optional[Tensor], labels: Tensor, active: Optional[Tensor],
     logits: Tensor, denom: Tensor,
 ) -> tuple[Tensor, Tensor, Tensor]:
@@ -375,6 +402,9 @@ def rtd_loss_bwd(
     return dx, dw, db
 
 
+rtd_loss_bwd = torch.library.custom_op("deberta_amd::rtd_loss_bwd", _rtd_loss_bwd_impl, mutates_args=(), device_types="cuda")
+
+
 @rtd_loss_bwd.register_fake
 def _rtd_loss_bwd_fake(dloss, x, w, b, labels, active, logits, denom):
     return x.new_empty(x.shape), w.new_empty(w.shape), (b.new_empty(b.shape) if b is not None else w.new_empty((0,)))
@@ -392,11 +422,20 @@ def _rtd_backward(ctx, dloss, dlogits, ddenom):
     x, w, b, labels, active, logits, denom = ctx.saved_tensors
     if dloss is None:
         return None, None, None, None, None
-    dx, dw, db = rtd_loss_bwd(dloss, x, w, b, labels, active, logits, denom)
+    dx, dw, db = _eager.on_eager(ctx, rtd_loss_bwd, _rtd_loss_bwd_impl)(dloss, x, w, b, labels, active, logits, denom)
     return dx, dw, (db if b is not None else None), None, None
 
 
 torch.library.register_autograd("deberta_amd::rtd_loss", _rtd_backward, setup_context=_rtd_setup)
+_RtdLossFunction = _eager.function("_RtdLossFunction", _rtd_loss_impl, _rtd_setup, _rtd_backward)
+
+
+def call_rtd_loss(x: Tensor, w: Tensor, b: Optional[Tensor], labels: Tensor, active: Optional[Tensor]):
+    """``deberta_amd::rtd_loss`` with its autograd (eager: the
+    implementation in a torch.autograd.Function)."""
+    if _eager.eager(x):
+        return _RtdLossFunction.apply(x, w, b, labels, active)
+    return torch.ops.deberta_amd.rtd_loss(x, w, b, labels, active)
 
 
 # ---------------------------------------------------------------------------
@@ -460,7 +499,7 @@ class FusedIntermediate(nn.Module):
         bias = self.dense.bias
         if bias is not None:
             bias = bias.to(x.dtype)
-        return torch.ops.deberta_amd.bias_gelu(x, bias)
+        return call_bias_gelu(x, bias)
 
 
 class FusedRTDHead(nn.Module):
@@ -505,7 +544,7 @@ class FusedRTDHead(nn.Module):
         bias = self.dense.bias
         if bias is not None:
             bias = bias.to(x.dtype)
-        return torch.ops.deberta_amd.bias_gelu(x, bias)
+        return call_bias_gelu(x, bias)
 
     def forward(self, hidden_states: Tensor, attention_mask: Optional[Tensor] = None) -> Tensor:
         """Per-token logits ``(B, S)``."""
@@ -526,7 +565,7 @@ class FusedRTDHead(nn.Module):
         b = self.classifier.bias
         if b is not None:
             b = b.to(w.dtype)
-        loss, logits, _ = torch.ops.deberta_amd.rtd_loss(x, w, b, labels, active)
+        loss, logits, _ = call_rtd_loss(x, w, b, labels, active)
         return loss, logits
 
 

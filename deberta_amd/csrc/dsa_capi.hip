@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -248,10 +249,14 @@ int fwd_mask(const dsa::FwdParams& p, int mode, hipStream_t st) {
   }
 }
 
+// Compute units of the current device (queried once per device).
 int device_cus() {
+  static std::atomic<int> cached[16] = {};
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (dev >= 0 && dev < 16 && (cus = cached[dev].load(std::memory_order_relaxed)) > 0) return cus;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return 256;
+  if (dev >= 0 && dev < 16) cached[dev].store(cus, std::memory_order_relaxed);
   return cus;
 }
 

@@ -33,7 +33,7 @@ from typing import Optional
 import torch
 from torch import Tensor
 
-from deberta_amd import _lib
+from deberta_amd import _eager, _lib
 
 _DTYPES = {torch.float32: _lib.DSA_F32, torch.bfloat16: _lib.DSA_BF16}
 
@@ -185,8 +185,7 @@ def _validate(
             raise ValueError(f"dsa: qc must match q ({tuple(q.shape)}, {q.dtype}), got {tuple(qc.shape)}, {qc.dtype}")
 
 
-@torch.library.custom_op("deberta_amd::dsa_fwd", mutates_args=(), device_types="cuda")
-def dsa_fwd(
+def _dsa_fwd_impl(
     q: Tensor,
     k: Tensor,
     v: Tensor,
@@ -222,9 +221,11 @@ def dsa_fwd(
     ws = torch.empty((nws,), dtype=torch.uint8, device=q.device) if nws else None
     if ws is not None:
         args.workspace, args.workspace_bytes = ws.data_ptr(), nws
-    stream = torch.cuda.current_stream(q.device).cuda_stream
-    _lib.check(lib.dsa_fwd(ctypes.byref(args), ctypes.c_void_p(stream)), "dsa_fwd")
+    _lib.check(lib.dsa_fwd(ctypes.byref(args), ctypes.c_void_p(_eager.stream_ptr(q))), "dsa_fwd")
     return out, lse, bias
+
+
+dsa_fwd = torch.library.custom_op("deberta_amd::dsa_fwd", _dsa_fwd_impl, mutates_args=(), device_types="cuda")
 
 
 @dsa_fwd.register_fake
@@ -308,8 +309,7 @@ def _alert_nondeterministic_tables() -> None:
         raise RuntimeError(msg)
 
 
-@torch.library.custom_op("deberta_amd::dsa_bwd", mutates_args=(), device_types="cuda")
-def dsa_bwd(
+def _dsa_bwd_impl(
     dout: Tensor,
     q: Tensor,
     k: Tensor,
@@ -360,9 +360,11 @@ def dsa_bwd(
     args.workspace = ws.data_ptr()
     args.workspace_bytes = ws.numel()
     lib = _lib.load()
-    stream = torch.cuda.current_stream(q.device).cuda_stream
-    _lib.check(lib.dsa_bwd(ctypes.byref(args), ctypes.c_void_p(stream)), "dsa_bwd")
+    _lib.check(lib.dsa_bwd(ctypes.byref(args), ctypes.c_void_p(_eager.stream_ptr(q))), "dsa_bwd")
     return dq, dk, dv, dkr, dqr, dqc
+
+
+dsa_bwd = torch.library.custom_op("deberta_amd::dsa_bwd", _dsa_bwd_impl, mutates_args=(), device_types="cuda")
 
 
 @dsa_bwd.register_fake
@@ -398,7 +400,7 @@ def _backward(ctx, dout, dlse, dbias):
     q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, qc = ctx.saved_tensors
     if dout is None:  # the output itself received no gradient
         return (None,) * 12
-    dq, dk, dv, dkr, dqr, dqc = dsa_bwd(
+    dq, dk, dv, dkr, dqr, dqc = _eager.on_eager(ctx, dsa_bwd, _dsa_bwd_impl)(
         dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, ctx.att_span, ctx.scale, qc
     )
     return (
@@ -408,10 +410,32 @@ def _backward(ctx, dout, dlse, dbias):
 
 
 torch.library.register_autograd("deberta_amd::dsa_fwd", _backward, setup_context=_setup_context)
+_DsaFwdFunction = _eager.function("_DsaFwdFunction", _dsa_fwd_impl, _setup_context, _backward)
 
 
-@torch.library.custom_op("deberta_amd::dsa_bias", mutates_args=(), device_types="cuda")
-def dsa_bias(
+def attention(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    kr: Optional[Tensor],
+    qr: Optional[Tensor],
+    rel_table: Optional[Tensor],
+    key_keep: Optional[Tensor],
+    pair_keep: Optional[Tensor],
+    att_span: int,
+    scale: float,
+    save_bias: bool = True,
+    qc: Optional[Tensor] = None,
+) -> tuple[Tensor, Tensor, Tensor]:
+    """``deberta_amd::dsa_fwd`` with its autograd: the op itself under
+    torch.compile or tracing, its implementation in a torch.autograd.Function
+    in plain eager mode (the same kernels, less host time)."""
+    if _eager.eager(q):
+        return _DsaFwdFunction.apply(q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias, qc)
+    return torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias, qc)
+
+
+def _dsa_bias_impl(
     q: Tensor,
     k: Tensor,
     kr: Optional[Tensor],
@@ -437,9 +461,12 @@ def dsa_bias(
     args = _fill_fwd_args(q, k, k, kr, qr, rel_table, None, None, q, dummy, att_span, scale, None, qc)
     strides = (ctypes.c_int64 * 3)(*out.stride()[:3])
     lib = _lib.load()
-    stream = torch.cuda.current_stream(q.device).cuda_stream
+    stream = _eager.stream_ptr(q)
     _lib.check(lib.dsa_bias(ctypes.byref(args), ctypes.c_void_p(out.data_ptr()), strides, ctypes.c_void_p(stream)), "dsa_bias")
     return out
+
+
+dsa_bias = torch.library.custom_op("deberta_amd::dsa_bias", _dsa_bias_impl, mutates_args=(), device_types="cuda")
 
 
 @dsa_bias.register_fake
