@@ -22,7 +22,7 @@ DSA_STAGE_DQ = 2
 DSA_STAGE_DKDV = 4
 DSA_STAGE_FOLD = 8
 
-EXPECTED_VERSION = 6
+EXPECTED_VERSION = 7
 
 _i64x3 = ctypes.c_int64 * 3
 _i64x2 = ctypes.c_int64 * 2
@@ -64,6 +64,7 @@ class DsaFwdArgs(ctypes.Structure):
         ("workspace_bytes", ctypes.c_size_t),
         ("qc", ctypes.c_void_p),
         ("qc_strides", _i64x3),
+        ("pair_keep_stride_h", ctypes.c_int64),
     ]
 
 

@@ -23,7 +23,9 @@ import torch.nn.functional as F
 from deberta_amd import ops
 from deberta_amd.config import normalize_attention_kernel, normalize_pos_att_type
 from deberta_amd.masks import SegmentMask, kernel_masks, normalize_keep_mask
+from deberta_amd.unfused import unfused_attention
 from deberta_amd.relpos import (
+    build_relative_position,
     is_monotone,
     is_toeplitz,
     normalize_relative_pos,
@@ -58,11 +60,13 @@ def table_for(
     buckets: int,
     max_position: int,
     device,
-) -> torch.Tensor:
+    strict: bool = True,
+) -> Optional[torch.Tensor]:
     """Offset table for the kernels from ``relative_pos`` (or the canonical
     one when it is None).  A given matrix must depend on ``i - j`` only and
     be non-decreasing in it (as every matrix build_relative_position returns);
-    this is verified once per tensor version in eager mode."""
+    this is verified once per tensor version in eager mode.  A matrix that is
+    not raises ``ValueError``, or returns None with ``strict=False``."""
     if relative_pos is None:
         return canonical_table(query_len, key_len, buckets, max_position, device)
     rp = normalize_relative_pos(relative_pos.to(device), query_len, key_len)
@@ -76,6 +80,8 @@ def table_for(
                 _TOEPLITZ_OK.clear()
             _TOEPLITZ_OK[key] = ok
         if not ok:
+            if not strict:
+                return None
             raise ValueError(
                 "relative_pos must depend on i - j only and be non-decreasing in it "
                 "(as build_relative_position produces) for the fused disentangled-attention kernels"
@@ -148,7 +154,7 @@ def fused_attention(
     _require_gpu(q)
     B, Lq = q.shape[0], q.shape[1]
     Lk = k.shape[1]
-    key_keep, pair_keep = kernel_masks(attention_mask, B, Lq, Lk, q.device)
+    key_keep, pair_keep = kernel_masks(attention_mask, B, Lq, Lk, q.device, heads=q.shape[2])
     if kr is not None:
         kr = kr.to(q.dtype)
     if qr is not None:
@@ -384,15 +390,15 @@ class DisentangledSelfAttention(nn.Module):
     ) -> tuple[torch.Tensor, Optional[torch.Tensor]]:
         """Same contract as the reference forward (deberta_v2_native.py:564-652).
 
-        Not provided by the fused kernels (raise ``NotImplementedError``):
-        ``output_attentions=True`` (probabilities are never materialised) and
-        attention dropout ``p > 0`` in training mode.
+        The fused kernels run the call unless it needs the probabilities
+        themselves: ``output_attentions=True``, attention dropout ``p > 0``
+        in training mode, or a ``relative_pos`` that does not depend on
+        ``i - j`` alone; those run the same chain in torch operations on the
+        device (``deberta_amd.unfused``) and return the probabilities when
+        asked.
         """
-        if output_attentions:
-            raise NotImplementedError("output_attentions=True: the fused kernels never materialise probabilities")
-        if self.training and self.dropout.p > 0.0:
-            raise NotImplementedError("attention dropout p > 0 is not supported by the fused kernels")
         _require_gpu(hidden_states)
+        unfused = output_attentions or (self.training and self.dropout.p > 0.0)
 
         q, k, v = self._project_qkv(hidden_states, query_states)
         model_dtype = hidden_states.dtype
@@ -400,22 +406,31 @@ class DisentangledSelfAttention(nn.Module):
         scale_factor = 1 + sum(t in self.pos_att_type for t in ("c2p", "p2c", "p2p"))
         scale = 1.0 / math.sqrt(float(self.attention_head_size * scale_factor))
 
-        kr = qr = qc = table = None
+        kr = qr = qc = table = kr_full = qr_full = None
         att_span = 1
-        if self.relative_attention and rel_embeddings is not None:
+        relative = self.relative_attention and rel_embeddings is not None
+        if relative:
             rel_embeddings = self.pos_dropout(rel_embeddings)
             att_span = int(self.pos_ebd_size)
             kr_full, qr_full = self._relative_tables(rel_embeddings, q.dtype)
-            kr, qr, qc = relative_operands(self.pos_att_type, q, kr_full, qr_full, att_span)
-            if kr is not None or qr is not None:
-                table = table_for(
-                    relative_pos,
-                    q.shape[1],
-                    k.shape[1],
-                    self.position_buckets,
-                    self.max_relative_positions,
-                    q.device,
-                )
+            if not unfused:
+                kr, qr, qc = relative_operands(self.pos_att_type, q, kr_full, qr_full, att_span)
+                if kr is not None or qr is not None:
+                    table = table_for(
+                        relative_pos,
+                        q.shape[1],
+                        k.shape[1],
+                        self.position_buckets,
+                        self.max_relative_positions,
+                        q.device,
+                        strict=False,
+                    )
+                    unfused = table is None  # not a function of i - j: used as given
+        if unfused:
+            return self._forward_unfused(
+                q, k, v, kr_full, qr_full, relative_pos if relative else None, relative, attention_mask,
+                att_span, scale, model_dtype, output_attentions,
+            )
 
         if attention_mask is not None and not isinstance(attention_mask, SegmentMask):
             attention_mask = normalize_keep_mask(attention_mask)
@@ -428,3 +443,33 @@ class DisentangledSelfAttention(nn.Module):
         bsz, seq_len = ctx.shape[0], ctx.shape[1]
         context_layer = ctx.reshape(bsz, seq_len, self.all_head_size).to(dtype=model_dtype)
         return context_layer, None
+
+    def _forward_unfused(
+        self, q, k, v, kr, qr, relative_pos, relative, attention_mask, att_span, scale, model_dtype, output_attentions
+    ) -> tuple[torch.Tensor, Optional[torch.Tensor]]:
+        """The torch-operation path (``deberta_amd.unfused``) with the
+        module's relative positions, mask and dropout."""
+        Lq, Lk = q.shape[1], k.shape[1]
+        rel_pos = None
+        types = self.pos_att_type if relative else []
+        if relative and any(t in types for t in ("c2p", "p2c", "p2p")):
+            if relative_pos is None:
+                rel_pos = build_relative_position(
+                    Lq, Lk, bucket_size=self.position_buckets, max_position=self.max_relative_positions, device=q.device
+                )
+            else:
+                rel_pos = normalize_relative_pos(relative_pos.to(q.device), Lq, Lk)
+        keep = None
+        if isinstance(attention_mask, SegmentMask):
+            keep = attention_mask.dense().to(q.device)
+        elif attention_mask is not None:
+            keep = normalize_keep_mask(attention_mask)
+            if keep.ndim != 4:
+                raise ValueError(f"attention_mask must be rank-4 [B,1,Q,K]; got shape={tuple(keep.shape)}")
+        ctx, probs = unfused_attention(
+            q, k, v, kr, qr, rel_pos, keep, att_span, scale, types, self.dropout if self.training else None
+        )
+        context_layer = ctx.reshape(ctx.shape[0], Lq, self.all_head_size).to(dtype=model_dtype)
+        if not output_attentions:
+            return context_layer, None
+        return context_layer, probs.to(v.dtype).to(model_dtype)

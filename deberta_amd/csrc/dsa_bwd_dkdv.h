@@ -112,7 +112,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
   const T* dobase = (const T*)bp.dout + (int64_t)b * bp.dos[0] + (int64_t)h * bp.dos[2];
   const BT* biasb = (const BT*)p.bias;
   const float* rib = bp.rowinfo + (int64_t)(b * p.H + h) * p.LqP * 2;
-  const uint8_t* pkb = (MASK == MASK_PAIR) ? p.pk + (int64_t)b * p.pkb : nullptr;
+  const uint8_t* pkb = (MASK == MASK_PAIR) ? p.pk + (int64_t)b * p.pkb + (int64_t)h * p.pkh : nullptr;
   const SegView<MASK> sv(p, b);
   T* dsw = (T*)bp.ds + (int64_t)(b * p.H + h) * p.LqP * p.LkP + jw;  // dS column jw, row 0
   const T* qrg = p2c ? (const T*)bp.qrgt + (int64_t)h * D * bp.TGP : nullptr;

@@ -128,8 +128,9 @@ int check_fwd(const dsa_fwd_args* a) {
   if (a->pair_keep) {  // the kernels read 16-byte chunks of the mask rows
     const int64_t k16 = (a->Lk + 15) / 16 * 16;
     if (!aligned16(a->pair_keep) || a->pair_keep_strides[0] % 16 || a->pair_keep_strides[1] % 16 ||
+        a->pair_keep_stride_h % 16 ||
         (a->pair_keep_strides[1] != 0 ? a->pair_keep_strides[1] < k16 : a->Lk % 16 != 0))
-      return fail("dsa: pair_keep must be 16-byte aligned, with batch and row strides multiples of 16 bytes "
+      return fail("dsa: pair_keep must be 16-byte aligned, with batch, head and row strides multiples of 16 bytes "
                   "and each row's allocation reaching a multiple of 16 bytes past Lk");
   }
   if ((a->key_keep || a->seg) && a->Lk > 32768)  // per-tile lists in LDS
@@ -175,6 +176,7 @@ dsa::FwdParams to_params(const dsa_fwd_args* a) {
   p.kkb = a->key_keep_stride_b;
   p.pkb = a->pair_keep_strides[0];
   p.pkq = a->pair_keep_strides[1];
+  p.pkh = a->pair_keep ? a->pair_keep_stride_h : 0;
   p.seg = a->seg;
   p.segb = a->seg_stride_b;
   p.order = nullptr;
@@ -658,7 +660,7 @@ dsa::rows::RtdParams rtd_params(const dsa_rtd_args* a) {
 
 extern "C" {
 
-int dsa_version(void) { return 6; }
+int dsa_version(void) { return 7; }
 
 const char* dsa_last_error(void) { return g_err.c_str(); }
 

@@ -28,7 +28,7 @@ struct FwdParams {
   const void* qc;   // query rows of the c2p term [B, Lq, H, D] (carries p2p), or null: q
   int64_t qs[3], ks[3], vs[3], os[3], qcs[3];
   int64_t krs[2], qrs[2];
-  int64_t kkb, pkb, pkq, segb;
+  int64_t kkb, pkb, pkq, pkh, segb;  // pkh: head stride of a per-head pair mask (0: shared)
   int B, H, Lq, Lk, A, flags;
   int LqP, LkP;     // Lq, Lk rounded up to 128 (extents of bias and dS^T)
   float scale;

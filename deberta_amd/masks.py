@@ -158,11 +158,13 @@ def kernel_masks(
     key_len: int,
     device: Optional[torch.device] = None,
     segments_from_dense: bool = True,
+    heads: Optional[int] = None,
 ) -> tuple[Optional[torch.Tensor], Optional[torch.Tensor]]:
     """Split a rank-4 keep mask into the kernels' ``(key_keep, pair_keep)``.
 
     ``(B|1, 1, 1, K)`` becomes a ``[B, K]`` byte view (``key_keep``),
-    ``(B|1, 1, Q, K)`` a ``[B, Q, K]`` byte view (``pair_keep``), or, for a
+    ``(B|1, 1, Q, K)`` a ``[B, Q, K]`` byte view (``pair_keep``), a per-head
+    ``(B|1, H, Q|1, K)`` mask (``heads`` = H given) a ``[B, H, Q, K]`` one, or, for a
     dense mask of the packed-document form on the GPU in eager mode, the
     equivalent int32 segment ids (``dense_as_segments``; off with
     ``segments_from_dense=False``).  A batch
@@ -182,8 +184,10 @@ def kernel_masks(
     keep = normalize_keep_mask(attention_mask)
     if keep.ndim != 4:
         raise ValueError(f"attention_mask must be rank-4 [B,1,Q,K]; got shape={tuple(keep.shape)}")
-    if keep.shape[1] != 1:
-        raise ValueError(f"attention_mask must have a singleton head dim [B,1,Q,K]; got shape={tuple(keep.shape)}")
+    if keep.shape[1] != 1 and (heads is None or keep.shape[1] != heads):
+        raise ValueError(
+            f"attention_mask head dim must be 1 or the number of heads ({heads}); got shape={tuple(keep.shape)}"
+        )
     if keep.shape[0] not in (1, batch) or keep.shape[-1] != key_len or keep.shape[-2] not in (1, query_len):
         raise ValueError(
             f"attention_mask shape {tuple(keep.shape)} does not broadcast to (B={batch},1,Q={query_len},K={key_len})"
@@ -191,6 +195,8 @@ def kernel_masks(
     if query_len != key_len:
         raise ValueError("masked attention needs query_len == key_len (query liveness is read from the mask)")
     bytes_ = keep.view(torch.uint8) if keep.dtype == torch.bool else keep.to(torch.uint8)
+    if keep.shape[1] != 1:
+        return None, _per_head_pair_mask(bytes_, batch, heads, query_len, key_len)
     if keep.shape[-2] == 1:
         kk = bytes_[:, 0, 0, :]
         if kk.stride(-1) != 1:
@@ -222,3 +228,27 @@ def kernel_masks(
         padded[:, :, :key_len] = pk
         pk = padded[:, :, :key_len]
     return None, pk.expand(batch, query_len, key_len)
+
+
+def _per_head_pair_mask(bytes_: torch.Tensor, batch: int, heads: int, query_len: int, key_len: int) -> torch.Tensor:
+    """``[B, H, Q, K]`` byte view of a per-head ``(B|1, H, Q|1, K)`` keep mask
+    in the layout the kernels read (rows in 16-byte chunks: 16-byte aligned,
+    row, head and batch strides multiples of 16 bytes, each row's allocation
+    reaching the next multiple of 16 past ``key_len``); copied into a
+    padded buffer when the view does not qualify."""
+    k16 = (key_len + 15) // 16 * 16
+    pk = bytes_
+    if pk.shape[-2] == 1:  # per-head key padding: one row per head, read for every query
+        pk = pk.expand(pk.shape[0], heads, query_len, key_len)
+    ok = (
+        pk.stride(-1) == 1
+        and pk.data_ptr() % 16 == 0
+        and (pk.stride(-2) % 16 == 0 and pk.stride(-2) >= k16 or pk.stride(-2) == 0 and key_len % 16 == 0)
+        and pk.stride(1) % 16 == 0
+        and (pk.shape[0] == 1 or pk.stride(0) % 16 == 0)
+    )
+    if not ok:
+        padded = torch.zeros(pk.shape[0], heads, query_len, k16, dtype=torch.uint8, device=pk.device)
+        padded[..., :key_len] = pk
+        pk = padded[..., :key_len]
+    return pk.expand(batch, heads, query_len, key_len)

@@ -14,7 +14,8 @@ Tensor layouts (see include/dsa.h):
   key_keep          uint8 [B, Lk] (broadcast keep mask), or int32 [B, L]
                     segment ids (0: inactive token; pair (i, j) kept iff
                     both ids are equal and nonzero), or None
-  pair_keep         uint8 [B, Lq, Lk] or None (pairwise keep mask)
+  pair_keep         uint8 [B, Lq, Lk] or [B, H, Lq, Lk] (per-head) or None
+                    (pairwise keep mask)
   out               [B, Lq, H, D] contiguous, dtype of q
   lse               float32 [B, H, Lq]
   bias              [B, H, pad128(Lq), pad128(Lk)] the relative score term
@@ -115,7 +116,11 @@ def _fill_fwd_args(
     if key_keep is not None:
         a.key_keep_stride_b = key_keep.stride(0)
     if pair_keep is not None:
-        a.pair_keep_strides[:] = (pair_keep.stride(0), pair_keep.stride(1))
+        if pair_keep.dim() == 4:  # per head: [B, H, Lq, Lk]
+            a.pair_keep_strides[:] = (pair_keep.stride(0), pair_keep.stride(2))
+            a.pair_keep_stride_h = pair_keep.stride(1)
+        else:
+            a.pair_keep_strides[:] = (pair_keep.stride(0), pair_keep.stride(1))
     a.B, a.H, a.Lq, a.Lk, a.D = B, H, Lq, Lk, D
     a.att_span = int(att_span)
     a.dtype = _DTYPES[q.dtype]
@@ -173,9 +178,10 @@ def _validate(
     if pair_keep is not None:
         if pair_keep.dtype != torch.uint8:
             raise TypeError(f"dsa: pair_keep must be uint8, got {pair_keep.dtype}")
-        if pair_keep.dim() != 3 or tuple(pair_keep.shape) != (B, Lq, Lk) or pair_keep.stride(-1) != 1:
-            raise ValueError(f"dsa: pair_keep must be [B={B}, Lq={Lq}, Lk={Lk}] with unit key stride, "
-                             f"got {tuple(pair_keep.shape)} strides {pair_keep.stride()}")
+        shapes = ((B, Lq, Lk), (B, H, Lq, Lk))
+        if tuple(pair_keep.shape) not in shapes or pair_keep.stride(-1) != 1:
+            raise ValueError(f"dsa: pair_keep must be [B={B}, Lq={Lq}, Lk={Lk}] or [B, H={H}, Lq, Lk] with unit "
+                             f"key stride, got {tuple(pair_keep.shape)} strides {pair_keep.stride()}")
         if pair_keep.device != q.device:
             raise ValueError("dsa: pair_keep must be on q's device")
     if qc is not None:

@@ -35,7 +35,9 @@
  *     (deberta_v2_native.py:377, 395, 407).
  *   - Masks: key_keep is a [B, Lk] byte mask (nonzero = keep) for the
  *     reference's broadcast (B,1,1,S) keep mask; pair_keep is a [B, Lq, Lk]
- *     byte mask for the pairwise (B,1,S,S) form.  At most one may be given.
+ *     byte mask for the pairwise (B,1,S,S) form, or [B, H, Lq, Lk] for a
+ *     per-head (B,H,S,S) mask (pair_keep_stride_h).  At most one may be
+ *     given.
  *     A zero batch stride broadcasts one mask over the batch.  Query liveness
  *     follows the reference (deberta_v2_native.py:625-639): key_keep[b,i]
  *     for the broadcast form, pair_keep[b,i,i] for the pairwise form; dead
@@ -124,6 +126,11 @@ typedef struct dsa_fwd_args {
      then hold DSA_C2P).  The saved relative term holds the c2p term of qc. */
   const void* qc;
   int64_t qc_strides[3];
+  /* Head stride of pair_keep (a multiple of 16): a per-head [B, H, Lq, Lk]
+     pairwise mask, the reference's (B, H, S, S) keep mask; 0 broadcasts one
+     [B, Lq, Lk] mask over the heads.  Query liveness is then per head:
+     pair_keep[b, h, i, i]. */
+  int64_t pair_keep_stride_h;
 } dsa_fwd_args;
 
 typedef struct dsa_bwd_args {

@@ -333,7 +333,8 @@ def test_module_rejects_bad_config_and_cpu():
     m = DisentangledSelfAttention(eager.make_config(hidden_size=64, num_attention_heads=4))
     with pytest.raises(RuntimeError, match="GPU"):
         m(torch.randn(1, 8, 64), None, rel_embeddings=torch.randn(512, 64))
-    with pytest.raises(NotImplementedError, match="output_attentions"):
+    # the probabilities path (torch operations on the device) is GPU-only too
+    with pytest.raises(RuntimeError, match="GPU"):
         m(torch.randn(1, 8, 64), None, output_attentions=True)
 
 
@@ -482,3 +483,26 @@ def test_fused_blocks_take_the_reference_state_dicts():
         FusedSelfOutput(cfg)(torch.randn(1, 4, 64), torch.randn(1, 4, 64))
     with pytest.raises(NotImplementedError, match="gelu"):
         FusedIntermediate(eager.make_config(hidden_size=64, intermediate_size=256, hidden_act="relu"))
+
+
+def test_per_head_masks_become_head_strided_pair_masks():
+    """A (B, H, S, S) keep mask reaches the kernels as a [B, H, S, S] byte
+    view whose batch, head and row strides are multiples of 16 bytes (rows
+    padded to 16 when they are not); (B, H, 1, S) repeats one row per head
+    for every query; a head count other than 1 or H is refused."""
+    B, H, S = 2, 3, 24
+    m = torch.rand(B, H, S, S) < 0.5
+    kk, pk = kernel_masks(m, B, S, S, heads=H)
+    assert kk is None and pk.shape == (B, H, S, S) and pk.dtype == torch.uint8
+    assert all(s % 16 == 0 for s in pk.stride()[:3]) and pk.stride(-1) == 1
+    assert torch.equal(pk.bool(), m)
+    m2 = torch.rand(1, H, 1, 32) < 0.5
+    _, pk2 = kernel_masks(m2, B, 32, 32, heads=H)
+    assert pk2.shape == (B, H, 32, 32) and pk2.stride(2) == 0 and pk2.stride(0) == 0
+    assert torch.equal(pk2[1, 2, 17].bool(), m2[0, 2, 0])
+    with pytest.raises(ValueError, match="head dim"):
+        kernel_masks(torch.ones(B, 2, S, S, dtype=torch.bool), B, S, S, heads=H)
+    q, k, v, _, _, _ = _inputs(B=B, L=S, H=H)
+    ops._validate(q, k, v, None, None, None, None, pk, 16)
+    args = ops._fill_fwd_args(q, k, v, None, None, None, None, pk, q, torch.empty(1), 16, 0.1)
+    assert args.pair_keep_stride_h == pk.stride(1) and tuple(args.pair_keep_strides) == (pk.stride(0), pk.stride(2))
