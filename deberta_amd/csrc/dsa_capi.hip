@@ -215,14 +215,25 @@ size_t order_bytes(const dsa_fwd_args* a, int ntiles) {
   return align_up((size_t)2 * n * sizeof(int), 256);
 }
 
-int launch_order(const dsa::FwdParams& p, int* buf, int ntiles, bool fwd, hipStream_t st) {
-  dsa::OrderParams op;
+// Up to two heaviest-first orders (dsa_order.h) in two launches, cost then
+// sort: each job a buffer of cost then order (B * ntiles ints each), its
+// tiles per row and its cost kind.
+int launch_orders(const dsa::FwdParams& p, int njobs, int* const* bufs, const int* ntiles, const bool* fwd,
+                  hipStream_t st) {
+  dsa::OrderParams2 op;
   op.f = p;
-  op.cost = buf;
-  op.order = buf + (int64_t)p.B * ntiles;
-  op.ntiles = ntiles;
-  op.fwd = fwd ? 1 : 0;
-  hipLaunchKernelGGL(dsa::dsa_order_cost_kernel, dim3((unsigned)p.B), dim3(256), 0, st, op);
+  op.njobs = njobs;
+  int maxt = 0;
+  for (int j = 0; j < 2; ++j) {
+    const int jj = j < njobs ? j : 0;
+    op.job[j].cost = bufs[jj];
+    op.job[j].order = bufs[jj] + (int64_t)p.B * ntiles[jj];
+    op.job[j].ntiles = ntiles[jj];
+    op.job[j].fwd = fwd[jj] ? 1 : 0;
+    maxt = std::max(maxt, ntiles[jj]);
+  }
+  const dim3 grid((unsigned)p.B, (unsigned)((maxt + dsa::ORDER_TPB - 1) / dsa::ORDER_TPB), (unsigned)njobs);
+  hipLaunchKernelGGL(dsa::dsa_order_cost_kernel, grid, dim3(256), 0, st, op);
   if (launch_check("dsa_order_cost_kernel")) return 1;
   hipLaunchKernelGGL(dsa::dsa_order_sort_kernel, dim3(1), dim3(1024), 0, st, op);
   return launch_check("dsa_order_sort_kernel");
@@ -391,9 +402,15 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
     hipLaunchKernelGGL((dsa::dsa_bwd_prep_kernel<T, D>),
                        dim3((unsigned)(nb.gather + nb.seg + nb.chunk + nb.zero + nb.delta)), dim3(256), 0, st, bp, nb);
     if (launch_check("dsa_bwd_prep_kernel")) return 1;
-    if (kbuf && launch_order(bp.f, kbuf, nkt, false, st)) return 1;
-    // dq's tiles (128 queries against 64-key tiles) weigh as the forward's
-    if (qbuf && launch_order(bp.f, qbuf, nqt, true, st)) return 1;
+    // dkdv's key tiles against 32-query chunks; dq's tiles (128 queries
+    // against 64-key tiles) weigh as the forward's
+    int* bufs[2];
+    int nts[2];
+    bool kinds[2];
+    int nj = 0;
+    if (kbuf) bufs[nj] = kbuf, nts[nj] = nkt, kinds[nj++] = false;
+    if (qbuf) bufs[nj] = qbuf, nts[nj] = nqt, kinds[nj++] = true;
+    if (nj && launch_orders(bp.f, nj, bufs, nts, kinds, st)) return 1;
   }
   if (stages & DSA_STAGE_DKDV) {
     dim3 grid((unsigned)(ws.LkP / dsa::kvcfg::BKW * f.H * f.B));
@@ -489,7 +506,10 @@ int run_fwd(const dsa_fwd_args* a, int* order_buf, hipStream_t st) {
   dsa::FwdParams p = to_params(a);
   const int mode = mask_mode(a);
   if (order_buf) {
-    if (launch_order(p, order_buf, fwd_tiles(a), true, st)) return 1;
+    int* bufs[1] = {order_buf};
+    const int nts[1] = {fwd_tiles(a)};
+    const bool kinds[1] = {true};
+    if (launch_orders(p, 1, bufs, nts, kinds, st)) return 1;
     p.order = order_buf + (int64_t)a->B * fwd_tiles(a);
   }
   if (a->dtype == DSA_BF16) {
