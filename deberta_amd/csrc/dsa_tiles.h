@@ -377,6 +377,9 @@ DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&
   // one mixed-precision FMA per element.  The uniform flag test sits
   // outside the loops.
   const float one = opaque_one();
+  // whether the term is saved: uniform (one pointer for the workgroup), so
+  // the stores sit behind a scalar branch
+  const bool save = __builtin_amdgcn_readfirstlane(bias != nullptr ? 1 : 0) != 0;
   auto gather = [&](auto with_c, auto with_p) {
 #pragma unroll
     for (int ib = 0; ib < 2; ++ib)
@@ -395,7 +398,7 @@ DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) y[ib][jb][e] = __builtin_fmaf((float)bs[e], one, y[ib][jb][e]);
-        if (bias) {
+        if (save) {
           *reinterpret_cast<b4*>(bias + (ib * 4 + jb) * 256) = b4{bs[0], bs[1], bs[2], bs[3]};
         }
       }
