@@ -29,10 +29,26 @@ constexpr int XW = 96;   // offset rows per wave (95 used)
 constexpr int ZC = 32;   // zero columns before each staged dS row
 }  // namespace dqcfg
 
-// QC: the c2p part (the gradient of the c2p term's query rows qc) is
-// accumulated apart and written to dqc; dq then holds the content part.
-template <typename T, int D, bool QC = false>
-__global__ __launch_bounds__(256, 2) void dsa_bwd_dq_kernel(BwdParams bp) {
+// LDS of a dq workgroup (a struct, so that the kernel that runs dq and table
+// workgroups in one launch can overlay it with the table kernel's).
+template <typename T, int D>
+struct DqLds {
+  static constexpr int SSTR = sizeof(T) == 2 ? 104 : 100;  // staged dS row stride (see dq_body)
+  static constexpr int GSTR = dqcfg::BQ + dqcfg::XW - dqcfg::WQ + Pad<T>::v;
+  static constexpr int KSTR = D + Pad<T>::v;
+  alignas(16) T Ss[(dqcfg::BQ + 1) * SSTR];
+  alignas(16) T Ks[dqcfg::BK * KSTR];
+  alignas(16) T KG[D * GSTR];
+  short klist[dqcfg::MAX_KT];  // key tiles that can hold nonzero dS
+  int segred[1];
+};
+
+// Workgroup blk of nblk (the logical index, whose remainder mod 8 is the
+// XCD it runs on).  QC: the c2p part (the gradient of the c2p term's query
+// rows qc) is accumulated apart and written to dqc; dq then holds the
+// content part.
+template <typename T, int D, bool QC>
+DSA_DEV void dq_body(const BwdParams& bp, int blk, int nblk, DqLds<T, D>& L) {
   using namespace dqcfg;
   using M = Mfma<T>;
   typedef typename M::frag frag;
@@ -41,23 +57,24 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dq_kernel(BwdParams bp) {
   constexpr int ND = D / 16;
   constexpr int FE = M::FRAG_ELEMS;               // k indices per lane per step
   static_assert(FE == VEC, "a fragment is one 16-byte chunk");
-  constexpr int KSTR = D + Pad<T>::v;             // K tile row stride
+  constexpr int KSTR = DqLds<T, D>::KSTR;          // K tile row stride
   // Staged dS row: ZC zeros, BK keys, zeros up to the stride, and then the
   // next row's leading zeros; the stride makes 16 rows' 16-byte reads hit
   // distinct banks.  The c2p walk reads key columns [BK - XW, WQ + BK - 2].
-  constexpr int SSTR = sizeof(T) == 2 ? 104 : 100;
+  constexpr int SSTR = DqLds<T, D>::SSTR;
   static_assert(ZC + BK - XW >= 0 && WQ + BK - 2 < SSTR && ZC + BK <= SSTR, "zero columns cover the walk");
   constexpr int GW = BQ + XW - WQ;                // krgt columns of the workgroup's window (192)
-  constexpr int GSTR = GW + Pad<T>::v;
+  constexpr int GSTR = DqLds<T, D>::GSTR;
+  static_assert(GSTR == GW + Pad<T>::v, "krgt window stride");
   constexpr int SV = BQ * BK / VEC, KV = BK * D / VEC, GV = D * GW / VEC;  // 16-byte chunks per tile
   constexpr int SCH = (SV + 255) / 256, KCH = (KV + 255) / 256, GCH = (GV + 255) / 256;
   const FwdParams& p = bp.f;
 
-  __shared__ __align__(16) T Ss[(BQ + 1) * SSTR];
-  __shared__ __align__(16) T Ks[BK * KSTR];
-  __shared__ __align__(16) T KG[D * GSTR];
-  __shared__ short klist[MAX_KT];  // key tiles that can hold nonzero dS
-  __shared__ int segred[1];
+  T* const Ss = L.Ss;
+  T* const Ks = L.Ks;
+  T* const KG = L.KG;
+  short* const klist = L.klist;
+  int* const segred = L.segred;
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, g = (tid & 63) >> 4, c16 = tid & 15;
@@ -66,10 +83,10 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dq_kernel(BwdParams bp) {
   // head r % H, heaviest first
   int qt, h, b;
   if (bp.qorder) {
-    const int it = bp.qorder[blockIdx.x / p.H];
-    h = blockIdx.x % p.H, qt = it % NQT, b = it / NQT;
+    const int it = bp.qorder[blk / p.H];
+    h = blk % p.H, qt = it % NQT, b = it / NQT;
   } else {
-    const int m = xcd_remap(blockIdx.x, gridDim.x);
+    const int m = xcd_remap(blk, nblk);
     qt = m % NQT, h = (m / NQT) % p.H, b = m / (NQT * p.H);
   }
   const int i0 = qt * BQ, iw = i0 + w * WQ;
@@ -263,6 +280,12 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dq_kernel(BwdParams bp) {
       }
     }
   }
+}
+
+template <typename T, int D, bool QC = false>
+__global__ __launch_bounds__(256, 2) void dsa_bwd_dq_kernel(BwdParams bp) {
+  __shared__ DqLds<T, D> L;
+  dq_body<T, D, QC>(bp, blockIdx.x, gridDim.x, L);
 }
 
 }  // namespace dsa

@@ -97,10 +97,25 @@ DSA_DEV void block_items(int dblk, int LkP, int Lq, int Lk, bool p2c, int* start
   *n = e > s ? (e - s + CH - 1) / CH : 0;
 }
 
-// LISTED: a key-padding or segment mask is given (bp.cinfo): items without
-// an active part are skipped and partials carry flags.
+// LDS of a table workgroup (a struct, so that the kernel that runs dq and
+// table workgroups in one launch can overlay it with the dq kernel's).
+template <typename T, int D>
+struct TabLds {
+  static constexpr int KSTR = D + Pad<T>::v;
+  static constexpr int XELEMS =
+      (tbcfg::CH * tbcfg::XS_C > tbcfg::PR * tbcfg::XS_P) ? tbcfg::CH * tbcfg::XS_C : tbcfg::PR * tbcfg::XS_P;
+  static constexpr int WELEMS = XELEMS + tbcfg::CH * KSTR;  // per wave
+  alignas(16) T lds[tbcfg::NW * WELEMS];
+  int ilist[tbcfg::NW][64];  // per wave: the active items of a window of 64 candidates
+  int nact_sh[tbcfg::NW];
+};
+
+// Workgroup blk of nblk (the logical index, whose remainder mod 8 is the
+// XCD it runs on).  LISTED: a key-padding or segment mask is given
+// (bp.cinfo): items without an active part are skipped and partials carry
+// flags.
 template <typename T, int D, bool LISTED>
-__global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
+DSA_DEV void table_body(const BwdParams& bp, int blk, int nblk, TabLds<T, D>& L) {
   using namespace tbcfg;
   using M = Mfma<T>;
   typedef typename M::frag frag;
@@ -110,18 +125,18 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
   constexpr int NEB = DBW / 16;         // 16-offset blocks
   constexpr int FE = M::FRAG_ELEMS;
   constexpr int NS = CH / M::KSTEP;     // k steps per item
-  constexpr int KSTR = D + Pad<T>::v;   // item rows (Q or K) stride
-  constexpr int DCH = D / VEC;          // 16-byte chunks per item row
-  constexpr int XELEMS = (CH * XS_C > PR * XS_P) ? CH * XS_C : PR * XS_P;
-  constexpr int WELEMS = XELEMS + CH * KSTR;  // per wave
+  constexpr int KSTR = TabLds<T, D>::KSTR;   // item rows (Q or K) stride
+  constexpr int DCH = D / VEC;               // 16-byte chunks per item row
+  constexpr int XELEMS = TabLds<T, D>::XELEMS;
+  constexpr int WELEMS = TabLds<T, D>::WELEMS;
   constexpr bool PREFETCH = sizeof(T) == 2;
   static_assert((XS_C * sizeof(T)) % 16 == 0 && (XS_P * sizeof(T)) % 16 == 0, "16-byte rows");
   static_assert(NW * WELEMS * sizeof(T) >= 2 * NEB * ND * 64 * 16, "LDS holds two waves' accumulators");
   const FwdParams& p = bp.f;
 
-  __shared__ __align__(16) T lds[NW * WELEMS];
-  __shared__ int ilist[NW][64];  // per wave: the active items of a window of 64 candidates
-  __shared__ int nact_sh[NW];
+  T* const lds = L.lds;
+  int(&ilist)[NW][64] = L.ilist;
+  int* const nact_sh = L.nact_sh;
 
   const int tid = threadIdx.x;
   // the wave index, known to the compiler as uniform (the item loop's
@@ -130,7 +145,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
   const bool p2c = w >= 2;  // wave kind: 0, 1 -> Gc; 2, 3 -> Gp
   const int sub = w & 1;
   // Work order.  Short sequences (fewer than 32 offset blocks, a grid of
-  // a few workgroups per CU): blockIdx.x enumerates (offset block, head,
+  // a few workgroups per CU): blk enumerates (offset block, head,
   // partial group) with the offset blocks that have the most items first,
   // so the shortest workgroups fill in at the end of the launch.  Longer
   // ones (many workgroups per CU): the logical index (xcd_remap)
@@ -141,11 +156,11 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
   // 33% more at L = 1024 and 25% more at L = 512).
   int rank, rem;
   if (bp.NDB >= 32) {
-    const int m = xcd_remap(blockIdx.x, gridDim.x);
+    const int m = xcd_remap(blk, nblk);
     rank = m % bp.NDB, rem = m / bp.NDB;
   } else {
     const int per_blk = p.H * bp.NPG;
-    rank = blockIdx.x / per_blk, rem = blockIdx.x % per_blk;
+    rank = blk / per_blk, rem = blk % per_blk;
   }
   const int h = rem / bp.NPG, pg = rem % bp.NPG;
   const int mid = (bp.NDB - 1) / 2;  // central blocks hold the most pairs
@@ -432,6 +447,12 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
       }
     }
   }
+}
+
+template <typename T, int D, bool LISTED>
+__global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
+  __shared__ TabLds<T, D> L;
+  table_body<T, D, LISTED>(bp, blockIdx.x, gridDim.x, L);
 }
 
 // tab[h][r][:] (+)= s * sum over offsets d with row(d) = r of the block

@@ -19,6 +19,7 @@
 #include "dsa_bwd.h"
 #include "dsa_bwd_dkdv.h"
 #include "dsa_bwd_dq.h"
+#include "dsa_bwd_dqtab.h"
 #include "dsa_bwd_table.h"
 #include "dsa_order.h"
 #include "dsa_fwd.h"
@@ -36,35 +37,6 @@ static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
 namespace {
 
 thread_local std::string g_err;
-
-// A side stream (default priority) and two events per device and host
-// thread, for running the DQ stage beside the FOLD stage: both only read
-// the workspace after DKDV.  Created on first use, kept for the thread's
-// lifetime.
-struct SideStream {
-  int device = -1;
-  hipStream_t stream = nullptr;
-  hipEvent_t fork = nullptr, join = nullptr;
-};
-thread_local SideStream g_side[16];
-
-SideStream* side_stream(hipStream_t st) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return nullptr;
-  // Under graph capture the stages run in order on the caller's stream: a
-  // fork/join across streams inside a capture ended in a host crash in the
-  // runtime's capture end.
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
-  SideStream& s = g_side[dev];
-  if (s.device != dev) {
-    if (hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking) != hipSuccess) return nullptr;
-    if (hipEventCreateWithFlags(&s.fork, hipEventDisableTiming) != hipSuccess) return nullptr;
-    if (hipEventCreateWithFlags(&s.join, hipEventDisableTiming) != hipSuccess) return nullptr;
-    s.device = dev;
-  }
-  return &s;
-}
 
 int fail(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
 int fail(const char* fmt, ...) {
@@ -292,9 +264,9 @@ WsLayout ws_layout(const dsa_bwd_args* a) {
   // Partial groups of the table kernel (ranges of an offset block's items
   // of one kind; a central block has about B * L / 32): about one and a
   // half workgroups per CU, whose fp32 atomics into the block accumulators
-  // stay few and which leave room for dq beside them (B=32, L=512: DQ and
-  // FOLD 166 us with three workgroups per CU, 157 with one and a half, 200
-  // with six).  Long sequences and masks concentrate the work in the
+  // stay few and which leave room for dq beside them (B=32, L=512, the two
+  // in one launch: backward 312 us with one workgroup per CU, 305 with one
+  // and a half, 307 with two, 319 with three).  Long sequences and masks concentrate the work in the
   // central blocks, whose workgroups then bound the launch: those get at
   // most 64 items of a kind each.
   const int per = f.H * w.NDB;
@@ -323,22 +295,6 @@ WsLayout ws_layout(const dsa_bwd_args* a) {
   off += order_bytes(&f, w.LqP / dsa::dqcfg::BQ);
   w.total = off;
   return w;
-}
-
-// Dynamic LDS that takes a table-kernel workgroup just past half of a CU's
-// 160 KB (queried once per instantiation; 0 if the query fails).
-template <typename T, int D, bool LISTED>
-unsigned half_cu_lds_pad() {
-  static const unsigned pad = [] {
-    hipFuncAttributes fa;
-    if (hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(&dsa::dsa_bwd_table_kernel<T, D, LISTED>)) !=
-        hipSuccess) {
-      (void)hipGetLastError();
-      return 0u;
-    }
-    return fa.sharedSizeBytes < 81920 + 256 ? (unsigned)(81920 + 256 - fa.sharedSizeBytes) : 0u;
-  }();
-  return pad;
 }
 
 template <typename T, int D>
@@ -429,44 +385,43 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
     }
     if (launch_check("dsa_bwd_dkdv_kernel")) return 1;
   }
-  // DQ and FOLD both only read dS: with both requested, DQ runs on a side
-  // stream (forked from and joined back into the caller's stream) so that
-  // the two kernels share the GPU; the table kernel, whose workgroups are
-  // longer, is launched first.
+  // DQ and FOLD both only read dS: with both requested, the dq and table
+  // workgroups run in one launch (dsa_bwd_dqtab.h) and share the GPU.
   const bool fold = (stages & DSA_STAGE_FOLD) && f.flags;
-  SideStream* side = ((stages & DSA_STAGE_DQ) && fold) ? side_stream(st) : nullptr;
-  if (side && (hipEventRecord(side->fork, st) != hipSuccess || hipStreamWaitEvent(side->stream, side->fork, 0) != hipSuccess))
-    return fail("dsa: side stream fork failed");
-  if (fold) {
-    // With DQ beside it and no mask, the table kernel (bound by memory
-    // throughput, as fast at one workgroup per CU as at two) asks for unused
-    // dynamic LDS that takes it just past half a CU's 160 KB, so that each
-    // CU keeps room for a dq workgroup next to one table workgroup (backward
-    // 344 -> 339 us at B=32, L=512).  Under a mask the table kernel's work
-    // sits in few workgroups that need the second slot (C4 segments: 962 ->
-    // 987 us with the pad), so it is not padded.
-    const unsigned dyn = (side && !bp.cinfo) ? half_cu_lds_pad<T, D, false>() : 0u;
-    // dKr sums dS_ij times the c2p term's query rows: qc when it is given
-    dsa::BwdParams tp = bp;
-    if (f.qc) {
-      tp.f.q = f.qc;
-      for (int s = 0; s < 3; ++s) tp.f.qs[s] = f.qc_strides[s];
-    }
-    if (bp.cinfo)
-      hipLaunchKernelGGL((dsa::dsa_bwd_table_kernel<T, D, true>), dim3(ws.NDB * f.H * ws.NPG), dim3(256), dyn, st, tp);
-    else
-      hipLaunchKernelGGL((dsa::dsa_bwd_table_kernel<T, D, false>), dim3(ws.NDB * f.H * ws.NPG), dim3(256), dyn, st, tp);
-    if (launch_check("dsa_bwd_table_kernel")) return 1;
+  const bool dq = (stages & DSA_STAGE_DQ) != 0;
+  // dKr sums dS_ij times the c2p term's query rows: qc when it is given
+  dsa::BwdParams tp = bp;
+  if (f.qc) {
+    tp.f.q = f.qc;
+    for (int s = 0; s < 3; ++s) tp.f.qs[s] = f.qc_strides[s];
   }
-  if (stages & DSA_STAGE_DQ) {
-    hipStream_t sq = side ? side->stream : st;
-    dim3 grid((unsigned)(ws.LqP / dsa::dqcfg::BQ * f.H * f.B));
-    if (f.qc)
-      hipLaunchKernelGGL((dsa::dsa_bwd_dq_kernel<T, D, true>), grid, dim3(256), 0, sq, bp);
+  const int ntab = ws.NDB * f.H * ws.NPG;
+  const int ndq = ws.LqP / dsa::dqcfg::BQ * f.H * f.B;
+  if (fold && dq) {
+    const int nt8 = (ntab + 7) / 8 * 8;
+    const dim3 grid((unsigned)(nt8 + ndq));
+    const bool listed = bp.cinfo != nullptr;
+    if (listed && f.qc)
+      hipLaunchKernelGGL((dsa::dsa_bwd_dqtab_kernel<T, D, true, true>), grid, dim3(256), 0, st, bp, tp, ntab, nt8, ndq);
+    else if (listed)
+      hipLaunchKernelGGL((dsa::dsa_bwd_dqtab_kernel<T, D, true, false>), grid, dim3(256), 0, st, bp, tp, ntab, nt8, ndq);
+    else if (f.qc)
+      hipLaunchKernelGGL((dsa::dsa_bwd_dqtab_kernel<T, D, false, true>), grid, dim3(256), 0, st, bp, tp, ntab, nt8, ndq);
     else
-      hipLaunchKernelGGL((dsa::dsa_bwd_dq_kernel<T, D, false>), grid, dim3(256), 0, sq, bp);
+      hipLaunchKernelGGL((dsa::dsa_bwd_dqtab_kernel<T, D, false, false>), grid, dim3(256), 0, st, bp, tp, ntab, nt8, ndq);
+    if (launch_check("dsa_bwd_dqtab_kernel")) return 1;
+  } else if (fold) {
+    if (bp.cinfo)
+      hipLaunchKernelGGL((dsa::dsa_bwd_table_kernel<T, D, true>), dim3(ntab), dim3(256), 0, st, tp);
+    else
+      hipLaunchKernelGGL((dsa::dsa_bwd_table_kernel<T, D, false>), dim3(ntab), dim3(256), 0, st, tp);
+    if (launch_check("dsa_bwd_table_kernel")) return 1;
+  } else if (dq) {
+    if (f.qc)
+      hipLaunchKernelGGL((dsa::dsa_bwd_dq_kernel<T, D, true>), dim3(ndq), dim3(256), 0, st, bp);
+    else
+      hipLaunchKernelGGL((dsa::dsa_bwd_dq_kernel<T, D, false>), dim3(ndq), dim3(256), 0, st, bp);
     if (launch_check("dsa_bwd_dq_kernel")) return 1;
-    if (side && hipEventRecord(side->join, sq) != hipSuccess) return fail("dsa: side stream join failed");
   }
   if (fold) {
     const dim3 fg((unsigned)(2 * f.H * (2 * f.att_span)));
@@ -476,7 +431,6 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
       hipLaunchKernelGGL((dsa::dsa_bwd_fold_kernel<D, 64>), fg, dim3(64), 0, st, bp);
     if (launch_check("dsa_bwd_fold_kernel")) return 1;
   }
-  if (side && hipStreamWaitEvent(st, side->join, 0) != hipSuccess) return fail("dsa: side stream join failed");
   return 0;
 }
 

@@ -1,8 +1,7 @@
 """The fused forward + backward under HIP graph capture.
 
-The backward forks its DQ stage onto a side stream and joins it back with
-events; captured, that becomes a fork/join in the graph.  Replays must equal
-the eager results exactly (dKr and dQr up to the order of their fp32
+Every launch of the library goes on the caller's stream.  Replays must
+equal the eager results exactly (dKr and dQr up to the order of their fp32
 atomic additions), several times in a row, with eager work and
 synchronisations between the replays.
 """
@@ -21,7 +20,7 @@ pytestmark = pytest.mark.gpu
 @pytest.mark.skip(
     reason="graph capture of the op ended in a host segmentation fault inside "
     "torch.cuda.graph's capture_end (hipStreamEndCapture / instantiation), with "
-    "and without the backward's side-stream fork/join; cause not yet shown, so "
+    "and without the side-stream fork/join an earlier backward had; cause not yet shown, so "
     "the case stays off the GPU"
 )
 def test_graph_capture_replays_match_eager(gpu):
@@ -41,7 +40,7 @@ def test_graph_capture_replays_match_eager(gpu):
         out, _, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, A, scale)
         return [out] + list(torch.autograd.grad(out, leaves, dout))
 
-    ref = [t.clone() for t in step()]  # eager (sets up the side stream outside capture)
+    ref = [t.clone() for t in step()]  # eager
     side = torch.cuda.Stream(gpu)
     side.wait_stream(torch.cuda.current_stream(gpu))
     with torch.cuda.stream(side):
