@@ -76,7 +76,8 @@ __global__ __launch_bounds__(256, 2) void dsa_bias_kernel(BiasParams bp) {
   if (p.flags) {
     const T* krh = (p.flags & 1) ? (const T*)p.kr + (int64_t)h * p.krs[0] : nullptr;
     const T* qrh = (p.flags & 2) ? (const T*)p.qr + (int64_t)h * p.qrs[0] : nullptr;
-    add_delta_bands_T<T, D, 6>(y, kf, qf, cb_all + w * CB_ELEMS, pb, crow, prow, w, g, c16, krh, qrh, p.flags);
+    add_delta_bands_T<T, D, 6>(y, kf, qf, cb_all + w * CB_ELEMS, pb, crow, prow, w, g, c16, krh, qrh, p.krk, p.qrk,
+                               p.flags);
   }
 
   // lane: query iw + 16 ib + c16, keys j0 + 16 jb + 4 g + [0, 4)

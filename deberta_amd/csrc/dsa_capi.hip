@@ -145,6 +145,7 @@ dsa::FwdParams to_params(const dsa_fwd_args* a) {
     p.krs[s] = a->kr_strides[s];
     p.qrs[s] = a->qr_strides[s];
   }
+  p.krk = p.qrk = 64 / elem_bytes(a->dtype);  // rows contiguous: k-steps adjacent
   p.kkb = a->key_keep_stride_b;
   p.pkb = a->pair_keep_strides[0];
   p.pkq = a->pair_keep_strides[1];
@@ -454,11 +455,46 @@ void* static_scratch(int* err_device) {
   return addr[dev];
 }
 
+// Bytes of the forward's k-step copy of one relative table (TableKs).
+size_t table_ks_bytes(const dsa_fwd_args* a) {
+  return align_up((size_t)a->H * (2 * a->att_span) * a->D * elem_bytes(a->dtype), 256);
+}
+size_t tables_ks_bytes(const dsa_fwd_args* a) {
+  if (!a->flags) return 0;
+  return table_ks_bytes(a) * (((a->flags & DSA_C2P) ? 1 : 0) + ((a->flags & DSA_P2C) ? 1 : 0));
+}
+
 // The forward with the launch-order scratch `order_buf` (NULL: no
-// heaviest-first order).  Arguments already checked.
-int run_fwd(const dsa_fwd_args* a, int* order_buf, hipStream_t st) {
+// heaviest-first order) and the scratch for the k-step copies of the
+// relative tables `tab_buf` (NULL: the bands read the caller's tables).
+// Arguments already checked.
+int run_fwd(const dsa_fwd_args* a, int* order_buf, void* tab_buf, hipStream_t st) {
   dsa::FwdParams p = to_params(a);
   const int mode = mask_mode(a);
+  if (tab_buf && a->flags) {
+    dsa::TableKs t;
+    const int R = 2 * a->att_span, ks = 64 / elem_bytes(a->dtype);
+    char* dst = static_cast<char*>(tab_buf);
+    const bool has[2] = {(a->flags & DSA_C2P) != 0, (a->flags & DSA_P2C) != 0};
+    const void* src[2] = {a->kr, a->qr};
+    const int64_t* str[2] = {a->kr_strides, a->qr_strides};
+    for (int k = 0; k < 2; ++k) {
+      t.src[k] = has[k] ? src[k] : nullptr;
+      t.hs[k] = str[k][0];
+      t.rs[k] = str[k][1];
+      t.dst[k] = has[k] ? dst : nullptr;
+      if (has[k]) dst += table_ks_bytes(a);
+    }
+    t.H = a->H, t.R = R, t.D = a->D, t.esize = elem_bytes(a->dtype);
+    const int64_t n = (int64_t)a->H * R * a->D * t.esize / 16;
+    hipLaunchKernelGGL(dsa::dsa_table_ks_kernel, dim3((unsigned)((n + 255) / 256), 2), dim3(256), 0, st, t);
+    if (launch_check("dsa_table_ks_kernel")) return 1;
+    // the bands read the copies: head stride NS * R * KS, row stride KS,
+    // k-step stride R * KS
+    const int64_t hs = (int64_t)(a->D / ks) * R * ks;
+    if (has[0]) p.kr = t.dst[0], p.krs[0] = hs, p.krs[1] = ks, p.krk = (int64_t)R * ks;
+    if (has[1]) p.qr = t.dst[1], p.qrs[0] = hs, p.qrs[1] = ks, p.qrk = (int64_t)R * ks;
+  }
   if (order_buf) {
     int* bufs[1] = {order_buf};
     const int nts[1] = {fwd_tiles(a)};
@@ -642,14 +678,18 @@ int dsa_fwd(const dsa_fwd_args* a, void* stream) {
   g_err.clear();
   if (check_fwd(a)) return 1;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const size_t ob = order_bytes(a, fwd_tiles(a));
+  const size_t ob = order_bytes(a, fwd_tiles(a)), tb = tables_ks_bytes(a);
   int* buf = nullptr;
-  if (ob && a->workspace) {
+  void* tabs = nullptr;
+  if (a->workspace && (ob || tb)) {
     if (a->workspace_bytes < ob) return fail("dsa: forward workspace of %zu bytes required, got %zu", ob, a->workspace_bytes);
     if (!aligned16(a->workspace)) return fail("dsa: forward workspace must be 16-byte aligned");
-    buf = static_cast<int*>(a->workspace);
+    if (ob) buf = static_cast<int*>(a->workspace);
+    // a workspace of the size without the table copies (earlier versions of
+    // dsa_fwd_workspace_bytes) runs the bands on the caller's tables
+    if (tb && a->workspace_bytes >= ob + tb) tabs = static_cast<char*>(a->workspace) + ob;
   }
-  return run_fwd(a, buf, st);
+  return run_fwd(a, buf, tabs, st);
 }
 
 int dsa_fwd_static(const dsa_fwd_args* a, void* stream) {
@@ -666,7 +706,7 @@ int dsa_fwd_static(const dsa_fwd_args* a, void* stream) {
     buf = static_cast<int*>(static_scratch(&dev));
     if (!buf) return fail("dsa_fwd_static: no address for the static scratch on device %d", dev);
   }
-  return run_fwd(a, buf, static_cast<hipStream_t>(stream));
+  return run_fwd(a, buf, nullptr, static_cast<hipStream_t>(stream));
 }
 
 int dsa_bias(const dsa_fwd_args* a, void* out, const int64_t* out_strides, void* stream) {
@@ -735,8 +775,9 @@ size_t dsa_fwd_bias_bytes(const dsa_fwd_args* a) {
 }
 
 size_t dsa_fwd_workspace_bytes(const dsa_fwd_args* a) {
-  if (!a || a->B < 1 || a->Lq < 1) return 0;
-  return order_bytes(a, fwd_tiles(a));
+  if (!a || a->B < 1 || a->Lq < 1 || a->H < 1 || a->D < 1) return 0;
+  if (a->flags && (a->att_span < 1 || a->att_span > 16383)) return 0;
+  return order_bytes(a, fwd_tiles(a)) + tables_ks_bytes(a);
 }
 
 size_t dsa_bwd_workspace_bytes(const dsa_bwd_args* a) {

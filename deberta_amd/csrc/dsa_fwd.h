@@ -279,8 +279,8 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
         st[ib][jb] = acc;
       }
     if (p.flags)
-      add_delta_bands_T<T, D, MASK == MASK_PAIR ? 3 : 6>(st, kf, pick<QC>(qcf, qf), cb, pb, crow, prow, w, g, c16, krh, qrh, p.flags,
-                              biasl ? biasl + (int64_t)kt * 8192 : nullptr);
+      add_delta_bands_T<T, D, MASK == MASK_PAIR ? 3 : 6>(st, kf, pick<QC>(qcf, qf), cb, pb, crow, prow, w, g, c16, krh, qrh,
+                                                         p.krk, p.qrk, p.flags, biasl ? biasl + (int64_t)kt * 8192 : nullptr);
     __builtin_amdgcn_s_setprio(0);
 
     // ---- mask: only where a key or query of the tile can be masked out ------

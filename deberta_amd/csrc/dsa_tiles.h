@@ -27,7 +27,8 @@ struct FwdParams {
   const int* order; // launch order of the (batch row, tile) items, heaviest first, or null (dsa_order.h)
   const void* qc;   // query rows of the c2p term [B, Lq, H, D] (carries p2p), or null: q
   int64_t qs[3], ks[3], vs[3], os[3], qcs[3];
-  int64_t krs[2], qrs[2];
+  int64_t krs[2], qrs[2];           // kr / qr element strides of head and table row
+  int64_t krk, qrk;                 // element stride between the 64-byte k-steps of a table row
   int64_t kkb, pkb, pkq, pkh, segb;  // pkh: head stride of a per-head pair mask (0: shared)
   int B, H, Lq, Lk, A, flags;
   int LqP, LkP;     // Lq, Lk rounded up to 128 (extents of bias and dS^T)
@@ -236,6 +237,35 @@ constexpr int CB_ELEMS = WQ * CTS;
 constexpr int PB_ELEMS = XG * PBT;
 }  // namespace dcfg
 
+// The relative tables re-laid by k-step for the forward's band loads:
+// element d of row r of head h at ((h * NS + d / KS) * R + r) * KS + d % KS,
+// KS the elements of 64 bytes and NS = D / KS.  The k-step of 16
+// consecutive table rows that one load instruction of the bands gathers is
+// then 1 KB of contiguous memory (8 cache lines; the rows of consecutive
+// offsets are consecutive or repeated) instead of 16 row segments in 16
+// lines.  One thread per 16 bytes; blockIdx.y = table (0: kr, 1: qr).
+struct TableKs {
+  const void* src[2];
+  int64_t hs[2], rs[2];  // source element strides of head and row
+  void* dst[2];
+  int H, R, D, esize;
+};
+__global__ __launch_bounds__(256) void dsa_table_ks_kernel(TableKs t) {
+  const int tb = blockIdx.y;
+  if (!t.src[tb]) return;
+  const int per16 = 16 / t.esize, ks = 64 / t.esize, ns = t.D / ks;
+  const int64_t n = (int64_t)t.H * ns * t.R * (ks / per16);
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= n) return;
+  const int q = (int)(c % (ks / per16));
+  int64_t rest = c / (ks / per16);
+  const int r = (int)(rest % t.R);
+  rest /= t.R;
+  const int s = (int)(rest % ns), h = (int)(rest / ns);
+  const char* src = (const char*)t.src[tb] + ((int64_t)h * t.hs[tb] + (int64_t)r * t.rs[tb] + s * ks + q * per16) * t.esize;
+  *reinterpret_cast<uint4*>((char*)t.dst[tb] + c * 16) = *reinterpret_cast<const uint4*>(src);
+}
+
 // Row tables of one tile: crow[x] / prow[x] are the element offsets (row *
 // row stride) of the c2p / p2c table rows of offset x (x = (i - i0) - (j -
 // j0) + 63, i0 / j0 the tile's first query / key), for x in [0, 192); the
@@ -307,6 +337,7 @@ DSA_DEV void store4_contig(B* p, const f32x4& v) {
 //   (the c2p term's query rows: q, or qc when it is given)
 //   cb: this wave's c2p band (WQ * CTS), pb: the shared p2c band (XG * PBT)
 //   crow, prow: the tile's table row offsets (store_row_tables)
+//   krk, qrk: element strides between the 64-byte k-steps of a table row
 //   GR: c2p row blocks whose table rows are loaded before their products
 //       (all six: one L2 round trip per tile instead of six)
 //   bias: if not null, where this lane's part of the tile's saved relative
@@ -318,13 +349,18 @@ template <typename T, int D, int GR>
 DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&kf)[4][D / Mfma<T>::KSTEP],
                                const typename Mfma<T>::frag (&qf)[2][D / Mfma<T>::KSTEP],
                                typename BandType<T>::type* cb, typename BandType<T>::type* pb, const int* crow,
-                               const int* prow, int w, int g, int c16, const T* krh, const T* qrh, int flags,
-                               typename BandType<T>::type* bias = nullptr) {
+                               const int* prow, int w, int g, int c16, const T* krh, const T* qrh, int64_t krk,
+                               int64_t qrk, int flags, typename BandType<T>::type* bias = nullptr) {
   using M = Mfma<T>;
   typedef typename M::frag frag;
   typedef typename BandType<T>::type BT;
   using namespace dcfg;
   constexpr int NS = D / M::KSTEP;
+  constexpr int FE = M::FRAG_ELEMS;
+  // k-step s of a table row: FE elements of lane group g at rowp + s * krk + FE * g
+  auto row_frag = [&](const T* rowp, int64_t ks, int s) {
+    return *reinterpret_cast<const frag*>(rowp + s * ks + FE * g);
+  };
   if (flags & 1) {
     // GR row blocks have their table rows requested together (one L2
     // round trip per group)
@@ -336,7 +372,7 @@ DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&
       for (int u = 0; u < GR; ++u) {
         const T* rowp = krh + crow[WQ * w + 16 * (rb0 + u) + c16];
 #pragma unroll
-        for (int s = 0; s < NS; ++s) af[u][s] = M::load_contig(rowp, s, g);
+        for (int s = 0; s < NS; ++s) af[u][s] = row_frag(rowp, krk, s);
       }
 #pragma unroll
       for (int u = 0; u < GR; ++u)
@@ -356,7 +392,7 @@ DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&
       const T* rowp = qrh + prow[16 * xb + c16];
       frag bf[NS];
 #pragma unroll
-      for (int s = 0; s < NS; ++s) bf[s] = M::load_contig(rowp, s, g);
+      for (int s = 0; s < NS; ++s) bf[s] = row_frag(rowp, qrk, s);
 #pragma unroll
       for (int jb = 0; jb < 4; ++jb) {
         f32x4 acc = zero4();

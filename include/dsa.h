@@ -73,6 +73,7 @@ enum { DSA_C2P = 1, DSA_P2C = 2 };
  *   DKDV  writes dv, dk and dS^T (into the workspace)
  *   DQ    writes dq from dS^T
  *   FOLD  adds the relative-table gradients (from dS^T) into dkr / dqr
+ * DQ and FOLD requested in one call run their main kernels as one launch.
  * Stages run in separate calls must keep this order and share one
  * workspace. */
 enum { DSA_STAGE_PREP = 1, DSA_STAGE_DQ = 2, DSA_STAGE_DKDV = 4, DSA_STAGE_FOLD = 8 };
@@ -111,10 +112,13 @@ typedef struct dsa_fwd_args {
   const int32_t* seg;     /* [B, L] segment ids or NULL (see Masks above) */
   int64_t seg_stride_b;
   /* Optional scratch of dsa_fwd_workspace_bytes(args) bytes (16-byte
-     aligned), used only under key_keep or seg: the forward then launches
+     aligned), for two things: under key_keep or seg, the forward launches
      its workgroups heaviest first (a small cost and sort pass before the
-     kernel).  NULL: the default order, same results.  Ignored by dsa_bwd,
-     which has its own workspace. */
+     kernel); with c2p / p2c, it reads a copy of kr / qr laid out by 64-byte
+     k-steps (one small copy kernel), whose row gathers touch half as many
+     cache lines.  NULL (or a scratch of only the launch order's bytes): the
+     default order and the caller's tables, same results.  Ignored by
+     dsa_bwd, which has its own workspace. */
   void* workspace;
   size_t workspace_bytes;
   /* Optional [B, Lq, H, D] (element strides qc_strides, D contiguous): the
@@ -147,7 +151,10 @@ typedef struct dsa_bwd_args {
   int64_t dv_strides[3];
   void* dkr;              /* [H, R, D] contiguous; NULL if !C2P */
   void* dqr;              /* [H, R, D] contiguous; NULL if !P2C */
-  /* workspace: dsa_bwd_workspace_bytes() bytes, caller-allocated */
+  /* workspace: dsa_bwd_workspace_bytes() bytes, caller-allocated, in
+     ordinary (coarse-grained) device memory such as hipMalloc returns: the
+     table-gradient accumulators in it take fp32 atomic adds, which
+     fine-grained or host-coherent memory does not support reliably */
   void* workspace;
   size_t workspace_bytes;
   int32_t stages;         /* DSA_STAGE_* mask; 0 = all */
@@ -207,9 +214,11 @@ size_t dsa_bwd_workspace_bytes(const dsa_bwd_args* args);
  * terms alive for autograd instead. */
 size_t dsa_fwd_bias_bytes(const dsa_fwd_args* args);
 
-/* Bytes of dsa_fwd_args.workspace for these arguments: nonzero only under
- * key_keep or seg (the heaviest-first launch order).  No counterpart in the
- * reference, whose eager path has no launch order to choose. */
+/* Bytes of dsa_fwd_args.workspace for these arguments: the heaviest-first
+ * launch order under key_keep or seg, then the k-step copies of kr / qr with
+ * c2p / p2c (0 without either).  No counterpart in the reference, whose
+ * eager path has no launch order to choose and reads its tables through
+ * torch's gathers. */
 size_t dsa_fwd_workspace_bytes(const dsa_fwd_args* args);
 
 /* Thread-local description of the last error (empty string if none). */

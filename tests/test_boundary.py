@@ -73,6 +73,29 @@ def test_argument_errors_return_codes_without_launching(lib):
     assert "unsupported dtype" in _lib.last_error()
 
 
+def test_forward_workspace_bytes(lib):
+    """The forward's optional scratch: the launch order under key-padding and
+    segment masks (two ints per (batch row, 128-query tile), 256-byte
+    aligned), then one k-step copy of each relative table in use
+    (H * 2A * D elements, 256-byte aligned); nothing without either."""
+    a = _lib.DsaFwdArgs()
+    a.B, a.H, a.Lq, a.Lk, a.D, a.dtype, a.att_span = 2, 12, 512, 512, 64, _lib.DSA_BF16, 256
+    a.flags = 0
+    assert lib.dsa_fwd_workspace_bytes(ctypes.byref(a)) == 0
+    table = 12 * 512 * 64 * 2
+    a.flags = _lib.DSA_C2P | _lib.DSA_P2C
+    assert lib.dsa_fwd_workspace_bytes(ctypes.byref(a)) == 2 * table
+    a.flags = _lib.DSA_P2C
+    assert lib.dsa_fwd_workspace_bytes(ctypes.byref(a)) == table
+    a.dtype = _lib.DSA_F32
+    assert lib.dsa_fwd_workspace_bytes(ctypes.byref(a)) == 2 * table
+    a.dtype, a.flags = _lib.DSA_BF16, _lib.DSA_C2P | _lib.DSA_P2C
+    kk = ctypes.create_string_buffer(2 * 512)
+    a.key_keep = ctypes.cast(kk, ctypes.c_void_p).value
+    order = (2 * 2 * 4 * 4 + 255) // 256 * 256  # cost and order of 2 x 4 items
+    assert lib.dsa_fwd_workspace_bytes(ctypes.byref(a)) == order + 2 * table
+
+
 C_LAYOUT_PROBE = r"""
 #include <stdio.h>
 #include <stddef.h>
