@@ -247,7 +247,22 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
       for (int e = 0; e < VEC; ++e) z[e] = (T)0.0f;
       static_assert(SW % VEC == 0, "whole chunks");
       for (int c = lane; c < SW / VEC; c += 64) reinterpret_cast<vecT*>(stg)[c] = z;
+      // without relative terms no saved term is copied in: the bias buffers
+      // hold zeros, so the scores add them unconditionally (no branch per
+      // product block)
+      if (!p.flags) {
+        typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+        constexpr int NCH = BE * (int)sizeof(BT) / 16;
+        for (int c = tid; c < NCH; c += 256) {
+          reinterpret_cast<u4*>(Bs0)[c] = u4{0u, 0u, 0u, 0u};
+          reinterpret_cast<u4*>(Bs1)[c] = u4{0u, 0u, 0u, 0u};
+        }
+      }
     }
+    // Unmasked workgroups whose 128 keys all lie below Lk: on query tiles
+    // below Lq every row is live and every pair kept, so P needs no keep
+    // test per element.
+    const bool keys_in = MASK == MASK_NONE && j0 + BKW <= Lk;
     // The qrgt ring holds blocks [qi, qi + 4] of the window (relative to
     // tw0 / 32) while tile qi is computed; block qi + 5 lands in the sixth
     // slot meanwhile when the next tile is qi + 1.  The first window:
@@ -332,9 +347,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
             acc = M::mma(qa[s], kf[jb][s], acc);
           {
             // rows 16*ib + 4*g + e of key column 32w + 16*jb + c16 (forward
-            // tile order).  The LDS read is issued whatever the flags (the
-            // buffer is in bounds; without relative terms it is not added),
-            // so it is not held behind a branch.
+            // tile order); without relative terms the buffer holds zeros
             const int jl = WK * w + 16 * jb;
             const int o = (jl / 64) * 2048 + ib * 1024 + ((jl % 64) / 16) * 256;
             if constexpr (sizeof(BT) == 2) {
@@ -342,16 +355,14 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
               typedef _Float16 h4 __attribute__((ext_vector_type(4)));
               const h4 v = __builtin_bit_cast(
                   h4, tr4_at(reinterpret_cast<const bf16*>(Bt) + o + (4 * g + (c16 >> 2)) * 16 + (c16 & 3) * 4));
-              if (p.flags)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf((float)v[e], one, acc[e]);
+              for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf((float)v[e], one, acc[e]);
             } else {
               float v[4];
 #pragma unroll
               for (int e = 0; e < 4; ++e) v[e] = Bt[o + (4 * g + e) * 16 + c16];
-              if (p.flags)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) acc[e] += v[e];
+              for (int e = 0; e < 4; ++e) acc[e] += v[e];
             }
           }
           sc[jb][ib] = acc;
@@ -361,32 +372,43 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
       __builtin_amdgcn_s_setprio(0);
       // ---- P, dP, dS -----------------------------------------------------------------------------
       f32x4 pp[2][BQ / 16], dsh[2][BQ / 16];
+      auto probs = [&](auto plain) {
 #pragma unroll
-      for (int ib = 0; ib < BQ / 16; ++ib) {
-        frag dof[NS];
+        for (int ib = 0; ib < BQ / 16; ++ib) {
+          frag dof[NS];
 #pragma unroll
-        for (int s = 0; s < NS; ++s) dof[s] = SQ::row_frag(dO, 16 * ib + c16, s, g);
+          for (int s = 0; s < NS; ++s) dof[s] = SQ::row_frag(dO, 16 * ib + c16, s, g);
 #pragma unroll
-        for (int jb = 0; jb < 2; ++jb) {
-          f32x4 dp = zero4();
+          for (int jb = 0; jb < 2; ++jb) {
+            f32x4 dp = zero4();
 #pragma unroll
-          for (int s = 0; s < NS; ++s)
-            dp = M::mma(dof[s], vf[jb][s], dp);
+            for (int s = 0; s < NS; ++s)
+              dp = M::mma(dof[s], vf[jb][s], dp);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int il = 16 * ib + 4 * g + e;
-            const float lr = R[2 * il];
-            // rows without probabilities (dead, padding) have lr = inf and may hold an
-            // unwritten saved term: they are never exponentiated
-            bool keep = jkeep[jb] && lr != INFINITY;
-            if (MASK == MASK_SEG && !full) keep = keep && qsg[n & 1][il] == jseg[jb];
-            if (MASK == MASK_PAIR) keep = keep && ((pmask[il][2 * w + jb] >> c16) & 1u);
-            const float pe = keep ? __builtin_amdgcn_exp2f(__builtin_fmaf(sc[jb][ib][e], sl2, -lr)) : 0.f;
-            pp[jb][ib][e] = pe;
-            dsh[jb][ib][e] = pe * (dp[e] - R[2 * il + 1]);
+            for (int e = 0; e < 4; ++e) {
+              const int il = 16 * ib + 4 * g + e;
+              const float lr = R[2 * il];
+              float pe;
+              if constexpr (decltype(plain)::value) {
+                pe = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[jb][ib][e], sl2, -lr));
+              } else {
+                // rows without probabilities (dead, padding) have lr = inf and may hold an
+                // unwritten saved term: they are never exponentiated
+                bool keep = jkeep[jb] && lr != INFINITY;
+                if (MASK == MASK_SEG && !full) keep = keep && qsg[n & 1][il] == jseg[jb];
+                if (MASK == MASK_PAIR) keep = keep && ((pmask[il][2 * w + jb] >> c16) & 1u);
+                pe = keep ? __builtin_amdgcn_exp2f(__builtin_fmaf(sc[jb][ib][e], sl2, -lr)) : 0.f;
+              }
+              pp[jb][ib][e] = pe;
+              dsh[jb][ib][e] = pe * (dp[e] - R[2 * il + 1]);
+            }
           }
         }
-      }
+      };
+      if (keys_in && i0 + BQ <= Lq)
+        probs(std::true_type{});
+      else
+        probs(std::false_type{});
       // dS^T of the tile into the wave's LDS tile (rows j), then dS rows to
       // the workspace, four consecutive keys per lane read transposed
 #pragma unroll

@@ -413,24 +413,53 @@ DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&
   // one mixed-precision FMA per element.  The uniform flag test sits
   // outside the loops.
   const float one = opaque_one();
-  // whether the term is saved: uniform (one pointer for the workgroup), so
-  // the stores sit behind a scalar branch
+  // c2p reads of a 16-bit band: the four elements at cbase + K (K a
+  // multiple of 16, so every read shares cbase's alignment) lie in three
+  // dwords from (cbase & ~3) + K; one byte selector per lane (by that
+  // alignment) picks the pairs (e = 0, 1) and (e = 2, 3) of bs below, which
+  // run down the band row (x descending), with one v_perm_b32 each.
+  typedef const __attribute__((address_space(3))) unsigned* lds_u32;
+  // (The base is moved 48 elements down, which keeps its alignment, so that
+  // every block's dword offset is non-negative: an immediate of the read.)
+  const lds_u32 cq = (lds_u32)((uintptr_t)(cbase - 48) & ~(uintptr_t)3);
+  const unsigned csel = ((uintptr_t)cbase & 2) ? 0x03020504u : 0x01000302u;
+  // Whether the term is saved is uniform (one pointer for the workgroup):
+  // the gather is compiled with and without the stores, so that no branch
+  // splits its eight blocks.
   const bool save = __builtin_amdgcn_readfirstlane(bias != nullptr ? 1 : 0) != 0;
-  auto gather = [&](auto with_c, auto with_p) {
+  auto gather = [&](auto with_c, auto with_p, auto with_s) {
+    typedef BT b4 __attribute__((ext_vector_type(4)));
+    typedef BT b2 __attribute__((ext_vector_type(2)));
 #pragma unroll
     for (int ib = 0; ib < 2; ++ib)
 #pragma unroll
       for (int jb = 0; jb < 4; ++jb) {
-        typedef BT b4 __attribute__((ext_vector_type(4)));
-        b4 cv;
-        if constexpr (decltype(with_c)::value) lds_read_elems<BT, 4>(cv, cbase + 16 * ib * CTS + 16 * (ib - jb));
         BT bs[4];
+        bool done = false;
+        if constexpr (sizeof(BT) == 2) {
+          if constexpr (decltype(with_c)::value) {
+            const int kd = (16 * ib * CTS + 16 * (ib - jb) + 48) / 2;
+            const unsigned d0 = cq[kd], d1 = cq[kd + 1], d2 = cq[kd + 2];
+            b2 hi = __builtin_bit_cast(b2, __builtin_amdgcn_perm(d2, d1, csel));  // elements 3, 2
+            b2 lo = __builtin_bit_cast(b2, __builtin_amdgcn_perm(d1, d0, csel));  // elements 1, 0
+            if constexpr (decltype(with_p)::value) {
+              hi = hi + b2{pbase[(16 * ib - 16 * jb) * PBT + 16 * jb], pbase[(16 * ib - 16 * jb - 1) * PBT + 16 * jb + 1]};
+              lo = lo + b2{pbase[(16 * ib - 16 * jb - 2) * PBT + 16 * jb + 2],
+                           pbase[(16 * ib - 16 * jb - 3) * PBT + 16 * jb + 3]};
+            }
+            bs[0] = hi[0], bs[1] = hi[1], bs[2] = lo[0], bs[3] = lo[1];
+            done = true;
+          }
+        }
+        if (!done) {
+          b4 cv;
+          if constexpr (decltype(with_c)::value) lds_read_elems<BT, 4>(cv, cbase + 16 * ib * CTS + 16 * (ib - jb));
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          BT v = (BT)0.0f;
-          if constexpr (decltype(with_c)::value) v = cv[3 - e];
-          if constexpr (decltype(with_p)::value) v = v + pbase[(16 * ib - 16 * jb - e) * PBT + 16 * jb + e];
-          bs[e] = v;
+          for (int e = 0; e < 4; ++e) {
+            const BT pv = decltype(with_p)::value ? pbase[(16 * ib - 16 * jb - e) * PBT + 16 * jb + e] : (BT)0.0f;
+            if constexpr (decltype(with_c)::value) bs[e] = decltype(with_p)::value ? cv[3 - e] + pv : cv[3 - e];
+            else bs[e] = pv;
+          }
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) y[ib][jb][e] = __builtin_fmaf((float)bs[e], one, y[ib][jb][e]);
@@ -440,14 +469,22 @@ DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&
         // them (ordinary stores leave the previous forward's term to be
         // written back from the caches meanwhile); one layer's forward
         // followed by its backward takes the same time either way.
-        if (save) __builtin_nontemporal_store(b4{bs[0], bs[1], bs[2], bs[3]}, reinterpret_cast<b4*>(bias + (ib * 4 + jb) * 256));
+        if constexpr (decltype(with_s)::value)
+          __builtin_nontemporal_store(b4{bs[0], bs[1], bs[2], bs[3]}, reinterpret_cast<b4*>(bias + (ib * 4 + jb) * 256));
       }
   };
   using yes = std::true_type;
   using no = std::false_type;
-  if ((flags & 3) == 3) gather(yes{}, yes{});
-  else if (flags & 1) gather(yes{}, no{});
-  else gather(no{}, yes{});
+  if ((flags & 3) == 3) {
+    if (save) gather(yes{}, yes{}, yes{});
+    else gather(yes{}, yes{}, no{});
+  } else if (flags & 1) {
+    if (save) gather(yes{}, no{}, yes{});
+    else gather(yes{}, no{}, no{});
+  } else {
+    if (save) gather(no{}, yes{}, yes{});
+    else gather(no{}, yes{}, no{});
+  }
 }
 
 }  // namespace dsa
