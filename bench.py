@@ -415,7 +415,11 @@ def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    # The GPU's clocks need about 60 to 80 steps (some 30 ms) of sustained
+    # load to settle: at B=32, L=512 the step takes 0.52 ms over the first 20
+    # steps of a process, 0.44 ms from the 80th on, and ramps again after an
+    # idle second.  The default warmup covers the ramp.
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument(
         "--workload",

@@ -10,8 +10,8 @@
 //                                    raised reference max
 //   O^T += V^T P^T                   MFMA, P fed from registers (ACC k-set),
 //                                    V^T read transposed from LDS
-// The next key tile is fetched into registers while the current one is
-// computed.
+// The next key tile is fetched into registers while the current one's
+// softmax and PV product run (requested after its band rows).
 //
 // The score tile is kept transposed (keys down, queries across) so that the
 // probabilities a lane holds are already the B operand of the PV product.
@@ -189,7 +189,7 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
   }
 
   // The next key tile (K and V rows) is fetched into registers while the
-  // current one is computed.
+  // current one's softmax and PV product run.
   vecT kr[KCH], vr[KCH];
   int relv = 0;  // this thread's relative position of the fetched tile (tid < XG)
   int ksn = 0;   // segment masks: this thread's key segment of the fetched tile (tid < BK)
@@ -212,6 +212,12 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
     kfetched = kt;
   };
   if (any_live && nlist > 0) fetch(SEGM ? __builtin_amdgcn_readfirstlane(klist[0]) : 0);
+  // The Q fragments and the first tile have landed before the loop (its
+  // first iteration waits for the tile anyway).  Without this wait the
+  // loads issued before the loop stay pending in the compiler's view of the
+  // loop, and the first score product of every tile waited for all
+  // outstanding loads: the next tile's prefetch included.
+  vm_wait<0>();
 
   for (int n = 0; any_live && n < nlist; ++n) {
     const int kt = SEGM ? __builtin_amdgcn_readfirstlane(klist[n]) : n;
@@ -243,6 +249,13 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
       if (!__syncthreads_or(keep != 0)) continue;
     }
     __syncthreads();  // previous tile's LDS reads are done
+    // Everything this wave requested in the previous tile has landed or been
+    // written by now (the prefetch and the saved-term stores were issued
+    // before its softmax and PV product).  Waiting here, unconditionally,
+    // tells the compiler so: with stores and loads both outstanding it
+    // cannot order them, and would otherwise wait for everything at the
+    // first reuse of a register that an earlier load wrote.
+    vm_wait<0>();
     if (kt != kfetched) fetch(kt);  // a tile after skipped ones was not prefetched
 #pragma unroll
     for (int k = 0; k < KCH; ++k) {
@@ -256,7 +269,6 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
     if (SEGM && tid < BK) ksg[tid] = ksn;
     if (p.flags) store_row_tables(crow, prow, relv, A, (int)p.krs[1], (int)p.qrs[1], tid);
     __syncthreads();
-    if (n + 1 < nlist) fetch(SEGM ? __builtin_amdgcn_readfirstlane(klist[n + 1]) : n + 1);
 
     // ---- y = K Q^T + c2p + p2c (unscaled) -------------------------------------
     frag kf[4][NS];
@@ -278,9 +290,17 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
         for (int s = 0; s < NS; ++s) acc = M::mma(kf[jb][s], qf[ib][s], acc);
         st[ib][jb] = acc;
       }
+    // The next tile is requested only after this tile's band rows have been
+    // waited for (a wave's vector-memory requests complete in issue order,
+    // so a request issued before them would be waited for with them) and
+    // before the saved-term stores (with stores outstanding the compiler
+    // cannot order the counts and waits for everything).  It has the gather,
+    // the softmax and the PV product to land.
     if (p.flags)
-      add_delta_bands_T<T, D, MASK == MASK_PAIR ? 3 : 6>(st, kf, pick<QC>(qcf, qf), cb, pb, crow, prow, w, g, c16, krh, qrh,
-                                                         p.krk, p.qrk, p.flags, biasl ? biasl + (int64_t)kt * 8192 : nullptr);
+      band_products_T<T, D, MASK == MASK_PAIR ? 3 : 6>(kf, pick<QC>(qcf, qf), cb, pb, crow, prow, w, g, c16, krh, qrh,
+                                                       p.krk, p.qrk, p.flags);
+    if (n + 1 < nlist) fetch(SEGM ? __builtin_amdgcn_readfirstlane(klist[n + 1]) : n + 1);
+    if (p.flags) band_gather_T<T, D>(st, cb, pb, w, g, c16, p.flags, biasl ? biasl + (int64_t)kt * 8192 : nullptr);
     __builtin_amdgcn_s_setprio(0);
 
     // ---- mask: only where a key or query of the tile can be masked out ------

@@ -343,14 +343,17 @@ DSA_DEV void store4_contig(B* p, const f32x4& v) {
 //   bias: if not null, where this lane's part of the tile's saved relative
 //         term goes (see bias_tile_offset): the unscaled c2p + p2c values,
 //         stored for the backward
-// Contains one __syncthreads (the p2c band is shared): call it from every
-// thread of the workgroup.
+// In two parts, so that a caller can issue loads between them:
+// band_products_T computes both bands into LDS (its table-row loads are all
+// waited for on return), band_gather_T (which begins with a __syncthreads:
+// the p2c band is shared) adds them to y and stores the saved term.  Call
+// both from every thread of the workgroup.
 template <typename T, int D, int GR>
-DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&kf)[4][D / Mfma<T>::KSTEP],
-                               const typename Mfma<T>::frag (&qf)[2][D / Mfma<T>::KSTEP],
-                               typename BandType<T>::type* cb, typename BandType<T>::type* pb, const int* crow,
-                               const int* prow, int w, int g, int c16, const T* krh, const T* qrh, int64_t krk,
-                               int64_t qrk, int flags, typename BandType<T>::type* bias = nullptr) {
+DSA_DEV void band_products_T(const typename Mfma<T>::frag (&kf)[4][D / Mfma<T>::KSTEP],
+                             const typename Mfma<T>::frag (&qf)[2][D / Mfma<T>::KSTEP],
+                             typename BandType<T>::type* cb, typename BandType<T>::type* pb, const int* crow,
+                             const int* prow, int w, int g, int c16, const T* krh, const T* qrh, int64_t krk,
+                             int64_t qrk, int flags) {
   using M = Mfma<T>;
   typedef typename M::frag frag;
   typedef typename BandType<T>::type BT;
@@ -402,6 +405,14 @@ DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&
       }
     }
   }
+}
+
+template <typename T, int D>
+DSA_DEV void band_gather_T(f32x4 (&y)[2][4], const typename BandType<T>::type* cb,
+                           const typename BandType<T>::type* pb, int w, int g, int c16, int flags,
+                           typename BandType<T>::type* bias) {
+  typedef typename BandType<T>::type BT;
+  using namespace dcfg;
   __syncthreads();
   // c2p: x - 32w = (16*ib + c16) - (16*jb + 4*g + e) + 63; the four e are
   // consecutive x (descending) of one query row
@@ -485,6 +496,16 @@ DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&
     if (save) gather(no{}, yes{}, yes{});
     else gather(no{}, yes{}, no{});
   }
+}
+
+template <typename T, int D, int GR>
+DSA_DEV void add_delta_bands_T(f32x4 (&y)[2][4], const typename Mfma<T>::frag (&kf)[4][D / Mfma<T>::KSTEP],
+                               const typename Mfma<T>::frag (&qf)[2][D / Mfma<T>::KSTEP],
+                               typename BandType<T>::type* cb, typename BandType<T>::type* pb, const int* crow,
+                               const int* prow, int w, int g, int c16, const T* krh, const T* qrh, int64_t krk,
+                               int64_t qrk, int flags, typename BandType<T>::type* bias = nullptr) {
+  band_products_T<T, D, GR>(kf, qf, cb, pb, crow, prow, w, g, c16, krh, qrh, krk, qrk, flags);
+  band_gather_T<T, D>(y, cb, pb, w, g, c16, flags, bias);
 }
 
 }  // namespace dsa
