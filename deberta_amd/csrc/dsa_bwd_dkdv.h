@@ -205,7 +205,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
         const int kk = pc / CPB;
         const BT* src = biasb + bias_tile_offset(b, h, p.H, i0 / 128, j0 / 64 + kk, p.LqP, p.LkP) +
                         ((i0 % 128) / 32) * 2048 + (pc % CPB) * (16 / (int)sizeof(BT));
-        lds_dma16(src, (char*)Bd + (w * BCW + 64 * k) * 16);
+        lds_dma16_nt(src, (char*)Bd + (w * BCW + 64 * k) * 16);  // read once: non-temporal
       }
     }
     if (w == 0 && lane < 2 * BQ * 4 / 16) lds_dma16(rib + 2 * i0 + 4 * lane, (char*)Rd);

@@ -131,7 +131,12 @@ DSA_DEV void dq_body(const BwdParams& bp, int blk, int nblk, DqLds<T, D>& L) {
 #pragma unroll
       for (int e = 0; e < VEC; ++e) sr[k][e] = (T)0.0f;
       if (c < SV && ((cmask >> (row / 32)) & 1))
-        sr[k] = *reinterpret_cast<const vecT*>(dsb + (int64_t)row * bp.f.LkP + j0 + (c % (BK / VEC)) * VEC);
+        // non-temporal: this kernel reads each dS element once, and the
+        // table kernel's band reads (in the same launch) keep the lines
+        // they share in the caches (full step 438 -> 427 us at the headline
+        // shape with the saved term's copies in dkdv also non-temporal)
+        sr[k] = __builtin_nontemporal_load(
+            reinterpret_cast<const vecT*>(dsb + (int64_t)row * bp.f.LkP + j0 + (c % (BK / VEC)) * VEC));
     }
 #pragma unroll
     for (int k = 0; k < KCH; ++k) {

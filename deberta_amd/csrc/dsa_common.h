@@ -258,6 +258,14 @@ DSA_DEV void lds_dma16(const void* src, void* lds_wave) {
       __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(__attribute__((address_space(3))) void*)lds_wave);
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
 }
+// The same copy with the non-temporal hint, for data read once (the
+// backward's pass over the saved relative term): the stream of it does not
+// displace reused lines from the caches.
+DSA_DEV void lds_dma16_nt(const void* src, void* lds_wave) {
+  const unsigned lds =
+      __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(__attribute__((address_space(3))) void*)lds_wave);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src), "s"(lds) : "memory", "m0");
+}
 // Waits until at most N of this wave's vector-memory instructions are
 // outstanding (they complete in issue order).
 template <int N>
