@@ -21,8 +21,10 @@ DSA_STAGE_PREP = 1
 DSA_STAGE_DQ = 2
 DSA_STAGE_DKDV = 4
 DSA_STAGE_FOLD = 8
+DSA_STAGE_TABLE = 16  # the first half of FOLD: per-offset sums (workspace)
+DSA_STAGE_SUM = 32  # the second half: their fold onto dkr / dqr
 
-EXPECTED_VERSION = 7
+EXPECTED_VERSION = 8
 
 _i64x3 = ctypes.c_int64 * 3
 _i64x2 = ctypes.c_int64 * 2

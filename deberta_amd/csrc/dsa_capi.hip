@@ -388,7 +388,9 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
   }
   // DQ and FOLD both only read dS: with both requested, the dq and table
   // workgroups run in one launch (dsa_bwd_dqtab.h) and share the GPU.
-  const bool fold = (stages & DSA_STAGE_FOLD) && f.flags;
+  // FOLD is TABLE (the table kernel) followed by SUM (the fold kernel).
+  const bool fold = (stages & (DSA_STAGE_FOLD | DSA_STAGE_TABLE)) && f.flags;
+  const bool sum = (stages & (DSA_STAGE_FOLD | DSA_STAGE_SUM)) && f.flags;
   const bool dq = (stages & DSA_STAGE_DQ) != 0;
   // dKr sums dS_ij times the c2p term's query rows: qc when it is given
   dsa::BwdParams tp = bp;
@@ -424,7 +426,7 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
       hipLaunchKernelGGL((dsa::dsa_bwd_dq_kernel<T, D, false>), dim3(ndq), dim3(256), 0, st, bp);
     if (launch_check("dsa_bwd_dq_kernel")) return 1;
   }
-  if (fold) {
+  if (sum) {
     const dim3 fg((unsigned)(2 * f.H * (2 * f.att_span)));
     if (f.Lq + f.Lk > 2048)  // long rows of saturated relative positions: four waves a row
       hipLaunchKernelGGL((dsa::dsa_bwd_fold_kernel<D, 256>), fg, dim3(256), 0, st, bp);
@@ -670,7 +672,7 @@ dsa::rows::RtdParams rtd_params(const dsa_rtd_args* a) {
 
 extern "C" {
 
-int dsa_version(void) { return 7; }
+int dsa_version(void) { return 8; }
 
 const char* dsa_last_error(void) { return g_err.c_str(); }
 

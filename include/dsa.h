@@ -72,11 +72,21 @@ enum { DSA_C2P = 1, DSA_P2C = 2 };
  *   PREP  rowsum(dO * O) and the relative tables gathered per offset
  *   DKDV  writes dv, dk and dS^T (into the workspace)
  *   DQ    writes dq from dS^T
- *   FOLD  adds the relative-table gradients (from dS^T) into dkr / dqr
- * DQ and FOLD requested in one call run their main kernels as one launch.
- * Stages run in separate calls must keep this order and share one
- * workspace. */
-enum { DSA_STAGE_PREP = 1, DSA_STAGE_DQ = 2, DSA_STAGE_DKDV = 4, DSA_STAGE_FOLD = 8 };
+ *   FOLD  adds the relative-table gradients (from dS^T) into dkr / dqr;
+ *         it is TABLE (the per-offset sums, kept in the workspace) followed
+ *         by SUM (their fold onto table rows, written to dkr / dqr), which
+ *         may also be requested on their own, in that order
+ * DQ and FOLD (or DQ and TABLE) requested in one call run their main
+ * kernels as one launch.  Stages run in separate calls must keep this
+ * order and share one workspace.  (Version 8: TABLE and SUM.) */
+enum {
+  DSA_STAGE_PREP = 1,
+  DSA_STAGE_DQ = 2,
+  DSA_STAGE_DKDV = 4,
+  DSA_STAGE_FOLD = 8,
+  DSA_STAGE_TABLE = 16,
+  DSA_STAGE_SUM = 32
+};
 
 typedef struct dsa_fwd_args {
   const void* q;          /* [B, Lq, H, D] */

@@ -184,3 +184,59 @@ def test_device_bucket_table_matches_oracle(buckets, max_pos, gpu):
     _say(f"[bucket table {buckets}/{max_pos}] values at the edges {edge}")
     assert torch.equal(dev, want)
     assert edge[L - 1] == edge[max_pos - 1] == -int(dev[0])  # saturated, odd
+
+
+@pytest.mark.parametrize(
+    "split",
+    [
+        ("PREP", "DKDV", "DQ|TABLE", "SUM"),
+        ("PREP", "DKDV", "DQ", "TABLE", "SUM"),
+        ("PREP", "DKDV", "DQ", "FOLD"),
+        ("PREP", "DKDV", "DQ|FOLD"),
+    ],
+    ids=["dqtable-sum", "dq-table-sum", "dq-fold", "dqfold"],
+)
+def test_backward_stages_in_separate_calls(split, gpu):
+    """dsa_bwd run as separate stage calls (include/dsa.h: PREP, DKDV, DQ,
+    FOLD = TABLE then SUM) gives the one-call backward's results: dq, dk, dv
+    bitwise; dkr, dqr up to the order of their fp32 atomic additions."""
+    import ctypes
+
+    from deberta_amd import _lib, ops
+
+    lib = _lib.load()
+    B, L, H, D, A = 2, 256, 4, 64, 256
+    g = torch.Generator().manual_seed(31)
+    mk = lambda *s: torch.randn(*s, generator=g).to(gpu, torch.bfloat16)
+    q, k, v, dout = mk(B, L, H, D), mk(B, L, H, D), mk(B, L, H, D), mk(B, L, H, D)
+    kr, qr = mk(H, 2 * A, D), mk(H, 2 * A, D)
+    table = relative_offset_table(L, L, bucket_size=256, max_position=512, device=gpu)
+    scale = 1 / math.sqrt(D * 3)
+    out, lse, bias = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, A, scale)
+    stream = ctypes.c_void_p(torch.cuda.current_stream(gpu).cuda_stream)
+    bits = {"PREP": _lib.DSA_STAGE_PREP, "DQ": _lib.DSA_STAGE_DQ, "DKDV": _lib.DSA_STAGE_DKDV,
+            "FOLD": _lib.DSA_STAGE_FOLD, "TABLE": _lib.DSA_STAGE_TABLE, "SUM": _lib.DSA_STAGE_SUM}
+
+    def run(calls):
+        grads = [torch.full_like(q, float("nan")) for _ in range(3)]
+        tabs = [torch.zeros((H, 2 * A, D), dtype=torch.float32, device=gpu) for _ in range(2)]
+        a = ops.fill_bwd_args(dout, q, k, v, kr, qr, table, None, None, out, lse, bias, A, scale, *grads, *tabs)
+        ws = torch.empty((ops.bwd_workspace_bytes(a),), dtype=torch.uint8, device=gpu)
+        a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+        for c in calls:
+            a.stages = 0
+            for s in c.split("|") if c else []:
+                a.stages |= bits[s]
+            _lib.check(lib.dsa_bwd(ctypes.byref(a), stream), "dsa_bwd")
+        torch.cuda.synchronize(gpu)
+        return grads + tabs
+
+    _say(f"[stages] split {'/'.join(split)}")
+    ref = run([""])
+    got = run(list(split))
+    for name, a, b in zip(["dq", "dk", "dv", "dkr", "dqr"], got, ref):
+        if name in ("dkr", "dqr"):
+            err = float((a - b).abs().max() / b.abs().max().clamp_min(1e-30))
+            assert err <= 1e-5, f"{name} differs from the one-call backward ({err:.3e})"
+        else:
+            assert torch.equal(a, b), f"{name} differs from the one-call backward"
