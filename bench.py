@@ -122,6 +122,45 @@ def mfma_peak_probe(dev) -> dict:
     return {"tflops": round(flops / (best * 1e-3) / 1e12, 1), "cus": cus, "workgroups": wgs, "ms": round(best, 4)}
 
 
+class HipEvents:
+    """HIP timing events without the system-scope fence (the runtime's
+    hipEventDisableSystemFence flag): torch's events write back and
+    invalidate the caches when recorded, which leaves a gap of about 6 us
+    before the next kernel and slows it, so an event between every two
+    kernels would inflate each kernel's time.  These only timestamp the
+    stream; nothing reads data through them."""
+
+    DISABLE_SYSTEM_FENCE = 0x20000000
+
+    def __init__(self, n: int):
+        self.rt = ctypes.CDLL("libamdhip64.so")  # the runtime torch has loaded
+        self.rt.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+        self.rt.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.rt.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.rt.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.ev = []
+        for _ in range(n):
+            e = ctypes.c_void_p()
+            if self.rt.hipEventCreateWithFlags(ctypes.byref(e), self.DISABLE_SYSTEM_FENCE) != 0:
+                raise RuntimeError("hipEventCreateWithFlags failed")
+            self.ev.append(e)
+
+    def record(self, i: int, stream_ptr: int) -> None:
+        if self.rt.hipEventRecord(self.ev[i], ctypes.c_void_p(stream_ptr)) != 0:
+            raise RuntimeError("hipEventRecord failed")
+
+    def ms(self, i: int, j: int) -> float:
+        """Milliseconds from event i to event j (both complete)."""
+        t = ctypes.c_float()
+        if self.rt.hipEventElapsedTime(ctypes.byref(t), self.ev[i], self.ev[j]) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return t.value
+
+    def __del__(self):
+        for e in getattr(self, "ev", []):
+            self.rt.hipEventDestroy(e)
+
+
 def flops_fwd(b: int, l: int, h: int, d: int, r: int) -> float:
     return 4.0 * b * h * d * l * l + 4.0 * b * h * d * l * r
 
@@ -505,15 +544,16 @@ def main() -> None:
         t0 = time.perf_counter()
         # an event between consecutive steps: per-step times for the median
         # and p10 / p90, and their span for the mean over exactly K steps
-        evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
-        evs[0].record()
+        sp = torch.cuda.current_stream(dev).cuda_stream
+        evs = HipEvents(args.steps + 1)
+        evs.record(0, sp)
         for n_ in range(args.steps):
             step()
-            evs[n_ + 1].record()
+            evs.record(n_ + 1, sp)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        ms_step = evs[0].elapsed_time(evs[-1]) / args.steps
-        per_step = sorted(evs[n_].elapsed_time(evs[n_ + 1]) for n_ in range(args.steps))
+        ms_step = evs.ms(0, args.steps) / args.steps
+        per_step = sorted(evs.ms(n_, n_ + 1) for n_ in range(args.steps))
         pct = lambda f: per_step[min(len(per_step) - 1, int(round(f * (len(per_step) - 1))))]
         ms_median, ms_p10, ms_p90 = pct(0.5), pct(0.1), pct(0.9)
     f_fwd = flops_fwd(B, L, H, D, R)
@@ -570,16 +610,17 @@ def main() -> None:
     for _ in range(20):  # keeps the clocks settled between the two timed loops
         for _, fn, _ in staged:
             fn()
-    evk = [[torch.cuda.Event(enable_timing=True) for _ in range(len(staged) + 1)] for _ in range(n_k)]
+    ns_ = len(staged) + 1
+    evk = HipEvents(n_k * ns_)
     for n_ in range(n_k):
-        evk[n_][0].record(stream)
+        evk.record(n_ * ns_, stream.cuda_stream)
         for i_, (_, fn, _) in enumerate(staged):
             fn()
-            evk[n_][i_ + 1].record(stream)
+            evk.record(n_ * ns_ + i_ + 1, stream.cuda_stream)
     torch.cuda.synchronize()
     per_kernel = {}
     for i_, (name, _, fl) in enumerate(staged):
-        ms = sum(e[i_].elapsed_time(e[i_ + 1]) for e in evk) / n_k
+        ms = sum(evk.ms(n_ * ns_ + i_, n_ * ns_ + i_ + 1) for n_ in range(n_k)) / n_k
         per_kernel[name] = {"ms": round(ms, 5), "tflops": round(fl / (ms * 1e-3) / 1e12, 2) if fl else None}
     flops_of = {name: fl for name, _, fl in staged}
     # the dq and table kernels launched apart (each alone, back to back):
