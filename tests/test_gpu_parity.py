@@ -50,6 +50,7 @@ def _check(c: Case, dtype: torch.dtype, gpu, grads: bool = True) -> dict:
     "c",
     [
         Case(B=2, H=12, L=512, D=64),  # config-2 shape, 2 batch rows
+        Case(B=32, H=12, L=512, D=64, seed=9),  # the benchmark's full shape (B=32)
         Case(B=1, H=2, L=200, D=64, seed=1),  # ragged tiles
         Case(B=2, H=3, L=130, D=64, types="c2p", seed=2),
         Case(B=2, H=3, L=130, D=64, types="p2c", seed=3),
