@@ -456,24 +456,28 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_table_kernel(BwdParams bp) {
 }
 
 // tab[h][r][:] (+)= s * sum over offsets d with row(d) = r of the block
-// accumulators (accumulated into fp32, or written in fp32 or bf16).  One
-// workgroup of NT threads per (table, h, r): NT / (D/4) parts split the
-// units of the row's offset range [begin, end) (from
-// prep_segments), each part with four independent sums so that four loads
-// are in flight; lanes of a part hold 4 columns each.  The parts are summed
-// with lane shuffles and, across waves, through LDS in a fixed order.  Long
-// sequences use NT = 256: the rows where the relative position saturates
-// then hold thousands of offsets.
-template <int D, int NT>
-__global__ __launch_bounds__(NT) void dsa_bwd_fold_kernel(BwdParams bp) {
+// accumulators (accumulated into fp32, or written in fp32 or bf16).  WPR
+// waves per (table, h, r), 256 / (64 WPR) rows per workgroup: the WPR * 64
+// / (D/4) parts of a row split the units of its offset range [begin, end)
+// (from prep_segments), each part with four independent sums so that four
+// loads are in flight; lanes of a part hold 4 columns each.  The parts are
+// summed with lane shuffles and, across waves, through LDS in a fixed
+// order.  Long sequences use WPR = 4: the rows where the relative position
+// saturates then hold thousands of offsets; short ones one wave a row, four
+// rows a workgroup (a quarter of the workgroups to launch).
+template <int D, int WPR>
+__global__ __launch_bounds__(256) void dsa_bwd_fold_kernel(BwdParams bp) {
   using namespace tbcfg;
   const FwdParams& p = bp.f;
   const int R = 2 * p.A;
-  constexpr int Q4 = D / 4, NP = NT / Q4, NWV = NT / 64;
-  const int t = blockIdx.x / (p.H * R), h = (blockIdx.x / R) % p.H, r = blockIdx.x % R;
+  constexpr int NT = 64 * WPR;  // threads of one row
+  constexpr int Q4 = D / 4, NP = NT / Q4, NWV = WPR;
+  const int unit = blockIdx.x * (4 / WPR) + (int)(threadIdx.x / NT);
+  if (unit >= 2 * p.H * R) return;  // uniform over a row's waves
+  const int t = unit / (p.H * R), h = (unit / R) % p.H, r = unit % R;
   if (!(p.flags & (1 << t))) return;
   const bool q = t == 1;  // false: dKr (c2p), true: dQr (p2c)
-  const int c4 = threadIdx.x % Q4, part = threadIdx.x / Q4;
+  const int c4 = threadIdx.x % Q4, part = (threadIdx.x % NT) / Q4;
   const int beg = bp.rowseg[(2 * t) * R + r], end = bp.rowseg[(2 * t + 1) * R + r];
   // The range splits into single offsets at its ends and whole offset
   // blocks between them (stored summed by the table kernel, row 0).

@@ -427,11 +427,11 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
     if (launch_check("dsa_bwd_dq_kernel")) return 1;
   }
   if (sum) {
-    const dim3 fg((unsigned)(2 * f.H * (2 * f.att_span)));
+    const int rows = 2 * f.H * (2 * f.att_span);
     if (f.Lq + f.Lk > 2048)  // long rows of saturated relative positions: four waves a row
-      hipLaunchKernelGGL((dsa::dsa_bwd_fold_kernel<D, 256>), fg, dim3(256), 0, st, bp);
-    else
-      hipLaunchKernelGGL((dsa::dsa_bwd_fold_kernel<D, 64>), fg, dim3(64), 0, st, bp);
+      hipLaunchKernelGGL((dsa::dsa_bwd_fold_kernel<D, 4>), dim3((unsigned)rows), dim3(256), 0, st, bp);
+    else  // one wave a row, four rows a workgroup
+      hipLaunchKernelGGL((dsa::dsa_bwd_fold_kernel<D, 1>), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, bp);
     if (launch_check("dsa_bwd_fold_kernel")) return 1;
   }
   return 0;
