@@ -790,6 +790,8 @@ size_t dsa_bwd_workspace_bytes(const dsa_bwd_args* a) {
 int dsa_bwd(const dsa_bwd_args* a, void* stream) {
   g_err.clear();
   if (!a) return fail("dsa: null arguments");
+  constexpr int kStages = DSA_STAGE_PREP | DSA_STAGE_DQ | DSA_STAGE_DKDV | DSA_STAGE_FOLD | DSA_STAGE_TABLE | DSA_STAGE_SUM;
+  if (a->stages & ~kStages) return fail("dsa: unknown backward stage bits 0x%x", (unsigned)(a->stages & ~kStages));
   if (check_fwd(&a->fwd)) return 1;
   const dsa_fwd_args& f = a->fwd;
   if (!a->dout || !a->dq || !a->dk || !a->dv) return fail("dsa: dout, dq, dk and dv are required");

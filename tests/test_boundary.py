@@ -73,6 +73,19 @@ def test_argument_errors_return_codes_without_launching(lib):
     assert "unsupported dtype" in _lib.last_error()
 
 
+def test_backward_stage_bits(lib):
+    """The stage constants of include/dsa.h and the package agree, and bits
+    outside them are refused before any device work."""
+    text = (ROOT / "include" / "dsa.h").read_text()
+    found = dict((m.group(1), int(m.group(2))) for m in re.finditer(r"(DSA_STAGE_[A-Z]+) = (\d+)", text))
+    assert found == {n: getattr(_lib, n) for n in found}
+    assert set(found) == {"DSA_STAGE_PREP", "DSA_STAGE_DQ", "DSA_STAGE_DKDV", "DSA_STAGE_FOLD", "DSA_STAGE_TABLE", "DSA_STAGE_SUM"}
+    a = _lib.DsaBwdArgs()
+    a.stages = 64
+    assert lib.dsa_bwd(ctypes.byref(a), None) != 0
+    assert "unknown backward stage bits 0x40" in _lib.last_error()
+
+
 def test_forward_workspace_bytes(lib):
     """The forward's optional scratch: the launch order under key-padding and
     segment masks (two ints per (batch row, 128-query tile), 256-byte
