@@ -457,7 +457,8 @@ def main() -> None:
     # The GPU's clocks need about 60 to 80 steps (some 30 ms) of sustained
     # load to settle: at B=32, L=512 the step takes 0.52 ms over the first 20
     # steps of a process, 0.44 ms from the 80th on, and ramps again after an
-    # idle second.  The default warmup covers the ramp.
+    # idle second.  The per-kernel timing runs before the timed steps and
+    # covers the ramp; the warm-up steps follow it.
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument(
@@ -530,35 +531,15 @@ def main() -> None:
         torch.cuda.synchronize()
         del src_t, dst_t
 
-    ms_step = wall = ms_median = ms_p10 = ms_p90 = float("nan")
     if args.kernels_only:
         # the same sustained load before the per-kernel timing as in a full
         # run (the GPU's clocks settle under it)
         for _ in range(args.warmup + args.steps):
             step()
         torch.cuda.synchronize()
-    else:
-        for _ in range(args.warmup):
-            step()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        # an event between consecutive steps: per-step times for the median
-        # and p10 / p90, and their span for the mean over exactly K steps
-        sp = torch.cuda.current_stream(dev).cuda_stream
-        evs = HipEvents(args.steps + 1)
-        evs.record(0, sp)
-        for n_ in range(args.steps):
-            step()
-            evs.record(n_ + 1, sp)
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-        ms_step = evs.ms(0, args.steps) / args.steps
-        per_step = sorted(evs.ms(n_, n_ + 1) for n_ in range(args.steps))
-        pct = lambda f: per_step[min(len(per_step) - 1, int(round(f * (len(per_step) - 1))))]
-        ms_median, ms_p10, ms_p90 = pct(0.5), pct(0.1), pct(0.9)
+
     f_fwd = flops_fwd(B, L, H, D, R)
     f_step = 3 * f_fwd
-    tflops = f_step / (ms_step * 1e-3) / 1e12
     # masked work counted over kept pairs and live rows only (the skipped
     # pairs are not work): 3 x (4 H D kept + 4 H D R live)
     f_kept = 3.0 * H * D * (4.0 * kept_pairs + 4.0 * R * live_rows)
@@ -607,7 +588,10 @@ def main() -> None:
         ("dsa_bwd_fold_kernel", run_stage(_lib.DSA_STAGE_SUM), 0.0),
     ]
     n_k = args.steps if args.kernels_only else max(10, args.steps)
-    for _ in range(20):  # keeps the clocks settled between the two timed loops
+    # Sustained load before the per-kernel timing: 100 stage-split steps
+    # (about 45 ms) bring the clocks of a fresh process to their settled
+    # level; with --kernels-only the op's steps above already did.
+    for _ in range(20 if args.kernels_only else 100):
         for _, fn, _ in staged:
             fn()
     ns_ = len(staged) + 1
@@ -647,6 +631,34 @@ def main() -> None:
     if args.kernels_only:
         print(json.dumps({"per_kernel": per_kernel, "per_kernel_alone": per_kernel_alone}), flush=True)
         return
+
+    # ---- the timed steps ----------------------------------------------------------
+    # They run after the per-kernel timing above, whose stage calls keep the
+    # GPU under sustained load for about 30 ms: its clocks take some 80 steps
+    # to settle after a process starts (0.52 ms a step over the first 20, 0.44
+    # from the 80th on), so the W warm-up steps alone would time the ramp when
+    # W is small.  The timed region itself is exactly W untimed and K timed
+    # fwd+bwd steps of the op.
+    ms_step = wall = ms_median = ms_p10 = ms_p90 = float("nan")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    # an event between consecutive steps: per-step times for the median
+    # and p10 / p90, and their span for the mean over exactly K steps
+    sp = torch.cuda.current_stream(dev).cuda_stream
+    evs = HipEvents(args.steps + 1)
+    evs.record(0, sp)
+    for n_ in range(args.steps):
+        step()
+        evs.record(n_ + 1, sp)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = evs.ms(0, args.steps) / args.steps
+    per_step = sorted(evs.ms(n_, n_ + 1) for n_ in range(args.steps))
+    pct = lambda f: per_step[min(len(per_step) - 1, int(round(f * (len(per_step) - 1))))]
+    ms_median, ms_p10, ms_p90 = pct(0.5), pct(0.1), pct(0.9)
+    tflops = f_step / (ms_step * 1e-3) / 1e12
     if not headline:
         # reference figures of another shape: not the metric (no roofline or
         # CPU leg; per-kernel TFLOP/s use the dense counts)

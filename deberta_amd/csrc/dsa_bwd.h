@@ -26,7 +26,7 @@
 //          onto table rows
 #pragma once
 
-#include "dsa_tiles.h"
+#include "dsa_order.h"
 
 namespace dsa {
 
@@ -168,12 +168,20 @@ DSA_DEV void prep_zero(const BwdParams& bp, int64_t gacc_floats, int blk) {
 }
 
 struct PrepBlocks {
-  int gather, seg, chunk, zero, delta;
+  int order, order_ny, gather, seg, chunk, zero, delta;
   int64_t gacc_floats;
 };
+// Blocks: the launch orders' cost blocks (dsa_order.h; batch row fastest,
+// then the tile group, then the job) first, then gather, segments, chunk
+// summaries, zeroing and rowinfo.
 template <typename T, int D>
-__global__ __launch_bounds__(256) void dsa_bwd_prep_kernel(BwdParams bp, PrepBlocks nb) {
-  const int blk = blockIdx.x;
+__global__ __launch_bounds__(256) void dsa_bwd_prep_kernel(BwdParams bp, PrepBlocks nb, OrderParams2 op2) {
+  if ((int)blockIdx.x < nb.order) {
+    const int k = blockIdx.x, B = op2.f.B;
+    order_cost_block(op2, k % B, (k / B) % nb.order_ny, k / (B * nb.order_ny));
+    return;
+  }
+  const int blk = blockIdx.x - nb.order;
   if (blk < nb.gather) {
     prep_gather<T, D>(bp, blk);
   } else if (blk < nb.gather + nb.seg) {

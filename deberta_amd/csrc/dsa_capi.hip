@@ -188,12 +188,14 @@ size_t order_bytes(const dsa_fwd_args* a, int ntiles) {
   return align_up((size_t)2 * n * sizeof(int), 256);
 }
 
-// Up to two heaviest-first orders (dsa_order.h) in two launches, cost then
-// sort: each job a buffer of cost then order (B * ntiles ints each), its
-// tiles per row and its cost kind.
-int launch_orders(const dsa::FwdParams& p, int njobs, int* const* bufs, const int* ntiles, const bool* fwd,
-                  hipStream_t st) {
-  dsa::OrderParams2 op;
+// Up to two heaviest-first orders (dsa_order.h): each job a buffer of cost
+// then order (B * ntiles ints each), its tiles per row and its cost kind.
+// fill_orders sets up the launches' parameters and the number of cost
+// blocks (batch row fastest, then the tile group, then the job);
+// launch_orders runs the cost and sort kernels, a caller that runs the cost
+// blocks inside another launch only the sort (launch_order_sort).
+int fill_orders(const dsa::FwdParams& p, int njobs, int* const* bufs, const int* ntiles, const bool* fwd,
+                dsa::OrderParams2& op, int& ny) {
   op.f = p;
   op.njobs = njobs;
   int maxt = 0;
@@ -205,11 +207,24 @@ int launch_orders(const dsa::FwdParams& p, int njobs, int* const* bufs, const in
     op.job[j].fwd = fwd[jj] ? 1 : 0;
     maxt = std::max(maxt, ntiles[jj]);
   }
-  const dim3 grid((unsigned)p.B, (unsigned)((maxt + dsa::ORDER_TPB - 1) / dsa::ORDER_TPB), (unsigned)njobs);
-  hipLaunchKernelGGL(dsa::dsa_order_cost_kernel, grid, dim3(256), 0, st, op);
-  if (launch_check("dsa_order_cost_kernel")) return 1;
+  ny = (maxt + dsa::ORDER_TPB - 1) / dsa::ORDER_TPB;
+  return p.B * ny * njobs;
+}
+
+int launch_order_sort(const dsa::OrderParams2& op, hipStream_t st) {
   hipLaunchKernelGGL(dsa::dsa_order_sort_kernel, dim3(1), dim3(1024), 0, st, op);
   return launch_check("dsa_order_sort_kernel");
+}
+
+int launch_orders(const dsa::FwdParams& p, int njobs, int* const* bufs, const int* ntiles, const bool* fwd,
+                  hipStream_t st) {
+  dsa::OrderParams2 op;
+  int ny = 0;
+  fill_orders(p, njobs, bufs, ntiles, fwd, op, ny);
+  const dim3 grid((unsigned)p.B, (unsigned)ny, (unsigned)njobs);
+  hipLaunchKernelGGL(dsa::dsa_order_cost_kernel, grid, dim3(256), 0, st, op);
+  if (launch_check("dsa_order_cost_kernel")) return 1;
+  return launch_order_sort(op, st);
 }
 
 int fwd_tiles(const dsa_fwd_args* a) { return (a->Lq + dsa::dcfg::BQ - 1) / dsa::dcfg::BQ; }
@@ -341,7 +356,22 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
       a->stages ? a->stages : (DSA_STAGE_PREP | DSA_STAGE_DQ | DSA_STAGE_DKDV | DSA_STAGE_FOLD);
 
   if (stages & DSA_STAGE_PREP) {
+    // dkdv's key tiles against 32-query chunks; dq's tiles (128 queries
+    // against 64-key tiles) weigh as the forward's.  Their cost blocks run
+    // first in the prep launch, the sort after it.
+    int* bufs[2];
+    int nts[2];
+    bool kinds[2];
+    int nj = 0;
+    if (kbuf) bufs[nj] = kbuf, nts[nj] = nkt, kinds[nj++] = false;
+    if (qbuf) bufs[nj] = qbuf, nts[nj] = nqt, kinds[nj++] = true;
+    dsa::OrderParams2 op;
+    op.f = bp.f;
+    op.njobs = 0;
     dsa::PrepBlocks nb;
+    nb.order = 0;
+    nb.order_ny = 1;
+    if (nj) nb.order = fill_orders(bp.f, nj, bufs, nts, kinds, op, nb.order_ny);
     const int64_t n = (int64_t)f.B * f.H * ws.LqP * (D / (16 / (int)sizeof(T)));
     nb.delta = (int)((n + 255) / 256);
     nb.gather = nb.seg = nb.chunk = nb.zero = 0;
@@ -357,17 +387,10 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
       nb.zero = (int)((nb.gacc_floats / 4 + 255) / 256);
     }
     hipLaunchKernelGGL((dsa::dsa_bwd_prep_kernel<T, D>),
-                       dim3((unsigned)(nb.gather + nb.seg + nb.chunk + nb.zero + nb.delta)), dim3(256), 0, st, bp, nb);
+                       dim3((unsigned)(nb.order + nb.gather + nb.seg + nb.chunk + nb.zero + nb.delta)), dim3(256), 0, st,
+                       bp, nb, op);
     if (launch_check("dsa_bwd_prep_kernel")) return 1;
-    // dkdv's key tiles against 32-query chunks; dq's tiles (128 queries
-    // against 64-key tiles) weigh as the forward's
-    int* bufs[2];
-    int nts[2];
-    bool kinds[2];
-    int nj = 0;
-    if (kbuf) bufs[nj] = kbuf, nts[nj] = nkt, kinds[nj++] = false;
-    if (qbuf) bufs[nj] = qbuf, nts[nj] = nqt, kinds[nj++] = true;
-    if (nj && launch_orders(bp.f, nj, bufs, nts, kinds, st)) return 1;
+    if (nj && launch_order_sort(op, st)) return 1;
   }
   if (stages & DSA_STAGE_DKDV) {
     dim3 grid((unsigned)(ws.LkP / dsa::kvcfg::BKW * f.H * f.B));
@@ -489,8 +512,25 @@ int run_fwd(const dsa_fwd_args* a, int* order_buf, void* tab_buf, hipStream_t st
     }
     t.H = a->H, t.R = R, t.D = a->D, t.esize = elem_bytes(a->dtype);
     const int64_t n = (int64_t)a->H * R * a->D * t.esize / 16;
-    hipLaunchKernelGGL(dsa::dsa_table_ks_kernel, dim3((unsigned)((n + 255) / 256), 2), dim3(256), 0, st, t);
-    if (launch_check("dsa_table_ks_kernel")) return 1;
+    const int ncopy = (int)((n + 255) / 256);
+    if (order_buf) {
+      // the order's cost blocks in the same launch as the copies; the sort after it
+      int* bufs[1] = {order_buf};
+      const int nts[1] = {fwd_tiles(a)};
+      const bool kinds[1] = {true};
+      dsa::OrderParams2 op;
+      int ny = 0;
+      const int ncost = fill_orders(p, 1, bufs, nts, kinds, op, ny);
+      hipLaunchKernelGGL(dsa::dsa_fwd_pre_kernel, dim3((unsigned)(ncost + 2 * ncopy)), dim3(256), 0, st, t, op, ncost,
+                         ncopy);
+      if (launch_check("dsa_fwd_pre_kernel")) return 1;
+      if (launch_order_sort(op, st)) return 1;
+      p.order = order_buf + (int64_t)a->B * fwd_tiles(a);
+      order_buf = nullptr;  // done
+    } else {
+      hipLaunchKernelGGL(dsa::dsa_table_ks_kernel, dim3((unsigned)ncopy, 2), dim3(256), 0, st, t);
+      if (launch_check("dsa_table_ks_kernel")) return 1;
+    }
     // the bands read the copies: head stride NS * R * KS, row stride KS,
     // k-step stride R * KS
     const int64_t hs = (int64_t)(a->D / ks) * R * ks;

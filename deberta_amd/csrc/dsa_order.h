@@ -19,6 +19,11 @@
 //   dsa_order_sort_kernel  one block: a counting sort of the (batch row,
 //                          tile) items by cost, heaviest first
 //
+// The cost blocks also run inside other launches that precede the order's
+// use: the forward's table copy (dsa_fwd_pre_kernel) and the backward's
+// preparation (dsa_bwd_prep_kernel), so that only the sort is a launch of
+// its own.
+//
 // Both take up to two orders at once (the backward's dkdv and dq orders):
 // launches of a few microseconds each dominate at C4 sizes.
 //
@@ -101,11 +106,13 @@ struct OrderParams2 {
 
 constexpr int ORDER_TPB = 4;  // tiles per cost block (one wave each)
 
-__global__ __launch_bounds__(256) void dsa_order_cost_kernel(OrderParams2 op2) {
+// Cost block (batch row b, tiles 4 by .. 4 by + 3, job jb) of 256 threads.
+// Holds a barrier: every thread of the block calls it.
+DSA_DEV void order_cost_block(const OrderParams2& op2, int b, int by, int jb) {
   const FwdParams& p = op2.f;
-  const OrderJob& op = op2.job[blockIdx.z];
+  const OrderJob& op = op2.job[jb];
   __shared__ int clo[ORDER_MAX_CHUNKS], chi[ORDER_MAX_CHUNKS];
-  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int L = p.Lk;  // masks need Lq == Lk
   const int nch = (L + 31) / 32;
   // chunk ranges: eight lanes per chunk, four tokens a lane; all of a
@@ -146,7 +153,7 @@ __global__ __launch_bounds__(256) void dsa_order_cost_kernel(OrderParams2 op2) {
     }
     return r;
   };
-  const int i = blockIdx.y * ORDER_TPB + w;  // this wave's tile
+  const int i = by * ORDER_TPB + w;  // this wave's tile
   if (i >= op.ntiles) return;
   const ChunkRange mine = range(4 * i, 4);
   // the other side: 64-key tiles (two chunks) for the forward, 32-query
@@ -160,6 +167,24 @@ __global__ __launch_bounds__(256) void dsa_order_cost_kernel(OrderParams2 op2) {
     n += __popcll(__ballot(hit));
   }
   if (lane == 0) op.cost[(int64_t)b * op.ntiles + i] = min(n, ORDER_MAX_COST);
+}
+
+__global__ __launch_bounds__(256) void dsa_order_cost_kernel(OrderParams2 op2) {
+  order_cost_block(op2, blockIdx.x, blockIdx.y, blockIdx.z);
+}
+
+// The forward's preparation in one launch: its launch-order cost blocks
+// (ncost of them, batch row fastest; none without an order) first, then the
+// k-step copies of the relative tables (ncopy blocks per table; none
+// without the copies).  The sort runs after it (dsa_order_sort_kernel).
+__global__ __launch_bounds__(256) void dsa_fwd_pre_kernel(TableKs t, OrderParams2 op2, int ncost, int ncopy) {
+  const int blk = blockIdx.x;
+  if (blk < ncost) {
+    order_cost_block(op2, blk % op2.f.B, blk / op2.f.B, 0);
+  } else {
+    const int k = blk - ncost;
+    table_ks_block(t, k % ncopy, k / ncopy);
+  }
 }
 
 __global__ __launch_bounds__(1024) void dsa_order_sort_kernel(OrderParams2 op) {

@@ -250,12 +250,12 @@ struct TableKs {
   void* dst[2];
   int H, R, D, esize;
 };
-__global__ __launch_bounds__(256) void dsa_table_ks_kernel(TableKs t) {
-  const int tb = blockIdx.y;
+// Block bx of table tb's copy (256 16-byte chunks).
+DSA_DEV void table_ks_block(const TableKs& t, int bx, int tb) {
   if (!t.src[tb]) return;
   const int per16 = 16 / t.esize, ks = 64 / t.esize, ns = t.D / ks;
   const int64_t n = (int64_t)t.H * ns * t.R * (ks / per16);
-  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t c = (int64_t)bx * 256 + threadIdx.x;
   if (c >= n) return;
   const int q = (int)(c % (ks / per16));
   int64_t rest = c / (ks / per16);
@@ -265,6 +265,7 @@ __global__ __launch_bounds__(256) void dsa_table_ks_kernel(TableKs t) {
   const char* src = (const char*)t.src[tb] + ((int64_t)h * t.hs[tb] + (int64_t)r * t.rs[tb] + s * ks + q * per16) * t.esize;
   *reinterpret_cast<uint4*>((char*)t.dst[tb] + c * 16) = *reinterpret_cast<const uint4*>(src);
 }
+__global__ __launch_bounds__(256) void dsa_table_ks_kernel(TableKs t) { table_ks_block(t, blockIdx.x, blockIdx.y); }
 
 // Row tables of one tile: crow[x] / prow[x] are the element offsets (row *
 // row stride) of the c2p / p2c table rows of offset x (x = (i - i0) - (j -

@@ -240,3 +240,82 @@ def test_backward_stages_in_separate_calls(split, gpu):
             assert err <= 1e-5, f"{name} differs from the one-call backward ({err:.3e})"
         else:
             assert torch.equal(a, b), f"{name} differs from the one-call backward"
+
+
+def _host_order_costs(seg, ntiles, per):
+    """Launch-order costs from the segment ids on the host: 1 + the number of
+    the other side's tiles (``per`` 32-token chunks each) whose segment range
+    meets the 128-token tile's (ranges over nonzero ids; an empty range
+    meets nothing), capped at 1025."""
+    B, L = seg.shape
+    nch = (L + 31) // 32
+    pad = torch.zeros(B, nch * 32, dtype=torch.int64)
+    pad[:, :L] = seg.long()
+    big = 1 << 40
+    lo = torch.where(pad > 0, pad, torch.full_like(pad, big)).view(B, nch, 32).amin(-1)
+    hi = torch.where(pad > 0, pad, torch.full_like(pad, -big)).view(B, nch, 32).amax(-1)
+
+    def ranges(width, n):
+        out_lo = torch.full((B, n), big, dtype=torch.int64)
+        out_hi = torch.full((B, n), -big, dtype=torch.int64)
+        for t in range(n):
+            c0, c1 = width * t, min(width * t + width, nch)
+            if c0 < c1:
+                out_lo[:, t] = lo[:, c0:c1].amin(-1)
+                out_hi[:, t] = hi[:, c0:c1].amax(-1)
+        return out_lo, out_hi
+
+    mlo, mhi = ranges(4, ntiles)
+    olo, ohi = ranges(per, (nch + per - 1) // per)
+    meets = (
+        (mlo[:, :, None] <= mhi[:, :, None]) & (olo[:, None, :] <= ohi[:, None, :])
+        & (mlo[:, :, None] <= ohi[:, None, :]) & (olo[:, None, :] <= mhi[:, :, None])
+    )
+    return (1 + meets.sum(-1)).clamp_max(1025)
+
+
+@pytest.mark.parametrize("B,L", [(4, 4096), (24, 2048)], ids=["C4", "B24"])
+def test_forward_launch_order(B, L, gpu):
+    """The forward's heaviest-first launch order under segment masks
+    (dsa_order.h): the cost of every (batch row, 128-query tile) equals the
+    host count, and the order is a permutation of the items with
+    non-increasing cost."""
+    import ctypes
+
+    from deberta_amd import _lib, ops
+
+    lib = _lib.load()
+    H, D, A = 1, 64, 256
+    g = torch.Generator().manual_seed(41)
+    seg = torch.zeros(B, L, dtype=torch.int32)
+    for b in range(B):  # packed documents with padding at the end of the row
+        t, doc = 0, 1
+        end = L - int(torch.randint(0, L // 4, (1,), generator=g))
+        while t < end:
+            n = min(int(torch.randint(1, 1200, (1,), generator=g)), end - t)
+            seg[b, t:t + n] = doc
+            t, doc = t + n, doc + 1
+    mk = lambda *s: torch.randn(*s, generator=g).to(gpu, torch.bfloat16)
+    q, k, v = mk(B, L, H, D), mk(B, L, H, D), mk(B, L, H, D)
+    kr, qr = mk(H, 2 * A, D), mk(H, 2 * A, D)
+    table = relative_offset_table(L, L, bucket_size=256, max_position=512, device=gpu)
+    segd = seg.to(gpu)
+    out = torch.empty_like(q)
+    lse = torch.empty((B, H, L), dtype=torch.float32, device=gpu)
+    bias = torch.empty(ops.bias_shape(q, k), dtype=torch.float16, device=gpu)
+    a = ops._fill_fwd_args(q, k, v, kr, qr, table, segd, None, out, lse, A, 1 / math.sqrt(3 * D), bias)
+    nws = lib.dsa_fwd_workspace_bytes(ctypes.byref(a))
+    ws = torch.zeros((nws,), dtype=torch.uint8, device=gpu)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), nws
+    _say(f"[order] B={B} L={L}")
+    stream = ctypes.c_void_p(torch.cuda.current_stream(gpu).cuda_stream)
+    _lib.check(lib.dsa_fwd(ctypes.byref(a), stream), "dsa_fwd")
+    torch.cuda.synchronize(gpu)
+    ntiles = (L + 127) // 128
+    n = B * ntiles
+    ints = ws[: 8 * n].view(torch.int32).cpu()
+    cost, order = ints[:n].long(), ints[n:2 * n].long()
+    want = _host_order_costs(seg, ntiles, per=2).reshape(-1)
+    assert torch.equal(cost, want), "launch-order costs differ from the host count"
+    assert torch.equal(torch.sort(order).values, torch.arange(n)), "the order is not a permutation of the items"
+    assert bool((cost[order][1:] <= cost[order][:-1]).all()), "the order is not heaviest first"
