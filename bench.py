@@ -631,6 +631,10 @@ def main() -> None:
     if args.kernels_only:
         print(json.dumps({"per_kernel": per_kernel, "per_kernel_alone": per_kernel_alone}), flush=True)
         return
+    # The stage calls' buffers go back to the caching allocator, which hands
+    # the same blocks to the op's steps below (same sizes).
+    del out, lse, bias, dq, dk, dv, dkr, dqr, bargs, fargs, ws, fws
+    torch.cuda.synchronize()
 
     # ---- the timed steps ----------------------------------------------------------
     # They run after the per-kernel timing above, whose stage calls keep the
