@@ -98,12 +98,15 @@ def _require_gpu(t: torch.Tensor) -> None:
 
 def position_query_rows(qr: torch.Tensor, query_len: int, att_span: int) -> torch.Tensor:
     """The p2p term's query rows ``Qr[:, A + min(i, A - 1)]`` for i <
-    query_len, as a ``[1, Lq, H, D]`` view (deberta_v2_native.py:330-342:
+    query_len, as ``[1, Lq, H, D]`` (deberta_v2_native.py:330-342:
     the positive half of the pos-query table, indexed by the clamped query
-    position)."""
+    position).  The gather runs in fp32, so that its backward sums the
+    gradients of the rows that share a table row (every query past A - 1
+    reads row 2A - 1) in fp32 and rounds once, where a bf16 scatter-add
+    rounded after every addition."""
     A = int(att_span)
     rows = torch.arange(query_len, device=qr.device).clamp(max=A - 1) + A
-    return qr.index_select(1, rows).permute(1, 0, 2).unsqueeze(0)
+    return qr.float().index_select(1, rows).permute(1, 0, 2).unsqueeze(0).to(qr.dtype)
 
 
 def relative_operands(
@@ -302,13 +305,16 @@ class DisentangledSelfAttention(nn.Module):
         if query_states is None:
             w = torch.cat([self.query_proj.weight, self.key_proj.weight, self.value_proj.weight])
             bias = torch.cat([self.query_proj.bias, self.key_proj.bias, self.value_proj.bias])
-            qkv = F.linear(hidden_states, w, bias).view(bsz, seq_len, 3, H, D)
-            return qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2]
+            # unbind, not three selects: the gradient is then assembled by
+            # one stack, where the selects' backward zero-filled and copied
+            # three (B, L, 3 H D) tensors and added them
+            q, k, v = F.linear(hidden_states, w, bias).view(bsz, seq_len, 3, H, D).unbind(2)
+            return q, k, v
         q = self._heads(self.query_proj(query_states))
         w = torch.cat([self.key_proj.weight, self.value_proj.weight])
         bias = torch.cat([self.key_proj.bias, self.value_proj.bias])
-        kv = F.linear(hidden_states, w, bias).view(bsz, seq_len, 2, H, D)
-        return q, kv[:, :, 0], kv[:, :, 1]
+        k, v = F.linear(hidden_states, w, bias).view(bsz, seq_len, 2, H, D).unbind(2)
+        return q, k, v
 
     def _project_rel(self, rel_embeddings: torch.Tensor, *, use_query: bool) -> torch.Tensor:
         """Projected relative table ``(H, 2A, D)`` as a view of the Linear
@@ -344,8 +350,8 @@ class DisentangledSelfAttention(nn.Module):
             A, H, D = int(self.pos_ebd_size), self.num_attention_heads, self.attention_head_size
             w = torch.cat([kl.weight, ql.weight])
             b = torch.cat([kl.bias, ql.bias])
-            both = F.linear(rel_embeddings[: 2 * A, :], w, b).to(dtype).view(2 * A, 2, H, D)
-            return both[:, 0].permute(1, 0, 2), both[:, 1].permute(1, 0, 2)
+            kr, qr = F.linear(rel_embeddings[: 2 * A, :], w, b).to(dtype).view(2 * A, 2, H, D).unbind(1)
+            return kr.permute(1, 0, 2), qr.permute(1, 0, 2)
         kr = self._project_rel(rel_embeddings, use_query=False).to(dtype) if need_k else None
         qr = self._project_rel(rel_embeddings, use_query=True).to(dtype) if need_q else None
         return kr, qr

@@ -151,6 +151,31 @@ def _segments_cached(mask: torch.Tensor, pair_keep: torch.Tensor) -> Optional[to
     return ids
 
 
+# key mask -> (its version, event, pinned flag): whether every key is kept,
+# found on the device without a host synchronisation.
+_ALL_KEPT: WeakIdKeyDictionary = WeakIdKeyDictionary()
+
+
+def _all_kept(mask: torch.Tensor, key_keep: torch.Tensor) -> bool:
+    """True when ``key_keep`` (a ``[B or 1, K]`` byte view of ``mask``) keeps
+    every key, as found by an earlier call with the same mask object and
+    version.  The check runs on the device and is read back through pinned
+    memory once its event has completed, so no call waits for the GPU: the
+    first call with a mask starts the check and answers False, later calls
+    answer True once the check has finished and found every key kept.  Such
+    a mask then runs as no mask (the same results: every pair is kept and
+    no row is dead), on the kernels without masking or launch order."""
+    hit = _ALL_KEPT.get(mask)
+    if hit is not None and hit[0] == mask._version:
+        return hit[1].query() and bool(hit[2])
+    flag = torch.empty((), dtype=torch.bool, pin_memory=True)
+    flag.copy_(key_keep.bool().all(), non_blocking=True)
+    ev = torch.cuda.Event()
+    ev.record()
+    _ALL_KEPT[mask] = (mask._version, ev, flag)
+    return False
+
+
 def kernel_masks(
     attention_mask: "Optional[torch.Tensor | SegmentMask]",
     batch: int,
@@ -162,7 +187,9 @@ def kernel_masks(
 ) -> tuple[Optional[torch.Tensor], Optional[torch.Tensor]]:
     """Split a rank-4 keep mask into the kernels' ``(key_keep, pair_keep)``.
 
-    ``(B|1, 1, 1, K)`` becomes a ``[B, K]`` byte view (``key_keep``),
+    ``(B|1, 1, 1, K)`` becomes a ``[B, K]`` byte view (``key_keep``), or
+    no mask once an asynchronous device check has found that it keeps every
+    key (``_all_kept``),
     ``(B|1, 1, Q, K)`` a ``[B, Q, K]`` byte view (``pair_keep``), a per-head
     ``(B|1, H, Q|1, K)`` mask (``heads`` = H given) a ``[B, H, Q, K]`` one, or, for a
     dense mask of the packed-document form on the GPU in eager mode, the
@@ -199,6 +226,15 @@ def kernel_masks(
         return None, _per_head_pair_mask(bytes_, batch, heads, query_len, key_len)
     if keep.shape[-2] == 1:
         kk = bytes_[:, 0, 0, :]
+        # a key mask that keeps every key runs as no mask (eager mode on the
+        # GPU; the check never waits for the device)
+        if (
+            kk.is_cuda
+            and not torch.compiler.is_compiling()
+            and not torch.cuda.is_current_stream_capturing()
+            and _all_kept(attention_mask, kk)
+        ):
+            return None, None
         if kk.stride(-1) != 1:
             kk = kk.contiguous()
         return kk.expand(batch, key_len), None

@@ -319,3 +319,45 @@ def test_forward_launch_order(B, L, gpu):
     assert torch.equal(cost, want), "launch-order costs differ from the host count"
     assert torch.equal(torch.sort(order).values, torch.arange(n)), "the order is not a permutation of the items"
     assert bool((cost[order][1:] <= cost[order][:-1]).all()), "the order is not heaviest first"
+
+
+def test_all_kept_key_mask_runs_as_no_mask(gpu):
+    """A (B, 1, 1, L) key mask that keeps every key is recognised by an
+    asynchronous device check (the first call starts it, no call waits):
+    once it has finished, the mask runs as no mask, with results equal to the
+    unmasked call's; a mask with one dropped key is never taken for one."""
+    from deberta_amd.masks import kernel_masks
+
+    B, L, H, D, A = 2, 256, 4, 64, 256
+    g = torch.Generator().manual_seed(81)
+    mk = lambda *s: torch.randn(*s, generator=g).to(gpu, torch.bfloat16)
+    q, k, v, dout = mk(B, L, H, D), mk(B, L, H, D), mk(B, L, H, D), mk(B, L, H, D)
+    kr, qr = mk(H, 2 * A, D), mk(H, 2 * A, D)
+    table = relative_offset_table(L, L, bucket_size=256, max_position=512, device=gpu)
+    ones = torch.ones(B, 1, 1, L, dtype=torch.bool, device=gpu)
+    holes = ones.clone()
+    holes[1, 0, 0, L - 1] = False
+    kk, pk = kernel_masks(ones, B, L, L, gpu)  # starts the check
+    assert kk is not None and pk is None
+    kernel_masks(holes, B, L, L, gpu)
+    torch.cuda.synchronize(gpu)
+    assert kernel_masks(ones, B, L, L, gpu) == (None, None)
+    kk, _ = kernel_masks(holes, B, L, L, gpu)
+    assert kk is not None and int(kk.sum()) == B * L - 1
+
+    def run(kkm):
+        leaves = [t.detach().clone().requires_grad_(True) for t in (q, k, v, kr, qr)]
+        out, _, _ = torch.ops.deberta_amd.dsa_fwd(*leaves, table, kkm, None, A, 1 / math.sqrt(3 * D))
+        return [out] + list(torch.autograd.grad(out, leaves, dout))
+
+    # the key-mask kernels on the all-kept mask give the unmasked results
+    ref = run(None)
+    got = run(ones.view(torch.uint8)[:, 0, 0, :])
+    for name, a, b in zip(["out", "dq", "dk", "dv", "dkr", "dqr"], got, ref):
+        if name in ("dkr", "dqr"):
+            # bf16 roundings of fp32 sums taken in other orders (the masked
+            # table kernel splits its items differently): one bf16 ulp
+            err = float((a.float() - b.float()).abs().max() / b.float().abs().max().clamp_min(1e-30))
+            assert err <= 1e-2, f"{name}: {err:.3e}"
+        else:
+            assert torch.equal(a, b), f"{name}: the key-mask kernels differ from the unmasked ones"
