@@ -150,27 +150,34 @@ def fused_attention(
     att_span: int,
     scale: float,
     qc: Optional[torch.Tensor] = None,
+    qkv: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Core call on ``[B, L, H, D]`` layers; returns ``[B, Lq, H, D]``.
     ``kr`` / ``qr`` are the c2p / p2c tables (None: term off); ``qc`` the
-    c2p term's query rows (None: q)."""
-    _require_gpu(q)
-    B, Lq = q.shape[0], q.shape[1]
-    Lk = k.shape[1]
-    key_keep, pair_keep = kernel_masks(attention_mask, B, Lq, Lk, q.device, heads=q.shape[2])
+    c2p term's query rows (None: q).  ``qkv``: q, k and v packed as one
+    ``[B, L, 3, H, D]`` tensor (q, k, v are then None); the op takes it
+    whole and its gradient comes back as one tensor."""
+    ref = qkv if qkv is not None else q  # shapes, dtype and device
+    _require_gpu(ref)
+    B, Lq, H = ref.shape[0], ref.shape[1], ref.shape[-2]
+    Lk = Lq if qkv is not None else k.shape[1]
+    key_keep, pair_keep = kernel_masks(attention_mask, B, Lq, Lk, ref.device, heads=H)
     if kr is not None:
-        kr = kr.to(q.dtype)
+        kr = kr.to(ref.dtype)
     if qr is not None:
-        qr = qr.to(q.dtype)
+        qr = qr.to(ref.dtype)
     if qc is not None:
-        qc = qc.to(q.dtype)
+        qc = qc.to(ref.dtype)
     if kr is None and qr is None:
         table = None
     # The relative term is saved only when a backward can follow.
     save_bias = torch.is_grad_enabled() and any(
-        t is not None and t.requires_grad for t in (q, k, v, kr, qr, qc)
+        t is not None and t.requires_grad for t in (q, k, v, qkv, kr, qr, qc)
     )
-    out, _, _ = ops.attention(q, k, v, kr, qr, table, key_keep, pair_keep, int(att_span), float(scale), save_bias, qc)
+    if qkv is not None:
+        out, _, _ = ops.attention_packed(qkv, kr, qr, table, key_keep, pair_keep, int(att_span), float(scale), save_bias, qc)
+    else:
+        out, _, _ = ops.attention(q, k, v, kr, qr, table, key_keep, pair_keep, int(att_span), float(scale), save_bias, qc)
     return out
 
 
@@ -293,28 +300,28 @@ class DisentangledSelfAttention(nn.Module):
 
     def _project_qkv(
         self, hidden_states: torch.Tensor, query_states: Optional[torch.Tensor]
-    ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-        """q, k, v as ``(B, L, H, D)`` views of one fused projection
-        (deberta_v2_native.py:587-589 as a single GEMM): the three weights
-        are concatenated at call time, so the parameters (and the state-dict
-        keys query_proj / key_proj / value_proj) stay the reference's.  With
-        separate ``query_states`` only the key and value projections are
-        fused."""
+    ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
+        """(q, k, v, qkv): one fused projection (deberta_v2_native.py:587-589
+        as a single GEMM) as ``qkv`` ``(B, L, 3, H, D)``, with q, k, v None
+        (callers that need them take ``qkv.unbind(2)``: where they reach
+        autograd separately their gradient is one stack, where three
+        ``select``s zero-filled and copied three ``(B, L, 3 H D)`` tensors and
+        added them).  The three weights are concatenated at call time, so
+        the parameters (and the state-dict keys query_proj / key_proj /
+        value_proj) stay the reference's.  With separate ``query_states``
+        only the key and value projections are fused, and q, k, v are
+        ``(B, L, H, D)`` views (qkv None)."""
         H, D = self.num_attention_heads, self.attention_head_size
         bsz, seq_len, _ = hidden_states.shape
         if query_states is None:
             w = torch.cat([self.query_proj.weight, self.key_proj.weight, self.value_proj.weight])
             bias = torch.cat([self.query_proj.bias, self.key_proj.bias, self.value_proj.bias])
-            # unbind, not three selects: the gradient is then assembled by
-            # one stack, where the selects' backward zero-filled and copied
-            # three (B, L, 3 H D) tensors and added them
-            q, k, v = F.linear(hidden_states, w, bias).view(bsz, seq_len, 3, H, D).unbind(2)
-            return q, k, v
+            return None, None, None, F.linear(hidden_states, w, bias).view(bsz, seq_len, 3, H, D)
         q = self._heads(self.query_proj(query_states))
         w = torch.cat([self.key_proj.weight, self.value_proj.weight])
         bias = torch.cat([self.key_proj.bias, self.value_proj.bias])
         k, v = F.linear(hidden_states, w, bias).view(bsz, seq_len, 2, H, D).unbind(2)
-        return q, k, v
+        return q, k, v, None
 
     def _project_rel(self, rel_embeddings: torch.Tensor, *, use_query: bool) -> torch.Tensor:
         """Projected relative table ``(H, 2A, D)`` as a view of the Linear
@@ -406,8 +413,11 @@ class DisentangledSelfAttention(nn.Module):
         _require_gpu(hidden_states)
         unfused = output_attentions or (self.training and self.dropout.p > 0.0)
 
-        q, k, v = self._project_qkv(hidden_states, query_states)
+        q, k, v, qkv = self._project_qkv(hidden_states, query_states)
         model_dtype = hidden_states.dtype
+        ref = qkv if qkv is not None else q  # dtype and device of the layers
+        Lq = ref.shape[1]
+        Lk = Lq if qkv is not None else k.shape[1]
 
         scale_factor = 1 + sum(t in self.pos_att_type for t in ("c2p", "p2c", "p2p"))
         scale = 1.0 / math.sqrt(float(self.attention_head_size * scale_factor))
@@ -418,21 +428,25 @@ class DisentangledSelfAttention(nn.Module):
         if relative:
             rel_embeddings = self.pos_dropout(rel_embeddings)
             att_span = int(self.pos_ebd_size)
-            kr_full, qr_full = self._relative_tables(rel_embeddings, q.dtype)
+            kr_full, qr_full = self._relative_tables(rel_embeddings, ref.dtype)
             if not unfused:
-                kr, qr, qc = relative_operands(self.pos_att_type, q, kr_full, qr_full, att_span)
+                # p2p's query rows add to q: only then is q needed on its own
+                qp = q if q is not None or "p2p" not in self.pos_att_type else qkv.unbind(2)[0]
+                kr, qr, qc = relative_operands(self.pos_att_type, qp, kr_full, qr_full, att_span)
                 if kr is not None or qr is not None:
                     table = table_for(
                         relative_pos,
-                        q.shape[1],
-                        k.shape[1],
+                        Lq,
+                        Lk,
                         self.position_buckets,
                         self.max_relative_positions,
-                        q.device,
+                        ref.device,
                         strict=False,
                     )
                     unfused = table is None  # not a function of i - j: used as given
         if unfused:
+            if qkv is not None:
+                q, k, v = qkv.unbind(2)
             return self._forward_unfused(
                 q, k, v, kr_full, qr_full, relative_pos if relative else None, relative, attention_mask,
                 att_span, scale, model_dtype, output_attentions,
@@ -445,7 +459,9 @@ class DisentangledSelfAttention(nn.Module):
                     f"attention_mask must be rank-4 [B,1,Q,K]; got shape={tuple(attention_mask.shape)}"
                 )
 
-        ctx = fused_attention(q, k, v, kr, qr, table, attention_mask, att_span, scale, qc)
+        # the op takes the packed projection whole (its gradient comes back
+        # as one tensor)
+        ctx = fused_attention(q, k, v, kr, qr, table, attention_mask, att_span, scale, qc, qkv=qkv)
         bsz, seq_len = ctx.shape[0], ctx.shape[1]
         context_layer = ctx.reshape(bsz, seq_len, self.all_head_size).to(dtype=model_dtype)
         return context_layer, None

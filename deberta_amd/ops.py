@@ -331,8 +331,11 @@ def _dsa_bwd_impl(
     att_span: int,
     scale: float,
     qc: Optional[Tensor] = None,
+    dqkv: Optional[Tensor] = None,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
-    """Gradients (dq, dk, dv, dkr, dqr, dqc).  dkr/dqr are [H, 2A, D] in the
+    """Gradients (dq, dk, dv, dkr, dqr, dqc).  With ``dqkv`` (a contiguous
+    ``[B, L, 3, H, D]`` buffer), dq, dk and dv are written into its three
+    slices and returned as views of it.  dkr/dqr are [H, 2A, D] in the
     tables' dtype (empty when the matching table is None).  ``bias`` is the
     relative term dsa_fwd saved (required with c2p/p2c).  With ``qc`` (the
     c2p term's query rows), dqc is its gradient and dq the content part;
@@ -349,9 +352,12 @@ def _dsa_bwd_impl(
     out = _kernel_ready(out)
     B, Lq, H, D = q.shape
     R = 2 * int(att_span)
-    dq = torch.empty_like(q, memory_format=torch.contiguous_format)
-    dk = torch.empty_like(k, memory_format=torch.contiguous_format)
-    dv = torch.empty_like(v, memory_format=torch.contiguous_format)
+    if dqkv is not None:  # the three gradients as slices of one packed buffer
+        dq, dk, dv = dqkv.unbind(2)
+    else:
+        dq = torch.empty_like(q, memory_format=torch.contiguous_format)
+        dk = torch.empty_like(k, memory_format=torch.contiguous_format)
+        dv = torch.empty_like(v, memory_format=torch.contiguous_format)
     # the table gradients are written in the tables' dtype (no zeroing, no cast)
     tab = dict(dtype=q.dtype, device=q.device)
     dkr = torch.empty((H, R, D), **tab) if kr is not None else torch.empty((0,), **tab)
@@ -439,6 +445,130 @@ def attention(
     if _eager.eager(q):
         return _DsaFwdFunction.apply(q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias, qc)
     return torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias, qc)
+
+
+# ---- packed q, k, v ----------------------------------------------------------------
+# The module's q, k and v are slices of one fused projection, (B, L, 3, H, D).
+# Given that tensor itself, the op's backward writes dq, dk and dv into one
+# buffer of the same layout and returns it as the projection's gradient: no
+# stack of three gradients and no copy.
+
+
+def _dsa_fwd_packed_impl(
+    qkv: Tensor,
+    kr: Optional[Tensor],
+    qr: Optional[Tensor],
+    rel_table: Optional[Tensor],
+    key_keep: Optional[Tensor],
+    pair_keep: Optional[Tensor],
+    att_span: int,
+    scale: float,
+    save_bias: bool = True,
+    qc: Optional[Tensor] = None,
+) -> tuple[Tensor, Tensor, Tensor]:
+    """``dsa_fwd`` on ``q, k, v = qkv.unbind(2)`` (qkv ``[B, L, 3, H, D]``)."""
+    if qkv.dim() != 5 or qkv.shape[2] != 3:
+        raise ValueError(f"dsa: qkv must be [B, L, 3, H, D], got {tuple(qkv.shape)}")
+    q, k, v = qkv.unbind(2)
+    return _dsa_fwd_impl(q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias, qc)
+
+
+dsa_fwd_packed = torch.library.custom_op(
+    "deberta_amd::dsa_fwd_packed", _dsa_fwd_packed_impl, mutates_args=(), device_types="cuda"
+)
+
+
+@dsa_fwd_packed.register_fake
+def _dsa_fwd_packed_fake(qkv, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias=True, qc=None):
+    q, k, _ = qkv.unbind(2)
+    return _dsa_fwd_fake(q, k, k, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias, qc)
+
+
+def _dsa_bwd_packed_impl(
+    dout: Tensor,
+    qkv: Tensor,
+    kr: Optional[Tensor],
+    qr: Optional[Tensor],
+    rel_table: Optional[Tensor],
+    key_keep: Optional[Tensor],
+    pair_keep: Optional[Tensor],
+    out: Tensor,
+    lse: Tensor,
+    bias: Tensor,
+    att_span: int,
+    scale: float,
+    qc: Optional[Tensor] = None,
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Gradients (dqkv, dkr, dqr, dqc) of ``dsa_fwd_packed``: dqkv a
+    contiguous ``[B, L, 3, H, D]`` tensor in qkv's dtype."""
+    q, k, v = qkv.unbind(2)
+    dqkv = torch.empty(qkv.shape, dtype=qkv.dtype, device=qkv.device)
+    _, _, _, dkr, dqr, dqc = _dsa_bwd_impl(
+        dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, att_span, scale, qc, dqkv=dqkv
+    )
+    return dqkv, dkr, dqr, dqc
+
+
+dsa_bwd_packed = torch.library.custom_op(
+    "deberta_amd::dsa_bwd_packed", _dsa_bwd_packed_impl, mutates_args=(), device_types="cuda"
+)
+
+
+@dsa_bwd_packed.register_fake
+def _dsa_bwd_packed_fake(dout, qkv, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, att_span, scale, qc=None):
+    q, k, v = qkv.unbind(2)
+    _, _, _, dkr, dqr, dqc = _dsa_bwd_fake(
+        dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, att_span, scale, qc
+    )
+    return qkv.new_empty(qkv.shape), dkr, dqr, dqc
+
+
+def _setup_context_packed(ctx, inputs, output):
+    qkv, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias, qc = inputs
+    out, lse, bias = output
+    ctx.mark_non_differentiable(lse, bias)
+    ctx.set_materialize_grads(False)
+    ctx.save_for_backward(qkv, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, qc)
+    ctx.att_span = att_span
+    ctx.scale = scale
+
+
+def _backward_packed(ctx, dout, dlse, dbias):
+    qkv, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, qc = ctx.saved_tensors
+    if dout is None:
+        return (None,) * 10
+    dqkv, dkr, dqr, dqc = _eager.on_eager(ctx, dsa_bwd_packed, _dsa_bwd_packed_impl)(
+        dout, qkv, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, ctx.att_span, ctx.scale, qc
+    )
+    return (
+        dqkv, (dkr if kr is not None else None), (dqr if qr is not None else None),
+        None, None, None, None, None, None, (dqc if qc is not None else None),
+    )
+
+
+torch.library.register_autograd("deberta_amd::dsa_fwd_packed", _backward_packed, setup_context=_setup_context_packed)
+_DsaFwdPackedFunction = _eager.function("_DsaFwdPackedFunction", _dsa_fwd_packed_impl, _setup_context_packed, _backward_packed)
+
+
+def attention_packed(
+    qkv: Tensor,
+    kr: Optional[Tensor],
+    qr: Optional[Tensor],
+    rel_table: Optional[Tensor],
+    key_keep: Optional[Tensor],
+    pair_keep: Optional[Tensor],
+    att_span: int,
+    scale: float,
+    save_bias: bool = True,
+    qc: Optional[Tensor] = None,
+) -> tuple[Tensor, Tensor, Tensor]:
+    """``attention`` on packed ``qkv`` ``[B, L, 3, H, D]``: the gradient of
+    qkv comes back as one tensor."""
+    if _eager.eager(qkv):
+        return _DsaFwdPackedFunction.apply(qkv, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias, qc)
+    return torch.ops.deberta_amd.dsa_fwd_packed(
+        qkv, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias, qc
+    )
 
 
 def _dsa_bias_impl(

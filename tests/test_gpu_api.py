@@ -361,3 +361,42 @@ def test_all_kept_key_mask_runs_as_no_mask(gpu):
             assert err <= 1e-2, f"{name}: {err:.3e}"
         else:
             assert torch.equal(a, b), f"{name}: the key-mask kernels differ from the unmasked ones"
+
+
+@pytest.mark.parametrize("types", ["c2p|p2c", "c2p|p2c|p2p"])
+def test_packed_qkv_op_equals_separate_op(types, gpu):
+    """``deberta_amd::dsa_fwd_packed`` (q, k, v as one ``[B, L, 3, H, D]``
+    tensor, its gradient returned as one tensor) gives the separate op's
+    output and gradients: out and the q, k, v gradients bit for bit, the
+    table gradients up to the order of their fp32 atomic additions."""
+    from deberta_amd import ops
+    from deberta_amd.attention import relative_operands
+
+    B, L, H, D, A = 2, 320, 4, 64, 256
+    g = torch.Generator().manual_seed(91)
+    qkv0 = torch.randn(B, L, 3, H, D, generator=g).to(gpu, torch.bfloat16)
+    kr0, qr0 = (torch.randn(H, 2 * A, D, generator=g).to(gpu, torch.bfloat16) for _ in range(2))
+    dout = torch.randn(B, L, H, D, generator=g).to(gpu, torch.bfloat16)
+    table = relative_offset_table(L, L, bucket_size=256, max_position=512, device=gpu)
+    scale = 1 / math.sqrt(D * (1 + len(types.split("|"))))
+    tl = types.split("|")
+
+    def run(packed):
+        qkv = qkv0.detach().clone().requires_grad_(True)
+        kr, qr = (t.detach().clone().requires_grad_(True) for t in (kr0, qr0))
+        q, k, v = qkv.unbind(2)
+        krx, qrx, qc = relative_operands(tl, q, kr, qr, A)
+        if packed:
+            out, _, _ = ops.attention_packed(qkv, krx, qrx, table, None, None, A, scale, True, qc)
+        else:
+            out, _, _ = ops.attention(q, k, v, krx, qrx, table, None, None, A, scale, True, qc)
+        return [out] + list(torch.autograd.grad(out, [qkv, kr, qr], dout))
+
+    _say(f"[packed] {types}")
+    ref, got = run(False), run(True)
+    for name, a, b in zip(["out", "dqkv", "dkr", "dqr"], got, ref):
+        if name in ("dkr", "dqr"):
+            err = float((a.float() - b.float()).abs().max() / b.float().abs().max().clamp_min(1e-30))
+            assert err <= 1e-2, f"{name}: {err:.3e}"  # bf16 roundings of fp32 sums in other orders
+        else:
+            assert torch.equal(a, b), f"{name} differs between the packed and the separate op"
