@@ -168,10 +168,12 @@ def _all_kept(mask: torch.Tensor, key_keep: torch.Tensor) -> bool:
     hit = _ALL_KEPT.get(mask)
     if hit is not None and hit[0] == mask._version:
         return hit[1].query() and bool(hit[2])
-    flag = torch.empty((), dtype=torch.bool, pin_memory=True)
-    flag.copy_(key_keep.bool().all(), non_blocking=True)
-    ev = torch.cuda.Event()
-    ev.record()
+    flag = torch.zeros((), dtype=torch.bool, pin_memory=True)
+    stream = torch.cuda.current_stream(key_keep.device)  # the copy's stream: the mask's device's
+    with torch.cuda.stream(stream):
+        flag.copy_(key_keep.bool().all(), non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record(stream)
     _ALL_KEPT[mask] = (mask._version, ev, flag)
     return False
 
