@@ -24,7 +24,10 @@ _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 def eager(t: torch.Tensor) -> bool:
     """True when a call with main input ``t`` may bypass ``torch.ops``."""
-    return type(t) is torch.Tensor and _dispatch_depth() == 0 and not torch.compiler.is_compiling()
+    # is_compiling() first: dynamo folds it to True while tracing, and the
+    # dispatch-stack query after it (a C function dynamo does not trace)
+    # would otherwise break the graph
+    return not torch.compiler.is_compiling() and type(t) is torch.Tensor and _dispatch_depth() == 0
 
 
 def stream_ptr(t: torch.Tensor) -> int:

@@ -231,7 +231,16 @@ def _dsa_fwd_impl(
     return out, lse, bias
 
 
-dsa_fwd = torch.library.custom_op("deberta_amd::dsa_fwd", _dsa_fwd_impl, mutates_args=(), device_types="cuda")
+# Tagged CUDA-graph unsafe: capturing the op's forward and backward in a HIP
+# graph ended in a host fault inside the runtime's capture end, whose cause is
+# not known.  Under torch.compile's CUDA-graph modes (reduce-overhead,
+# max-autotune) inductor then runs these ops outside the captured graphs
+# (graph partitions around them) instead of capturing them.
+_TAGS = (torch.Tag.cudagraph_unsafe,)
+
+dsa_fwd = torch.library.custom_op(
+    "deberta_amd::dsa_fwd", _dsa_fwd_impl, mutates_args=(), device_types="cuda", tags=_TAGS
+)
 
 
 @dsa_fwd.register_fake
@@ -376,7 +385,9 @@ def _dsa_bwd_impl(
     return dq, dk, dv, dkr, dqr, dqc
 
 
-dsa_bwd = torch.library.custom_op("deberta_amd::dsa_bwd", _dsa_bwd_impl, mutates_args=(), device_types="cuda")
+dsa_bwd = torch.library.custom_op(
+    "deberta_amd::dsa_bwd", _dsa_bwd_impl, mutates_args=(), device_types="cuda", tags=_TAGS
+)
 
 
 @dsa_bwd.register_fake
@@ -474,7 +485,7 @@ def _dsa_fwd_packed_impl(
 
 
 dsa_fwd_packed = torch.library.custom_op(
-    "deberta_amd::dsa_fwd_packed", _dsa_fwd_packed_impl, mutates_args=(), device_types="cuda"
+    "deberta_amd::dsa_fwd_packed", _dsa_fwd_packed_impl, mutates_args=(), device_types="cuda", tags=_TAGS
 )
 
 
@@ -510,7 +521,7 @@ def _dsa_bwd_packed_impl(
 
 
 dsa_bwd_packed = torch.library.custom_op(
-    "deberta_amd::dsa_bwd_packed", _dsa_bwd_packed_impl, mutates_args=(), device_types="cuda"
+    "deberta_amd::dsa_bwd_packed", _dsa_bwd_packed_impl, mutates_args=(), device_types="cuda", tags=_TAGS
 )
 
 
@@ -602,7 +613,9 @@ def _dsa_bias_impl(
     return out
 
 
-dsa_bias = torch.library.custom_op("deberta_amd::dsa_bias", _dsa_bias_impl, mutates_args=(), device_types="cuda")
+dsa_bias = torch.library.custom_op(
+    "deberta_amd::dsa_bias", _dsa_bias_impl, mutates_args=(), device_types="cuda", tags=_TAGS
+)
 
 
 @dsa_bias.register_fake
