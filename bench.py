@@ -588,10 +588,11 @@ def main() -> None:
         ("dsa_bwd_fold_kernel", run_stage(_lib.DSA_STAGE_SUM), 0.0),
     ]
     n_k = args.steps if args.kernels_only else max(10, args.steps)
-    # Sustained load before the per-kernel timing: 100 stage-split steps
-    # (about 45 ms) bring the clocks of a fresh process to their settled
-    # level; with --kernels-only the op's steps above already did.
-    for _ in range(20 if args.kernels_only else 100):
+    # Sustained load before the per-kernel timing: 300 stage-split steps
+    # (about 0.13 s) bring the clocks of a fresh process to their settled
+    # level (100 were not always enough on a box's first run); with
+    # --kernels-only the op's steps above already did.
+    for _ in range(20 if args.kernels_only else 300):
         for _, fn, _ in staged:
             fn()
     ns_ = len(staged) + 1
