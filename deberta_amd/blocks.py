@@ -37,6 +37,12 @@ from torch import Tensor
 
 from deberta_amd import _eager, _lib
 
+# As the attention ops (deberta_amd/ops.py): under torch.compile's CUDA-graph
+# modes these run between the captured graph partitions, not inside them
+# (capturing the library's launches in a HIP graph ended in a host fault
+# whose cause is not known).
+_TAGS = (torch.Tag.cudagraph_unsafe,)
+
 _DT = {torch.float32: _lib.DSA_F32, torch.bfloat16: _lib.DSA_BF16}
 
 
@@ -127,7 +133,7 @@ def _add_ln_impl(
     return y, mean, rstd
 
 
-add_ln = torch.library.custom_op("deberta_amd::add_ln", _add_ln_impl, mutates_args=(), device_types="cuda")
+add_ln = torch.library.custom_op("deberta_amd::add_ln", _add_ln_impl, mutates_args=(), device_types="cuda", tags=_TAGS)
 
 
 @add_ln.register_fake
@@ -179,7 +185,7 @@ def _add_ln_bwd_impl(
     return dz, dgamma, dbeta, dbias
 
 
-add_ln_bwd = torch.library.custom_op("deberta_amd::add_ln_bwd", _add_ln_bwd_impl, mutates_args=(), device_types="cuda")
+add_ln_bwd = torch.library.custom_op("deberta_amd::add_ln_bwd", _add_ln_bwd_impl, mutates_args=(), device_types="cuda", tags=_TAGS)
 
 
 @add_ln_bwd.register_fake
@@ -260,7 +266,7 @@ def _bias_gelu_impl(x: Tensor, bias: Optional[Tensor]) -> Tensor:
     return y
 
 
-bias_gelu = torch.library.custom_op("deberta_amd::bias_gelu", _bias_gelu_impl, mutates_args=(), device_types="cuda")
+bias_gelu = torch.library.custom_op("deberta_amd::bias_gelu", _bias_gelu_impl, mutates_args=(), device_types="cuda", tags=_TAGS)
 
 
 @bias_gelu.register_fake
@@ -293,7 +299,7 @@ def _bias_gelu_bwd_impl(dy: Tensor, x: Tensor, bias: Optional[Tensor]) -> tuple[
     return dz, dbias
 
 
-bias_gelu_bwd = torch.library.custom_op("deberta_amd::bias_gelu_bwd", _bias_gelu_bwd_impl, mutates_args=(), device_types="cuda")
+bias_gelu_bwd = torch.library.custom_op("deberta_amd::bias_gelu_bwd", _bias_gelu_bwd_impl, mutates_args=(), device_types="cuda", tags=_TAGS)
 
 
 @bias_gelu_bwd.register_fake
@@ -357,7 +363,7 @@ def _rtd_loss_impl(
     return loss, logits.view(x.shape[:-1]), denom
 
 
-rtd_loss = torch.library.custom_op("deberta_amd::rtd_loss", _rtd_loss_impl, mutates_args=(), device_types="cuda")
+rtd_loss = torch.library.custom_op("deberta_amd::rtd_loss", _rtd_loss_impl, mutates_args=(), device_types="cuda", tags=_TAGS)
 
 
 @rtd_loss.register_fake
@@ -402,7 +408,7 @@ def _rtd_loss_bwd_impl(
     return dx, dw, db
 
 
-rtd_loss_bwd = torch.library.custom_op("deberta_amd::rtd_loss_bwd", _rtd_loss_bwd_impl, mutates_args=(), device_types="cuda")
+rtd_loss_bwd = torch.library.custom_op("deberta_amd::rtd_loss_bwd", _rtd_loss_bwd_impl, mutates_args=(), device_types="cuda", tags=_TAGS)
 
 
 @rtd_loss_bwd.register_fake
