@@ -179,3 +179,37 @@ def test_full_headline_shape_batch_consistency(gpu):
     for b in range(B):
         dkr_sum += run(slice(b, b + 1))[2][3].float()
     assert max_rel(gr[3].float(), dkr_sum) <= 2e-2
+
+
+@pytest.mark.parametrize("share", [True, False])
+def test_query_states_against_oracle(share, gpu):
+    """``query_states`` (deberta_v2_native.py:585-588: the query projection
+    reads them instead of the hidden states) on the fused module: output and
+    the gradients of the hidden states, the query states, the relative
+    embeddings and every parameter against the oracle module, fp32, max|err|
+    / max|ref| <= 1e-4 (key biases on their weights' scale)."""
+    cfg = eager.make_config(hidden_size=128, num_attention_heads=4, share_att_key=share,
+                            pos_att_type="c2p|p2c", position_buckets=256, max_relative_positions=512)
+    ref, ours = _pair(cfg, seed=5)
+    ours = ours.to(gpu)
+    g = torch.Generator().manual_seed(66)
+    x = torch.randn(2, 160, 128, generator=g)
+    qs = torch.randn(2, 160, 128, generator=g)
+    rel = torch.randn(512, 128, generator=g)
+    dout = torch.randn(2, 160, 128, generator=g)
+
+    def run(module, dev):
+        xx, qq, rr = (t.to(dev).clone().requires_grad_(True) for t in (x, qs, rel))
+        out, _ = module(xx, None, query_states=qq, rel_embeddings=rr)
+        params = [p for _, p in module.named_parameters()]
+        grads = torch.autograd.grad(out, [xx, qq, rr] + params, dout.to(dev), allow_unused=True)
+        res = {"out": out.detach().float().cpu()}
+        for n, gr in zip(["dx", "dqs", "drel"] + ["d" + n for n, _ in module.named_parameters()], grads):
+            res[n] = torch.zeros(1) if gr is None else gr.float().cpu()
+        return res
+
+    a = run(ref, "cpu")
+    b = run(ours, gpu)
+    errs = _errors(a, b)
+    _say(f"[query_states share={share}] {errs}")
+    assert all(e <= 1e-4 for e in errs.values()), errs
