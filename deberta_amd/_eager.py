@@ -30,6 +30,21 @@ def eager(t: torch.Tensor) -> bool:
     return not torch.compiler.is_compiling() and type(t) is torch.Tensor and _dispatch_depth() == 0
 
 
+def refuse_capture(what: str) -> None:
+    """Raise when the current stream is capturing a CUDA/HIP graph.  Capturing
+    the library's launches (torch.cuda.graph around the attention op) ended
+    in a host fault inside the runtime's capture end, whose cause is not
+    known, so the ops refuse to run under capture.  torch.compile's
+    CUDA-graph modes run them between the captured partitions instead (the
+    ops are tagged cudagraph_unsafe)."""
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError(
+            f"{what}: the current stream is capturing a CUDA/HIP graph; the fused kernels are not supported "
+            "under graph capture (torch.compile's reduce-overhead / max-autotune modes run them outside the "
+            "captured partitions)"
+        )
+
+
 def stream_ptr(t: torch.Tensor) -> int:
     """The raw handle of the current HIP stream of ``t``'s device."""
     if _raw_stream is not None:

@@ -19,11 +19,12 @@ from typing import Any, Optional
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
+from torch.utils.weak import WeakIdKeyDictionary
 
 from deberta_amd import ops
 from deberta_amd.config import normalize_attention_kernel, normalize_pos_att_type
-from deberta_amd.masks import SegmentMask, kernel_masks, normalize_keep_mask
-from deberta_amd.unfused import unfused_attention
+from deberta_amd.masks import SegmentMask, kernel_masks, normalize_keep_mask, tensor_version
+from deberta_amd.unfused import relative_terms, unfused_attention
 from deberta_amd.relpos import (
     build_relative_position,
     is_monotone,
@@ -34,7 +35,10 @@ from deberta_amd.relpos import (
 )
 
 _TABLE_CACHE: dict[tuple, torch.Tensor] = {}
-_TOEPLITZ_OK: dict[tuple, bool] = {}
+# relative_pos tensor -> (version, (Lq, Lk, device), verdict, offset table),
+# keyed by object identity (WeakIdKeyDictionary: Tensor.__eq__ is
+# elementwise and cannot decide a lookup)
+_TOEPLITZ_OK: WeakIdKeyDictionary = WeakIdKeyDictionary()
 
 
 def _compiling() -> bool:
@@ -65,27 +69,34 @@ def table_for(
     """Offset table for the kernels from ``relative_pos`` (or the canonical
     one when it is None).  A given matrix must depend on ``i - j`` only and
     be non-decreasing in it (as every matrix build_relative_position returns);
-    this is verified once per tensor version in eager mode.  A matrix that is
+    this is verified once per tensor object and version in eager mode (on
+    every call for inference tensors, which keep no version).  A matrix that is
     not raises ``ValueError``, or returns None with ``strict=False``."""
     if relative_pos is None:
         return canonical_table(query_len, key_len, buckets, max_position, device)
-    rp = normalize_relative_pos(relative_pos.to(device), query_len, key_len)
-    table = table_from_matrix(rp)
-    if not _compiling():
-        key = (rp.data_ptr(), rp._version, tuple(rp.shape), tuple(rp.stride()), str(rp.device))
-        ok = _TOEPLITZ_OK.get(key)
-        if ok is None:
-            ok = is_toeplitz(rp, table) and is_monotone(table)
-            if len(_TOEPLITZ_OK) > 256:
-                _TOEPLITZ_OK.clear()
-            _TOEPLITZ_OK[key] = ok
-        if not ok:
-            if not strict:
-                return None
-            raise ValueError(
-                "relative_pos must depend on i - j only and be non-decreasing in it "
-                "(as build_relative_position produces) for the fused disentangled-attention kernels"
-            )
+    if _compiling():
+        return table_from_matrix(normalize_relative_pos(relative_pos.to(device), query_len, key_len))
+    # The verdict (and the table) is kept per caller tensor object and
+    # version: a temporary made from it (a cast, a copy to the device) may
+    # reuse a freed block of another matrix, so no address can key it.
+    version = tensor_version(relative_pos)
+    where = (int(query_len), int(key_len), str(torch.device(device)))
+    hit = _TOEPLITZ_OK.get(relative_pos) if version is not None else None
+    if hit is not None and hit[0] == version and hit[1] == where:
+        ok, table = hit[2], hit[3]
+    else:
+        rp = normalize_relative_pos(relative_pos.to(device), query_len, key_len)
+        table = table_from_matrix(rp)
+        ok = is_toeplitz(rp, table) and is_monotone(table)
+        if version is not None:
+            _TOEPLITZ_OK[relative_pos] = (version, where, ok, table)
+    if not ok:
+        if not strict:
+            return None
+        raise ValueError(
+            "relative_pos must depend on i - j only and be non-decreasing in it "
+            "(as build_relative_position produces) for the fused disentangled-attention kernels"
+        )
     return table
 
 
@@ -94,6 +105,42 @@ def _require_gpu(t: torch.Tensor) -> None:
         raise RuntimeError(
             f"fused disentangled attention runs on the GPU (HIP) only; got a tensor on {t.device}"
         )
+
+
+def _relative_matrix(
+    relative_pos: Optional[torch.Tensor], query_len: int, key_len: int, buckets: int, max_position: int, device
+) -> torch.Tensor:
+    """The ``(Lq, Lk)`` relative positions the reference's score terms use:
+    ``build_relative_position`` when None, else the given matrix with the
+    reference's rank handling (deberta_v2_native.py:235-271), as given."""
+    if relative_pos is None:
+        return build_relative_position(query_len, key_len, bucket_size=buckets, max_position=max_position, device=device)
+    return normalize_relative_pos(relative_pos.to(device), query_len, key_len)
+
+
+def _dense_keep(attention_mask, device) -> Optional[torch.Tensor]:
+    """The rank-4 boolean keep mask of ``attention_mask`` (None, a keep mask
+    or a ``SegmentMask``) for the torch-operation path."""
+    if attention_mask is None:
+        return None
+    if isinstance(attention_mask, SegmentMask):
+        return attention_mask.dense().to(device)
+    keep = normalize_keep_mask(attention_mask)
+    if keep.ndim != 4:
+        raise ValueError(f"attention_mask must be rank-4 [B,1,Q,K]; got shape={tuple(keep.shape)}")
+    return keep
+
+
+def _check_mask_rank(attention_mask) -> None:
+    """The reference's mask contract (mask_utils.py:8-32 and the rank check
+    of deberta_v2_native.py:619-623), checked without replacing the caller's
+    tensor: per-mask checks are cached on the caller's object."""
+    if attention_mask is None or isinstance(attention_mask, SegmentMask):
+        return
+    if not isinstance(attention_mask, torch.Tensor) or torch.is_floating_point(attention_mask):
+        normalize_keep_mask(attention_mask)  # raises the reference's TypeError / ValueError
+    if attention_mask.ndim != 4:
+        raise ValueError(f"attention_mask must be rank-4 [B,1,Q,K]; got shape={tuple(attention_mask.shape)}")
 
 
 def position_query_rows(qr: torch.Tensor, query_len: int, att_span: int) -> torch.Tensor:
@@ -220,6 +267,18 @@ def disentangled_attention(
     scale = 1.0 / math.sqrt(float(D * scale_factor))
     tables = [t for t in (pos_key_layer, pos_query_layer) if t is not None]
     att_span = tables[0].shape[1] // 2 if tables else 1
+    if q.device.type != "cuda":
+        # CPU tensors: the same chain in torch operations (deberta_amd.unfused)
+        rel_pos = None
+        if any(t in types for t in ("c2p", "p2c", "p2p")):
+            rel_pos = _relative_matrix(
+                relative_pos, q.shape[1], k.shape[1], position_buckets, max_relative_positions, q.device
+            )
+        out, _ = unfused_attention(
+            q, k, v, pos_key_layer, pos_query_layer, rel_pos, _dense_keep(attention_mask, q.device),
+            att_span, scale, types,
+        )
+        return out.transpose(1, 2) if layout == "bhld" else out
     kr, qr, qc = relative_operands(
         types, q,
         None if pos_key_layer is None else pos_key_layer.to(q.dtype),
@@ -229,12 +288,7 @@ def disentangled_attention(
     table = None
     if kr is not None or qr is not None:
         table = table_for(relative_pos, q.shape[1], k.shape[1], position_buckets, max_relative_positions, q.device)
-    if attention_mask is not None and not isinstance(attention_mask, SegmentMask):
-        attention_mask = normalize_keep_mask(attention_mask)
-        if attention_mask.ndim != 4:
-            raise ValueError(
-                f"attention_mask must be rank-4 [B,1,Q,K]; got shape={tuple(attention_mask.shape)}"
-            )
+    _check_mask_rank(attention_mask)
     out = fused_attention(q, k, v, kr, qr, table, attention_mask, att_span, scale, qc)
     return out.transpose(1, 2) if layout == "bhld" else out
 
@@ -376,8 +430,10 @@ class DisentangledSelfAttention(nn.Module):
         query's dtype (deberta_v2_native.py:530-562; every kernel choice
         computes the same function).  Computed by the fused kernels' band
         code (``deberta_amd::dsa_bias``), unmasked; forward only (training
-        differentiates through ``forward``)."""
-        _require_gpu(query_layer)
+        differentiates through ``forward``).  CPU tensors take the same
+        terms in torch operations (``deberta_amd.unfused.relative_terms``)."""
+        if query_layer.device.type != "cuda":
+            return self._bias_unfused(query_layer, key_layer, relative_pos, rel_embeddings, scale_factor)
         if query_layer.dtype not in (torch.float32, torch.bfloat16):
             raise TypeError(f"disentangled_attention_bias: query dtype must be float32 or bfloat16, got {query_layer.dtype}")
         q = query_layer.transpose(1, 2)
@@ -392,6 +448,31 @@ class DisentangledSelfAttention(nn.Module):
         scale = 1.0 / math.sqrt(float(self.attention_head_size * int(scale_factor)))
         return torch.ops.deberta_amd.dsa_bias(q, k, kr, qr, table, att_span, scale, qc)
 
+    def _bias_unfused(
+        self,
+        query_layer: torch.Tensor,
+        key_layer: torch.Tensor,
+        relative_pos: Optional[torch.Tensor],
+        rel_embeddings: torch.Tensor,
+        scale_factor: int,
+    ) -> torch.Tensor:
+        """``disentangled_attention_bias`` in torch operations (CPU tensors)."""
+        Lq, Lk = query_layer.shape[2], key_layer.shape[2]
+        kr, qr = self._relative_tables(rel_embeddings, query_layer.dtype)
+        rel_pos = None
+        if any(t in self.pos_att_type for t in ("c2p", "p2c", "p2p")):
+            rel_pos = _relative_matrix(
+                relative_pos, Lq, Lk, self.position_buckets, self.max_relative_positions, query_layer.device
+            )
+        scale = 1.0 / math.sqrt(float(self.attention_head_size * int(scale_factor)))
+        qh, kh = query_layer.float(), key_layer.float()
+        rel = relative_terms(qh, kh, kr, qr, rel_pos, int(self.pos_ebd_size), scale, self.pos_att_type)
+        if rel is None:
+            return torch.zeros(
+                (qh.shape[0], qh.shape[1], Lq, Lk), device=query_layer.device, dtype=query_layer.dtype
+            )
+        return rel.to(query_layer.dtype)
+
     def forward(
         self,
         hidden_states: torch.Tensor,
@@ -403,15 +484,15 @@ class DisentangledSelfAttention(nn.Module):
     ) -> tuple[torch.Tensor, Optional[torch.Tensor]]:
         """Same contract as the reference forward (deberta_v2_native.py:564-652).
 
-        The fused kernels run the call unless it needs the probabilities
-        themselves: ``output_attentions=True``, attention dropout ``p > 0``
-        in training mode, or a ``relative_pos`` that does not depend on
-        ``i - j`` alone; those run the same chain in torch operations on the
-        device (``deberta_amd.unfused``) and return the probabilities when
-        asked.
+        The fused kernels run the call unless it is on CPU tensors or needs
+        the probabilities themselves: ``output_attentions=True``, attention
+        dropout ``p > 0`` in training mode, or a ``relative_pos`` that does
+        not depend on ``i - j`` alone; those run the same chain in torch
+        operations on the tensors' device (``deberta_amd.unfused``) and
+        return the probabilities when asked.
         """
-        _require_gpu(hidden_states)
-        unfused = output_attentions or (self.training and self.dropout.p > 0.0)
+        on_gpu = hidden_states.device.type == "cuda"
+        unfused = (not on_gpu) or output_attentions or (self.training and self.dropout.p > 0.0)
 
         q, k, v, qkv = self._project_qkv(hidden_states, query_states)
         model_dtype = hidden_states.dtype
@@ -452,12 +533,7 @@ class DisentangledSelfAttention(nn.Module):
                 att_span, scale, model_dtype, output_attentions,
             )
 
-        if attention_mask is not None and not isinstance(attention_mask, SegmentMask):
-            attention_mask = normalize_keep_mask(attention_mask)
-            if attention_mask.ndim != 4:
-                raise ValueError(
-                    f"attention_mask must be rank-4 [B,1,Q,K]; got shape={tuple(attention_mask.shape)}"
-                )
+        _check_mask_rank(attention_mask)
 
         # the op takes the packed projection whole (its gradient comes back
         # as one tensor)
@@ -475,19 +551,10 @@ class DisentangledSelfAttention(nn.Module):
         rel_pos = None
         types = self.pos_att_type if relative else []
         if relative and any(t in types for t in ("c2p", "p2c", "p2p")):
-            if relative_pos is None:
-                rel_pos = build_relative_position(
-                    Lq, Lk, bucket_size=self.position_buckets, max_position=self.max_relative_positions, device=q.device
-                )
-            else:
-                rel_pos = normalize_relative_pos(relative_pos.to(q.device), Lq, Lk)
-        keep = None
-        if isinstance(attention_mask, SegmentMask):
-            keep = attention_mask.dense().to(q.device)
-        elif attention_mask is not None:
-            keep = normalize_keep_mask(attention_mask)
-            if keep.ndim != 4:
-                raise ValueError(f"attention_mask must be rank-4 [B,1,Q,K]; got shape={tuple(keep.shape)}")
+            rel_pos = _relative_matrix(
+                relative_pos, Lq, Lk, self.position_buckets, self.max_relative_positions, q.device
+            )
+        keep = _dense_keep(attention_mask, q.device)
         ctx, probs = unfused_attention(
             q, k, v, kr, qr, rel_pos, keep, att_span, scale, types, self.dropout if self.training else None
         )

@@ -21,8 +21,10 @@ Parameter names are the reference's, so state dicts load unchanged.  The
 GEMMs stay plain library GEMMs (hipBLASLt); everything between them runs in
 the HIP kernels through the ``torch.library`` ops below, which have fake
 implementations for ``torch.compile`` and autograd registrations.  Hidden
-dropout is refused in training (the kernels have no dropout), as the fused
-attention refuses attention dropout.
+dropout p > 0 in training runs torch's dropout on the dense output (bias
+included, as the reference's ``dropout(dense(x))``) and then the residual
+LayerNorm kernel.  CPU tensors run the reference's blocks in torch
+operations (the kernels run on the GPU only).
 """
 
 from __future__ import annotations
@@ -106,6 +108,7 @@ def _add_ln_impl(
     """``y = LayerNorm(x + bias + res) * gamma + beta`` over the last dim;
     returns (y in ``out_dtype``, mean, rstd).  ``res`` has x's shape (a
     broadcast view is read in place)."""
+    _eager.refuse_capture("deberta_amd::add_ln")
     C = x.shape[-1]
     xr = _rows(x)
     N = xr.shape[0]
@@ -155,6 +158,7 @@ def _add_ln_bwd_impl(
     """(dz, dgamma, dbeta, dbias): dz the gradient of ``x + bias + res`` in
     ``dz_dtype``; the parameter gradients in gamma's dtype (dbias empty
     without a bias)."""
+    _eager.refuse_capture("deberta_amd::add_ln_bwd")
     C = x.shape[-1]
     xr = _rows(x)
     N = xr.shape[0]
@@ -252,6 +256,7 @@ def fused_add_layer_norm(
 
 def _bias_gelu_impl(x: Tensor, bias: Optional[Tensor]) -> Tensor:
     """``gelu(x + bias)`` (erf form) in x's dtype."""
+    _eager.refuse_capture("deberta_amd::bias_gelu")
     C = x.shape[-1]
     xr = _rows(x)
     y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
@@ -277,6 +282,7 @@ def _bias_gelu_fake(x, bias):
 def _bias_gelu_bwd_impl(dy: Tensor, x: Tensor, bias: Optional[Tensor]) -> tuple[Tensor, Tensor]:
     """(dz, dbias): the gradient of ``x + bias`` in x's dtype and dbias in
     the bias dtype (empty without a bias)."""
+    _eager.refuse_capture("deberta_amd::bias_gelu_bwd")
     C = x.shape[-1]
     xr, dyr = _rows(x), _rows(dy)
     N = xr.shape[0]
@@ -339,6 +345,7 @@ def _rtd_loss_impl(
 ) -> tuple[Tensor, Tensor, Tensor]:
     """(loss, logits, denom): ``logits = x @ w + b`` per row (float32) and
     ``loss = sum(active * BCE(logits, labels)) / max(sum(active), 1)``."""
+    _eager.refuse_capture("deberta_amd::rtd_loss")
     C = x.shape[-1]
     xr = _rows(x)
     N = xr.shape[0]
@@ -381,6 +388,7 @@ def _rtd_loss_bwd_impl(
 ) -> tuple[Tensor, Tensor, Tensor]:
     """(dx, dw, db) of the loss: dx in x's dtype, dw / db in w's dtype (db
     empty without a bias)."""
+    _eager.refuse_capture("deberta_amd::rtd_loss_bwd")
     C = x.shape[-1]
     xr = _rows(x)
     N = xr.shape[0]
@@ -448,14 +456,17 @@ def call_rtd_loss(x: Tensor, w: Tensor, b: Optional[Tensor], labels: Tensor, act
 # modules
 
 
-def _require_gpu(t: Tensor) -> None:
-    if t.device.type != "cuda":
-        raise RuntimeError(f"the fused blocks run on the GPU (HIP) only; got a tensor on {t.device}")
+def _on_gpu(t: Tensor) -> bool:
+    return t.device.type == "cuda"
 
 
-def _no_dropout(module: nn.Module, drop: nn.Dropout) -> None:
-    if module.training and drop.p > 0.0:
-        raise NotImplementedError("hidden dropout p > 0 in training is not supported by the fused row kernels")
+def _bce_loss(logits: Tensor, labels: Tensor, active: Optional[Tensor]) -> Tensor:
+    """The discriminator loss in torch operations (rtd.py:1129-1139): BCE with
+    logits per token in float32, summed over the active tokens, over
+    max(#active, 1)."""
+    act = torch.ones_like(logits, dtype=torch.float32) if active is None else active.to(torch.float32)
+    per_token = F.binary_cross_entropy_with_logits(logits.float(), labels.float(), reduction="none")
+    return (per_token * act).sum() / act.sum().clamp(min=1.0)
 
 
 class FusedSelfOutput(nn.Module):
@@ -471,8 +482,12 @@ class FusedSelfOutput(nn.Module):
         self.dropout = nn.Dropout(float(getattr(config, "hidden_dropout_prob", 0.0)))
 
     def forward(self, hidden_states: Tensor, input_tensor: Tensor) -> Tensor:
-        _require_gpu(hidden_states)
-        _no_dropout(self, self.dropout)
+        if not _on_gpu(hidden_states):  # the reference's block in torch operations
+            return self.LayerNorm(self.dropout(self.dense(hidden_states)) + input_tensor)
+        if self.training and self.dropout.p > 0.0:
+            # dropout acts on dense(x) with its bias: torch's dropout, then
+            # the residual LayerNorm in one kernel
+            return fused_add_layer_norm(self.dropout(self.dense(hidden_states)), None, input_tensor, self.LayerNorm)
         # the bias is added in float32 inside the LayerNorm kernel (in its
         # own dtype, the LayerNorm's)
         x = F.linear(hidden_states, self.dense.weight)
@@ -500,7 +515,8 @@ class FusedIntermediate(nn.Module):
         self.dense = nn.Linear(int(config.hidden_size), int(config.intermediate_size))
 
     def forward(self, hidden_states: Tensor) -> Tensor:
-        _require_gpu(hidden_states)
+        if not _on_gpu(hidden_states):
+            return F.gelu(self.dense(hidden_states))
         x = F.linear(hidden_states, self.dense.weight)
         bias = self.dense.bias
         if bias is not None:
@@ -541,10 +557,12 @@ class FusedRTDHead(nn.Module):
         return not (mask.ndim == 3 and mask.shape[-2] != 1)
 
     def _features(self, hidden_states: Tensor, attention_mask: Optional[Tensor]) -> Tensor:
-        _require_gpu(hidden_states)
         res = None
         if self._use_global_cls_context(attention_mask):
             res = hidden_states[:, 0:1, :].expand(hidden_states.shape)
+        if not _on_gpu(hidden_states):  # the reference's head in torch operations
+            x = self.norm(hidden_states + res if res is not None else hidden_states)
+            return self.act(self.dense(x))
         x = fused_add_layer_norm(hidden_states, None, res, self.norm)
         x = F.linear(x, self.dense.weight)
         bias = self.dense.bias
@@ -567,6 +585,9 @@ class FusedRTDHead(nn.Module):
         labels)) / max(sum(active), 1)`` and the float32 logits, the
         classifier and the loss in one kernel."""
         x = self._features(hidden_states, attention_mask)
+        if not _on_gpu(x):
+            logits = self.classifier(x).squeeze(-1).float()
+            return _bce_loss(logits, labels, active), logits
         w = self.classifier.weight.reshape(-1)
         b = self.classifier.bias
         if b is not None:
@@ -595,5 +616,6 @@ class RelativeEmbeddings(nn.Module):
 
     def forward(self) -> Tensor:
         w = self.rel_embeddings.weight
-        _require_gpu(w)
+        if not _on_gpu(w):
+            return self.LayerNorm(w)
         return fused_add_layer_norm(w, None, None, self.LayerNorm)

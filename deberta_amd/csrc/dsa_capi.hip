@@ -28,9 +28,9 @@
 // Library-owned scratch of dsa_fwd_static: the launch order's cost and
 // order arrays for up to 65536 (batch row, query tile) items, 512 KiB, one
 // copy per GPU for the life of the process.  Host code never uses the
-// array's name as an address: static_scratch() resolves this GPU's copy
-// once per device (hipGetSymbolAddress with that device current) and keeps
-// it.
+// array's name as an address: static_scratch_locked() resolves this GPU's
+// copy (hipGetSymbolAddress with that device current) and keeps it once the
+// lookup has succeeded.
 constexpr size_t kStaticScratchBytes = 512 * 1024;
 static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
 
@@ -464,20 +464,52 @@ static_assert(kStaticScratchBytes == 2 * kMaxOrderItems * sizeof(int), "the stat
 
 constexpr int kMaxDevices = 64;
 
-void* static_scratch(int* err_device) {
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
-    *err_device = dev;
-    return nullptr;
-  }
-  static std::once_flag once[kMaxDevices];
-  static void* addr[kMaxDevices];
-  std::call_once(once[dev], [dev] {
+// Per-device state of dsa_fwd_static: this GPU's address of `scratch` and an
+// event recorded after each static forward (the next one, on any stream,
+// waits for it: the calls share the array).  Set up once per device with
+// that device current; a failed lookup is not kept, so a later call tries
+// again.
+struct StaticState {
+  std::mutex mu;
+  void* addr = nullptr;
+  hipEvent_t done = nullptr;
+};
+
+StaticState& static_state(int dev) {
+  static StaticState st[kMaxDevices];
+  return st[dev];
+}
+
+// With the device's lock held: the scratch address (nullptr on failure).
+void* static_scratch_locked(StaticState& s) {
+  if (!s.addr) {
     void* ptr = nullptr;
-    addr[dev] = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) == hipSuccess ? ptr : nullptr;
-  });
-  *err_device = dev;
-  return addr[dev];
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    s.addr = ptr;
+  }
+  if (!s.done && hipEventCreateWithFlags(&s.done, hipEventDisableTiming) != hipSuccess) {
+    (void)hipGetLastError();
+    s.done = nullptr;
+  }
+  return s.done ? s.addr : nullptr;
+}
+
+// Refuses a stream that is being captured into a HIP graph: capturing the
+// library's launches ended in a host fault inside the runtime's capture end
+// whose cause is not known, so the library does not run under capture.
+int refuse_capture(hipStream_t st, const char* what) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  if (cs != hipStreamCaptureStatusNone)
+    return fail("%s: the stream is capturing a HIP graph; the library's launches are not supported under graph capture",
+                what);
+  return 0;
 }
 
 // Bytes of the forward's k-step copy of one relative table (TableKs).
@@ -720,6 +752,7 @@ int dsa_fwd(const dsa_fwd_args* a, void* stream) {
   g_err.clear();
   if (check_fwd(a)) return 1;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (refuse_capture(st, "dsa_fwd")) return 1;
   const size_t ob = order_bytes(a, fwd_tiles(a)), tb = tables_ks_bytes(a);
   int* buf = nullptr;
   void* tabs = nullptr;
@@ -737,18 +770,31 @@ int dsa_fwd(const dsa_fwd_args* a, void* stream) {
 int dsa_fwd_static(const dsa_fwd_args* a, void* stream) {
   g_err.clear();
   if (check_fwd(a)) return 1;
-  int* buf = nullptr;
-  if (a->key_keep || a->seg) {
-    const int64_t n = (int64_t)a->B * fwd_tiles(a);
-    if (n > kMaxOrderItems)
-      return fail("dsa_fwd_static: B * ceil(Lq / 128) = %lld launch-order items exceed the static scratch's "
-                  "%lld (%zu bytes); use dsa_fwd with a caller workspace",
-                  (long long)n, (long long)kMaxOrderItems, kStaticScratchBytes);
-    int dev = -1;
-    buf = static_cast<int*>(static_scratch(&dev));
-    if (!buf) return fail("dsa_fwd_static: no address for the static scratch on device %d", dev);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (refuse_capture(st, "dsa_fwd_static")) return 1;
+  if (!(a->key_keep || a->seg)) return run_fwd(a, nullptr, nullptr, st);  // no scratch used
+  const int64_t n = (int64_t)a->B * fwd_tiles(a);
+  if (n > kMaxOrderItems)
+    return fail("dsa_fwd_static: B * ceil(Lq / 128) = %lld launch-order items exceed the static scratch's "
+                "%lld (%zu bytes); use dsa_fwd with a caller workspace",
+                (long long)n, (long long)kMaxOrderItems, kStaticScratchBytes);
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail("dsa_fwd_static: no current device below %d (got %d)", kMaxDevices, dev);
+  StaticState& s = static_state(dev);
+  // The lock orders the calls of this process on the device: each waits on
+  // its stream for the previous static forward (on any stream) and records
+  // its own end, so no two of them use the array at once.
+  std::lock_guard<std::mutex> lock(s.mu);
+  int* buf = static_cast<int*>(static_scratch_locked(s));
+  if (!buf) return fail("dsa_fwd_static: no address for the static scratch (or its event) on device %d", dev);
+  if (hipStreamWaitEvent(st, s.done, 0) != hipSuccess) return fail("dsa_fwd_static: hipStreamWaitEvent failed");
+  const int rc = run_fwd(a, buf, nullptr, st);
+  if (hipEventRecord(s.done, st) != hipSuccess) {
+    (void)hipGetLastError();
+    return rc ? rc : fail("dsa_fwd_static: hipEventRecord failed");
   }
-  return run_fwd(a, buf, nullptr, static_cast<hipStream_t>(stream));
+  return rc;
 }
 
 int dsa_bias(const dsa_fwd_args* a, void* out, const int64_t* out_strides, void* stream) {
@@ -784,11 +830,12 @@ int dsa_bias(const dsa_fwd_args* a, void* out, const int64_t* out_strides, void*
     return fail("dsa: qr must be 16-byte aligned with strides that are multiples of %d", vec);
   if (check_qc(a)) return 1;
   if ((reinterpret_cast<uintptr_t>(out) % elem_bytes(a->dtype)) != 0) return fail("dsa: out must be aligned to its element size");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (refuse_capture(st, "dsa_bias")) return 1;
   dsa::BiasParams bp;
   bp.f = to_params(a);
   bp.out = out;
   for (int s = 0; s < 3; ++s) bp.obs[s] = out_strides[s];
-  hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)(a->B * (int64_t)a->H * nqt * nkt));
   const bool qc = a->qc != nullptr;
   if (a->dtype == DSA_BF16) {
@@ -869,6 +916,7 @@ int dsa_bwd(const dsa_bwd_args* a, void* stream) {
     return fail("dsa: workspace of %zu bytes required, got %zu", ws.total, a->workspace_bytes);
   if (!aligned16(a->workspace)) return fail("dsa: workspace must be 16-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (refuse_capture(st, "dsa_bwd")) return 1;
   const int mode = mask_mode(&f);
   if (f.dtype == DSA_BF16) {
     return f.D == 64 ? launch_bwd<dsa::bf16, 64>(a, ws, mode, st) : launch_bwd<dsa::bf16, 32>(a, ws, mode, st);
@@ -925,6 +973,7 @@ size_t dsa_block_workspace_bytes(int kind, int64_t N, int32_t C) {
 int dsa_add_ln_fwd(const dsa_ln_args* a, void* stream) {
   g_err.clear();
   if (check_ln(a, false)) return 1;
+  if (refuse_capture(static_cast<hipStream_t>(stream), "dsa_add_ln_fwd")) return 1;
   const dsa::rows::LnParams p = ln_params(a);
   by_chunks(a->C, [&](auto nc) {
     by_dtype(a->x_dtype, [&](auto tx) {
@@ -943,6 +992,7 @@ int dsa_add_ln_fwd(const dsa_ln_args* a, void* stream) {
 int dsa_add_ln_bwd(const dsa_ln_args* a, void* stream) {
   g_err.clear();
   if (check_ln(a, true)) return 1;
+  if (refuse_capture(static_cast<hipStream_t>(stream), "dsa_add_ln_bwd")) return 1;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dsa::rows::LnParams p = ln_params(a);
   const int64_t nb = cdiv(a->N, dsa::rows::LN_RB);
@@ -966,6 +1016,7 @@ int dsa_add_ln_bwd(const dsa_ln_args* a, void* stream) {
 int dsa_bias_gelu_fwd(const dsa_gelu_args* a, void* stream) {
   g_err.clear();
   if (check_gelu(a, false)) return 1;
+  if (refuse_capture(static_cast<hipStream_t>(stream), "dsa_bias_gelu_fwd")) return 1;
   const dsa::rows::GeluParams p = gelu_params(a);
   if (cdiv(a->N, dsa::rows::GELU_RB) > 65535)
     return fail("dsa_bias_gelu: N too large (%lld rows, at most %d)", (long long)a->N, 65535 * dsa::rows::GELU_RB);
@@ -982,6 +1033,7 @@ int dsa_bias_gelu_fwd(const dsa_gelu_args* a, void* stream) {
 int dsa_bias_gelu_bwd(const dsa_gelu_args* a, void* stream) {
   g_err.clear();
   if (check_gelu(a, true)) return 1;
+  if (refuse_capture(static_cast<hipStream_t>(stream), "dsa_bias_gelu_bwd")) return 1;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dsa::rows::GeluParams p = gelu_params(a);
   const int64_t nb = cdiv(a->N, dsa::rows::GELU_RB);
@@ -1002,6 +1054,7 @@ int dsa_bias_gelu_bwd(const dsa_gelu_args* a, void* stream) {
 int dsa_rtd_loss_fwd(const dsa_rtd_args* a, void* stream) {
   g_err.clear();
   if (check_rtd(a, false)) return 1;
+  if (refuse_capture(static_cast<hipStream_t>(stream), "dsa_rtd_loss_fwd")) return 1;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dsa::rows::RtdParams p = rtd_params(a);
   const int64_t nb = cdiv(a->N, dsa::rows::RTD_RB);
@@ -1019,6 +1072,7 @@ int dsa_rtd_loss_fwd(const dsa_rtd_args* a, void* stream) {
 int dsa_rtd_loss_bwd(const dsa_rtd_args* a, void* stream) {
   g_err.clear();
   if (check_rtd(a, true)) return 1;
+  if (refuse_capture(static_cast<hipStream_t>(stream), "dsa_rtd_loss_bwd")) return 1;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dsa::rows::RtdParams p = rtd_params(a);
   const int64_t nb = cdiv(a->N, dsa::rows::RTD_RB);

@@ -63,7 +63,15 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
   // head r % H, heaviest first
   int qt, h, b;
   if (p.order) {
-    const int it = p.order[blockIdx.x / p.H];
+    // one read of the item, shared through LDS, so that the whole workgroup
+    // takes one decision; an item outside [0, B * NQT) (an order another
+    // call overwrote meanwhile) ends the workgroup before it indexes
+    // anything
+    __shared__ int item;
+    if (tid == 0) item = p.order[blockIdx.x / p.H];
+    __syncthreads();
+    const int it = item;
+    if (it < 0 || it >= p.B * NQT) return;
     h = blockIdx.x % p.H, qt = it % NQT, b = it / NQT;
   } else {
     const int m = xcd_remap(blockIdx.x, gridDim.x);

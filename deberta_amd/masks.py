@@ -14,6 +14,13 @@ import torch
 from torch.utils.weak import WeakIdKeyDictionary
 
 
+def tensor_version(t: torch.Tensor) -> Optional[int]:
+    """``t``'s version counter (bumped by every in-place write), or None for
+    an inference tensor, which keeps none: results cached per tensor object
+    are then recomputed on every call."""
+    return None if t.is_inference() else t._version
+
+
 def normalize_keep_mask(mask: torch.Tensor, *, name: str = "attention_mask") -> torch.Tensor:
     """Bool keep mask: bool passes through, integers become ``!= 0``, floating
     masks raise ``ValueError`` and non-tensors ``TypeError`` (same messages as
@@ -143,11 +150,13 @@ def _segments_cached(mask: torch.Tensor, pair_keep: torch.Tensor) -> Optional[to
     """Segment ids of ``pair_keep`` (a ``[B or 1, L, L]`` view of ``mask``,
     not expanded over the batch), cached per mask object and version.  The
     ids keep the mask's own batch extent; callers expand them."""
-    hit = _SEGMENTS_OF.get(mask)
-    if hit is not None and hit[0] == mask._version:
+    version = tensor_version(mask)
+    hit = _SEGMENTS_OF.get(mask) if version is not None else None
+    if hit is not None and hit[0] == version:
         return hit[1]
     ids = dense_as_segments(pair_keep)
-    _SEGMENTS_OF[mask] = (mask._version, ids)
+    if version is not None:
+        _SEGMENTS_OF[mask] = (version, ids)
     return ids
 
 
@@ -165,8 +174,11 @@ def _all_kept(mask: torch.Tensor, key_keep: torch.Tensor) -> bool:
     answer True once the check has finished and found every key kept.  Such
     a mask then runs as no mask (the same results: every pair is kept and
     no row is dead), on the kernels without masking or launch order."""
+    version = tensor_version(mask)
+    if version is None:  # no version counter: no check can be reused
+        return False
     hit = _ALL_KEPT.get(mask)
-    if hit is not None and hit[0] == mask._version:
+    if hit is not None and hit[0] == version:
         return hit[1].query() and bool(hit[2])
     flag = torch.zeros((), dtype=torch.bool, pin_memory=True)
     stream = torch.cuda.current_stream(key_keep.device)  # the copy's stream: the mask's device's
@@ -174,7 +186,7 @@ def _all_kept(mask: torch.Tensor, key_keep: torch.Tensor) -> bool:
         flag.copy_(key_keep.bool().all(), non_blocking=True)
         ev = torch.cuda.Event()
         ev.record(stream)
-    _ALL_KEPT[mask] = (mask._version, ev, flag)
+    _ALL_KEPT[mask] = (version, ev, flag)
     return False
 
 

@@ -208,6 +208,7 @@ def _dsa_fwd_impl(
     """(out, lse, bias).  With c2p/p2c and ``save_bias`` the relative score
     term is written to ``bias`` for the backward (which needs it); else
     ``bias`` is empty.  ``qc``: the c2p term's query rows (q when None)."""
+    _eager.refuse_capture("deberta_amd::dsa_fwd")
     _validate(q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, qc)
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
     kr = None if kr is None else _kernel_ready(kr)
@@ -349,6 +350,7 @@ def _dsa_bwd_impl(
     relative term dsa_fwd saved (required with c2p/p2c).  With ``qc`` (the
     c2p term's query rows), dqc is its gradient and dq the content part;
     else dqc is empty."""
+    _eager.refuse_capture("deberta_amd::dsa_bwd")
     if kr is not None or qr is not None:
         _alert_nondeterministic_tables()
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
@@ -596,6 +598,7 @@ def _dsa_bias_impl(
     in q's dtype (the reference's ``disentangled_attention_bias``,
     deberta_v2_native.py:530-562), unmasked; zeros without tables.  q, k are
     ``[B, L, H, D]`` views; ``qc`` the c2p term's query rows (q when None)."""
+    _eager.refuse_capture("deberta_amd::dsa_bias")
     _validate(q, k, k, kr, qr, rel_table, None, None, att_span, qc)
     q, k = _kernel_ready(q), _kernel_ready(k)
     kr = None if kr is None else _kernel_ready(kr)

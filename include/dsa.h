@@ -190,17 +190,21 @@ int dsa_fwd(const dsa_fwd_args* args, void* stream);
 int dsa_bwd(const dsa_bwd_args* args, void* stream);
 
 /* dsa_fwd without any caller-provided scratch: no counterpart in the
- * reference.  For callers that cannot allocate device memory (code under
- * HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc): under key_keep or seg masks the heaviest-first launch order's
- * cost and order arrays (what dsa_fwd_args.workspace brings to dsa_fwd)
- * live in a library-owned static device array of DSA_FWD_STATIC_SCRATCH_BYTES
- * per GPU, held until the process ends; args->workspace is ignored.
- * Results equal dsa_fwd's.  Sizes whose order needs more than the array
- * (B * ceil(Lq / 128) > 65536 items) are refused with an error.  Calls that
- * overlap on one GPU (concurrent streams or host threads) race on the array;
- * every call writes each element it reads, so nothing carries over between
- * calls.  Call with the stream's device current. */
+ * reference.  For callers that cannot allocate device memory (tight serving
+ * loops, harnesses that forbid hipMalloc): under key_keep or seg masks the
+ * heaviest-first launch order's cost and order arrays (what
+ * dsa_fwd_args.workspace brings to dsa_fwd) live in a library-owned static
+ * device array of DSA_FWD_STATIC_SCRATCH_BYTES per GPU, held until the
+ * process ends; args->workspace is ignored.  Results equal dsa_fwd's.
+ * Sizes whose order needs more than the array (B * ceil(Lq / 128) > 65536
+ * items) are refused with an error.  The calls of one process on one GPU
+ * share the array and are serialised: each waits on its stream for the
+ * previous one (a per-device event) before it writes the array, whatever
+ * stream or host thread made it; calls from other processes have their own
+ * copy.  Every call writes each element it reads, so nothing carries over
+ * between calls.  Call with the stream's device current.  Like every entry
+ * point here it refuses a stream that is capturing a HIP graph (the
+ * library's launches are not supported under capture). */
 #define DSA_FWD_STATIC_SCRATCH_BYTES (512u * 1024u)
 int dsa_fwd_static(const dsa_fwd_args* args, void* stream);
 

@@ -361,17 +361,18 @@ def test_module_layout_matches_the_reference_shape(share, types):
     assert ours.pos_ebd_size == 256 and ours.attn_kernel == "dynamic"
 
 
-def test_module_rejects_bad_config_and_cpu():
+def test_module_rejects_bad_config_and_the_op_rejects_cpu():
     with pytest.raises(ValueError, match="divisible"):
         DisentangledSelfAttention(eager.make_config(hidden_size=30, num_attention_heads=4))
     with pytest.raises(ValueError, match="model.hf.attention_kernel must be one of"):
         DisentangledSelfAttention(eager.make_config(hf_attention_kernel="nope"))
-    m = DisentangledSelfAttention(eager.make_config(hidden_size=64, num_attention_heads=4))
+    # the module runs CPU tensors on its torch path (tests/test_module_cpu.py);
+    # the kernels' own entry, fused_attention, refuses them
+    from deberta_amd.attention import fused_attention
+
+    q = torch.randn(1, 8, 4, 16)
     with pytest.raises(RuntimeError, match="GPU"):
-        m(torch.randn(1, 8, 64), None, rel_embeddings=torch.randn(512, 64))
-    # the probabilities path (torch operations on the device) is GPU-only too
-    with pytest.raises(RuntimeError, match="GPU"):
-        m(torch.randn(1, 8, 64), None, output_attentions=True)
+        fused_attention(q, q, q, None, None, None, None, 1, 0.25)
 
 
 def test_package_surface():
@@ -515,8 +516,6 @@ def test_fused_blocks_take_the_reference_state_dicts():
     ):
         assert {k: v.shape for k, v in ours.state_dict().items()} == {k: v.shape for k, v in ref.state_dict().items()}
         ours.load_state_dict(ref.state_dict(), strict=True)
-    with pytest.raises(RuntimeError, match="GPU"):
-        FusedSelfOutput(cfg)(torch.randn(1, 4, 64), torch.randn(1, 4, 64))
     with pytest.raises(NotImplementedError, match="gelu"):
         FusedIntermediate(eager.make_config(hidden_size=64, intermediate_size=256, hidden_act="relu"))
 
@@ -542,3 +541,29 @@ def test_per_head_masks_become_head_strided_pair_masks():
     ops._validate(q, k, v, None, None, None, None, pk, 16)
     args = ops._fill_fwd_args(q, k, v, None, None, None, None, pk, q, torch.empty(1), 16, 0.1)
     assert args.pair_keep_stride_h == pk.stride(1) and tuple(args.pair_keep_strides) == (pk.stride(0), pk.stride(2))
+
+
+def test_ops_refuse_graph_capture(monkeypatch):
+    """Every op implementation refuses to launch while the current stream is
+    capturing a CUDA/HIP graph (the query is patched: no graph is captured
+    here), before it validates or allocates anything."""
+    import deberta_amd.blocks as blocks
+    from deberta_amd import ops
+
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    q, k, v, kr, qr, table = _inputs()
+    calls = [
+        lambda: ops._dsa_fwd_impl(q, k, v, kr, qr, table, None, None, 16, 0.1),
+        lambda: ops._dsa_bwd_impl(q, q, k, v, kr, qr, table, None, None, q, q, q, 16, 0.1),
+        lambda: ops._dsa_bias_impl(q, k, kr, qr, table, 16, 0.1),
+        lambda: ops._dsa_fwd_packed_impl(torch.stack([q, k, v], 2), kr, qr, table, None, None, 16, 0.1),
+        lambda: blocks._add_ln_impl(q, None, None, q, q, 1e-7, q.dtype),
+        lambda: blocks._add_ln_bwd_impl(q, q, None, None, q, q, q, q.dtype),
+        lambda: blocks._bias_gelu_impl(q, None),
+        lambda: blocks._bias_gelu_bwd_impl(q, q, None),
+        lambda: blocks._rtd_loss_impl(q, q, None, q, None),
+        lambda: blocks._rtd_loss_bwd_impl(q, q, q, None, q, None, q, q),
+    ]
+    for call in calls:
+        with pytest.raises(RuntimeError, match="capturing a CUDA/HIP graph"):
+            call()

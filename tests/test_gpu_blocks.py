@@ -183,3 +183,35 @@ def test_autocast_output_dtypes_follow_torch(gpu):
                                                (768,), so.LayerNorm.weight, so.LayerNorm.bias, 1e-7)
     assert y.dtype == ref_y.dtype == torch.float32 and z.dtype == torch.bfloat16
     assert max_abs(y, ref_y) <= 5e-2
+
+
+def test_hidden_dropout_in_training(gpu):
+    """Hidden dropout p > 0 in training: torch's dropout on the dense output
+    (bias included), then the residual LayerNorm kernel.  With one seed the
+    reference block in torch operations on the GPU draws the same mask, so
+    the outputs and every gradient agree (fp32, 1e-4 of scale); the dropped
+    share is near p."""
+    cfg = _cfg()
+    cfg.hidden_dropout_prob = 0.1
+    ref = ob.OutputResidualNorm(cfg).to(gpu)
+    ours = FusedSelfOutput(cfg).to(gpu)
+    ours.load_state_dict(ref.state_dict(), strict=True)
+    ref.train(), ours.train()
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(4, 128, 768, generator=g).to(gpu)
+    res = torch.randn(4, 128, 768, generator=g).to(gpu)
+    outs = []
+    for m in (ref, ours):
+        xs, rs = x.clone().requires_grad_(True), res.clone().requires_grad_(True)
+        torch.manual_seed(5)
+        out = m(xs, rs)
+        dout = torch.randn(out.shape, generator=torch.Generator().manual_seed(2)).to(gpu)
+        grads = torch.autograd.grad(out, [xs, rs] + list(m.parameters()), dout)
+        outs.append([out.detach()] + [gr.detach() for gr in grads])
+    errs = [max_rel(b.cpu(), a.cpu()) for a, b in zip(*outs)]
+    _say(f"[hidden dropout] {errs}")
+    assert all(e <= 1e-4 for e in errs), errs
+    with torch.no_grad():
+        torch.manual_seed(6)
+        kept = ours.dropout(torch.ones(1 << 20, device=gpu)).ne(0).float().mean()
+    assert abs(float(kept) - 0.9) < 0.01

@@ -60,7 +60,9 @@ def test_config1_fp32(share, mask, gpu):
 
 def test_bf16_autocast_base_shape(gpu):
     """config-2 layer shape (hidden 768, 12 heads x 64) on 2 rows of 512,
-    under bf16 autocast, against the fp32 oracle: max|err|/max|ref| <= 3e-2."""
+    under bf16 autocast, against the fp32 oracle: the output and the input
+    gradient max|err| <= 2e-2 (the north star's bf16 bound), the relative
+    table's and every parameter's gradient max|err| / max|ref| <= 2e-2."""
     cfg = eager.make_config(hidden_size=768, num_attention_heads=12, share_att_key=True)
     ref, ours = _pair(cfg, seed=1)
     ours = ours.to(gpu)
@@ -72,14 +74,14 @@ def test_bf16_autocast_base_shape(gpu):
     m = keep[:, None, None, :]
     a = _run(ref, x, m, rel, "cpu")
     b = _run(ours, x, m, rel, gpu, autocast=True)
-    # Under autocast the projections themselves run in bf16, so the module's
-    # gradients are compared relative to their scale (the op-level bound of
-    # 2e-2 absolute is checked in test_gpu_parity.py).
+    # Under autocast the projections themselves run in bf16, and parameter
+    # gradients sum over every row: those are compared relative to their
+    # scale; the output and the input gradient absolutely.
     errs = _errors(a, b)
-    out_abs = max_abs(b["out"], a["out"])
-    _say(f"[module bf16 autocast] {errs} out max|err| {out_abs:.3e}")
-    assert all(e <= 3e-2 for e in errs.values()), errs
-    assert out_abs <= 2e-2  # the output itself: the north star's bf16 bound
+    abs_errs = {k: max_abs(b[k], a[k]) for k in ("out", "dx")}
+    _say(f"[module bf16 autocast] abs {abs_errs} rel-to-scale {errs}")
+    assert all(e <= 2e-2 for e in abs_errs.values()), abs_errs
+    assert all(e <= 2e-2 for k, e in errs.items() if k not in abs_errs), errs
 
 
 def test_explicit_relative_pos_matches_none(gpu):
@@ -213,3 +215,32 @@ def test_query_states_against_oracle(share, gpu):
     errs = _errors(a, b)
     _say(f"[query_states share={share}] {errs}")
     assert all(e <= 1e-4 for e in errs.values()), errs
+
+
+def test_alternating_relative_pos_matches_oracle_every_call(gpu):
+    """Fresh int32 relative_pos matrices of one shape, canonical and not in
+    turn (the module's int64 copy of each is a new temporary that reuses
+    freed blocks): every call matches the oracle with that call's matrix
+    (canonical ones on the kernels, the others on the torch path)."""
+    cfg = _config1()
+    ref, ours = _pair(cfg)
+    ours = ours.to(gpu)
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(2, 128, 128, generator=g)
+    rel = torch.randn(512, 128, generator=g) * 0.02
+    from deberta_amd import build_relative_position
+
+    canon = build_relative_position(128, 128, bucket_size=256, max_position=512)
+    errs = []
+    with torch.no_grad():
+        for n in range(12):
+            rp = canon.clone()
+            if n % 2:
+                i, j = torch.randint(0, 128, (2,), generator=g).tolist()
+                rp[i, j] += 3
+            rp = rp.to(torch.int32)
+            want, _ = ref(x, None, relative_pos=rp, rel_embeddings=rel)
+            got, _ = ours(x.to(gpu), None, relative_pos=rp.to(gpu), rel_embeddings=rel.to(gpu))
+            errs.append(max_rel(got.cpu(), want))
+    _say(f"[alternating relative_pos] {errs}")
+    assert all(e <= 1e-4 for e in errs), errs

@@ -234,3 +234,63 @@ def test_keep_mask_contract():
     with pytest.raises(ValueError):
         eager.keep_mask(torch.ones(2, 2))
     assert torch.equal(eager.keep_mask(torch.tensor([2, 0, -1])), torch.tensor([True, False, True]))
+
+
+def test_encoder_mask_values_by_element():
+    """The oracle's encoder mask (deberta_v2_native.py:1049-1068) element by
+    element, from loops: rank 2 (B, S) -> (B, 1, 1, S) with value m[b, j];
+    rank 3 (B, S, S) -> (B, 1, S, S) with m[b, i, j]; rank 4 with a head
+    axis -> (B, 1, S, S) with OR over heads; integer masks are != 0.  The
+    package's get_attention_mask gives the same tensors."""
+    from deberta_amd.masks import get_attention_mask
+
+    g = torch.Generator().manual_seed(0)
+    B, H, S = 2, 3, 5
+    m2 = torch.randint(0, 3, (B, S), generator=g)
+    m3 = torch.rand(B, S, S, generator=g) < 0.5
+    m4 = torch.rand(B, H, S, S, generator=g) < 0.3
+    e2, e3, e4 = eager.encoder_mask(m2), eager.encoder_mask(m3), eager.encoder_mask(m4)
+    assert e2.shape == (B, 1, 1, S) and e3.shape == (B, 1, S, S) and e4.shape == (B, 1, S, S)
+    for b in range(B):
+        for i in range(S):
+            for j in range(S):
+                assert bool(e2[b, 0, 0, j]) == (int(m2[b, j]) != 0)
+                assert bool(e3[b, 0, i, j]) == bool(m3[b, i, j])
+                assert bool(e4[b, 0, i, j]) == any(bool(m4[b, h, i, j]) for h in range(H))
+    one_head = m4[:, :1]
+    assert torch.equal(eager.encoder_mask(one_head), one_head)
+    for m in (m2, m3, m4, one_head):
+        assert torch.equal(get_attention_mask(m), eager.encoder_mask(m))
+    with pytest.raises(ValueError, match="rank"):
+        eager.encoder_mask(torch.ones(1, 1, 1, 1, 2, dtype=torch.bool))
+    with pytest.raises(ValueError, match="rank"):
+        get_attention_mask(torch.ones(1, 1, 1, 1, 2, dtype=torch.bool))
+
+
+def test_canonical_rel_rank_handling_by_element():
+    """The oracle's relative_pos normalisation (deberta_v2_native.py:235-271):
+    None builds the canonical matrix; rank 4 takes [0, 0], rank 3 takes
+    [0] (batch-shared only), rank 2 is used as is, all sliced to
+    [:Lq, :Lk] and cast to long; other ranks raise.  Checked against
+    matrices whose entries name their own indices, so a wrong pick of
+    batch, head, row or column shows."""
+    from deberta_amd.relpos import normalize_relative_pos
+
+    def coded(*shape):
+        return torch.arange(int(torch.tensor(shape).prod()), dtype=torch.int32).reshape(shape)
+
+    Lq, Lk = 3, 4
+    r4, r3, r2 = coded(2, 2, 5, 6), coded(2, 5, 6), coded(5, 6)
+    want4 = torch.tensor([[r4[0, 0, i, j] for j in range(Lk)] for i in range(Lq)], dtype=torch.long)
+    want3 = torch.tensor([[r3[0, i, j] for j in range(Lk)] for i in range(Lq)], dtype=torch.long)
+    want2 = torch.tensor([[r2[i, j] for j in range(Lk)] for i in range(Lq)], dtype=torch.long)
+    for given, want in ((r4, want4), (r3, want3), (r2, want2)):
+        got = eager.canonical_rel(given, Lq, Lk, 8, 16)
+        assert got.dtype == torch.long and torch.equal(got, want)
+        assert torch.equal(normalize_relative_pos(given, Lq, Lk), want)
+    assert torch.equal(eager.canonical_rel(None, Lq, Lk, 8, 16), eager.relative_positions(Lq, Lk, 8, 16))
+    for bad in (torch.zeros(5, dtype=torch.long), torch.zeros(1, 1, 1, 3, 3, dtype=torch.long)):
+        with pytest.raises(ValueError, match="rank"):
+            eager.canonical_rel(bad, 3, 3, 8, 16)
+        with pytest.raises(ValueError, match="rank"):
+            normalize_relative_pos(bad, 3, 3)
