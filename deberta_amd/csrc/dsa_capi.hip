@@ -681,6 +681,18 @@ int check_gelu(const dsa_gelu_args* a, bool bwd) {
   return 0;
 }
 
+// The 8-wide GELU kernels: rows in 8-element vectors (C, the row strides and
+// the tensors' element offsets multiples of 8; the bias, in its own dtype,
+// too).
+bool gelu_wide(const dsa_gelu_args* a, bool bwd) {
+  auto ok8 = [](const void* p, int64_t stride, int dt) {
+    return !p || ((reinterpret_cast<uintptr_t>(p) % (8u * (uintptr_t)elem_bytes(dt))) == 0 && stride % 8 == 0);
+  };
+  if (a->C % 8 || !ok8(a->x, a->x_stride, a->x_dtype) || !ok8(a->bias, 0, a->param_dtype)) return false;
+  if (!bwd) return ok8(a->y, a->y_stride, a->y_dtype);
+  return ok8(a->dy, a->dy_stride, a->dy_dtype) && ok8(a->dz, a->dz_stride, a->dz_dtype);
+}
+
 dsa::rows::GeluParams gelu_params(const dsa_gelu_args* a) {
   dsa::rows::GeluParams p;
   p.x = a->x;
@@ -1020,11 +1032,18 @@ int dsa_bias_gelu_fwd(const dsa_gelu_args* a, void* stream) {
   const dsa::rows::GeluParams p = gelu_params(a);
   if (cdiv(a->N, dsa::rows::GELU_RB) > 65535)
     return fail("dsa_bias_gelu: N too large (%lld rows, at most %d)", (long long)a->N, 65535 * dsa::rows::GELU_RB);
+  const bool wide = gelu_wide(a, false);
   by_dtype(a->x_dtype, [&](auto tx) {
     by_dtype(a->y_dtype, [&](auto ty) {
-      auto k = dsa::rows::gelu_fwd_kernel<typename decltype(tx)::type, typename decltype(ty)::type>;
-      hipLaunchKernelGGL(k, dim3((unsigned)cdiv(a->C / 4, 256), (unsigned)cdiv(a->N, dsa::rows::GELU_RB)), dim3(256), 0,
-                         static_cast<hipStream_t>(stream), p);
+      typedef typename decltype(tx)::type TX;
+      typedef typename decltype(ty)::type TY;
+      const dim3 rows_grid((unsigned)cdiv(a->N, dsa::rows::GELU_RB));
+      if (wide)
+        hipLaunchKernelGGL((dsa::rows::gelu8_fwd_kernel<TX, TY>), dim3((unsigned)cdiv(a->C, 1024), rows_grid.x), dim3(128),
+                           0, static_cast<hipStream_t>(stream), p);
+      else
+        hipLaunchKernelGGL((dsa::rows::gelu_fwd_kernel<TX, TY>), dim3((unsigned)cdiv(a->C / 4, 256), rows_grid.x),
+                           dim3(256), 0, static_cast<hipStream_t>(stream), p);
     });
   });
   return launch_check("gelu_fwd_kernel");
@@ -1038,10 +1057,17 @@ int dsa_bias_gelu_bwd(const dsa_gelu_args* a, void* stream) {
   const dsa::rows::GeluParams p = gelu_params(a);
   const int64_t nb = cdiv(a->N, dsa::rows::GELU_RB);
   if (nb > 65535) return fail("dsa_bias_gelu: N too large (%lld rows, at most %d)", (long long)a->N, 65535 * dsa::rows::GELU_RB);
+  const bool wide = gelu_wide(a, true);
   by_dtype(a->x_dtype, [&](auto tx) {
     by_dtype(a->dy_dtype, [&](auto tdy) {
-      auto k = dsa::rows::gelu_bwd_kernel<typename decltype(tx)::type, typename decltype(tdy)::type>;
-      hipLaunchKernelGGL(k, dim3((unsigned)cdiv(a->C / 4, 256), (unsigned)nb), dim3(256), 0, st, p);
+      typedef typename decltype(tx)::type TX;
+      typedef typename decltype(tdy)::type TDY;
+      if (wide)
+        hipLaunchKernelGGL((dsa::rows::gelu8_bwd_kernel<TX, TDY>), dim3((unsigned)cdiv(a->C, 1024), (unsigned)nb), dim3(128),
+                           0, st, p);
+      else
+        hipLaunchKernelGGL((dsa::rows::gelu_bwd_kernel<TX, TDY>), dim3((unsigned)cdiv(a->C / 4, 256), (unsigned)nb),
+                           dim3(256), 0, st, p);
     });
   });
   if (launch_check("gelu_bwd_kernel")) return 1;

@@ -28,7 +28,7 @@ constexpr int MAXC4 = 8;  // 4-element chunks a lane holds: C <= 64 * 4 * MAXC4 
 // column sums of the blocks are then many and short, summed by
 // reduce_cols_kernel with sixteen waves a column group.
 constexpr int LN_RB = 16;   // LayerNorm backward: 4 rows a wave
-constexpr int GELU_RB = 8;  // GELU forward and backward: rows per thread
+constexpr int GELU_RB = 8;   // GELU forward and backward: rows per thread
 constexpr int RTD_RB = 8;   // RTD loss: 2 rows a wave
 
 typedef float f4 __attribute__((ext_vector_type(4)));
@@ -228,9 +228,40 @@ struct GeluParams {
   int C, pdt;
 };
 
-DSA_DEV float gelu(float z) { return 0.5f * z * (1.f + erff(z * 0.70710678118654752f)); }
+// The erf GELU from one rational-exponential approximation of the
+// complementary error function, Abramowitz & Stegun 7.1.26 (|error of erf|
+// <= 1.5e-7 on x >= 0):
+//   erfc(x) = t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) exp(-x^2),  t = 1 / (1 + p x)
+// With x = |z| / sqrt 2:  h = Phi(-|z|) = erfc(x) / 2 (the halving folded
+// into the a_i, p divided by sqrt 2) and e = exp(-z^2 / 2), so
+//   gelu(z)  = z Phi(z) = max(z, 0) - |z| h
+//   gelu'(z) = Phi(z) + z phi(z) = (z >= 0 ? 1 - h : h) + z e / sqrt(2 pi)
+// and the forward and the backward share the exponential: about 12 VALU
+// operations and two transcendentals (v_rcp_f32, v_exp_f32) a value, where
+// the library erff takes about 40 (the forward was bound by them).
+struct GeluTail {
+  float h;  // Phi(-|z|)
+  float e;  // exp(-z^2 / 2)
+};
+DSA_DEV GeluTail gelu_tail(float z) {
+  constexpr float kP = 0.3275911f * 0.70710678118654752f;
+  constexpr float kA1 = 0.5f * 0.254829592f, kA2 = 0.5f * -0.284496736f, kA3 = 0.5f * 1.421413741f,
+                  kA4 = 0.5f * -1.453152027f, kA5 = 0.5f * 1.061405429f;
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(kP, fabsf(z), 1.f));
+  float poly = __builtin_fmaf(t, kA5, kA4);
+  poly = __builtin_fmaf(t, poly, kA3);
+  poly = __builtin_fmaf(t, poly, kA2);
+  poly = __builtin_fmaf(t, poly, kA1);
+  GeluTail r;
+  r.e = __builtin_amdgcn_exp2f((z * z) * (-0.5f * kLog2e));
+  r.h = (poly * t) * r.e;
+  return r;
+}
+DSA_DEV float gelu(float z) { return __builtin_fmaf(-fabsf(z), gelu_tail(z).h, fmaxf(z, 0.f)); }
 DSA_DEV float gelu_grad(float z) {
-  return 0.5f * (1.f + erff(z * 0.70710678118654752f)) + z * 0.39894228040143268f * __expf(-0.5f * z * z);
+  const GeluTail g = gelu_tail(z);
+  const float phi_pos = z >= 0.f ? 1.f - g.h : g.h;
+  return __builtin_fmaf(z * 0.39894228040143268f, g.e, phi_pos);
 }
 
 // block (column block, row block): thread per 4 columns, rows [GELU_RB *
@@ -292,6 +323,106 @@ __global__ __launch_bounds__(256) void gelu_bwd_kernel(GeluParams p) {
     }
   }
   if (p.dbias) *reinterpret_cast<f4*>(p.part + (int64_t)blockIdx.y * p.C + c) = acc;
+}
+
+// Eight consecutive elements of a row as two 4-element halves (one 16-byte
+// access for bf16, two for fp32).
+template <typename T>
+struct Io8 {
+  typedef T v8 __attribute__((ext_vector_type(8)));
+  static DSA_DEV void ld(const void* p, int64_t i, f4& a, f4& b) {
+    if constexpr (sizeof(T) == 2) {
+      const v8 v = *reinterpret_cast<const v8*>(static_cast<const T*>(p) + i);
+      a = f4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+      b = f4{(float)v[4], (float)v[5], (float)v[6], (float)v[7]};
+    } else {
+      a = Io<T>::ld(p, i);
+      b = Io<T>::ld(p, i + 4);
+    }
+  }
+  static DSA_DEV void st(void* p, int64_t i, const f4& a, const f4& b) {
+    if constexpr (sizeof(T) == 2) {
+      v8 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = (T)a[e], v[4 + e] = (T)b[e];
+      *reinterpret_cast<v8*>(static_cast<T*>(p) + i) = v;
+    } else {
+      Io<T>::st(p, i, a);
+      Io<T>::st(p, i + 4, b);
+    }
+  }
+};
+
+// bias + GELU on rows whose element offsets and stride are multiples of 8
+// (x, y and the bias aligned to 8 elements, C a multiple of 8): block
+// (1024-column slab, row block), thread per 8 columns, rows [GELU_RB *
+// blockIdx.y, + GELU_RB) with all their loads issued before the first
+// store.
+template <typename TX, typename TY>
+__global__ __launch_bounds__(128) void gelu8_fwd_kernel(GeluParams p) {
+  const int c = (blockIdx.x * 128 + threadIdx.x) * 8;
+  if (c >= p.C) return;
+  const f4 b0 = p.bias ? ld4(p.bias, c, p.pdt) : zero4(), b1 = p.bias ? ld4(p.bias, c + 4, p.pdt) : zero4();
+  const int64_t r0 = (int64_t)blockIdx.y * GELU_RB;
+  constexpr int NB = GELU_RB < 8 ? GELU_RB : 8;  // rows whose loads are issued together
+#pragma unroll
+  for (int u0 = 0; u0 < GELU_RB; u0 += NB) {
+    f4 za[NB], zb[NB];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) Io8<TX>::ld(p.x, min(r0 + u0 + u, p.N - 1) * p.xs + c, za[u], zb[u]);
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const int64_t r = r0 + u0 + u;
+      if (r < p.N) {
+        f4 oa, ob;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) oa[e] = gelu(za[u][e] + b0[e]), ob[e] = gelu(zb[u][e] + b1[e]);
+        Io8<TY>::st(p.y, r * p.ys + c, oa, ob);
+      }
+    }
+  }
+}
+
+// the backward of gelu8_fwd_kernel: dz = dy gelu'(x + bias) in x's type, and
+// the row block's dbias partial (column sums of dz) to part[y][C] when
+// dbias is asked for
+template <typename TX, typename TDY>
+__global__ __launch_bounds__(128) void gelu8_bwd_kernel(GeluParams p) {
+  const int c = (blockIdx.x * 128 + threadIdx.x) * 8;
+  if (c >= p.C) return;
+  const f4 b0 = p.bias ? ld4(p.bias, c, p.pdt) : zero4(), b1 = p.bias ? ld4(p.bias, c + 4, p.pdt) : zero4();
+  const int64_t r0 = (int64_t)blockIdx.y * GELU_RB;
+  f4 acc0 = zero4(), acc1 = zero4();
+  constexpr int NB = 4;  // rows whose loads (x and dy) are issued together
+#pragma unroll
+  for (int u0 = 0; u0 < GELU_RB; u0 += NB) {
+    f4 za[NB], zb[NB], ga[NB], gb[NB];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const int64_t r = min(r0 + u0 + u, p.N - 1);
+      Io8<TX>::ld(p.x, r * p.xs + c, za[u], zb[u]);
+      Io8<TDY>::ld(p.dy, r * p.dys + c, ga[u], gb[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const int64_t r = r0 + u0 + u;
+      if (r < p.N) {
+        f4 da, db;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          da[e] = ga[u][e] * gelu_grad(za[u][e] + b0[e]);
+          db[e] = gb[u][e] * gelu_grad(zb[u][e] + b1[e]);
+        }
+        Io8<TX>::st(p.dz, r * p.dzs + c, da, db);
+        acc0 += da;
+        acc1 += db;
+      }
+    }
+  }
+  if (p.dbias) {
+    *reinterpret_cast<f4*>(p.part + (int64_t)blockIdx.y * p.C + c) = acc0;
+    *reinterpret_cast<f4*>(p.part + (int64_t)blockIdx.y * p.C + c + 4) = acc1;
+  }
 }
 
 // ---------------------------------------------------------------------------
