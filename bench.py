@@ -209,6 +209,9 @@ def run_encoder(args) -> None:
 
     import deberta_amd
     from deberta_amd.relpos import relative_offset_table
+    # The encoder is test code shared with the C3 GPU tests; only this
+    # workload imports it (tests/ resolves as a namespace package from the
+    # repository root, bench.py's directory).
     from tests._encoder import Encoder, init_weights, synthetic_batch
 
     dev = torch.device("cuda:0")
