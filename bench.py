@@ -471,6 +471,12 @@ def main() -> None:
         help="shape and mask; the headline is the metric, the others print reference figures",
     )
     ap.add_argument(
+        "--dropout",
+        type=float,
+        default=0.0,
+        help="attention dropout probability in the kernels (a fresh seed per step); reference figures, not the metric",
+    )
+    ap.add_argument(
         "--kernels-only",
         action="store_true",
         help="only run each kernel --steps times (for rocprofv3 counter passes); prints per-kernel times",
@@ -507,7 +513,10 @@ def main() -> None:
     lib = _lib.load()
     dev = torch.device("cuda:0")
     B, L, H, mask_kind, wl_desc = WORKLOADS[args.workload]
-    headline = args.workload == "headline"
+    headline = args.workload == "headline" and not args.dropout
+    drop_t = ops.dropout_threshold(args.dropout) if args.dropout > 0 else 0
+    if args.dropout > 0 and not 0 < drop_t < 65536:
+        sys.exit(f"--dropout {args.dropout} has no kernel form")
     g = torch.Generator(device="cpu").manual_seed(0)
     mk = lambda *s: torch.randn(*s, generator=g).to(device=dev, dtype=torch.bfloat16)
     q, k, v = mk(B, L, H, D), mk(B, L, H, D), mk(B, L, H, D)
@@ -522,7 +531,8 @@ def main() -> None:
     kk, pk = kernel_masks(mask, B, L, L, dev)
 
     def step():
-        out, _, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, kk, pk, A, scale)
+        seed = ops.draw_dropout_seed() if drop_t else None
+        out, _, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, kk, pk, A, scale, True, None, drop_t, seed)
         return torch.autograd.grad(out, leaves, dout)
 
     if args.copy_probe_mib:
@@ -549,15 +559,20 @@ def main() -> None:
 
     # ---- per-kernel times: each launch timed on the stream it runs on ------------
     stream = torch.cuda.current_stream(dev)
-    out, lse, bias = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, kk, pk, A, scale)
+    dseed = ops.draw_dropout_seed() if drop_t else None
+    out, lse, bias = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, kk, pk, A, scale, True, None, drop_t, dseed)
     f32 = dict(dtype=torch.float32, device=dev)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     dkr, dqr = torch.zeros((H, R, D), **f32), torch.zeros((H, R, D), **f32)
-    bargs = ops.fill_bwd_args(dout, q, k, v, kr, qr, table, kk, pk, out, lse, bias, A, scale, dq, dk, dv, dkr, dqr)
+    bargs = ops.fill_bwd_args(
+        dout, q, k, v, kr, qr, table, kk, pk, out, lse, bias, A, scale, dq, dk, dv, dkr, dqr,
+        dropout_t=drop_t, dropout_seed=dseed,
+    )
     ws = torch.empty((ops.bwd_workspace_bytes(bargs),), dtype=torch.uint8, device=dev)
     bargs.workspace, bargs.workspace_bytes = ws.data_ptr(), ws.numel()
     fargs = bargs.fwd
-    nfws = lib.dsa_fwd_workspace_bytes(ctypes.byref(fargs))  # launch-order scratch under masks
+    # launch-order scratch under masks, table copies, dropout's keep bits
+    nfws = lib.dsa_fwd_workspace_bytes(ctypes.byref(fargs))
     fws = torch.empty((max(nfws, 16),), dtype=torch.uint8, device=dev)
     if nfws:
         fargs.workspace, fargs.workspace_bytes = fws.data_ptr(), nfws
@@ -584,8 +599,10 @@ def main() -> None:
     # step at the clocks of a sustained run; the forward's entry includes its
     # table copy (dsa_table_ks_kernel), which the same call launches first.
     staged = [
-        ("dsa_fwd_kernel (after dsa_table_ks_kernel)", run_fwd, f_fwd),
-        ("dsa_bwd_prep_kernel", run_stage(_lib.DSA_STAGE_PREP), 0.0),
+        ("dsa_fwd_kernel (after dsa_table_ks_kernel" + (" and dsa_dropout_bits_kernel)" if drop_t else ")"), run_fwd,
+         f_fwd),
+        ("dsa_bwd_prep_kernel" + (" (with dsa_dropout_bits_kernel)" if drop_t else ""), run_stage(_lib.DSA_STAGE_PREP),
+         0.0),
         ("dsa_bwd_dkdv_kernel", run_stage(_lib.DSA_STAGE_DKDV), f_dkdv),
         ("dsa_bwd_dqtab_kernel", run_stage(_lib.DSA_STAGE_DQ | _lib.DSA_STAGE_TABLE), f_dq + f_table),
         ("dsa_bwd_fold_kernel", run_stage(_lib.DSA_STAGE_SUM), 0.0),
@@ -675,6 +692,7 @@ def main() -> None:
                 {
                     "workload": args.workload,
                     "description": wl_desc,
+                    "attention_dropout": args.dropout,
                     "ms_per_step": round(ms_step, 4),
                     "tflops_dense_count": round(tflops, 2),
                     "kept_pair_fraction": round(kept_pairs / (B * L * L), 4),

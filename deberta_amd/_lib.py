@@ -24,7 +24,7 @@ DSA_STAGE_FOLD = 8
 DSA_STAGE_TABLE = 16  # the first half of FOLD: per-offset sums (workspace)
 DSA_STAGE_SUM = 32  # the second half: their fold onto dkr / dqr
 
-EXPECTED_VERSION = 8
+EXPECTED_VERSION = 9
 
 _i64x3 = ctypes.c_int64 * 3
 _i64x2 = ctypes.c_int64 * 2
@@ -67,6 +67,8 @@ class DsaFwdArgs(ctypes.Structure):
         ("qc", ctypes.c_void_p),
         ("qc_strides", _i64x3),
         ("pair_keep_stride_h", ctypes.c_int64),
+        ("dropout_threshold", ctypes.c_uint32),
+        ("dropout_seed", ctypes.c_uint64),
     ]
 
 

@@ -198,12 +198,15 @@ def fused_attention(
     scale: float,
     qc: Optional[torch.Tensor] = None,
     qkv: Optional[torch.Tensor] = None,
+    dropout_p: float = 0.0,
 ) -> torch.Tensor:
     """Core call on ``[B, L, H, D]`` layers; returns ``[B, Lq, H, D]``.
     ``kr`` / ``qr`` are the c2p / p2c tables (None: term off); ``qc`` the
     c2p term's query rows (None: q).  ``qkv``: q, k and v packed as one
     ``[B, L, 3, H, D]`` tensor (q, k, v are then None); the op takes it
-    whole and its gradient comes back as one tensor."""
+    whole and its gradient comes back as one tensor.  ``dropout_p``:
+    attention dropout in the kernels, with a fresh seed from torch's CPU
+    generator (``ops.dropout_threshold(dropout_p)`` must lie in [1, 65535])."""
     ref = qkv if qkv is not None else q  # shapes, dtype and device
     _require_gpu(ref)
     B, Lq, H = ref.shape[0], ref.shape[1], ref.shape[-2]
@@ -221,10 +224,20 @@ def fused_attention(
     save_bias = torch.is_grad_enabled() and any(
         t is not None and t.requires_grad for t in (q, k, v, qkv, kr, qr, qc)
     )
+    drop_t, seed = 0, None
+    if dropout_p > 0.0:
+        drop_t = ops.dropout_threshold(dropout_p)
+        if not 0 < drop_t < 65536:
+            raise ValueError(f"dropout_p={dropout_p} has no kernel form (threshold {drop_t} outside [1, 65535])")
+        seed = ops.draw_dropout_seed()
     if qkv is not None:
-        out, _, _ = ops.attention_packed(qkv, kr, qr, table, key_keep, pair_keep, int(att_span), float(scale), save_bias, qc)
+        out, _, _ = ops.attention_packed(
+            qkv, kr, qr, table, key_keep, pair_keep, int(att_span), float(scale), save_bias, qc, drop_t, seed
+        )
     else:
-        out, _, _ = ops.attention(q, k, v, kr, qr, table, key_keep, pair_keep, int(att_span), float(scale), save_bias, qc)
+        out, _, _ = ops.attention(
+            q, k, v, kr, qr, table, key_keep, pair_keep, int(att_span), float(scale), save_bias, qc, drop_t, seed
+        )
     return out
 
 
@@ -242,6 +255,7 @@ def disentangled_attention(
     att_type: Any = "c2p|p2c",
     scale_factor: Optional[int] = None,
     layout: str = "bhld",
+    dropout_p: float = 0.0,
 ) -> torch.Tensor:
     """Fused disentangled attention on already-projected layers.
 
@@ -251,8 +265,12 @@ def disentangled_attention(
     ``pos_query_layer`` are the projected relative tables ``(H, 2A, D)``
     (``_project_rel``); the c2p / p2c / p2p terms are used when ``att_type``
     names them.  ``relative_pos`` and ``attention_mask`` follow the module's
-    contract.  ``scale_factor`` defaults to ``1 + #att_type terms``.  The
-    result has the layout of ``query_layer``.
+    contract.  ``scale_factor`` defaults to ``1 + #att_type terms``.
+    ``dropout_p``: attention dropout on the probabilities (applied as
+    given: the caller decides whether it is training), in the kernels when
+    its threshold (``ops.dropout_threshold``) is in [1, 65535], else with
+    torch's dropout on the torch path.  The result has the layout of
+    ``query_layer``.
     """
     types = normalize_pos_att_type(att_type)
     if layout not in ("bhld", "blhd"):
@@ -267,8 +285,10 @@ def disentangled_attention(
     scale = 1.0 / math.sqrt(float(D * scale_factor))
     tables = [t for t in (pos_key_layer, pos_query_layer) if t is not None]
     att_span = tables[0].shape[1] // 2 if tables else 1
-    if q.device.type != "cuda":
-        # CPU tensors: the same chain in torch operations (deberta_amd.unfused)
+    in_kernels = dropout_p <= 0.0 or 0 < ops.dropout_threshold(dropout_p) < 65536
+    if q.device.type != "cuda" or not in_kernels:
+        # CPU tensors (and a dropout probability the kernels cannot draw):
+        # the same chain in torch operations (deberta_amd.unfused)
         rel_pos = None
         if any(t in types for t in ("c2p", "p2c", "p2p")):
             rel_pos = _relative_matrix(
@@ -276,7 +296,7 @@ def disentangled_attention(
             )
         out, _ = unfused_attention(
             q, k, v, pos_key_layer, pos_query_layer, rel_pos, _dense_keep(attention_mask, q.device),
-            att_span, scale, types,
+            att_span, scale, types, nn.Dropout(dropout_p) if dropout_p > 0.0 else None,
         )
         return out.transpose(1, 2) if layout == "bhld" else out
     kr, qr, qc = relative_operands(
@@ -289,7 +309,7 @@ def disentangled_attention(
     if kr is not None or qr is not None:
         table = table_for(relative_pos, q.shape[1], k.shape[1], position_buckets, max_relative_positions, q.device)
     _check_mask_rank(attention_mask)
-    out = fused_attention(q, k, v, kr, qr, table, attention_mask, att_span, scale, qc)
+    out = fused_attention(q, k, v, kr, qr, table, attention_mask, att_span, scale, qc, dropout_p=dropout_p)
     return out.transpose(1, 2) if layout == "bhld" else out
 
 
@@ -484,15 +504,19 @@ class DisentangledSelfAttention(nn.Module):
     ) -> tuple[torch.Tensor, Optional[torch.Tensor]]:
         """Same contract as the reference forward (deberta_v2_native.py:564-652).
 
-        The fused kernels run the call unless it is on CPU tensors or needs
-        the probabilities themselves: ``output_attentions=True``, attention
-        dropout ``p > 0`` in training mode, or a ``relative_pos`` that does
-        not depend on ``i - j`` alone; those run the same chain in torch
-        operations on the tensors' device (``deberta_amd.unfused``) and
-        return the probabilities when asked.
+        The fused kernels run the call, attention dropout in training
+        included (the kernels draw the keep bits, ``deberta_amd.ops``),
+        unless it is on CPU tensors or needs the probabilities themselves
+        (``output_attentions=True``), its ``relative_pos`` does not depend
+        on ``i - j`` alone, or its dropout probability has no kernel form
+        (below 2^-17 or above 1 - 2^-17); those run the same chain in torch
+        operations on the tensors' device (``deberta_amd.unfused``, with
+        torch's dropout) and return the probabilities when asked.
         """
         on_gpu = hidden_states.device.type == "cuda"
-        unfused = (not on_gpu) or output_attentions or (self.training and self.dropout.p > 0.0)
+        drop_p = float(self.dropout.p) if self.training else 0.0
+        drop_in_kernels = drop_p <= 0.0 or 0 < ops.dropout_threshold(drop_p) < 65536
+        unfused = (not on_gpu) or output_attentions or not drop_in_kernels
 
         q, k, v, qkv = self._project_qkv(hidden_states, query_states)
         model_dtype = hidden_states.dtype
@@ -537,7 +561,7 @@ class DisentangledSelfAttention(nn.Module):
 
         # the op takes the packed projection whole (its gradient comes back
         # as one tensor)
-        ctx = fused_attention(q, k, v, kr, qr, table, attention_mask, att_span, scale, qc, qkv=qkv)
+        ctx = fused_attention(q, k, v, kr, qr, table, attention_mask, att_span, scale, qc, qkv=qkv, dropout_p=drop_p)
         bsz, seq_len = ctx.shape[0], ctx.shape[1]
         context_layer = ctx.reshape(bsz, seq_len, self.all_head_size).to(dtype=model_dtype)
         return context_layer, None

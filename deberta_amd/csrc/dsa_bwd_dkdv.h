@@ -30,6 +30,7 @@
 #pragma once
 
 #include "dsa_bwd.h"
+#include "dsa_dropout.h"
 
 namespace dsa {
 
@@ -37,7 +38,10 @@ namespace kvcfg {
 constexpr int NW = 4, WK = 32, BKW = 128, BQ = 32;
 }  // namespace kvcfg
 
-template <typename T, int D, int MASK>
+// DROP: attention dropout with the forward's keep bits p.drop
+// (dsa_dropout.h): dV sums the kept probabilities, scaled by p.drop_scale,
+// and dP keeps the kept pairs' dO . v, scaled the same way.
+template <typename T, int D, int MASK, bool DROP = false>
 __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
   using namespace kvcfg;
   using M = Mfma<T>;
@@ -75,6 +79,8 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
   __shared__ __align__(16) float Rs0[2 * BQ], Rs1[2 * BQ];  // per query: lse*log2e (inf: no probabilities), Delta
   __shared__ __align__(16) T Ring[NRB * RBE];     // qrgt window (p2c)
   __shared__ __align__(16) T Stg[NW * SW];        // each wave's dS^T tile
+  // dropout: each wave's keep words of the tile (one per lane), double-buffered
+  __shared__ __align__(16) uint32_t Dk0[DROP ? NW * 64 : 1], Dk1[DROP ? NW * 64 : 1];
   constexpr bool SEGM = seg_mode(MASK);
   constexpr int MAXQT = 1024;  // query tiles (Lq <= 32768)
   // segment masks: the active query tiles in order (tile | 0x4000 if it
@@ -177,12 +183,21 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
     }
   };
 
+  // Dropout: the keep words of the 32-query block qi and the 64-key tile of
+  // the wave's keys, in the dkdv layout (dsa_dropout.h), copied to LDS with
+  // the tile (16 lanes x 16 bytes); lane l's word, shifted by 16 (w % 2),
+  // has bit 8 ib + 4 jb + e for the pair (query i0 + 16 ib + 4 g + e, key
+  // jw + 16 jb + c16).
+  const uint32_t* dropw = nullptr;
+  const int NKT64 = p.LkP / 64;
+  if constexpr (DROP) dropw = p.drop + drop_word0(b, h, p.H, p.LqP / 32, NKT64, 0, jw / 64);
   // Issues the LDS copies of query tile qi into the given buffers (lane
   // order = physical chunk order; Q and dO rows are clamped to Lq - 1, where
   // probabilities are zero anyway), and, with ring set, its qrgt block
-  // (whose ring slot was last read two tiles earlier).
+  // (whose ring slot was last read two tiles earlier); with dropout, the
+  // wave's keep words.
   int qseg_next = 0;  // MASK_SEG: query segment of lane (w = 1, lane < 32) in the next tile
-  auto issue = [&](int qi, bool ring, T* Qd, T* dOd, BT* Bd, float* Rd) {
+  auto issue = [&](int qi, bool ring, T* Qd, T* dOd, BT* Bd, float* Rd, uint32_t* Dd) {
     const int i0 = qi * BQ;
     if (MASK == MASK_SEG && w == 1 && lane < BQ) qseg_next = (i0 + lane < Lq) ? sv(i0 + lane) : 0;
 #pragma unroll
@@ -210,6 +225,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
     }
     if (w == 0 && lane < 2 * BQ * 4 / 16) lds_dma16(rib + 2 * i0 + 4 * lane, (char*)Rd);
     if (p2c && ring) issue_ring(tw0 / 32 + qi + 4);
+    if (DROP && lane < 16) lds_dma16(dropw + (int64_t)qi * NKT64 * 64 + 4 * lane, (char*)(Dd + w * 64));
   };
 
   // dS rows i of the wave's 32 keys: lane (g, c16) writes keys jw + 16 kk +
@@ -269,10 +285,10 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
     const int qfirst = SEGM ? (__builtin_amdgcn_readfirstlane(qlist[0]) & 0x3ff) : 0;
     if (p2c)
       for (int r = 0; r < 4; ++r) issue_ring(tw0 / 32 + qfirst + r);
-    issue(qfirst, true, Qs0, dOs0, Bs0, Rs0);
+    issue(qfirst, true, Qs0, dOs0, Bs0, Rs0, Dk0);
     lds_dma_wait();
-    auto tile = [&](int n, const T* Q, const T* dO, const BT* Bt, const float* R, T* nQ, T* ndO, BT* nBt,
-                    float* nR) {
+    auto tile = [&](int n, const T* Q, const T* dO, const BT* Bt, const float* R, const uint32_t* Dw, T* nQ, T* ndO,
+                    BT* nBt, float* nR, uint32_t* nDw) {
       const int ent = SEGM ? __builtin_amdgcn_readfirstlane(qlist[n]) : n;
       const int qi = ent & 0x3ff, i0 = qi * BQ;
       // This wave's copies of tile qi have landed: they were issued before
@@ -293,7 +309,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
       }
       if (n + 1 < nlist) {
         const int qn = SEGM ? (__builtin_amdgcn_readfirstlane(qlist[n + 1]) & 0x3ff) : n + 1;
-        issue(qn, qn == qi + 1, nQ, ndO, nBt, nR);
+        issue(qn, qn == qi + 1, nQ, ndO, nBt, nR, nDw);
       }
       // With segments, a tile whose queries all share the workgroup's single
       // key segment needs no masking beyond the dead-row test.  Other modes:
@@ -372,6 +388,8 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
       __builtin_amdgcn_s_setprio(0);
       // ---- P, dP, dS -----------------------------------------------------------------------------
       f32x4 pp[2][BQ / 16], dsh[2][BQ / 16];
+      uint32_t dm = 0;
+      if constexpr (DROP) dm = Dw[w * 64 + lane] >> (16 * (w & 1));
       auto probs = [&](auto plain) {
 #pragma unroll
         for (int ib = 0; ib < BQ / 16; ++ib) {
@@ -399,13 +417,19 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
                 if (MASK == MASK_PAIR) keep = keep && ((pmask[il][2 * w + jb] >> c16) & 1u);
                 pe = keep ? __builtin_amdgcn_exp2f(__builtin_fmaf(sc[jb][ib][e], sl2, -lr)) : 0.f;
               }
-              pp[jb][ib][e] = pe;
-              dsh[jb][ib][e] = pe * (dp[e] - R[2 * il + 1]);
+              if constexpr (DROP) {
+                const bool kept = (dm >> (8 * ib + 4 * jb + e)) & 1u;
+                pp[jb][ib][e] = kept ? pe : 0.f;
+                dsh[jb][ib][e] = pe * ((kept ? dp[e] * p.drop_scale : 0.f) - R[2 * il + 1]);
+              } else {
+                pp[jb][ib][e] = pe;
+                dsh[jb][ib][e] = pe * (dp[e] - R[2 * il + 1]);
+              }
             }
           }
         }
       };
-      if (keys_in && i0 + BQ <= Lq)
+      if (!DROP && keys_in && i0 + BQ <= Lq)
         probs(std::true_type{});
       else
         probs(std::false_type{});
@@ -473,8 +497,8 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
       __builtin_amdgcn_s_setprio(0);
     };
     for (int n = 0; n < nlist; n += 2) {
-      tile(n, Qs0, dOs0, Bs0, Rs0, Qs1, dOs1, Bs1, Rs1);
-      if (n + 1 < nlist) tile(n + 1, Qs1, dOs1, Bs1, Rs1, Qs0, dOs0, Bs0, Rs0);
+      tile(n, Qs0, dOs0, Bs0, Rs0, Dk0, Qs1, dOs1, Bs1, Rs1, Dk1);
+      if (n + 1 < nlist) tile(n + 1, Qs1, dOs1, Bs1, Rs1, Dk1, Qs0, dOs0, Bs0, Rs0, Dk0);
     }
   }
 
@@ -494,7 +518,7 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           kv[e] = (T)(dka[db][jb][e] * p.scale);
-          vv[e] = (T)(dva[db][jb][e]);
+          vv[e] = (T)(DROP ? dva[db][jb][e] * p.drop_scale : dva[db][jb][e]);
         }
         *reinterpret_cast<vec4*>(krow + 16 * db + 4 * g) = kv;
         *reinterpret_cast<vec4*>(vrow + 16 * db + 4 * g) = vv;

@@ -21,6 +21,7 @@
 #include "dsa_bwd_dq.h"
 #include "dsa_bwd_dqtab.h"
 #include "dsa_bwd_table.h"
+#include "dsa_dropout.h"
 #include "dsa_order.h"
 #include "dsa_fwd.h"
 #include "dsa_rows.h"
@@ -86,6 +87,8 @@ int check_fwd(const dsa_fwd_args* a) {
     if (a->att_span < 1 || a->att_span > 16383) return fail("dsa: att_span must be in [1, 16383], got %d", a->att_span);
     if (!a->rel_table) return fail("dsa: rel_table is required when c2p/p2c is enabled");
   }
+  if (a->dropout_threshold > 65535u)
+    return fail("dsa: dropout_threshold must be in [0, 65535] (units of 1/65536), got %u", a->dropout_threshold);
   if ((a->flags & DSA_C2P) && !a->kr) return fail("dsa: c2p needs the pos-key table kr");
   // the forward addresses table rows with 32-bit element offsets
   if ((a->flags & DSA_C2P) && (int64_t)(2 * a->att_span - 1) * llabs(a->kr_strides[1]) + a->D > 0x7fffffffLL)
@@ -164,6 +167,8 @@ dsa::FwdParams to_params(const dsa_fwd_args* a) {
   p.LqP = round_up(a->Lq, 128);
   p.LkP = round_up(a->Lk, 128);
   p.scale = a->scale;
+  p.drop = nullptr;  // set where the keep bits are generated
+  p.drop_scale = 1.f;
   return p;
 }
 
@@ -229,15 +234,53 @@ int launch_orders(const dsa::FwdParams& p, int njobs, int* const* bufs, const in
 
 int fwd_tiles(const dsa_fwd_args* a) { return (a->Lq + dsa::dcfg::BQ - 1) / dsa::dcfg::BQ; }
 
+// ---- attention dropout (dsa_dropout.h) ----
+// Bytes of the keep bits in the forward's and the backward's workspaces (0
+// without dropout).
+size_t drop_bytes(const dsa_fwd_args* a) {
+  if (!a->dropout_threshold) return 0;
+  return align_up(dsa::dropout_bits_bytes(a->B, a->H, round_up(a->Lq, 128), round_up(a->Lk, 128)), 256);
+}
 
-template <typename T, int D, int MASK>
+// Generates the call's keep bits into `bits` and points the kernels'
+// parameters at them.
+// `dkdv`: the layout the dkdv kernel reads, else the forward's.
+int launch_dropout_bits(const dsa_fwd_args* a, uint32_t* bits, bool dkdv, dsa::FwdParams& p, hipStream_t st) {
+  dsa::DropParams d;
+  d.bits = bits;
+  d.B = a->B;
+  d.H = a->H;
+  d.NQB = round_up(a->Lq, 128) / 32;
+  d.NKT = round_up(a->Lk, 128) / 64;
+  d.t = a->dropout_threshold;
+  d.k0 = (uint32_t)(a->dropout_seed & 0xffffffffu);
+  d.k1 = (uint32_t)(a->dropout_seed >> 32);
+  const int64_t nw = (int64_t)d.B * d.H * d.NQB * d.NKT * 64;
+  const dim3 grid((unsigned)((nw + 255) / 256));
+  if (dkdv)
+    hipLaunchKernelGGL(dsa::dsa_dropout_bits_kernel<true>, grid, dim3(256), 0, st, d);
+  else
+    hipLaunchKernelGGL(dsa::dsa_dropout_bits_kernel<false>, grid, dim3(256), 0, st, d);
+  if (launch_check("dsa_dropout_bits_kernel")) return 1;
+  p.drop = bits;
+  p.drop_scale = 65536.f / (float)(65536u - a->dropout_threshold);
+  return 0;
+}
+
+
+template <typename T, int D, int MASK, bool DROP>
 int launch_fwd(const dsa::FwdParams& p, hipStream_t st) {
   dim3 grid((unsigned)((p.Lq + dsa::dcfg::BQ - 1) / dsa::dcfg::BQ * p.H * p.B));
   if (p.qc)
-    hipLaunchKernelGGL((dsa::dsa_fwd_kernel<T, D, MASK, true>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((dsa::dsa_fwd_kernel<T, D, MASK, true, DROP>), grid, dim3(256), 0, st, p);
   else
-    hipLaunchKernelGGL((dsa::dsa_fwd_kernel<T, D, MASK, false>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((dsa::dsa_fwd_kernel<T, D, MASK, false, DROP>), grid, dim3(256), 0, st, p);
   return launch_check("dsa_fwd_kernel");
+}
+
+template <typename T, int D, int MASK>
+int launch_fwd(const dsa::FwdParams& p, hipStream_t st) {
+  return p.drop ? launch_fwd<T, D, MASK, true>(p, st) : launch_fwd<T, D, MASK, false>(p, st);
 }
 
 template <typename T, int D>
@@ -265,7 +308,7 @@ int device_cus() {
 // extents the kernels share.
 struct WsLayout {
   int LqP, LkP, TGP, OFF, NDB, NPG;
-  size_t rowinfo, krgt, qrgt, ds, gpart, seg, cinfo, korder, qorder, total;
+  size_t rowinfo, krgt, qrgt, ds, gpart, seg, cinfo, korder, qorder, drop, total;
 };
 
 WsLayout ws_layout(const dsa_bwd_args* a) {
@@ -309,8 +352,30 @@ WsLayout ws_layout(const dsa_bwd_args* a) {
   off += order_bytes(&f, w.LkP / dsa::kvcfg::BKW);
   w.qorder = off;  // dq launch order
   off += order_bytes(&f, w.LqP / dsa::dqcfg::BQ);
+  w.drop = off;  // attention dropout's keep bits, regenerated by PREP
+  off += drop_bytes(&f);
   w.total = off;
   return w;
+}
+
+template <typename T, int D, bool DROP>
+int launch_dkdv(const dsa::BwdParams& bp, const WsLayout& ws, int mode, hipStream_t st) {
+  const dsa::FwdParams& f = bp.f;
+  dim3 grid((unsigned)(ws.LkP / dsa::kvcfg::BKW * f.H * f.B));
+  switch (mode) {
+    case dsa::MASK_KEY:
+      hipLaunchKernelGGL((dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_KEY, DROP>), grid, dim3(256), 0, st, bp);
+      break;
+    case dsa::MASK_PAIR:
+      hipLaunchKernelGGL((dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_PAIR, DROP>), grid, dim3(256), 0, st, bp);
+      break;
+    case dsa::MASK_SEG:
+      hipLaunchKernelGGL((dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_SEG, DROP>), grid, dim3(256), 0, st, bp);
+      break;
+    default:
+      hipLaunchKernelGGL((dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_NONE, DROP>), grid, dim3(256), 0, st, bp);
+  }
+  return launch_check("dsa_bwd_dkdv_kernel");
 }
 
 template <typename T, int D>
@@ -354,6 +419,18 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
   bp.NPG = ws.NPG;
   const int stages =
       a->stages ? a->stages : (DSA_STAGE_PREP | DSA_STAGE_DQ | DSA_STAGE_DKDV | DSA_STAGE_FOLD);
+  uint32_t* dbits = f.dropout_threshold ? reinterpret_cast<uint32_t*>(base + ws.drop) : nullptr;
+  if (dbits) {
+    // PREP regenerates the forward's keep bits (same seed, same bits) in
+    // the layout dkdv reads; a DKDV run in a later call reads the ones an
+    // earlier PREP left
+    if (stages & DSA_STAGE_PREP) {
+      if (launch_dropout_bits(&f, dbits, true, bp.f, st)) return 1;
+    } else {
+      bp.f.drop = dbits;
+      bp.f.drop_scale = 65536.f / (float)(65536u - f.dropout_threshold);
+    }
+  }
 
   if (stages & DSA_STAGE_PREP) {
     // dkdv's key tiles against 32-query chunks; dq's tiles (128 queries
@@ -393,21 +470,7 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
     if (nj && launch_order_sort(op, st)) return 1;
   }
   if (stages & DSA_STAGE_DKDV) {
-    dim3 grid((unsigned)(ws.LkP / dsa::kvcfg::BKW * f.H * f.B));
-    switch (mode) {
-      case dsa::MASK_KEY:
-        hipLaunchKernelGGL((dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_KEY>), grid, dim3(256), 0, st, bp);
-        break;
-      case dsa::MASK_PAIR:
-        hipLaunchKernelGGL((dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_PAIR>), grid, dim3(256), 0, st, bp);
-        break;
-      case dsa::MASK_SEG:
-        hipLaunchKernelGGL((dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_SEG>), grid, dim3(256), 0, st, bp);
-        break;
-      default:
-        hipLaunchKernelGGL((dsa::dsa_bwd_dkdv_kernel<T, D, dsa::MASK_NONE>), grid, dim3(256), 0, st, bp);
-    }
-    if (launch_check("dsa_bwd_dkdv_kernel")) return 1;
+    if (bp.f.drop ? launch_dkdv<T, D, true>(bp, ws, mode, st) : launch_dkdv<T, D, false>(bp, ws, mode, st)) return 1;
   }
   // DQ and FOLD both only read dS: with both requested, the dq and table
   // workgroups run in one launch (dsa_bwd_dqtab.h) and share the GPU.
@@ -522,12 +585,14 @@ size_t tables_ks_bytes(const dsa_fwd_args* a) {
 }
 
 // The forward with the launch-order scratch `order_buf` (NULL: no
-// heaviest-first order) and the scratch for the k-step copies of the
-// relative tables `tab_buf` (NULL: the bands read the caller's tables).
-// Arguments already checked.
-int run_fwd(const dsa_fwd_args* a, int* order_buf, void* tab_buf, hipStream_t st) {
+// heaviest-first order), the scratch for the k-step copies of the relative
+// tables `tab_buf` (NULL: the bands read the caller's tables) and, with
+// dropout, the scratch for its keep bits `drop_buf`.  Arguments already
+// checked.
+int run_fwd(const dsa_fwd_args* a, int* order_buf, void* tab_buf, uint32_t* drop_buf, hipStream_t st) {
   dsa::FwdParams p = to_params(a);
   const int mode = mask_mode(a);
+  if (drop_buf && launch_dropout_bits(a, drop_buf, false, p, st)) return 1;
   if (tab_buf && a->flags) {
     dsa::TableKs t;
     const int R = 2 * a->att_span, ks = 64 / elem_bytes(a->dtype);
@@ -756,7 +821,7 @@ dsa::rows::RtdParams rtd_params(const dsa_rtd_args* a) {
 
 extern "C" {
 
-int dsa_version(void) { return 8; }
+int dsa_version(void) { return 9; }
 
 const char* dsa_last_error(void) { return g_err.c_str(); }
 
@@ -765,18 +830,23 @@ int dsa_fwd(const dsa_fwd_args* a, void* stream) {
   if (check_fwd(a)) return 1;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (refuse_capture(st, "dsa_fwd")) return 1;
-  const size_t ob = order_bytes(a, fwd_tiles(a)), tb = tables_ks_bytes(a);
+  const size_t ob = order_bytes(a, fwd_tiles(a)), tb = tables_ks_bytes(a), db = drop_bytes(a);
+  if (db && (!a->workspace || a->workspace_bytes < ob + tb + db))
+    return fail("dsa: attention dropout needs the forward workspace of %zu bytes (its keep bits), got %zu", ob + tb + db,
+                a->workspace ? a->workspace_bytes : (size_t)0);
   int* buf = nullptr;
   void* tabs = nullptr;
-  if (a->workspace && (ob || tb)) {
+  uint32_t* dbits = nullptr;
+  if (a->workspace && (ob || tb || db)) {
     if (a->workspace_bytes < ob) return fail("dsa: forward workspace of %zu bytes required, got %zu", ob, a->workspace_bytes);
     if (!aligned16(a->workspace)) return fail("dsa: forward workspace must be 16-byte aligned");
     if (ob) buf = static_cast<int*>(a->workspace);
     // a workspace of the size without the table copies (earlier versions of
     // dsa_fwd_workspace_bytes) runs the bands on the caller's tables
     if (tb && a->workspace_bytes >= ob + tb) tabs = static_cast<char*>(a->workspace) + ob;
+    if (db) dbits = reinterpret_cast<uint32_t*>(static_cast<char*>(a->workspace) + ob + tb);
   }
-  return run_fwd(a, buf, tabs, st);
+  return run_fwd(a, buf, tabs, dbits, st);
 }
 
 int dsa_fwd_static(const dsa_fwd_args* a, void* stream) {
@@ -784,7 +854,9 @@ int dsa_fwd_static(const dsa_fwd_args* a, void* stream) {
   if (check_fwd(a)) return 1;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (refuse_capture(st, "dsa_fwd_static")) return 1;
-  if (!(a->key_keep || a->seg)) return run_fwd(a, nullptr, nullptr, st);  // no scratch used
+  if (a->dropout_threshold)
+    return fail("dsa_fwd_static: attention dropout needs dsa_fwd and its workspace (the keep bits)");
+  if (!(a->key_keep || a->seg)) return run_fwd(a, nullptr, nullptr, nullptr, st);  // no scratch used
   const int64_t n = (int64_t)a->B * fwd_tiles(a);
   if (n > kMaxOrderItems)
     return fail("dsa_fwd_static: B * ceil(Lq / 128) = %lld launch-order items exceed the static scratch's "
@@ -801,7 +873,7 @@ int dsa_fwd_static(const dsa_fwd_args* a, void* stream) {
   int* buf = static_cast<int*>(static_scratch_locked(s));
   if (!buf) return fail("dsa_fwd_static: no address for the static scratch (or its event) on device %d", dev);
   if (hipStreamWaitEvent(st, s.done, 0) != hipSuccess) return fail("dsa_fwd_static: hipStreamWaitEvent failed");
-  const int rc = run_fwd(a, buf, nullptr, st);
+  const int rc = run_fwd(a, buf, nullptr, nullptr, st);
   if (hipEventRecord(s.done, st) != hipSuccess) {
     (void)hipGetLastError();
     return rc ? rc : fail("dsa_fwd_static: hipEventRecord failed");
@@ -878,7 +950,7 @@ size_t dsa_fwd_bias_bytes(const dsa_fwd_args* a) {
 size_t dsa_fwd_workspace_bytes(const dsa_fwd_args* a) {
   if (!a || a->B < 1 || a->Lq < 1 || a->H < 1 || a->D < 1) return 0;
   if (a->flags && (a->att_span < 1 || a->att_span > 16383)) return 0;
-  return order_bytes(a, fwd_tiles(a)) + tables_ks_bytes(a);
+  return order_bytes(a, fwd_tiles(a)) + tables_ks_bytes(a) + drop_bytes(a);
 }
 
 size_t dsa_bwd_workspace_bytes(const dsa_bwd_args* a) {

@@ -20,13 +20,16 @@
 // compile-time offset from a per-lane base.
 #pragma once
 
+#include "dsa_dropout.h"
 #include "dsa_tiles.h"
 
 namespace dsa {
 
 // QC: the c2p term reads the query rows p.qc (which carry the p2p term)
-// instead of q.
-template <typename T, int D, int MASK, bool QC = false>
+// instead of q.  DROP: attention dropout with the keep bits p.drop
+// (dsa_dropout.h): dropped probabilities leave the PV product, the row sums
+// (and so the lse) keep them, and the output is scaled by p.drop_scale.
+template <typename T, int D, int MASK, bool QC = false, bool DROP = false>
 __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
   using namespace dcfg;
   using M = Mfma<T>;
@@ -202,8 +205,16 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
   int relv = 0;  // this thread's relative position of the fetched tile (tid < XG)
   int ksn = 0;   // segment masks: this thread's key segment of the fetched tile (tid < BK)
   int kfetched = -1;
+  // dropout: this lane's keep word of the fetched tile (bit 16 ib + 4 jb + e)
+  uint32_t dwn = 0;
+  const uint32_t* dropw = nullptr;
+  if constexpr (DROP) {
+    static_assert(BK == 64 && WQ == 32, "one keep word per lane, 32-query block and 64-key tile");
+    dropw = p.drop + drop_word0(b, h, p.H, p.LqP / 32, p.LkP / 64, iw / 32, 0) + (tid & 63);
+  }
   auto fetch = [&](int kt) {
     const int j0 = kt * BK;
+    if constexpr (DROP) dwn = dropw[(int64_t)kt * 64];
     if (p.flags && tid < XG) relv = rel_of_tile(p.rel, i0, j0, Lq, Lk, tid);
     if (SEGM && tid < BK) ksn = j0 + tid < Lk ? sv(j0 + tid) : 0;
 #pragma unroll
@@ -265,6 +276,8 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
     // first reuse of a register that an earlier load wrote.
     vm_wait<0>();
     if (kt != kfetched) fetch(kt);  // a tile after skipped ones was not prefetched
+    uint32_t dw = 0;
+    if constexpr (DROP) dw = dwn;  // the next fetch overwrites dwn
 #pragma unroll
     for (int k = 0; k < KCH; ++k) {
       const int c = tid + 256 * k;
@@ -383,6 +396,16 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
         }
       lrow[ib] += ls;
     }
+    if constexpr (DROP) {
+      // dropped probabilities leave the PV product (after the row sums)
+#pragma unroll
+      for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (!((dw >> (16 * ib + 4 * jb + e)) & 1u)) st[ib][jb][e] = 0.f;
+    }
 
     // ---- O^T += V^T P^T -------------------------------------------------------
     __builtin_amdgcn_s_setprio(1);
@@ -408,7 +431,7 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
     const int i = irow[ib];
     const float lsum = col_sum(lrow[ib]);
     const bool ok = ilive[ib] && lsum > 0.f;
-    const float inv = ok ? 1.f / lsum : 0.f;
+    const float inv = ok ? (DROP ? p.drop_scale : 1.f) / lsum : 0.f;
     if (i < Lq) {
       T* orow = obase + (int64_t)i * p.os[1];
 #pragma unroll

@@ -33,6 +33,10 @@ struct FwdParams {
   int B, H, Lq, Lk, A, flags;
   int LqP, LkP;     // Lq, Lk rounded up to 128 (extents of bias and dS^T)
   float scale;
+  // attention dropout: the keep bits (dsa_dropout.h) and the scale of the
+  // kept probabilities, 65536 / (65536 - t); null without dropout
+  const uint32_t* drop;
+  float drop_scale;
 };
 
 struct BwdParams {

@@ -23,6 +23,12 @@ Tensor layouts (see include/dsa.h):
                     inputs, float32 for float32); empty when not saved
   qc                [B, Lq, H, D] or None: the query rows of the c2p term
                     (q when None); the p2p term rides on it (attention.py)
+  dropout_t         attention dropout threshold in [0, 65535]: each
+                    probability is dropped with probability t / 65536, the
+                    kept ones scaled by 65536 / (65536 - t); 0: no dropout
+  dropout_seed      int64 CPU tensor of one element (or None without
+                    dropout): the 64-bit seed of the keep bits, which the
+                    backward regenerates from it
 """
 
 from __future__ import annotations
@@ -77,6 +83,34 @@ def bias_dtype(dtype: torch.dtype) -> torch.dtype:
     return torch.float16 if dtype == torch.bfloat16 else torch.float32
 
 
+def dropout_threshold(p: float) -> int:
+    """The kernels' dropout threshold for probability ``p``: ``round(p *
+    65536)``.  The kernels drop with probability ``t / 65536`` exactly, so a
+    ``p`` whose threshold is 0 or 65536 (``p < 2^-17`` or ``p > 1 - 2^-17``)
+    has no kernel form; the module runs those on its torch path."""
+    return int(round(float(p) * 65536.0))
+
+
+def draw_dropout_seed() -> Tensor:
+    """A fresh 62-bit seed for the keep bits, drawn from torch's default CPU
+    generator (so ``torch.manual_seed`` reproduces it, and activation
+    checkpointing, which restores the RNG states, redraws the same one)."""
+    return torch.randint(0, 1 << 62, (1,), dtype=torch.int64)
+
+
+def _seed_value(seed: Optional[Tensor], t: int) -> int:
+    if not t:
+        return 0
+    if seed is None or seed.numel() != 1 or seed.dtype != torch.int64 or seed.device.type != "cpu":
+        raise ValueError("dsa: dropout needs dropout_seed, an int64 CPU tensor of one element")
+    return int(seed.reshape(()).item()) & 0xFFFFFFFFFFFFFFFF
+
+
+def _check_threshold(t: int) -> None:
+    if not 0 <= int(t) <= 65535:
+        raise ValueError(f"dsa: dropout threshold must be in [0, 65535] (units of 1/65536), got {t}")
+
+
 def _fill_fwd_args(
     q: Tensor,
     k: Tensor,
@@ -92,6 +126,8 @@ def _fill_fwd_args(
     scale: float,
     bias: Optional[Tensor] = None,
     qc: Optional[Tensor] = None,
+    dropout_t: int = 0,
+    dropout_seed: Optional[Tensor] = None,
 ) -> _lib.DsaFwdArgs:
     B, Lq, H, D = q.shape
     Lk = k.shape[1]
@@ -129,6 +165,9 @@ def _fill_fwd_args(
     if qc is not None:
         a.qc = qc.data_ptr()
         a.qc_strides[:] = _strides3(qc)
+    _check_threshold(dropout_t)
+    a.dropout_threshold = int(dropout_t)
+    a.dropout_seed = _seed_value(dropout_seed, int(dropout_t))
     return a
 
 
@@ -204,10 +243,14 @@ def _dsa_fwd_impl(
     scale: float,
     save_bias: bool = True,
     qc: Optional[Tensor] = None,
+    dropout_t: int = 0,
+    dropout_seed: Optional[Tensor] = None,
 ) -> tuple[Tensor, Tensor, Tensor]:
     """(out, lse, bias).  With c2p/p2c and ``save_bias`` the relative score
     term is written to ``bias`` for the backward (which needs it); else
-    ``bias`` is empty.  ``qc``: the c2p term's query rows (q when None)."""
+    ``bias`` is empty.  ``qc``: the c2p term's query rows (q when None).
+    ``dropout_t`` / ``dropout_seed``: attention dropout (lse is that of the
+    probabilities before dropout)."""
     _eager.refuse_capture("deberta_amd::dsa_fwd")
     _validate(q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, qc)
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
@@ -221,9 +264,12 @@ def _dsa_fwd_impl(
         bias = torch.empty(bias_shape(q, k), dtype=bias_dtype(q.dtype), device=q.device)
     else:
         bias = torch.empty((0,), dtype=bias_dtype(q.dtype), device=q.device)
-    args = _fill_fwd_args(q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, att_span, scale, bias, qc)
+    args = _fill_fwd_args(
+        q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, att_span, scale, bias, qc, dropout_t, dropout_seed
+    )
     lib = _lib.load()
-    # scratch for the heaviest-first launch order under key / segment masks
+    # scratch for the heaviest-first launch order under key / segment masks,
+    # the table copies and dropout's keep bits
     nws = lib.dsa_fwd_workspace_bytes(ctypes.byref(args))
     ws = torch.empty((nws,), dtype=torch.uint8, device=q.device) if nws else None
     if ws is not None:
@@ -245,7 +291,10 @@ dsa_fwd = torch.library.custom_op(
 
 
 @dsa_fwd.register_fake
-def _dsa_fwd_fake(q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias=True, qc=None):
+def _dsa_fwd_fake(
+    q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias=True, qc=None, dropout_t=0,
+    dropout_seed=None,
+):
     B, Lq, H, D = q.shape
     out = q.new_empty((B, Lq, H, D))
     lse = q.new_empty((B, H, Lq), dtype=torch.float32)
@@ -283,12 +332,17 @@ def fill_bwd_args(
     dtab_overwrite: bool = False,
     qc: Optional[Tensor] = None,
     dqc: Optional[Tensor] = None,
+    dropout_t: int = 0,
+    dropout_seed: Optional[Tensor] = None,
 ) -> _lib.DsaBwdArgs:
     """Backward arguments.  dkr / dqr are fp32 and accumulated into, or, with
     ``dtab_overwrite``, written (fp32 or bf16, their dtype).  With ``qc``,
-    ``dqc`` receives its gradient (the c2p part of dq)."""
+    ``dqc`` receives its gradient (the c2p part of dq).  The dropout
+    arguments are the forward's."""
     a = _lib.DsaBwdArgs()
-    a.fwd = _fill_fwd_args(q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, att_span, scale, bias, qc)
+    a.fwd = _fill_fwd_args(
+        q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, att_span, scale, bias, qc, dropout_t, dropout_seed
+    )
     if dqc is not None:
         a.dqc = dqc.data_ptr()
         a.dqc_strides[:] = _strides3(dqc)
@@ -342,6 +396,8 @@ def _dsa_bwd_impl(
     scale: float,
     qc: Optional[Tensor] = None,
     dqkv: Optional[Tensor] = None,
+    dropout_t: int = 0,
+    dropout_seed: Optional[Tensor] = None,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     """Gradients (dq, dk, dv, dkr, dqr, dqc).  With ``dqkv`` (a contiguous
     ``[B, L, 3, H, D]`` buffer), dq, dk and dv are written into its three
@@ -349,7 +405,8 @@ def _dsa_bwd_impl(
     tables' dtype (empty when the matching table is None).  ``bias`` is the
     relative term dsa_fwd saved (required with c2p/p2c).  With ``qc`` (the
     c2p term's query rows), dqc is its gradient and dq the content part;
-    else dqc is empty."""
+    else dqc is empty.  ``dropout_t`` / ``dropout_seed``: the forward's
+    (the kernels regenerate its keep bits)."""
     _eager.refuse_capture("deberta_amd::dsa_bwd")
     if kr is not None or qr is not None:
         _alert_nondeterministic_tables()
@@ -377,7 +434,7 @@ def _dsa_bwd_impl(
     args = fill_bwd_args(
         dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, att_span, scale,
         dq, dk, dv, dkr if kr is not None else None, dqr if qr is not None else None, dtab_overwrite=True,
-        qc=qc, dqc=dqc if qc is not None else None,
+        qc=qc, dqc=dqc if qc is not None else None, dropout_t=dropout_t, dropout_seed=dropout_seed,
     )
     ws = torch.empty((max(bwd_workspace_bytes(args), 16),), dtype=torch.uint8, device=q.device)
     args.workspace = ws.data_ptr()
@@ -393,7 +450,10 @@ dsa_bwd = torch.library.custom_op(
 
 
 @dsa_bwd.register_fake
-def _dsa_bwd_fake(dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, att_span, scale, qc=None):
+def _dsa_bwd_fake(
+    dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, att_span, scale, qc=None, dqkv=None,
+    dropout_t=0, dropout_seed=None,
+):
     H, D = q.shape[2], q.shape[3]
     R = 2 * int(att_span)
     dkr = q.new_empty((H, R, D)) if kr is not None else q.new_empty((0,))
@@ -410,27 +470,37 @@ def _dsa_bwd_fake(dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, ls
 
 
 def _setup_context(ctx, inputs, output):
-    q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias, qc = inputs
+    q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias, qc, dropout_t, dropout_seed = (
+        _with_dropout(inputs, 12)
+    )
     out, lse, bias = output
     ctx.mark_non_differentiable(lse, bias)
     # lse and the saved term get no gradient: do not materialise zeros for
     # them (the saved term is (B, H, L, L)-sized)
     ctx.set_materialize_grads(False)
-    ctx.save_for_backward(q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, qc)
+    ctx.save_for_backward(q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, qc, dropout_seed)
     ctx.att_span = att_span
     ctx.scale = scale
+    ctx.dropout_t = dropout_t
+
+
+def _with_dropout(inputs: tuple, n: int) -> tuple:
+    """The op's inputs with the two trailing dropout arguments filled in
+    (callers may leave them out)."""
+    return tuple(inputs) + (0, None)[len(inputs) - n:] if len(inputs) < n + 2 else tuple(inputs)
 
 
 def _backward(ctx, dout, dlse, dbias):
-    q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, qc = ctx.saved_tensors
+    q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, qc, dropout_seed = ctx.saved_tensors
     if dout is None:  # the output itself received no gradient
-        return (None,) * 12
+        return (None,) * 14
     dq, dk, dv, dkr, dqr, dqc = _eager.on_eager(ctx, dsa_bwd, _dsa_bwd_impl)(
-        dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, ctx.att_span, ctx.scale, qc
+        dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, ctx.att_span, ctx.scale, qc, None,
+        ctx.dropout_t, dropout_seed,
     )
     return (
         dq, dk, dv, (dkr if kr is not None else None), (dqr if qr is not None else None),
-        None, None, None, None, None, None, (dqc if qc is not None else None),
+        None, None, None, None, None, None, (dqc if qc is not None else None), None, None,
     )
 
 
@@ -451,13 +521,19 @@ def attention(
     scale: float,
     save_bias: bool = True,
     qc: Optional[Tensor] = None,
+    dropout_t: int = 0,
+    dropout_seed: Optional[Tensor] = None,
 ) -> tuple[Tensor, Tensor, Tensor]:
     """``deberta_amd::dsa_fwd`` with its autograd: the op itself under
     torch.compile or tracing, its implementation in a torch.autograd.Function
     in plain eager mode (the same kernels, less host time)."""
     if _eager.eager(q):
-        return _DsaFwdFunction.apply(q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias, qc)
-    return torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias, qc)
+        return _DsaFwdFunction.apply(
+            q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias, qc, dropout_t, dropout_seed
+        )
+    return torch.ops.deberta_amd.dsa_fwd(
+        q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias, qc, dropout_t, dropout_seed
+    )
 
 
 # ---- packed q, k, v ----------------------------------------------------------------
@@ -478,12 +554,16 @@ def _dsa_fwd_packed_impl(
     scale: float,
     save_bias: bool = True,
     qc: Optional[Tensor] = None,
+    dropout_t: int = 0,
+    dropout_seed: Optional[Tensor] = None,
 ) -> tuple[Tensor, Tensor, Tensor]:
     """``dsa_fwd`` on ``q, k, v = qkv.unbind(2)`` (qkv ``[B, L, 3, H, D]``)."""
     if qkv.dim() != 5 or qkv.shape[2] != 3:
         raise ValueError(f"dsa: qkv must be [B, L, 3, H, D], got {tuple(qkv.shape)}")
     q, k, v = qkv.unbind(2)
-    return _dsa_fwd_impl(q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias, qc)
+    return _dsa_fwd_impl(
+        q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias, qc, dropout_t, dropout_seed
+    )
 
 
 dsa_fwd_packed = torch.library.custom_op(
@@ -492,7 +572,10 @@ dsa_fwd_packed = torch.library.custom_op(
 
 
 @dsa_fwd_packed.register_fake
-def _dsa_fwd_packed_fake(qkv, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias=True, qc=None):
+def _dsa_fwd_packed_fake(
+    qkv, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias=True, qc=None, dropout_t=0,
+    dropout_seed=None,
+):
     q, k, _ = qkv.unbind(2)
     return _dsa_fwd_fake(q, k, k, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias, qc)
 
@@ -511,13 +594,16 @@ def _dsa_bwd_packed_impl(
     att_span: int,
     scale: float,
     qc: Optional[Tensor] = None,
+    dropout_t: int = 0,
+    dropout_seed: Optional[Tensor] = None,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """Gradients (dqkv, dkr, dqr, dqc) of ``dsa_fwd_packed``: dqkv a
     contiguous ``[B, L, 3, H, D]`` tensor in qkv's dtype."""
     q, k, v = qkv.unbind(2)
     dqkv = torch.empty(qkv.shape, dtype=qkv.dtype, device=qkv.device)
     _, _, _, dkr, dqr, dqc = _dsa_bwd_impl(
-        dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, att_span, scale, qc, dqkv=dqkv
+        dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, att_span, scale, qc, dqkv=dqkv,
+        dropout_t=dropout_t, dropout_seed=dropout_seed,
     )
     return dqkv, dkr, dqr, dqc
 
@@ -528,7 +614,10 @@ dsa_bwd_packed = torch.library.custom_op(
 
 
 @dsa_bwd_packed.register_fake
-def _dsa_bwd_packed_fake(dout, qkv, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, att_span, scale, qc=None):
+def _dsa_bwd_packed_fake(
+    dout, qkv, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, att_span, scale, qc=None, dropout_t=0,
+    dropout_seed=None,
+):
     q, k, v = qkv.unbind(2)
     _, _, _, dkr, dqr, dqc = _dsa_bwd_fake(
         dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, att_span, scale, qc
@@ -537,25 +626,29 @@ def _dsa_bwd_packed_fake(dout, qkv, kr, qr, rel_table, key_keep, pair_keep, out,
 
 
 def _setup_context_packed(ctx, inputs, output):
-    qkv, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias, qc = inputs
+    qkv, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias, qc, dropout_t, dropout_seed = (
+        _with_dropout(inputs, 10)
+    )
     out, lse, bias = output
     ctx.mark_non_differentiable(lse, bias)
     ctx.set_materialize_grads(False)
-    ctx.save_for_backward(qkv, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, qc)
+    ctx.save_for_backward(qkv, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, qc, dropout_seed)
     ctx.att_span = att_span
     ctx.scale = scale
+    ctx.dropout_t = dropout_t
 
 
 def _backward_packed(ctx, dout, dlse, dbias):
-    qkv, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, qc = ctx.saved_tensors
+    qkv, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, qc, dropout_seed = ctx.saved_tensors
     if dout is None:
-        return (None,) * 10
+        return (None,) * 12
     dqkv, dkr, dqr, dqc = _eager.on_eager(ctx, dsa_bwd_packed, _dsa_bwd_packed_impl)(
-        dout, qkv, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, ctx.att_span, ctx.scale, qc
+        dout, qkv, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, ctx.att_span, ctx.scale, qc,
+        ctx.dropout_t, dropout_seed,
     )
     return (
         dqkv, (dkr if kr is not None else None), (dqr if qr is not None else None),
-        None, None, None, None, None, None, (dqc if qc is not None else None),
+        None, None, None, None, None, None, (dqc if qc is not None else None), None, None,
     )
 
 
@@ -574,13 +667,17 @@ def attention_packed(
     scale: float,
     save_bias: bool = True,
     qc: Optional[Tensor] = None,
+    dropout_t: int = 0,
+    dropout_seed: Optional[Tensor] = None,
 ) -> tuple[Tensor, Tensor, Tensor]:
     """``attention`` on packed ``qkv`` ``[B, L, 3, H, D]``: the gradient of
     qkv comes back as one tensor."""
     if _eager.eager(qkv):
-        return _DsaFwdPackedFunction.apply(qkv, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias, qc)
+        return _DsaFwdPackedFunction.apply(
+            qkv, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias, qc, dropout_t, dropout_seed
+        )
     return torch.ops.deberta_amd.dsa_fwd_packed(
-        qkv, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias, qc
+        qkv, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias, qc, dropout_t, dropout_seed
     )
 
 

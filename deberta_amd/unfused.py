@@ -8,8 +8,9 @@ fused kernels do not take.
   the GPU only);
 * ``output_attentions=True``: the probabilities are returned, so they are
   materialised;
-* attention dropout ``p > 0`` in training mode: dropout acts on the
-  materialised probabilities;
+* attention dropout in training mode with a probability the kernels
+  cannot draw (below 2^-17 or above 1 - 2^-17; every other probability runs
+  in the kernels): torch's dropout acts on the materialised probabilities;
 * a ``relative_pos`` matrix that does not depend on ``i - j`` alone (the
   kernels take a per-offset table), used as given.
 

@@ -145,6 +145,21 @@ typedef struct dsa_fwd_args {
      [B, Lq, Lk] mask over the heads.  Query liveness is then per head:
      pair_keep[b, h, i, i]. */
   int64_t pair_keep_stride_h;
+  /* Attention dropout on the probabilities (deberta_v2_native.py:222, 636:
+     probs = dropout(probs), the reference's nn.Dropout in training).
+     dropout_threshold t in [0, 65535], in units of 1/65536: each (query,
+     key) probability is dropped with probability t / 65536 and the kept
+     ones are scaled by 65536 / (65536 - t); 0 turns dropout off.  The keep
+     bits are a function of (b, h, i, j) and dropout_seed (Philox4x32-10;
+     the counter layout is stated in deberta_amd/csrc/dsa_dropout.h), so
+     dsa_bwd, given the same arguments, regenerates the forward's mask.  The
+     logsumexp (lse) is that of the probabilities before dropout.  dsa_fwd
+     keeps the bits in its workspace (dsa_fwd_workspace_bytes counts them;
+     a dropout call without that workspace is refused), dsa_bwd in its own
+     (dsa_bwd_workspace_bytes); dsa_fwd_static refuses dropout and dsa_bias
+     ignores it.  (Version 9.) */
+  uint32_t dropout_threshold;
+  uint64_t dropout_seed;
 } dsa_fwd_args;
 
 typedef struct dsa_bwd_args {

@@ -185,9 +185,13 @@ def attend(
     att_span: int,
     use_relative: bool = True,
     variant: str = "einsum",
+    dropout_keep: Optional[torch.Tensor] = None,
+    dropout_p: float = 0.0,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Context ``(B, H, Lq, D)`` (in v's dtype) and probabilities.  q, k, v
-    are ``(B, H, L, D)``; kr / qr ``(H, 2A, D)``; rel ``(Lq, Lk)``."""
+    are ``(B, H, L, D)``; kr / qr ``(H, 2A, D)``; rel ``(Lq, Lk)``.
+    ``dropout_keep`` (bool ``(B, H, Lq, Lk)``) with ``dropout_p``: the
+    reference's attention dropout (:636) with its mask given."""
     D = q.shape[-1]
     sf = 1 + sum(t in types for t in ("c2p", "p2c", "p2p"))
     denom = math.sqrt(float(D * sf))
@@ -212,6 +216,9 @@ def attend(
             live = torch.diagonal(keep, dim1=-2, dim2=-1).unsqueeze(-1)
         scores = torch.where(live, scores, torch.zeros_like(scores))
     probs = torch.softmax(scores, dim=-1)
+    if dropout_keep is not None:
+        # nn.Dropout in training: kept elements scaled by 1 / (1 - p) (:636)
+        probs = probs * dropout_keep.to(probs.dtype) / (1.0 - dropout_p)
     if live is not None:
         probs = probs * live.to(probs.dtype)
     probs = probs.to(v.dtype)
@@ -272,7 +279,11 @@ class EagerDisentangledSelfAttention(nn.Module):
         query_states: Optional[torch.Tensor] = None,
         relative_pos: Optional[torch.Tensor] = None,
         rel_embeddings: Optional[torch.Tensor] = None,
+        dropout_keep: Optional[torch.Tensor] = None,
+        dropout_p: float = 0.0,
     ) -> tuple[torch.Tensor, Optional[torch.Tensor]]:
+        """The reference forward; ``dropout_keep`` / ``dropout_p``: its
+        attention dropout with the mask given (``attend``)."""
         if query_states is None:
             query_states = hidden_states
         q = self.heads(self.query_proj(query_states))
@@ -291,6 +302,7 @@ class EagerDisentangledSelfAttention(nn.Module):
         ctx, probs = attend(
             q, k, v, kr, qr, rel, attention_mask,
             types=self.pos_att_type, att_span=self.pos_ebd_size, use_relative=use_rel, variant=self.variant,
+            dropout_keep=dropout_keep, dropout_p=dropout_p,
         )
         B, H, L, D = ctx.shape
         ctx = ctx.permute(0, 2, 1, 3).contiguous().view(B, L, H * D).to(hidden_states.dtype)

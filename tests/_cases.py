@@ -27,6 +27,12 @@ class Case:
     Lk: Optional[int] = None
     std: float = 1.0
     ramp: float = 0.0  # key j scaled by 1 + ramp * j / Lk (score maxima grow along the keys)
+    dropout: float = 0.0  # attention dropout probability (kernel threshold round(p * 65536))
+    drop_seed: int = 0x1234_5678_9ABC_DEF
+
+    @property
+    def drop_t(self) -> int:
+        return int(round(self.dropout * 65536)) if self.dropout > 0 else 0
 
     @property
     def A(self) -> int:
@@ -98,7 +104,16 @@ def oracle_run(c: Case, x: dict, dtype: torch.dtype, grads: bool = True) -> dict
     use_rel = kr is not None or qr is not None
     Lk = c.Lk or c.L
     rel = eager.relative_positions(c.L, Lk, c.buckets, c.max_pos) if use_rel else None
-    ctx, _ = eager.attend(q, k, v, kr, qr, rel, x["mask"], types=types, att_span=c.A, use_relative=use_rel)
+    keep, p = None, 0.0
+    if c.drop_t:
+        from oracle.dropout import keep_mask
+
+        keep = torch.from_numpy(keep_mask(c.drop_seed, c.drop_t, c.B, c.H, c.L, Lk))
+        p = c.drop_t / 65536
+    ctx, _ = eager.attend(
+        q, k, v, kr, qr, rel, x["mask"], types=types, att_span=c.A, use_relative=use_rel, dropout_keep=keep,
+        dropout_p=p,
+    )
     out = ctx.permute(0, 2, 1, 3)
     res = {"out": out.detach()}
     if grads:
@@ -140,7 +155,8 @@ def hip_run(c: Case, x: dict, dtype: torch.dtype, device, grads: bool = True) ->
         assert pk is None and kk is not None and kk.dtype == torch.int32, "document mask not recognised"
     sf = 1 + sum(t in types for t in ("c2p", "p2c", "p2p"))
     scale = 1.0 / math.sqrt(c.D * sf)
-    out, lse, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, kk, pk, c.A, scale)
+    seed = torch.tensor([c.drop_seed], dtype=torch.int64) if c.drop_t else None
+    out, lse, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, kk, pk, c.A, scale, True, None, c.drop_t, seed)
     res = {"out": out.detach().float().cpu(), "lse": lse.detach().cpu()}
     if grads:
         dout = x["dout"].to(device=device, dtype=dtype)

@@ -567,3 +567,34 @@ def test_ops_refuse_graph_capture(monkeypatch):
     for call in calls:
         with pytest.raises(RuntimeError, match="capturing a CUDA/HIP graph"):
             call()
+
+
+def test_dropout_argument_errors(lib):
+    """Attention dropout's threshold is checked before any device work, and
+    the package's helpers map a probability to the kernels' threshold and
+    refuse a missing or malformed seed."""
+    a = _lib.DsaFwdArgs()
+    a.B, a.H, a.Lq, a.Lk, a.D, a.dtype = 1, 1, 8, 8, 64, _lib.DSA_BF16
+    buf = (ctypes.c_uint8 * 64)()
+    p = ctypes.cast(buf, ctypes.c_void_p).value
+    for f in ("q", "k", "v", "out", "lse"):
+        setattr(a, f, p)
+    a.dropout_threshold = 65536
+    assert lib.dsa_fwd(ctypes.byref(a), None) != 0
+    assert "dropout_threshold must be in [0, 65535]" in _lib.last_error()
+    assert ops.dropout_threshold(0.1) == 6554 and ops.dropout_threshold(0.5) == 32768
+    assert ops.dropout_threshold(1e-6) == 0 and ops.dropout_threshold(1 - 1e-6) == 65536
+    with pytest.raises(ValueError, match="dropout threshold"):
+        ops._check_threshold(70000)
+    with pytest.raises(ValueError, match="dropout_seed"):
+        ops._seed_value(None, 6554)
+    with pytest.raises(ValueError, match="dropout_seed"):
+        ops._seed_value(torch.tensor([1, 2]), 6554)
+    assert ops._seed_value(None, 0) == 0
+    assert ops._seed_value(torch.tensor([-1]), 6554) == (1 << 64) - 1
+    s = ops.draw_dropout_seed()
+    assert s.dtype == torch.int64 and s.numel() == 1 and s.device.type == "cpu" and 0 <= int(s) < (1 << 62)
+    torch.manual_seed(5)
+    s1 = ops.draw_dropout_seed()
+    torch.manual_seed(5)
+    assert torch.equal(s1, ops.draw_dropout_seed())
