@@ -255,8 +255,7 @@ int launch_dropout_bits(const dsa_fwd_args* a, uint32_t* bits, bool dkdv, dsa::F
   d.t = a->dropout_threshold;
   d.k0 = (uint32_t)(a->dropout_seed & 0xffffffffu);
   d.k1 = (uint32_t)(a->dropout_seed >> 32);
-  const int64_t nw = (int64_t)d.B * d.H * d.NQB * d.NKT * 64;
-  const dim3 grid((unsigned)((nw + 255) / 256));
+  const dim3 grid((unsigned)((d.NKT + 3) / 4 * d.NQB), (unsigned)d.H, (unsigned)d.B);
   if (dkdv)
     hipLaunchKernelGGL(dsa::dsa_dropout_bits_kernel<true>, grid, dim3(256), 0, st, d);
   else
