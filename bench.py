@@ -279,7 +279,7 @@ def run_encoder(args) -> None:
     scale = 1.0 / math.sqrt(D * 3)
 
     def attn_step():
-        out, _, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, A, scale)
+        out, _, _, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, A, scale)
         torch.autograd.grad(out, (q, k, v, kr, qr), dout)
 
     ms_attn = timed(attn_step, 10)
@@ -532,7 +532,7 @@ def main() -> None:
 
     def step():
         seed = ops.draw_dropout_seed() if drop_t else None
-        out, _, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, kk, pk, A, scale, True, None, drop_t, seed)
+        out, _, _, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, kk, pk, A, scale, True, None, drop_t, seed)
         return torch.autograd.grad(out, leaves, dout)
 
     if args.copy_probe_mib:
@@ -560,13 +560,15 @@ def main() -> None:
     # ---- per-kernel times: each launch timed on the stream it runs on ------------
     stream = torch.cuda.current_stream(dev)
     dseed = ops.draw_dropout_seed() if drop_t else None
-    out, lse, bias = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, kk, pk, A, scale, True, None, drop_t, dseed)
+    out, lse, bias, dbits = torch.ops.deberta_amd.dsa_fwd(
+        q, k, v, kr, qr, table, kk, pk, A, scale, True, None, drop_t, dseed
+    )
     f32 = dict(dtype=torch.float32, device=dev)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     dkr, dqr = torch.zeros((H, R, D), **f32), torch.zeros((H, R, D), **f32)
     bargs = ops.fill_bwd_args(
         dout, q, k, v, kr, qr, table, kk, pk, out, lse, bias, A, scale, dq, dk, dv, dkr, dqr,
-        dropout_t=drop_t, dropout_seed=dseed,
+        dropout_t=drop_t, dropout_seed=dseed, dropout_bits=dbits,
     )
     ws = torch.empty((ops.bwd_workspace_bytes(bargs),), dtype=torch.uint8, device=dev)
     bargs.workspace, bargs.workspace_bytes = ws.data_ptr(), ws.numel()
@@ -601,8 +603,7 @@ def main() -> None:
     staged = [
         ("dsa_fwd_kernel (after dsa_table_ks_kernel" + (" and dsa_dropout_bits_kernel)" if drop_t else ")"), run_fwd,
          f_fwd),
-        ("dsa_bwd_prep_kernel" + (" (with dsa_dropout_bits_kernel)" if drop_t else ""), run_stage(_lib.DSA_STAGE_PREP),
-         0.0),
+        ("dsa_bwd_prep_kernel", run_stage(_lib.DSA_STAGE_PREP), 0.0),
         ("dsa_bwd_dkdv_kernel", run_stage(_lib.DSA_STAGE_DKDV), f_dkdv),
         ("dsa_bwd_dqtab_kernel", run_stage(_lib.DSA_STAGE_DQ | _lib.DSA_STAGE_TABLE), f_dq + f_table),
         ("dsa_bwd_fold_kernel", run_stage(_lib.DSA_STAGE_SUM), 0.0),
@@ -654,7 +655,7 @@ def main() -> None:
         return
     # The stage calls' buffers go back to the caching allocator, which hands
     # the same blocks to the op's steps below (same sizes).
-    del out, lse, bias, dq, dk, dv, dkr, dqr, bargs, fargs, ws, fws
+    del out, lse, bias, dbits, dq, dk, dv, dkr, dqr, bargs, fargs, ws, fws
     torch.cuda.synchronize()
 
     # ---- the timed steps ----------------------------------------------------------

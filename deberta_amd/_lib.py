@@ -24,7 +24,7 @@ DSA_STAGE_FOLD = 8
 DSA_STAGE_TABLE = 16  # the first half of FOLD: per-offset sums (workspace)
 DSA_STAGE_SUM = 32  # the second half: their fold onto dkr / dqr
 
-EXPECTED_VERSION = 9
+EXPECTED_VERSION = 10
 
 _i64x3 = ctypes.c_int64 * 3
 _i64x2 = ctypes.c_int64 * 2
@@ -69,6 +69,7 @@ class DsaFwdArgs(ctypes.Structure):
         ("pair_keep_stride_h", ctypes.c_int64),
         ("dropout_threshold", ctypes.c_uint32),
         ("dropout_seed", ctypes.c_uint64),
+        ("dropout_bits", ctypes.c_void_p),
     ]
 
 
@@ -211,6 +212,7 @@ EXPORTS = (
     "dsa_bwd_workspace_bytes",
     "dsa_fwd_bias_bytes",
     "dsa_fwd_workspace_bytes",
+    "dsa_fwd_dropout_bytes",
     "dsa_last_error",
     "dsa_version",
 )
@@ -251,6 +253,8 @@ def load() -> ctypes.CDLL:
         lib.dsa_fwd_bias_bytes.restype = ctypes.c_size_t
         lib.dsa_fwd_workspace_bytes.argtypes = [ctypes.POINTER(DsaFwdArgs)]
         lib.dsa_fwd_workspace_bytes.restype = ctypes.c_size_t
+        lib.dsa_fwd_dropout_bytes.argtypes = [ctypes.POINTER(DsaFwdArgs)]
+        lib.dsa_fwd_dropout_bytes.restype = ctypes.c_size_t
         lib.dsa_last_error.argtypes = []
         lib.dsa_last_error.restype = ctypes.c_char_p
         lib.dsa_version.argtypes = []

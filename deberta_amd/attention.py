@@ -231,11 +231,11 @@ def fused_attention(
             raise ValueError(f"dropout_p={dropout_p} has no kernel form (threshold {drop_t} outside [1, 65535])")
         seed = ops.draw_dropout_seed()
     if qkv is not None:
-        out, _, _ = ops.attention_packed(
+        out, _, _, _ = ops.attention_packed(
             qkv, kr, qr, table, key_keep, pair_keep, int(att_span), float(scale), save_bias, qc, drop_t, seed
         )
     else:
-        out, _, _ = ops.attention(
+        out, _, _, _ = ops.attention(
             q, k, v, kr, qr, table, key_keep, pair_keep, int(att_span), float(scale), save_bias, qc, drop_t, seed
         )
     return out

@@ -183,11 +183,12 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
     }
   };
 
-  // Dropout: the keep words of the 32-query block qi and the 64-key tile of
-  // the wave's keys, in the dkdv layout (dsa_dropout.h), copied to LDS with
-  // the tile (16 lanes x 16 bytes); lane l's word, shifted by 16 (w % 2),
-  // has bit 8 ib + 4 jb + e for the pair (query i0 + 16 ib + 4 g + e, key
-  // jw + 16 jb + c16).
+  // Dropout: the forward's 64 keep words of the 32-query block qi and the
+  // 64-key tile of the wave's keys (dsa_dropout.h), copied to LDS with the
+  // tile (16 lanes x 16 bytes).  The pair (query i0 + 16 ib + 4 g + e, key
+  // jw + 16 jb + c16) is bit 16 ib + 4 (2 (w % 2) + jb) + c16 % 4 of the word
+  // of forward lane 16 (c16 / 4) + 4 g + e: a lane's four words are 16
+  // contiguous bytes.
   const uint32_t* dropw = nullptr;
   const int NKT64 = p.LkP / 64;
   if constexpr (DROP) dropw = p.drop + drop_word0(b, h, p.H, p.LqP / 32, NKT64, 0, jw / 64);
@@ -388,8 +389,21 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
       __builtin_amdgcn_s_setprio(0);
       // ---- P, dP, dS -----------------------------------------------------------------------------
       f32x4 pp[2][BQ / 16], dsh[2][BQ / 16];
+      // dropout: this lane's 16 keep bits, bit 8 ib + 4 jb + e
       uint32_t dm = 0;
-      if constexpr (DROP) dm = Dw[w * 64 + lane] >> (16 * (w & 1));
+      if constexpr (DROP) {
+        const uint4 f4 = *reinterpret_cast<const uint4*>(Dw + w * 64 + 16 * (c16 >> 2) + 4 * g);
+        const uint32_t f[4] = {f4.x, f4.y, f4.z, f4.w};
+        // word e, shifted by 8 (w % 2) + c16 % 4, holds the pair (ib, jb) at
+        // bit 16 ib + 4 jb: bits 0 and 4 stay, bits 16 and 20 move to 8
+        // and 12, then the word's four bits go to 8 ib + 4 jb + e
+        const int sh = 8 * (w & 1) + (c16 & 3);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t t = f[e] >> sh;
+          dm |= ((t & 0x11u) | ((t >> 8) & 0x1100u)) << e;
+        }
+      }
       auto probs = [&](auto plain) {
 #pragma unroll
         for (int ib = 0; ib < BQ / 16; ++ib) {

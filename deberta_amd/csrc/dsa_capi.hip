@@ -89,6 +89,8 @@ int check_fwd(const dsa_fwd_args* a) {
   }
   if (a->dropout_threshold > 65535u)
     return fail("dsa: dropout_threshold must be in [0, 65535] (units of 1/65536), got %u", a->dropout_threshold);
+  if (a->dropout_threshold && a->dropout_bits && !aligned16(a->dropout_bits))
+    return fail("dsa: dropout_bits must be 16-byte aligned");
   if ((a->flags & DSA_C2P) && !a->kr) return fail("dsa: c2p needs the pos-key table kr");
   // the forward addresses table rows with 32-bit element offsets
   if ((a->flags & DSA_C2P) && (int64_t)(2 * a->att_span - 1) * llabs(a->kr_strides[1]) + a->D > 0x7fffffffLL)
@@ -235,17 +237,21 @@ int launch_orders(const dsa::FwdParams& p, int njobs, int* const* bufs, const in
 int fwd_tiles(const dsa_fwd_args* a) { return (a->Lq + dsa::dcfg::BQ - 1) / dsa::dcfg::BQ; }
 
 // ---- attention dropout (dsa_dropout.h) ----
-// Bytes of the keep bits in the forward's and the backward's workspaces (0
-// without dropout).
-size_t drop_bytes(const dsa_fwd_args* a) {
+// Bytes of the keep bits (0 without dropout).
+size_t drop_bits_bytes(const dsa_fwd_args* a) {
   if (!a->dropout_threshold) return 0;
-  return align_up(dsa::dropout_bits_bytes(a->B, a->H, round_up(a->Lq, 128), round_up(a->Lk, 128)), 256);
+  return dsa::dropout_bits_bytes(a->B, a->H, round_up(a->Lq, 128), round_up(a->Lk, 128));
 }
+// Bytes of them in the forward's or the backward's workspace: none when the
+// caller keeps them (dropout_bits).
+size_t drop_bytes(const dsa_fwd_args* a) {
+  return a->dropout_bits ? 0 : align_up(drop_bits_bytes(a), 256);
+}
+float drop_scale(const dsa_fwd_args* a) { return 65536.f / (float)(65536u - a->dropout_threshold); }
 
 // Generates the call's keep bits into `bits` and points the kernels'
 // parameters at them.
-// `dkdv`: the layout the dkdv kernel reads, else the forward's.
-int launch_dropout_bits(const dsa_fwd_args* a, uint32_t* bits, bool dkdv, dsa::FwdParams& p, hipStream_t st) {
+int launch_dropout_bits(const dsa_fwd_args* a, uint32_t* bits, dsa::FwdParams& p, hipStream_t st) {
   dsa::DropParams d;
   d.bits = bits;
   d.B = a->B;
@@ -256,13 +262,10 @@ int launch_dropout_bits(const dsa_fwd_args* a, uint32_t* bits, bool dkdv, dsa::F
   d.k0 = (uint32_t)(a->dropout_seed & 0xffffffffu);
   d.k1 = (uint32_t)(a->dropout_seed >> 32);
   const dim3 grid((unsigned)((d.NKT + 3) / 4 * d.NQB), (unsigned)d.H, (unsigned)d.B);
-  if (dkdv)
-    hipLaunchKernelGGL(dsa::dsa_dropout_bits_kernel<true>, grid, dim3(256), 0, st, d);
-  else
-    hipLaunchKernelGGL(dsa::dsa_dropout_bits_kernel<false>, grid, dim3(256), 0, st, d);
+  hipLaunchKernelGGL(dsa::dsa_dropout_bits_kernel, grid, dim3(256), 0, st, d);
   if (launch_check("dsa_dropout_bits_kernel")) return 1;
   p.drop = bits;
-  p.drop_scale = 65536.f / (float)(65536u - a->dropout_threshold);
+  p.drop_scale = drop_scale(a);
   return 0;
 }
 
@@ -418,16 +421,21 @@ int launch_bwd(const dsa_bwd_args* a, const WsLayout& ws, int mode, hipStream_t 
   bp.NPG = ws.NPG;
   const int stages =
       a->stages ? a->stages : (DSA_STAGE_PREP | DSA_STAGE_DQ | DSA_STAGE_DKDV | DSA_STAGE_FOLD);
-  uint32_t* dbits = f.dropout_threshold ? reinterpret_cast<uint32_t*>(base + ws.drop) : nullptr;
-  if (dbits) {
-    // PREP regenerates the forward's keep bits (same seed, same bits) in
-    // the layout dkdv reads; a DKDV run in a later call reads the ones an
-    // earlier PREP left
-    if (stages & DSA_STAGE_PREP) {
-      if (launch_dropout_bits(&f, dbits, true, bp.f, st)) return 1;
+  if (f.dropout_threshold) {
+    if (f.dropout_bits) {
+      // the forward's keep bits, kept by the caller
+      bp.f.drop = static_cast<const uint32_t*>(f.dropout_bits);
+      bp.f.drop_scale = drop_scale(&f);
     } else {
-      bp.f.drop = dbits;
-      bp.f.drop_scale = 65536.f / (float)(65536u - f.dropout_threshold);
+      // PREP regenerates them (same seed, same bits) into the workspace; a
+      // DKDV run in a later call reads the ones an earlier PREP left
+      uint32_t* dbits = reinterpret_cast<uint32_t*>(base + ws.drop);
+      if (stages & DSA_STAGE_PREP) {
+        if (launch_dropout_bits(&f, dbits, bp.f, st)) return 1;
+      } else {
+        bp.f.drop = dbits;
+        bp.f.drop_scale = drop_scale(&f);
+      }
     }
   }
 
@@ -591,7 +599,7 @@ size_t tables_ks_bytes(const dsa_fwd_args* a) {
 int run_fwd(const dsa_fwd_args* a, int* order_buf, void* tab_buf, uint32_t* drop_buf, hipStream_t st) {
   dsa::FwdParams p = to_params(a);
   const int mode = mask_mode(a);
-  if (drop_buf && launch_dropout_bits(a, drop_buf, false, p, st)) return 1;
+  if (drop_buf && launch_dropout_bits(a, drop_buf, p, st)) return 1;
   if (tab_buf && a->flags) {
     dsa::TableKs t;
     const int R = 2 * a->att_span, ks = 64 / elem_bytes(a->dtype);
@@ -820,7 +828,7 @@ dsa::rows::RtdParams rtd_params(const dsa_rtd_args* a) {
 
 extern "C" {
 
-int dsa_version(void) { return 9; }
+int dsa_version(void) { return 10; }
 
 const char* dsa_last_error(void) { return g_err.c_str(); }
 
@@ -831,8 +839,8 @@ int dsa_fwd(const dsa_fwd_args* a, void* stream) {
   if (refuse_capture(st, "dsa_fwd")) return 1;
   const size_t ob = order_bytes(a, fwd_tiles(a)), tb = tables_ks_bytes(a), db = drop_bytes(a);
   if (db && (!a->workspace || a->workspace_bytes < ob + tb + db))
-    return fail("dsa: attention dropout needs the forward workspace of %zu bytes (its keep bits), got %zu", ob + tb + db,
-                a->workspace ? a->workspace_bytes : (size_t)0);
+    return fail("dsa: attention dropout needs dropout_bits or the forward workspace of %zu bytes (its keep bits), "
+                "got %zu", ob + tb + db, a->workspace ? a->workspace_bytes : (size_t)0);
   int* buf = nullptr;
   void* tabs = nullptr;
   uint32_t* dbits = nullptr;
@@ -845,6 +853,7 @@ int dsa_fwd(const dsa_fwd_args* a, void* stream) {
     if (tb && a->workspace_bytes >= ob + tb) tabs = static_cast<char*>(a->workspace) + ob;
     if (db) dbits = reinterpret_cast<uint32_t*>(static_cast<char*>(a->workspace) + ob + tb);
   }
+  if (a->dropout_threshold && a->dropout_bits) dbits = static_cast<uint32_t*>(a->dropout_bits);
   return run_fwd(a, buf, tabs, dbits, st);
 }
 
@@ -944,6 +953,11 @@ int dsa_bias(const dsa_fwd_args* a, void* out, const int64_t* out_strides, void*
 size_t dsa_fwd_bias_bytes(const dsa_fwd_args* a) {
   if (!a || !a->flags) return 0;
   return (size_t)a->B * a->H * round_up(a->Lq, 128) * round_up(a->Lk, 128) * (a->dtype == DSA_BF16 ? 2 : 4);
+}
+
+size_t dsa_fwd_dropout_bytes(const dsa_fwd_args* a) {
+  if (!a || a->B < 1 || a->Lq < 1 || a->Lk < 1 || a->H < 1) return 0;
+  return drop_bits_bytes(a);
 }
 
 size_t dsa_fwd_workspace_bytes(const dsa_fwd_args* a) {

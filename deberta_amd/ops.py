@@ -27,8 +27,9 @@ Tensor layouts (see include/dsa.h):
                     probability is dropped with probability t / 65536, the
                     kept ones scaled by 65536 / (65536 - t); 0: no dropout
   dropout_seed      int64 CPU tensor of one element (or None without
-                    dropout): the 64-bit seed of the keep bits, which the
-                    backward regenerates from it
+                    dropout): the 64-bit seed of the keep bits
+  drop_bits         uint8 [dropout_bytes]: the keep bits dsa_fwd generated,
+                    saved for the backward (empty without dropout)
 """
 
 from __future__ import annotations
@@ -83,6 +84,15 @@ def bias_dtype(dtype: torch.dtype) -> torch.dtype:
     return torch.float16 if dtype == torch.bfloat16 else torch.float32
 
 
+def dropout_bytes(q: Tensor, k: Tensor, dropout_t: int) -> int:
+    """Bytes of the keep bits (``dsa_fwd_dropout_bytes``): one 32-bit word
+    per (b, h, 32 queries, 64 keys, lane) of the padded extents."""
+    if not dropout_t:
+        return 0
+    B, Lq, H = q.shape[0], q.shape[1], q.shape[2]
+    return B * H * (_pad128(Lq) // 32) * (_pad128(k.shape[1]) // 64) * 64 * 4
+
+
 def dropout_threshold(p: float) -> int:
     """The kernels' dropout threshold for probability ``p``: ``round(p *
     65536)``.  The kernels drop with probability ``t / 65536`` exactly, so a
@@ -128,6 +138,7 @@ def _fill_fwd_args(
     qc: Optional[Tensor] = None,
     dropout_t: int = 0,
     dropout_seed: Optional[Tensor] = None,
+    dropout_bits: Optional[Tensor] = None,
 ) -> _lib.DsaFwdArgs:
     B, Lq, H, D = q.shape
     Lk = k.shape[1]
@@ -168,6 +179,10 @@ def _fill_fwd_args(
     _check_threshold(dropout_t)
     a.dropout_threshold = int(dropout_t)
     a.dropout_seed = _seed_value(dropout_seed, int(dropout_t))
+    if dropout_t and dropout_bits is not None and dropout_bits.numel():
+        if dropout_bits.numel() * dropout_bits.element_size() < dropout_bytes(q, k, dropout_t):
+            raise ValueError("dsa: dropout_bits is smaller than the call's keep bits")
+        a.dropout_bits = dropout_bits.data_ptr()
     return a
 
 
@@ -245,12 +260,13 @@ def _dsa_fwd_impl(
     qc: Optional[Tensor] = None,
     dropout_t: int = 0,
     dropout_seed: Optional[Tensor] = None,
-) -> tuple[Tensor, Tensor, Tensor]:
-    """(out, lse, bias).  With c2p/p2c and ``save_bias`` the relative score
-    term is written to ``bias`` for the backward (which needs it); else
-    ``bias`` is empty.  ``qc``: the c2p term's query rows (q when None).
-    ``dropout_t`` / ``dropout_seed``: attention dropout (lse is that of the
-    probabilities before dropout)."""
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """(out, lse, bias, drop_bits).  With c2p/p2c and ``save_bias`` the
+    relative score term is written to ``bias`` for the backward (which
+    needs it); else ``bias`` is empty.  ``qc``: the c2p term's query rows (q
+    when None).  ``dropout_t`` / ``dropout_seed``: attention dropout (lse is
+    that of the probabilities before dropout); its keep bits come back in
+    ``drop_bits`` for the backward (empty without dropout)."""
     _eager.refuse_capture("deberta_amd::dsa_fwd")
     _validate(q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, qc)
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
@@ -264,8 +280,10 @@ def _dsa_fwd_impl(
         bias = torch.empty(bias_shape(q, k), dtype=bias_dtype(q.dtype), device=q.device)
     else:
         bias = torch.empty((0,), dtype=bias_dtype(q.dtype), device=q.device)
+    drop_bits = torch.empty((dropout_bytes(q, k, dropout_t),), dtype=torch.uint8, device=q.device)
     args = _fill_fwd_args(
-        q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, att_span, scale, bias, qc, dropout_t, dropout_seed
+        q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, att_span, scale, bias, qc, dropout_t, dropout_seed,
+        drop_bits,
     )
     lib = _lib.load()
     # scratch for the heaviest-first launch order under key / segment masks,
@@ -275,7 +293,7 @@ def _dsa_fwd_impl(
     if ws is not None:
         args.workspace, args.workspace_bytes = ws.data_ptr(), nws
     _lib.check(lib.dsa_fwd(ctypes.byref(args), ctypes.c_void_p(_eager.stream_ptr(q))), "dsa_fwd")
-    return out, lse, bias
+    return out, lse, bias, drop_bits
 
 
 # Tagged CUDA-graph unsafe: capturing the op's forward and backward in a HIP
@@ -302,7 +320,7 @@ def _dsa_fwd_fake(
         bias = q.new_empty(bias_shape(q, k), dtype=bias_dtype(q.dtype))
     else:
         bias = q.new_empty((0,), dtype=bias_dtype(q.dtype))
-    return out, lse, bias
+    return out, lse, bias, q.new_empty((dropout_bytes(q, k, dropout_t),), dtype=torch.uint8)
 
 
 def bwd_workspace_bytes(args: _lib.DsaBwdArgs) -> int:
@@ -334,14 +352,17 @@ def fill_bwd_args(
     dqc: Optional[Tensor] = None,
     dropout_t: int = 0,
     dropout_seed: Optional[Tensor] = None,
+    dropout_bits: Optional[Tensor] = None,
 ) -> _lib.DsaBwdArgs:
     """Backward arguments.  dkr / dqr are fp32 and accumulated into, or, with
     ``dtab_overwrite``, written (fp32 or bf16, their dtype).  With ``qc``,
     ``dqc`` receives its gradient (the c2p part of dq).  The dropout
-    arguments are the forward's."""
+    arguments are the forward's (with its keep bits, none are generated;
+    without, they are regenerated from the seed)."""
     a = _lib.DsaBwdArgs()
     a.fwd = _fill_fwd_args(
-        q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, att_span, scale, bias, qc, dropout_t, dropout_seed
+        q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, att_span, scale, bias, qc, dropout_t, dropout_seed,
+        dropout_bits,
     )
     if dqc is not None:
         a.dqc = dqc.data_ptr()
@@ -398,6 +419,7 @@ def _dsa_bwd_impl(
     dqkv: Optional[Tensor] = None,
     dropout_t: int = 0,
     dropout_seed: Optional[Tensor] = None,
+    drop_bits: Optional[Tensor] = None,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     """Gradients (dq, dk, dv, dkr, dqr, dqc).  With ``dqkv`` (a contiguous
     ``[B, L, 3, H, D]`` buffer), dq, dk and dv are written into its three
@@ -405,8 +427,8 @@ def _dsa_bwd_impl(
     tables' dtype (empty when the matching table is None).  ``bias`` is the
     relative term dsa_fwd saved (required with c2p/p2c).  With ``qc`` (the
     c2p term's query rows), dqc is its gradient and dq the content part;
-    else dqc is empty.  ``dropout_t`` / ``dropout_seed``: the forward's
-    (the kernels regenerate its keep bits)."""
+    else dqc is empty.  ``dropout_t`` / ``dropout_seed`` / ``drop_bits``:
+    the forward's (without its keep bits the kernels regenerate them)."""
     _eager.refuse_capture("deberta_amd::dsa_bwd")
     if kr is not None or qr is not None:
         _alert_nondeterministic_tables()
@@ -435,6 +457,7 @@ def _dsa_bwd_impl(
         dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, att_span, scale,
         dq, dk, dv, dkr if kr is not None else None, dqr if qr is not None else None, dtab_overwrite=True,
         qc=qc, dqc=dqc if qc is not None else None, dropout_t=dropout_t, dropout_seed=dropout_seed,
+        dropout_bits=drop_bits,
     )
     ws = torch.empty((max(bwd_workspace_bytes(args), 16),), dtype=torch.uint8, device=q.device)
     args.workspace = ws.data_ptr()
@@ -452,7 +475,7 @@ dsa_bwd = torch.library.custom_op(
 @dsa_bwd.register_fake
 def _dsa_bwd_fake(
     dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, att_span, scale, qc=None, dqkv=None,
-    dropout_t=0, dropout_seed=None,
+    dropout_t=0, dropout_seed=None, drop_bits=None,
 ):
     H, D = q.shape[2], q.shape[3]
     R = 2 * int(att_span)
@@ -473,12 +496,12 @@ def _setup_context(ctx, inputs, output):
     q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias, qc, dropout_t, dropout_seed = (
         _with_dropout(inputs, 12)
     )
-    out, lse, bias = output
-    ctx.mark_non_differentiable(lse, bias)
-    # lse and the saved term get no gradient: do not materialise zeros for
-    # them (the saved term is (B, H, L, L)-sized)
+    out, lse, bias, drop_bits = output
+    ctx.mark_non_differentiable(lse, bias, drop_bits)
+    # lse, the saved term and the keep bits get no gradient: do not
+    # materialise zeros for them (the saved term is (B, H, L, L)-sized)
     ctx.set_materialize_grads(False)
-    ctx.save_for_backward(q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, qc, dropout_seed)
+    ctx.save_for_backward(q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, qc, dropout_seed, drop_bits)
     ctx.att_span = att_span
     ctx.scale = scale
     ctx.dropout_t = dropout_t
@@ -490,13 +513,13 @@ def _with_dropout(inputs: tuple, n: int) -> tuple:
     return tuple(inputs) + (0, None)[len(inputs) - n:] if len(inputs) < n + 2 else tuple(inputs)
 
 
-def _backward(ctx, dout, dlse, dbias):
-    q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, qc, dropout_seed = ctx.saved_tensors
+def _backward(ctx, dout, dlse, dbias, ddrop):
+    q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, qc, dropout_seed, drop_bits = ctx.saved_tensors
     if dout is None:  # the output itself received no gradient
         return (None,) * 14
     dq, dk, dv, dkr, dqr, dqc = _eager.on_eager(ctx, dsa_bwd, _dsa_bwd_impl)(
         dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, ctx.att_span, ctx.scale, qc, None,
-        ctx.dropout_t, dropout_seed,
+        ctx.dropout_t, dropout_seed, drop_bits,
     )
     return (
         dq, dk, dv, (dkr if kr is not None else None), (dqr if qr is not None else None),
@@ -523,7 +546,7 @@ def attention(
     qc: Optional[Tensor] = None,
     dropout_t: int = 0,
     dropout_seed: Optional[Tensor] = None,
-) -> tuple[Tensor, Tensor, Tensor]:
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """``deberta_amd::dsa_fwd`` with its autograd: the op itself under
     torch.compile or tracing, its implementation in a torch.autograd.Function
     in plain eager mode (the same kernels, less host time)."""
@@ -556,7 +579,7 @@ def _dsa_fwd_packed_impl(
     qc: Optional[Tensor] = None,
     dropout_t: int = 0,
     dropout_seed: Optional[Tensor] = None,
-) -> tuple[Tensor, Tensor, Tensor]:
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """``dsa_fwd`` on ``q, k, v = qkv.unbind(2)`` (qkv ``[B, L, 3, H, D]``)."""
     if qkv.dim() != 5 or qkv.shape[2] != 3:
         raise ValueError(f"dsa: qkv must be [B, L, 3, H, D], got {tuple(qkv.shape)}")
@@ -577,7 +600,9 @@ def _dsa_fwd_packed_fake(
     dropout_seed=None,
 ):
     q, k, _ = qkv.unbind(2)
-    return _dsa_fwd_fake(q, k, k, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias, qc)
+    return _dsa_fwd_fake(
+        q, k, k, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias, qc, dropout_t, dropout_seed
+    )
 
 
 def _dsa_bwd_packed_impl(
@@ -596,6 +621,7 @@ def _dsa_bwd_packed_impl(
     qc: Optional[Tensor] = None,
     dropout_t: int = 0,
     dropout_seed: Optional[Tensor] = None,
+    drop_bits: Optional[Tensor] = None,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """Gradients (dqkv, dkr, dqr, dqc) of ``dsa_fwd_packed``: dqkv a
     contiguous ``[B, L, 3, H, D]`` tensor in qkv's dtype."""
@@ -603,7 +629,7 @@ def _dsa_bwd_packed_impl(
     dqkv = torch.empty(qkv.shape, dtype=qkv.dtype, device=qkv.device)
     _, _, _, dkr, dqr, dqc = _dsa_bwd_impl(
         dout, q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, att_span, scale, qc, dqkv=dqkv,
-        dropout_t=dropout_t, dropout_seed=dropout_seed,
+        dropout_t=dropout_t, dropout_seed=dropout_seed, drop_bits=drop_bits,
     )
     return dqkv, dkr, dqr, dqc
 
@@ -616,7 +642,7 @@ dsa_bwd_packed = torch.library.custom_op(
 @dsa_bwd_packed.register_fake
 def _dsa_bwd_packed_fake(
     dout, qkv, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, att_span, scale, qc=None, dropout_t=0,
-    dropout_seed=None,
+    dropout_seed=None, drop_bits=None,
 ):
     q, k, v = qkv.unbind(2)
     _, _, _, dkr, dqr, dqc = _dsa_bwd_fake(
@@ -629,22 +655,22 @@ def _setup_context_packed(ctx, inputs, output):
     qkv, kr, qr, rel_table, key_keep, pair_keep, att_span, scale, save_bias, qc, dropout_t, dropout_seed = (
         _with_dropout(inputs, 10)
     )
-    out, lse, bias = output
-    ctx.mark_non_differentiable(lse, bias)
+    out, lse, bias, drop_bits = output
+    ctx.mark_non_differentiable(lse, bias, drop_bits)
     ctx.set_materialize_grads(False)
-    ctx.save_for_backward(qkv, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, qc, dropout_seed)
+    ctx.save_for_backward(qkv, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, qc, dropout_seed, drop_bits)
     ctx.att_span = att_span
     ctx.scale = scale
     ctx.dropout_t = dropout_t
 
 
-def _backward_packed(ctx, dout, dlse, dbias):
-    qkv, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, qc, dropout_seed = ctx.saved_tensors
+def _backward_packed(ctx, dout, dlse, dbias, ddrop):
+    qkv, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, qc, dropout_seed, drop_bits = ctx.saved_tensors
     if dout is None:
         return (None,) * 12
     dqkv, dkr, dqr, dqc = _eager.on_eager(ctx, dsa_bwd_packed, _dsa_bwd_packed_impl)(
         dout, qkv, kr, qr, rel_table, key_keep, pair_keep, out, lse, bias, ctx.att_span, ctx.scale, qc,
-        ctx.dropout_t, dropout_seed,
+        ctx.dropout_t, dropout_seed, drop_bits,
     )
     return (
         dqkv, (dkr if kr is not None else None), (dqr if qr is not None else None),
@@ -669,7 +695,7 @@ def attention_packed(
     qc: Optional[Tensor] = None,
     dropout_t: int = 0,
     dropout_seed: Optional[Tensor] = None,
-) -> tuple[Tensor, Tensor, Tensor]:
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """``attention`` on packed ``qkv`` ``[B, L, 3, H, D]``: the gradient of
     qkv comes back as one tensor."""
     if _eager.eager(qkv):

@@ -152,14 +152,19 @@ typedef struct dsa_fwd_args {
      ones are scaled by 65536 / (65536 - t); 0 turns dropout off.  The keep
      bits are a function of (b, h, i, j) and dropout_seed (Philox4x32-10;
      the counter layout is stated in deberta_amd/csrc/dsa_dropout.h), so
-     dsa_bwd, given the same arguments, regenerates the forward's mask.  The
-     logsumexp (lse) is that of the probabilities before dropout.  dsa_fwd
-     keeps the bits in its workspace (dsa_fwd_workspace_bytes counts them;
-     a dropout call without that workspace is refused), dsa_bwd in its own
-     (dsa_bwd_workspace_bytes); dsa_fwd_static refuses dropout and dsa_bias
-     ignores it.  (Version 9.) */
+     dsa_bwd, given the same arguments, reproduces the forward's mask.  The
+     logsumexp (lse) is that of the probabilities before dropout.
+     dsa_fwd_static refuses dropout and dsa_bias ignores it.  (Version 9.) */
   uint32_t dropout_threshold;
   uint64_t dropout_seed;
+  /* Optional keep bits of the call, dsa_fwd_dropout_bytes(args) bytes,
+     16-byte aligned: dsa_fwd writes them here and dsa_bwd (given the same
+     pointer) reads them, so the backward generates nothing.  NULL: dsa_fwd
+     keeps them in its workspace (dsa_fwd_workspace_bytes then counts them;
+     a dropout call without that workspace is refused) and dsa_bwd
+     regenerates them from the seed in its own (dsa_bwd_workspace_bytes
+     counts them).  (Version 10.) */
+  void* dropout_bits;
 } dsa_fwd_args;
 
 typedef struct dsa_bwd_args {
@@ -243,6 +248,10 @@ size_t dsa_bwd_workspace_bytes(const dsa_bwd_args* args);
  * terms alive for autograd instead. */
 size_t dsa_fwd_bias_bytes(const dsa_fwd_args* args);
 
+/* Bytes of dsa_fwd_args.dropout_bits for these arguments (0 without
+ * dropout).  No counterpart in the reference, whose nn.Dropout keeps its
+ * mask in autograd's saved tensors. */
+size_t dsa_fwd_dropout_bytes(const dsa_fwd_args* args);
 /* Bytes of dsa_fwd_args.workspace for these arguments: the heaviest-first
  * launch order under key_keep or seg, then the k-step copies of kr / qr with
  * c2p / p2c (0 without either).  No counterpart in the reference, whose

@@ -156,7 +156,7 @@ def hip_run(c: Case, x: dict, dtype: torch.dtype, device, grads: bool = True) ->
     sf = 1 + sum(t in types for t in ("c2p", "p2c", "p2p"))
     scale = 1.0 / math.sqrt(c.D * sf)
     seed = torch.tensor([c.drop_seed], dtype=torch.int64) if c.drop_t else None
-    out, lse, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, kk, pk, c.A, scale, True, None, c.drop_t, seed)
+    out, lse, _, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, kk, pk, c.A, scale, True, None, c.drop_t, seed)
     res = {"out": out.detach().float().cpu(), "lse": lse.detach().cpu()}
     if grads:
         dout = x["dout"].to(device=device, dtype=dtype)

@@ -168,7 +168,7 @@ def test_fake_shapes():
 
     with FakeTensorMode():
         q, k, v, kr, qr, table = _inputs()
-        out, lse, bias = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, 16, 0.1)
+        out, lse, bias, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, 16, 0.1)
         assert out.shape == q.shape and out.dtype == q.dtype
         assert lse.shape == (2, 2, 64) and lse.dtype == torch.float32
         assert bias.shape == (2, 2, 128, 128) and bias.dtype == torch.float16
@@ -180,6 +180,10 @@ def test_fake_shapes():
         assert g[5].shape == q.shape
         b = torch.ops.deberta_amd.dsa_bias(q, k, kr, qr, table, 16, 0.1, None)
         assert b.shape == (2, 2, 64, 64) and b.dtype == q.dtype
+        # with attention dropout: the keep bits come back as a fourth output
+        seed = torch.tensor([7], dtype=torch.int64)
+        *_, bits = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, 16, 0.1, True, None, 6554, seed)
+        assert bits.shape == (2 * 2 * 4 * 2 * 64 * 4,) and bits.dtype == torch.uint8
 
 
 def test_trace_forward_and_backward_with_fake_tensors():
@@ -188,7 +192,7 @@ def test_trace_forward_and_backward_with_fake_tensors():
     from torch.fx.experimental.proxy_tensor import make_fx
 
     def f(q, k, v, kr, qr, table, dout):
-        out, _, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, 16, 0.1)
+        out, _, _, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, 16, 0.1)
         return torch.autograd.grad(out, (q, k, v, kr, qr), dout)
 
     q, k, v, kr, qr, table = _inputs()
@@ -598,3 +602,17 @@ def test_dropout_argument_errors(lib):
     s1 = ops.draw_dropout_seed()
     torch.manual_seed(5)
     assert torch.equal(s1, ops.draw_dropout_seed())
+
+
+def test_dropout_bytes_match_the_library(lib):
+    """The package's size of the keep bits (fake implementations use it)
+    equals the library's dsa_fwd_dropout_bytes."""
+    for B, H, Lq, Lk in ((1, 1, 1, 1), (2, 3, 200, 200), (4, 12, 4096, 4096), (2, 2, 64, 300)):
+        a = _lib.DsaFwdArgs()
+        a.B, a.H, a.Lq, a.Lk, a.D, a.dtype = B, H, Lq, Lk, 64, _lib.DSA_BF16
+        a.dropout_threshold = 6554
+        q = torch.empty(B, Lq, H, 64, device="meta")
+        k = torch.empty(B, Lk, H, 64, device="meta")
+        assert lib.dsa_fwd_dropout_bytes(ctypes.byref(a)) == ops.dropout_bytes(q, k, 6554)
+        a.dropout_threshold = 0
+        assert lib.dsa_fwd_dropout_bytes(ctypes.byref(a)) == 0 == ops.dropout_bytes(q, k, 0)

@@ -212,7 +212,7 @@ def test_backward_stages_in_separate_calls(split, gpu):
     kr, qr = mk(H, 2 * A, D), mk(H, 2 * A, D)
     table = relative_offset_table(L, L, bucket_size=256, max_position=512, device=gpu)
     scale = 1 / math.sqrt(D * 3)
-    out, lse, bias = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, A, scale)
+    out, lse, bias, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, A, scale)
     stream = ctypes.c_void_p(torch.cuda.current_stream(gpu).cuda_stream)
     bits = {"PREP": _lib.DSA_STAGE_PREP, "DQ": _lib.DSA_STAGE_DQ, "DKDV": _lib.DSA_STAGE_DKDV,
             "FOLD": _lib.DSA_STAGE_FOLD, "TABLE": _lib.DSA_STAGE_TABLE, "SUM": _lib.DSA_STAGE_SUM}
@@ -347,7 +347,7 @@ def test_all_kept_key_mask_runs_as_no_mask(gpu):
 
     def run(kkm):
         leaves = [t.detach().clone().requires_grad_(True) for t in (q, k, v, kr, qr)]
-        out, _, _ = torch.ops.deberta_amd.dsa_fwd(*leaves, table, kkm, None, A, 1 / math.sqrt(3 * D))
+        out, _, _, _ = torch.ops.deberta_amd.dsa_fwd(*leaves, table, kkm, None, A, 1 / math.sqrt(3 * D))
         return [out] + list(torch.autograd.grad(out, leaves, dout))
 
     # the key-mask kernels on the all-kept mask give the unmasked results
@@ -387,9 +387,9 @@ def test_packed_qkv_op_equals_separate_op(types, gpu):
         q, k, v = qkv.unbind(2)
         krx, qrx, qc = relative_operands(tl, q, kr, qr, A)
         if packed:
-            out, _, _ = ops.attention_packed(qkv, krx, qrx, table, None, None, A, scale, True, qc)
+            out, _, _, _ = ops.attention_packed(qkv, krx, qrx, table, None, None, A, scale, True, qc)
         else:
-            out, _, _ = ops.attention(q, k, v, krx, qrx, table, None, None, A, scale, True, qc)
+            out, _, _, _ = ops.attention(q, k, v, krx, qrx, table, None, None, A, scale, True, qc)
         return [out] + list(torch.autograd.grad(out, [qkv, kr, qr], dout))
 
     _say(f"[packed] {types}")

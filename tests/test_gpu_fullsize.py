@@ -51,7 +51,7 @@ def _run(q, k, v, kr, qr, dout, mask):
     leaves = [t.detach().clone().requires_grad_(True) for t in (q, k, v, kr, qr)]
     table = relative_offset_table(L, L, bucket_size=256, max_position=512, device=dev)
     kk, pk = kernel_masks(mask, B, L, L, dev) if mask is not None else (None, None)
-    out, _, _ = torch.ops.deberta_amd.dsa_fwd(*leaves, table, kk, pk, A, 1.0 / math.sqrt(3 * D))
+    out, _, _, _ = torch.ops.deberta_amd.dsa_fwd(*leaves, table, kk, pk, A, 1.0 / math.sqrt(3 * D))
     grads = torch.autograd.grad(out, leaves, dout)
     return [out.detach().float()] + [g.float() for g in grads]
 

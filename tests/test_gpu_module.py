@@ -166,7 +166,7 @@ def test_full_headline_shape_batch_consistency(gpu):
     def run(sl):
         ls = [t[sl].detach().clone().requires_grad_(True) for t in (q, k, v)]
         lr = [t.detach().clone().requires_grad_(True) for t in (kr, qr)]
-        out, lse, _ = torch.ops.deberta_amd.dsa_fwd(*ls, *lr, table, None, None, A, scale)
+        out, lse, _, _ = torch.ops.deberta_amd.dsa_fwd(*ls, *lr, table, None, None, A, scale)
         gr = torch.autograd.grad(out, ls + lr, dO[sl])
         return out, lse, gr
 

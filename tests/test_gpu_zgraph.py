@@ -37,7 +37,7 @@ def test_graph_capture_replays_match_eager(gpu):
     leaves = [q, k, v, kr, qr]
 
     def step():
-        out, _, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, A, scale)
+        out, _, _, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, A, scale)
         return [out] + list(torch.autograd.grad(out, leaves, dout))
 
     ref = [t.clone() for t in step()]  # eager
