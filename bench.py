@@ -122,6 +122,47 @@ def mfma_peak_probe(dev) -> dict:
     return {"tflops": round(flops / (best * 1e-3) / 1e12, 1), "cus": cus, "workgroups": wgs, "ms": round(best, 4)}
 
 
+def dsfree_flush_probe(dev, B: int, H: int, L: int) -> dict:
+    """Time of the fp32 atomic traffic that a backward without its dS
+    workspace would make to reduce the relative-table gradients over the
+    batch (libdsa_probe.so: one workgroup per (b, h, 128-key tile) adding
+    one 64-float row per offset its keys meet and per kind, after summing
+    its four waves), beside the bytes of dS's own round trip."""
+    import ctypes
+
+    import torch
+
+    from deberta_amd._build import PROBE_PATH
+
+    lib = ctypes.CDLL(str(PROBE_PATH))
+    lib.dsa_probe_dsfree_flush.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    lib.dsa_probe_dsfree_flush.restype = ctypes.c_int
+    acc = torch.zeros(H * 2 * 2 * L * 64, dtype=torch.float32, device=dev)
+    st = torch.cuda.current_stream(dev)
+    run = lambda: lib.dsa_probe_dsfree_flush(B, H, L, ctypes.c_void_p(acc.data_ptr()), ctypes.c_void_p(st.cuda_stream))
+    for _ in range(3):
+        if run():
+            raise RuntimeError("atomics probe launch failed")
+    ms = []
+    for _ in range(10):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(st)
+        run()
+        b.record(st)
+        torch.cuda.synchronize(dev)
+        ms.append(a.elapsed_time(b))
+    ms.sort()
+    nbytes = B * H * (L // 128) * 2 * (L + 127) * 256
+    med = ms[len(ms) // 2]
+    return {
+        "workload": f"B={B} H={H} L={L}",
+        "atomic_bytes": nbytes,
+        "ms_median": round(med, 4),
+        "tb_per_s": round(nbytes / (med * 1e-3) / 1e12, 3),
+        "ds_round_trip_bytes": B * H * L * L * 2 * 2,
+    }
+
+
 class HipEvents:
     """HIP timing events without the system-scope fence (the runtime's
     hipEventDisableSystemFence flag): torch's events write back and
@@ -482,6 +523,11 @@ def main() -> None:
         help="only run each kernel --steps times (for rocprofv3 counter passes); prints per-kernel times",
     )
     ap.add_argument(
+        "--atomics-probe",
+        action="store_true",
+        help="only time the fp32 atomic flush a backward without dS would make at the workload's shape, and exit",
+    )
+    ap.add_argument(
         "--copy-probe-mib",
         type=int,
         default=0,
@@ -513,6 +559,9 @@ def main() -> None:
     lib = _lib.load()
     dev = torch.device("cuda:0")
     B, L, H, mask_kind, wl_desc = WORKLOADS[args.workload]
+    if args.atomics_probe:
+        print(json.dumps({"dsfree_flush_probe": dsfree_flush_probe(dev, B, H, L)}), flush=True)
+        return
     headline = args.workload == "headline" and not args.dropout
     drop_t = ops.dropout_threshold(args.dropout) if args.dropout > 0 else 0
     if args.dropout > 0 and not 0 < drop_t < 65536:

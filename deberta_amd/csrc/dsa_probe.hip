@@ -38,7 +38,38 @@ __global__ __launch_bounds__(256) void mfma_bf16_probe(float* sink, int iters) {
   sink[(size_t)blockIdx.x * 256 + threadIdx.x] = s;
 }
 
+// The table-gradient traffic a backward without a dS workspace would make:
+// one workgroup per (b, h, 128-key tile), which meets the L + 127 offsets
+// d = i - j of its keys and all L queries, adds one fp32 row of 64 values
+// (D = 64) per offset and per kind (c2p, p2c) into per-head accumulators
+// [H][2][nrows][64] (row d + LkP - 1), after summing its four waves:
+// global_atomic_add_f32, one row of 64 consecutive floats per wave
+// instruction.  The added values are ones (the rate, not the sums, is
+// measured).
+__global__ __launch_bounds__(256) void dsfree_flush_probe(float* acc, int H, int NKT, int L, int nrows) {
+  const int w = blockIdx.x;
+  const int kt = w % NKT, h = (w / NKT) % H;
+  const int d_lo = -(kt * 128 + 127), n = L + 127;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int LkP = NKT * 128;
+  for (int kind = 0; kind < 2; ++kind) {
+    float* base = acc + (size_t)(h * 2 + kind) * nrows * 64;
+    for (int r = wave; r < n; r += 4) {
+      const int row = d_lo + r + LkP - 1;
+      if (row >= 0 && row < nrows) unsafeAtomicAdd(base + (size_t)row * 64 + lane, 1.0f);
+    }
+  }
+}
+
 }  // namespace
+
+extern "C" int dsa_probe_dsfree_flush(int B, int H, int L, float* acc, void* stream) {
+  if (B < 1 || H < 1 || L < 1 || L % 128 || !acc) return 1;
+  const int NKT = L / 128;
+  hipLaunchKernelGGL(dsfree_flush_probe, dim3((unsigned)(B * H * NKT)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     acc, H, NKT, L, 2 * L);
+  return hipGetLastError() == hipSuccess ? 0 : 1;
+}
 
 extern "C" int dsa_probe_mfma_bf16(int workgroups, int iters, float* sink, void* stream) {
   if (workgroups < 1 || iters < 1 || !sink) return 1;

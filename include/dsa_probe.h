@@ -22,6 +22,16 @@ extern "C" {
  * workgroups * 4 * iters * 4 * 32768. */
 int dsa_probe_mfma_bf16(int workgroups, int iters, float* sink, void* stream);
 
+/* The fp32 atomic traffic that a backward without its dS workspace would
+ * make to reduce the relative-table gradients over the batch: B * H * L / 128
+ * workgroups, one per (b, h, 128-key tile), each adding one row of 64 floats
+ * per kind (2) and per offset its keys meet (L + 127 of them) into
+ * `acc`, device memory of H * 2 * (2 L) * 64 floats (zero it first; every
+ * element receives a count of ones).  L a multiple of 128.  Bytes added:
+ * B * H * (L / 128) * 2 * (L + 127) * 256.  Returns 0, or nonzero for bad
+ * arguments or a failed launch.  No counterpart in the reference. */
+int dsa_probe_dsfree_flush(int B, int H, int L, float* acc, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
