@@ -100,6 +100,16 @@ def table_for(
     return table
 
 
+# The kernels' forms: element types and head dims (anything else runs the
+# torch path, as the reference runs every dtype and head dim)
+_KERNEL_DTYPES = (torch.float32, torch.bfloat16)
+_KERNEL_HEAD_DIMS = (32, 64)
+
+
+def _kernel_form(t: torch.Tensor, head_dim: int) -> bool:
+    return t.device.type == "cuda" and t.dtype in _KERNEL_DTYPES and int(head_dim) in _KERNEL_HEAD_DIMS
+
+
 def _require_gpu(t: torch.Tensor) -> None:
     if t.device.type != "cuda":
         raise RuntimeError(
@@ -285,10 +295,11 @@ def disentangled_attention(
     scale = 1.0 / math.sqrt(float(D * scale_factor))
     tables = [t for t in (pos_key_layer, pos_query_layer) if t is not None]
     att_span = tables[0].shape[1] // 2 if tables else 1
-    in_kernels = dropout_p <= 0.0 or 0 < ops.dropout_threshold(dropout_p) < 65536
-    if q.device.type != "cuda" or not in_kernels:
-        # CPU tensors (and a dropout probability the kernels cannot draw):
-        # the same chain in torch operations (deberta_amd.unfused)
+    in_kernels = (dropout_p <= 0.0 or 0 < ops.dropout_threshold(dropout_p) < 65536) and _kernel_form(q, D)
+    if not in_kernels:
+        # CPU tensors, dtypes and head dims the kernels do not take, and a
+        # dropout probability they cannot draw: the same chain in torch
+        # operations (deberta_amd.unfused)
         rel_pos = None
         if any(t in types for t in ("c2p", "p2c", "p2p")):
             rel_pos = _relative_matrix(
@@ -452,10 +463,8 @@ class DisentangledSelfAttention(nn.Module):
         code (``deberta_amd::dsa_bias``), unmasked; forward only (training
         differentiates through ``forward``).  CPU tensors take the same
         terms in torch operations (``deberta_amd.unfused.relative_terms``)."""
-        if query_layer.device.type != "cuda":
+        if not _kernel_form(query_layer, query_layer.shape[-1]):
             return self._bias_unfused(query_layer, key_layer, relative_pos, rel_embeddings, scale_factor)
-        if query_layer.dtype not in (torch.float32, torch.bfloat16):
-            raise TypeError(f"disentangled_attention_bias: query dtype must be float32 or bfloat16, got {query_layer.dtype}")
         q = query_layer.transpose(1, 2)
         k = key_layer.to(q.dtype).transpose(1, 2)
         Lq, Lk = q.shape[1], k.shape[1]
@@ -464,7 +473,11 @@ class DisentangledSelfAttention(nn.Module):
         kr, qr, qc = relative_operands(self.pos_att_type, q, kr_full, qr_full, att_span)
         table = None
         if kr is not None or qr is not None:
-            table = table_for(relative_pos, Lq, Lk, self.position_buckets, self.max_relative_positions, q.device)
+            table = table_for(
+                relative_pos, Lq, Lk, self.position_buckets, self.max_relative_positions, q.device, strict=False
+            )
+            if table is None:  # not a function of i - j: used as given
+                return self._bias_unfused(query_layer, key_layer, relative_pos, rel_embeddings, scale_factor)
         scale = 1.0 / math.sqrt(float(self.attention_head_size * int(scale_factor)))
         return torch.ops.deberta_amd.dsa_bias(q, k, kr, qr, table, att_span, scale, qc)
 
@@ -476,7 +489,8 @@ class DisentangledSelfAttention(nn.Module):
         rel_embeddings: torch.Tensor,
         scale_factor: int,
     ) -> torch.Tensor:
-        """``disentangled_attention_bias`` in torch operations (CPU tensors)."""
+        """``disentangled_attention_bias`` in torch operations (CPU tensors,
+        other dtypes and head dims, a ``relative_pos`` used as given)."""
         Lq, Lk = query_layer.shape[2], key_layer.shape[2]
         kr, qr = self._relative_tables(rel_embeddings, query_layer.dtype)
         rel_pos = None
@@ -506,21 +520,22 @@ class DisentangledSelfAttention(nn.Module):
 
         The fused kernels run the call, attention dropout in training
         included (the kernels draw the keep bits, ``deberta_amd.ops``),
-        unless it is on CPU tensors or needs the probabilities themselves
-        (``output_attentions=True``), its ``relative_pos`` does not depend
-        on ``i - j`` alone, or its dropout probability has no kernel form
-        (below 2^-17 or above 1 - 2^-17); those run the same chain in torch
+        unless it is on CPU tensors, in a dtype other than float32 /
+        bfloat16 or with a head dim other than 32 / 64, needs the
+        probabilities themselves (``output_attentions=True``), its
+        ``relative_pos`` does not depend on ``i - j`` alone, or its dropout
+        probability has no kernel form (below 2^-17 or above 1 - 2^-17);
+        those run the same chain in torch
         operations on the tensors' device (``deberta_amd.unfused``, with
         torch's dropout) and return the probabilities when asked.
         """
-        on_gpu = hidden_states.device.type == "cuda"
         drop_p = float(self.dropout.p) if self.training else 0.0
         drop_in_kernels = drop_p <= 0.0 or 0 < ops.dropout_threshold(drop_p) < 65536
-        unfused = (not on_gpu) or output_attentions or not drop_in_kernels
 
         q, k, v, qkv = self._project_qkv(hidden_states, query_states)
         model_dtype = hidden_states.dtype
         ref = qkv if qkv is not None else q  # dtype and device of the layers
+        unfused = (not _kernel_form(ref, self.attention_head_size)) or output_attentions or not drop_in_kernels
         Lq = ref.shape[1]
         Lk = Lq if qkv is not None else k.shape[1]
 

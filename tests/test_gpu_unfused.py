@@ -162,3 +162,96 @@ def test_attention_dropout_in_training(gpu):
     assert max_rel(out.detach(), want.detach()) <= 1e-5
     (gx,) = torch.autograd.grad(out, (xx,), torch.ones_like(out))
     assert torch.isfinite(gx).all()
+
+
+def _plain_run(module, x, mask, rel, device, relative_pos=None):
+    """Output and gradients without output_attentions (the module decides
+    its path by itself)."""
+    x = x.to(device).detach().clone().requires_grad_(True)
+    rel = rel.to(device).detach().clone().requires_grad_(True)
+    m = mask.to(device) if mask is not None else None
+    rp = relative_pos.to(device) if relative_pos is not None else None
+    out, _ = module(x, m, relative_pos=rp, rel_embeddings=rel)
+    dout = torch.randn(out.shape, generator=torch.Generator().manual_seed(4)).to(device=device, dtype=out.dtype)
+    names = [n for n, _ in module.named_parameters()]
+    params = [p for _, p in module.named_parameters()]
+    grads = torch.autograd.grad(out, [x, rel] + params, dout, allow_unused=True)
+    res = {"out": out.detach().double().cpu(), "dx": grads[0].double().cpu(), "drel": grads[1].double().cpu()}
+    for n, gr in zip(names, grads[2:]):
+        res["d" + n] = torch.zeros(1) if gr is None else gr.double().cpu()
+    return res
+
+
+def test_head_dims_the_kernels_do_not_take_run_the_torch_path(gpu, monkeypatch):
+    """The reference's own test shape (hidden 32, 4 heads, head dim 8) and
+    head dim 128 on the GPU: the module runs the torch path (the kernels are
+    switched off for the test) and matches the oracle module (fp32)."""
+    import deberta_amd.attention as att
+
+    def _no_kernels(*a, **k):
+        raise AssertionError("the kernels ran")
+
+    monkeypatch.setattr(att, "fused_attention", _no_kernels)
+    for hidden, heads in ((32, 4), (256, 2)):
+        cfg = eager.make_config(hidden_size=hidden, num_attention_heads=heads, position_buckets=32,
+                                max_relative_positions=64)
+        ref, ours = _pair(cfg)
+        ours = ours.to(gpu)
+        g = torch.Generator().manual_seed(hidden)
+        x = torch.randn(2, 40, hidden, generator=g)
+        rel = torch.randn(64, hidden, generator=g) * 0.02
+        keep = torch.ones(2, 40, dtype=torch.bool)
+        keep[1, 29:] = False
+        m = keep[:, None, None, :]
+        a = _plain_run(ref, x, m, rel, "cpu")
+        b = _plain_run(ours, x, m, rel, gpu)
+        errs = _errors(a, b)
+        _say(f"[head dim {hidden // heads}] {errs}")
+        assert all(e <= 1e-4 for e in errs.values()), errs
+
+
+def test_float16_runs_the_torch_path(gpu, monkeypatch):
+    """A float16 module on the GPU (the kernels take float32 and bfloat16):
+    the torch path, against the oracle in float32 on the float16-rounded
+    weights and inputs; output and input gradient to 2e-2 absolute."""
+    import deberta_amd.attention as att
+
+    def _no_kernels(*a, **k):
+        raise AssertionError("the kernels ran")
+
+    monkeypatch.setattr(att, "fused_attention", _no_kernels)
+    ref, ours = _pair(_cfg())
+    with torch.no_grad():
+        for p_ in ref.parameters():
+            p_.copy_(p_.half().float())
+    ours.load_state_dict(ref.state_dict())
+    ours = ours.to(gpu).half()
+    x, rel = _inputs(seed=5)
+    x, rel = x.half().float(), rel.half().float()
+    a = _plain_run(ref, x, None, rel, "cpu")
+    b = _plain_run(ours, x.half(), None, rel.half(), gpu)
+    errs = {k: max_abs(b[k], a[k]) for k in ("out", "dx")}
+    _say(f"[float16 module] {errs}")
+    assert all(e <= 2e-2 for e in errs.values()), errs
+
+
+def test_bias_api_with_a_matrix_used_as_given(gpu):
+    """disentangled_attention_bias with a relative_pos that is not a function
+    of i - j (the reference uses it as given) on the GPU equals the oracle's
+    relative term (fp32, 1e-5 of scale)."""
+    cfg = _cfg(pos_att_type="c2p|p2c")
+    ref, ours = _pair(cfg)
+    ours = ours.to(gpu)
+    g = torch.Generator().manual_seed(6)
+    B, H, L, D = 2, 4, 48, 32
+    q, k = (torch.randn(B, H, L, D, generator=g) for _ in range(2))
+    rel = torch.randn(64, 128, generator=g) * 0.02
+    rp = eager.relative_positions(L, L, 32, 64).clone()
+    rp[5, 7] += 3  # no longer Toeplitz
+    got = ours.disentangled_attention_bias(q.to(gpu), k.to(gpu), rp.to(gpu), rel.to(gpu), 3)
+    kr = ref.project_rel(rel, use_query=False)
+    qr = ref.project_rel(rel, use_query=True)
+    want = eager.relative_bias(q, k, kr, qr, eager.canonical_rel(rp, L, L, 32, 64), 32, ["c2p", "p2c"], 3, D, "einsum")
+    err = max_rel(got.float().cpu(), want)
+    _say(f"[bias api, matrix as given] {err:.2e}")
+    assert err <= 1e-5
