@@ -47,6 +47,7 @@ WORKLOADS = {
     "C5layer": (64, 512, 16, None, "DeBERTa-v3-large-shaped attention layer (hidden 1024, projections included) fwd+bwd, bf16, inside torch.compile"),
     "C4": (4, 4096, 12, "doc", "B=4 L=4096 H=12, packed documents (lengths ~Geometric(mean 600)) as the dense (B,1,L,L) doc-block mask (recognised once and run as segment ids)"),
     "C4seg": (4, 4096, 12, "seg", "as C4, the same documents given as segment ids (SegmentMask)"),
+    "plain": (32, 512, 12, None, "headline shape without relative terms, beside torch's scaled_dot_product_attention (flash backend)"),
 }
 
 
@@ -343,6 +344,70 @@ def run_encoder(args) -> None:
     )
 
 
+def run_plain(args) -> None:
+    """The headline shape without relative terms (plain softmax attention,
+    scale 1/sqrt(D)): the op's forward and fwd+bwd beside torch's
+    scaled_dot_product_attention with the flash backend (bf16, (B, H, L, D)
+    contiguous inputs), each timed over 50 launches after 300 warm-up ones.
+    A reference figure for the kernels' attention machinery without the
+    disentangled terms, not the metric."""
+    import torch
+    import torch.nn.functional as F
+
+    import deberta_amd  # noqa: F401
+
+    dev = torch.device("cuda:0")
+    B, L, H, _, desc = WORKLOADS["plain"]
+    g = torch.Generator(device="cpu").manual_seed(0)
+    mk = lambda *s: torch.randn(*s, generator=g).to(device=dev, dtype=torch.bfloat16)
+    q, k, v, dout = (mk(B, L, H, D) for _ in range(4))
+    scale = 1.0 / math.sqrt(D)
+
+    def timed(fn, n=50):
+        for _ in range(300):
+            fn()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(n):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / n
+
+    leaves = [t.detach().clone().requires_grad_(True) for t in (q, k, v)]
+
+    def ours_step():
+        out, _, _, _ = torch.ops.deberta_amd.dsa_fwd(*leaves, None, None, None, None, None, 1, scale)
+        torch.autograd.grad(out, leaves, dout)
+
+    res = {
+        "ours_fwd_ms": timed(lambda: torch.ops.deberta_amd.dsa_fwd(q, k, v, None, None, None, None, None, 1, scale)),
+        "ours_fwd_bwd_ms": timed(ours_step),
+    }
+    qh, kh, vh, dh = (t.permute(0, 2, 1, 3).contiguous() for t in (q, k, v, dout))
+    sl = [t.detach().clone().requires_grad_(True) for t in (qh, kh, vh)]
+    flash = torch.nn.attention.SDPBackend.FLASH_ATTENTION
+
+    def sdpa_fwd():
+        with torch.nn.attention.sdpa_kernel(flash):
+            return F.scaled_dot_product_attention(qh, kh, vh)
+
+    def sdpa_step():
+        with torch.nn.attention.sdpa_kernel(flash):
+            o = F.scaled_dot_product_attention(*sl)
+        torch.autograd.grad(o, sl, dh)
+
+    res["sdpa_flash_fwd_ms"] = timed(sdpa_fwd)
+    res["sdpa_flash_fwd_bwd_ms"] = timed(sdpa_step)
+    f = 4.0 * B * H * D * L * L  # QK^T and PV
+    out = {"workload": "plain", "description": desc}
+    for key, ms in res.items():
+        fl = 3 * f if "bwd" in key else f
+        out[key] = round(ms, 4)
+        out[key.replace("_ms", "_tflops")] = round(fl / (ms * 1e-3) / 1e12, 1)
+    print(json.dumps(out), flush=True)
+
+
 def run_compiled_layer(args) -> None:
     """C5 as BASELINE states it: one DeBERTa-v3-large-shaped attention
     layer (hidden 1024, 16 heads x 64, relative projections shared with the
@@ -547,6 +612,9 @@ def main() -> None:
         return
     if args.workload == "C5layer":
         run_compiled_layer(args)
+        return
+    if args.workload == "plain":
+        run_plain(args)
         return
 
     import torch
