@@ -48,6 +48,7 @@ WORKLOADS = {
     "C4": (4, 4096, 12, "doc", "B=4 L=4096 H=12, packed documents (lengths ~Geometric(mean 600)) as the dense (B,1,L,L) doc-block mask (recognised once and run as segment ids)"),
     "C4seg": (4, 4096, 12, "seg", "as C4, the same documents given as segment ids (SegmentMask)"),
     "plain": (32, 512, 12, None, "headline shape without relative terms, beside torch's scaled_dot_product_attention (flash backend)"),
+    "eager": (32, 512, 12, None, "headline op fwd+bwd beside the reference's op chain in torch operations on the same GPU (deberta_amd.unfused: float32 scores and relative terms, gathers, softmax, value product)"),
 }
 
 
@@ -408,6 +409,63 @@ def run_plain(args) -> None:
     print(json.dumps(out), flush=True)
 
 
+def run_eager(args) -> None:
+    """The headline fwd+bwd of the fused op beside the same attention as the
+    reference computes it, in torch operations on the GPU (the package's
+    torch path, deberta_amd.unfused: the reference's score chain of
+    deberta_v2_native.py:592-652 with the dynamic bias of :349-432), both on
+    the same bf16 leaves (the fused op over 50 steps after 300 warm-up
+    ones, the eager chain over 20 after 10: each warm-up is over 0.1 s).  A
+    reference figure (the eager path's speed on this GPU), not the metric."""
+    import torch
+
+    import deberta_amd  # noqa: F401
+    from deberta_amd.relpos import build_relative_position, relative_offset_table
+    from deberta_amd.unfused import unfused_attention
+
+    dev = torch.device("cuda:0")
+    B, L, H, _, desc = WORKLOADS["eager"]
+    g = torch.Generator(device="cpu").manual_seed(0)
+    mk = lambda *s: torch.randn(*s, generator=g).to(device=dev, dtype=torch.bfloat16)
+    leaves = [mk(B, L, H, D) for _ in range(3)] + [mk(H, R, D) for _ in range(2)]
+    for t in leaves:
+        t.requires_grad_(True)
+    dout = mk(B, L, H, D)
+    scale = 1.0 / math.sqrt(D * 3)
+    table = relative_offset_table(L, L, bucket_size=BUCKETS, max_position=MAX_POS, device=dev)
+    rel_pos = build_relative_position(L, L, bucket_size=BUCKETS, max_position=MAX_POS, device=dev)
+
+    def fused_step():
+        out, _, _, _ = torch.ops.deberta_amd.dsa_fwd(*leaves, table, None, None, A, scale)
+        torch.autograd.grad(out, leaves, dout)
+
+    def eager_step():
+        out, _ = unfused_attention(*leaves, rel_pos, None, A, scale, ["c2p", "p2c"])
+        torch.autograd.grad(out, leaves, dout)
+
+    def timed(fn, warm, n):
+        for _ in range(warm):
+            fn()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(n):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / n
+
+    f = 3 * flops_fwd(B, L, H, D, R)
+    res = {"workload": "eager", "description": desc}
+    # warm-up long enough (over 0.1 s) for the clocks to settle under either
+    for name, fn, warm, n in (("fused", fused_step, 300, 50), ("eager_torch_ops", eager_step, 10, 20)):
+        ms = timed(fn, warm, n)
+        res[name + "_ms"] = round(ms, 4)
+        res[name + "_tflops"] = round(f / (ms * 1e-3) / 1e12, 1)
+    res["speedup"] = round(res["eager_torch_ops_ms"] / res["fused_ms"], 2)
+    res["eager_peak_mem_gib"] = round(torch.cuda.max_memory_allocated(dev) / 2**30, 1)
+    print(json.dumps(res), flush=True)
+
+
 def run_compiled_layer(args) -> None:
     """C5 as BASELINE states it: one DeBERTa-v3-large-shaped attention
     layer (hidden 1024, 16 heads x 64, relative projections shared with the
@@ -615,6 +673,9 @@ def main() -> None:
         return
     if args.workload == "plain":
         run_plain(args)
+        return
+    if args.workload == "eager":
+        run_eager(args)
         return
 
     import torch
