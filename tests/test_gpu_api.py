@@ -344,6 +344,12 @@ def test_all_kept_key_mask_runs_as_no_mask(gpu):
     assert kernel_masks(ones, B, L, L, gpu) == (None, None)
     kk, _ = kernel_masks(holes, B, L, L, gpu)
     assert kk is not None and int(kk.sum()) == B * L - 1
+    # an integer mask handed over directly (as the reference's callers may):
+    # the check is kept on the caller's tensor, not on its boolean copy
+    ones_int = torch.ones(B, 1, 1, L, dtype=torch.int64, device=gpu)
+    kernel_masks(ones_int, B, L, L, gpu)
+    torch.cuda.synchronize(gpu)
+    assert kernel_masks(ones_int, B, L, L, gpu) == (None, None)
 
     def run(kkm):
         leaves = [t.detach().clone().requires_grad_(True) for t in (q, k, v, kr, qr)]
