@@ -52,6 +52,9 @@ WORKLOADS = {
 }
 
 
+# untimed op steps between the per-kernel timing and the W warm-up steps
+SETTLE_STEPS = 100
+
 # HBM bytes per launch at this workload come from the committed rocprofv3
 # summary of this build's kernels (two --pmc passes over `bench.py
 # --kernels-only`, FETCH_SIZE then WRITE_SIZE in KiB per dispatch, each
@@ -841,24 +844,36 @@ def main() -> None:
     # GPU under sustained load for about 30 ms: its clocks take some 80 steps
     # to settle after a process starts (0.52 ms a step over the first 20, 0.44
     # from the 80th on), so the W warm-up steps alone would time the ramp when
-    # W is small.  The timed region itself is exactly W untimed and K timed
-    # fwd+bwd steps of the op.
+    # W is small.  The op's own first steps after the stage calls still ran
+    # slower (with the driver's --warmup 5, the K = 20 steps after them
+    # averaged 0.443 ms against 0.427 for the next 20 on one box), so
+    # SETTLE_STEPS untimed steps of the op come first, whatever W is: then W
+    # untimed warm-up steps and exactly K timed fwd+bwd steps of the op.
     ms_step = wall = ms_median = ms_p10 = ms_p90 = float("nan")
-    for _ in range(args.warmup):
+    for _ in range(SETTLE_STEPS + args.warmup):
         step()
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    # an event between consecutive steps: per-step times for the median
-    # and p10 / p90, and their span for the mean over exactly K steps
     sp = torch.cuda.current_stream(dev).cuda_stream
+    # The timed region: exactly K steps between two events (an event between
+    # steps is itself a few microseconds of queue work: 4.4 us a step in a
+    # kernel trace, the only gap between the step's kernels).
+    t0 = time.perf_counter()
+    ev2 = HipEvents(2)
+    ev2.record(0, sp)
+    for _ in range(args.steps):
+        step()
+    ev2.record(1, sp)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = ev2.ms(0, 1) / args.steps
+    # Then K more steps with an event between consecutive ones: per-step
+    # times for the median and p10 / p90.
     evs = HipEvents(args.steps + 1)
     evs.record(0, sp)
     for n_ in range(args.steps):
         step()
         evs.record(n_ + 1, sp)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_step = evs.ms(0, args.steps) / args.steps
     per_step = sorted(evs.ms(n_, n_ + 1) for n_ in range(args.steps))
     pct = lambda f: per_step[min(len(per_step) - 1, int(round(f * (len(per_step) - 1))))]
     ms_median, ms_p10, ms_p90 = pct(0.5), pct(0.1), pct(0.9)
