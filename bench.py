@@ -254,6 +254,7 @@ def run_encoder(args) -> None:
     import torch
 
     import deberta_amd
+    from deberta_amd import ops
     from deberta_amd.relpos import relative_offset_table
     # The encoder is test code shared with the C3 GPU tests; only this
     # workload imports it (tests/ resolves as a namespace package from the
@@ -325,7 +326,7 @@ def run_encoder(args) -> None:
     scale = 1.0 / math.sqrt(D * 3)
 
     def attn_step():
-        out, _, _, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, A, scale)
+        out, _, _, _ = ops.attention(q, k, v, kr, qr, table, None, None, A, scale)
         torch.autograd.grad(out, (q, k, v, kr, qr), dout)
 
     ms_attn = timed(attn_step, 10)
@@ -359,6 +360,7 @@ def run_plain(args) -> None:
     import torch.nn.functional as F
 
     import deberta_amd  # noqa: F401
+    from deberta_amd import ops
 
     dev = torch.device("cuda:0")
     B, L, H, _, desc = WORKLOADS["plain"]
@@ -381,11 +383,11 @@ def run_plain(args) -> None:
     leaves = [t.detach().clone().requires_grad_(True) for t in (q, k, v)]
 
     def ours_step():
-        out, _, _, _ = torch.ops.deberta_amd.dsa_fwd(*leaves, None, None, None, None, None, 1, scale)
+        out, _, _, _ = ops.attention(*leaves, None, None, None, None, None, 1, scale)
         torch.autograd.grad(out, leaves, dout)
 
     res = {
-        "ours_fwd_ms": timed(lambda: torch.ops.deberta_amd.dsa_fwd(q, k, v, None, None, None, None, None, 1, scale)),
+        "ours_fwd_ms": timed(lambda: ops.attention(q, k, v, None, None, None, None, None, 1, scale)),
         "ours_fwd_bwd_ms": timed(ours_step),
     }
     qh, kh, vh, dh = (t.permute(0, 2, 1, 3).contiguous() for t in (q, k, v, dout))
@@ -423,6 +425,7 @@ def run_eager(args) -> None:
     import torch
 
     import deberta_amd  # noqa: F401
+    from deberta_amd import ops
     from deberta_amd.relpos import build_relative_position, relative_offset_table
     from deberta_amd.unfused import unfused_attention
 
@@ -439,7 +442,7 @@ def run_eager(args) -> None:
     rel_pos = build_relative_position(L, L, bucket_size=BUCKETS, max_position=MAX_POS, device=dev)
 
     def fused_step():
-        out, _, _, _ = torch.ops.deberta_amd.dsa_fwd(*leaves, table, None, None, A, scale)
+        out, _, _, _ = ops.attention(*leaves, table, None, None, A, scale)
         torch.autograd.grad(out, leaves, dout)
 
     def eager_step():
@@ -713,7 +716,7 @@ def main() -> None:
 
     def step():
         seed = ops.draw_dropout_seed() if drop_t else None
-        out, _, _, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, kk, pk, A, scale, True, None, drop_t, seed)
+        out, _, _, _ = ops.attention(q, k, v, kr, qr, table, kk, pk, A, scale, True, None, drop_t, seed)
         return torch.autograd.grad(out, leaves, dout)
 
     if args.copy_probe_mib:
