@@ -545,28 +545,49 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(budget_s: float = 15.0) -> dict:
+def cpu_baseline(c2_runs: int = 3, slice_budget_s: float = 5.0) -> dict:
     """fp32 eager oracle fwd+bwd (the reference's op chain restated) on the
-    host's cores, on a bounded sample of the same workload: batch rows of
-    the headline shape, repeated for about budget_s seconds; the value is
-    the sample's algorithmic FLOPs over its total time."""
+    host's cores at the headline shape, B=32 whole: one warm-up step, then
+    the median of c2_runs timed steps (BASELINE configs[1] as its CPU
+    figure is specified).  Also reported: the rate over about slice_budget_s
+    seconds of 2-row slices of the same shape, whose tensors fit the host's
+    caches (several times the whole batch's rate: a slice rate is no
+    estimate of the full step)."""
     import torch
 
     from oracle import eager
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    g = torch.Generator().manual_seed(0)
-    b = 2
-    q, k, v = (torch.randn(b, H, L, D, generator=g, requires_grad=True) for _ in range(3))
-    kr, qr = (torch.randn(H, R, D, generator=g, requires_grad=True) for _ in range(2))
-    dout = torch.randn(b, H, L, D, generator=g)
     rel = eager.relative_positions(L, L, BUCKETS, MAX_POS)
 
-    def step():
-        ctx, _ = eager.attend(q, k, v, kr, qr, rel, None, types=["c2p", "p2c"], att_span=A)
-        torch.autograd.grad(ctx, (q, k, v, kr, qr), dout)
+    def make(b):
+        g = torch.Generator().manual_seed(0)
+        q, k, v = (torch.randn(b, H, L, D, generator=g, requires_grad=True) for _ in range(3))
+        kr, qr = (torch.randn(H, R, D, generator=g, requires_grad=True) for _ in range(2))
+        dout = torch.randn(b, H, L, D, generator=g)
 
+        def step():
+            ctx, _ = eager.attend(q, k, v, kr, qr, rel, None, types=["c2p", "p2c"], att_span=A)
+            torch.autograd.grad(ctx, (q, k, v, kr, qr), dout)
+
+        return step
+
+    step = make(B)
+    t0 = time.perf_counter()
+    step()  # warm-up
+    warm = time.perf_counter() - t0
+    ts = []
+    for _ in range(c2_runs):
+        t0 = time.perf_counter()
+        step()
+        ts.append(time.perf_counter() - t0)
+    del step
+    med = sorted(ts)[len(ts) // 2]
+    f_step = 3 * flops_fwd(B, L, H, D, R)
+
+    b = 2
+    step = make(b)
     step()  # warm-up
     runs = 0
     t0 = time.perf_counter()
@@ -574,18 +595,24 @@ def cpu_baseline(budget_s: float = 15.0) -> dict:
         step()
         runs += 1
         total = time.perf_counter() - t0
-        if total >= budget_s:
+        if total >= slice_budget_s:
             break
-    tflops = runs * 3 * flops_fwd(b, L, H, D, R) / total / 1e12
     c1 = c1_cpu_forward()
     return {
-        "value": round(tflops, 4),
+        "value": round(f_step / med / 1e12, 4),
         "unit": "TFLOP/s",
         "cores": cores,
         "kind": "port",
-        "sample": f"fp32 eager oracle fwd+bwd on {runs} x {b} batch rows of B={B} L={L} H={H} D={D} R={R} "
-        f"(no mask) = {runs * b / B:.1f} steps' worth in {total:.1f} s ({total / runs * 1e3:.1f} ms per run); "
-        f"CPU: {cpu_model()}",
+        "sample": f"fp32 eager oracle fwd+bwd at the headline shape B={B} L={L} H={H} D={D} R={R} (no mask): "
+        f"median of {c2_runs} steps after one warm-up step ({warm:.1f} s): "
+        + ", ".join(f"{t:.2f}" for t in ts)
+        + f" s; CPU: {cpu_model()}",
+        "ms_per_step": round(med * 1e3, 1),
+        "slices": {
+            "tflops": round(runs * 3 * flops_fwd(b, L, H, D, R) / total / 1e12, 4),
+            "sample": f"{runs} runs of {b} batch rows of the same shape in {total:.1f} s "
+            f"({total / runs * 1e3:.1f} ms per run)",
+        },
         "c1_forward": c1,
     }
 
