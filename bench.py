@@ -650,6 +650,38 @@ def c1_cpu_forward(runs: int = 20) -> dict:
             "sample": "BASELINE configs[0]: oracle module forward, fp32, B=2 L=128 H=4 D=32, median of 20"}
 
 
+def cpu_c4(q, k, v, kr, qr, dout, mask, table_l: int, f_dense: float, f_kept: float) -> dict:
+    """BASELINE configs[3] on the host: one fp32 eager-oracle fwd+bwd (no
+    warm-up: its (4, 12, 4096, 4096) fp32 tensors take about 18 GB) on the
+    workload's own inputs and dense document mask, all host cores."""
+    import torch
+
+    from oracle import eager
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    to_cpu = lambda t: t.detach().float().cpu()
+    heads = lambda t: to_cpu(t).permute(0, 2, 1, 3).contiguous().requires_grad_(True)
+    qc, kc, vc = heads(q), heads(k), heads(v)
+    krc, qrc = (to_cpu(t).requires_grad_(True) for t in (kr, qr))
+    doc = to_cpu(dout).permute(0, 2, 1, 3).contiguous()
+    keep = mask.cpu()
+    rel = eager.relative_positions(table_l, table_l, BUCKETS, MAX_POS)
+    t0 = time.perf_counter()
+    ctx, _ = eager.attend(qc, kc, vc, krc, qrc, rel, keep, types=["c2p", "p2c"], att_span=A)
+    torch.autograd.grad(ctx, (qc, kc, vc, krc, qrc), doc)
+    sec = time.perf_counter() - t0
+    return {
+        "s_per_step": round(sec, 2),
+        "tflops_dense_count": round(f_dense / sec / 1e12, 4),
+        "tflops_kept_pairs": round(f_kept / sec / 1e12, 4),
+        "cores": cores,
+        "kind": "port",
+        "sample": f"fp32 eager oracle fwd+bwd, one step (no warm-up), B={qc.shape[0]} L={table_l} H={qc.shape[1]} "
+        f"D={qc.shape[3]} with the dense document mask; CPU: {cpu_model()}",
+    }
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -682,6 +714,11 @@ def main() -> None:
         "--atomics-probe",
         action="store_true",
         help="only time the fp32 atomic flush a backward without dS would make at the workload's shape, and exit",
+    )
+    ap.add_argument(
+        "--cpu-c4",
+        action="store_true",
+        help="with --workload C4: also time one fp32 oracle fwd+bwd of the same step on the host (about 18 GB)",
     )
     ap.add_argument(
         "--copy-probe-mib",
@@ -924,6 +961,11 @@ def main() -> None:
                     "steps": args.steps,
                     "per_kernel": per_kernel,
                     "per_kernel_alone": per_kernel_alone,
+                    **(
+                        {"cpu_c4": cpu_c4(q, k, v, kr, qr, dout, mask, L, f_step, f_kept)}
+                        if args.cpu_c4 and args.workload == "C4"
+                        else {}
+                    ),
                 }
             ),
             flush=True,
