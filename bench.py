@@ -650,6 +650,62 @@ def c1_cpu_forward(runs: int = 20) -> dict:
             "sample": "BASELINE configs[0]: oracle module forward, fp32, B=2 L=128 H=4 D=32, median of 20"}
 
 
+def masked_figures(dev, names=("C2pad", "C4seg"), warmup: int = 100, steps: int = 20) -> dict:
+    """Step time of the masked BASELINE workloads, for the record of the
+    default run (reference figures, not the metric): each workload's inputs
+    and mask are drawn as `--workload NAME` draws them (so the figures agree
+    with those runs), then `warmup` untimed and `steps` timed fwd+bwd steps
+    of the op between two HIP events.  TFLOP/s are counted over kept pairs
+    and live rows."""
+    import torch
+
+    from deberta_amd import ops
+    from deberta_amd.masks import kernel_masks
+    from deberta_amd.relpos import relative_offset_table
+
+    res = {}
+    for name in names:
+        b, l, h, kind, _ = WORKLOADS[name]
+        g = torch.Generator(device="cpu").manual_seed(0)
+        mk = lambda *s: torch.randn(*s, generator=g).to(device=dev, dtype=torch.bfloat16)
+        q, k, v = mk(b, l, h, D), mk(b, l, h, D), mk(b, l, h, D)
+        kr, qr = mk(h, R, D), mk(h, R, D)
+        dout = mk(b, l, h, D)
+        leaves = (q, k, v, kr, qr)
+        for t in leaves:
+            t.requires_grad_(True)
+        table = relative_offset_table(l, l, bucket_size=BUCKETS, max_position=MAX_POS, device=dev)
+        scale = 1.0 / math.sqrt(D * 3)
+        mask, kept_pairs, live_rows = workload_mask(kind, b, l, g, dev)
+        kk, pk = kernel_masks(mask, b, l, l, dev)
+
+        def step():
+            out, _, _, _ = ops.attention(q, k, v, kr, qr, table, kk, pk, A, scale, True, None, 0, None)
+            return torch.autograd.grad(out, leaves, dout)
+
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        sp = torch.cuda.current_stream(dev).cuda_stream
+        ev = HipEvents(2)
+        ev.record(0, sp)
+        for _ in range(steps):
+            step()
+        ev.record(1, sp)
+        torch.cuda.synchronize()
+        ms = ev.ms(0, 1) / steps
+        f_kept = 3.0 * h * D * (4.0 * kept_pairs + 4.0 * R * live_rows)
+        res[name] = {
+            "ms_per_step": round(ms, 4),
+            "tflops_kept_pairs": round(f_kept / (ms * 1e-3) / 1e12, 2),
+            "kept_pair_fraction": round(kept_pairs / (b * l * l), 4),
+            "steps": steps,
+            "warmup": warmup,
+        }
+        del q, k, v, kr, qr, dout, mask, kk, pk, leaves
+    return res
+
+
 def cpu_c4(q, k, v, kr, qr, dout, mask, table_l: int, f_dense: float, f_kept: float) -> dict:
     """BASELINE configs[3] on the host: one fp32 eager-oracle fwd+bwd (no
     warm-up: its (4, 12, 4096, 4096) fp32 tensors take about 18 GB) on the
@@ -693,6 +749,11 @@ def main() -> None:
     # covers the ramp; the warm-up steps follow it.
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument(
+        "--no-masked",
+        action="store_true",
+        help="skip the short C2pad / C4seg step timings that follow the headline's timed steps",
+    )
     ap.add_argument(
         "--workload",
         choices=sorted(WORKLOADS),
@@ -1014,6 +1075,13 @@ def main() -> None:
         },
         "wall_s_timed": round(wall, 3),
     }
+    if not args.no_masked:
+        # after the headline's timed steps, so they cannot affect its figures;
+        # an error here is reported in the line rather than losing the line
+        try:
+            res["masked_workloads"] = masked_figures(dev)
+        except Exception as e:  # noqa: BLE001
+            res["masked_workloads"] = {"error": f"{type(e).__name__}: {e}"}
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline()
     print(json.dumps(res), flush=True)
