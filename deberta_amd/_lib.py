@@ -24,7 +24,7 @@ DSA_STAGE_FOLD = 8
 DSA_STAGE_TABLE = 16  # the first half of FOLD: per-offset sums (workspace)
 DSA_STAGE_SUM = 32  # the second half: their fold onto dkr / dqr
 
-EXPECTED_VERSION = 10
+EXPECTED_VERSION = 11
 
 _i64x3 = ctypes.c_int64 * 3
 _i64x2 = ctypes.c_int64 * 2
@@ -70,6 +70,7 @@ class DsaFwdArgs(ctypes.Structure):
         ("dropout_threshold", ctypes.c_uint32),
         ("dropout_seed", ctypes.c_uint64),
         ("dropout_bits", ctypes.c_void_p),
+        ("out_lo", ctypes.c_void_p),
     ]
 
 

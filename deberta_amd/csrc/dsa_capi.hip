@@ -89,6 +89,7 @@ int check_fwd(const dsa_fwd_args* a) {
   }
   if (a->dropout_threshold > 65535u)
     return fail("dsa: dropout_threshold must be in [0, 65535] (units of 1/65536), got %u", a->dropout_threshold);
+  if (a->dtype == DSA_BF16 && a->out_lo && !aligned16(a->out_lo)) return fail("dsa: out_lo must be 16-byte aligned");
   if (a->dropout_threshold && a->dropout_bits && !aligned16(a->dropout_bits))
     return fail("dsa: dropout_bits must be 16-byte aligned");
   if ((a->flags & DSA_C2P) && !a->kr) return fail("dsa: c2p needs the pos-key table kr");
@@ -171,6 +172,7 @@ dsa::FwdParams to_params(const dsa_fwd_args* a) {
   p.scale = a->scale;
   p.drop = nullptr;  // set where the keep bits are generated
   p.drop_scale = 1.f;
+  p.olo = a->dtype == DSA_BF16 ? a->out_lo : nullptr;
   return p;
 }
 
@@ -828,7 +830,7 @@ dsa::rows::RtdParams rtd_params(const dsa_rtd_args* a) {
 
 extern "C" {
 
-int dsa_version(void) { return 10; }
+int dsa_version(void) { return 11; }
 
 const char* dsa_last_error(void) { return g_err.c_str(); }
 

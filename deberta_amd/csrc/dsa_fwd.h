@@ -434,13 +434,23 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
     const float inv = ok ? (DROP ? p.drop_scale : 1.f) / lsum : 0.f;
     if (i < Lq) {
       T* orow = obase + (int64_t)i * p.os[1];
+      // bf16 with p.olo: also the rounding residual of each element, for
+      // the backward's row sums dO . O
+      T* lrow = (sizeof(T) == 2 && p.olo)
+                    ? (T*)p.olo + (int64_t)b * p.os[0] + (int64_t)h * p.os[2] + (int64_t)i * p.os[1]
+                    : nullptr;
 #pragma unroll
       for (int db = 0; db < ND; ++db) {
         typedef T vec4 __attribute__((ext_vector_type(4)));
-        vec4 v;
+        vec4 v, r;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = (T)(o[db][ib][e] * inv);
+        for (int e = 0; e < 4; ++e) {
+          const float f = o[db][ib][e] * inv;
+          v[e] = (T)f;
+          r[e] = (T)(f - (float)v[e]);
+        }
         *reinterpret_cast<vec4*>(orow + 16 * db + 4 * g) = v;
+        if (lrow) *reinterpret_cast<vec4*>(lrow + 16 * db + 4 * g) = r;
       }
       if (g == 0) p.lse[((int64_t)b * p.H + h) * Lq + i] = ok ? (mref[ib] * p.scale + logf(lsum)) : INFINITY;
     }

@@ -37,6 +37,7 @@ struct FwdParams {
   // kept probabilities, 65536 / (65536 - t); null without dropout
   const uint32_t* drop;
   float drop_scale;
+  void* olo;        // bf16 only: O's rounding residual, with out's strides, or null
 };
 
 struct BwdParams {

@@ -28,8 +28,13 @@ Tensor layouts (see include/dsa.h):
                     kept ones scaled by 65536 / (65536 - t); 0: no dropout
   dropout_seed      int64 CPU tensor of one element (or None without
                     dropout): the 64-bit seed of the keep bits
-  drop_bits         uint8 [dropout_bytes]: the keep bits dsa_fwd generated,
-                    saved for the backward (empty without dropout)
+  drop_bits         uint8 [aux_bytes]: what the forward leaves for the
+                    backward besides bias: the keep bits dsa_fwd generated
+                    (dropout_bytes; none without dropout), then, for bfloat16
+                    with the relative term saved and sequences longer than
+                    2 att_span, O's rounding residual (dsa_fwd_args.out_lo,
+                    bfloat16 [B, Lq, H, D] at a 256-byte aligned offset);
+                    empty when there is neither
 """
 
 from __future__ import annotations
@@ -116,6 +121,27 @@ def _seed_value(seed: Optional[Tensor], t: int) -> int:
     return int(seed.reshape(()).item()) & 0xFFFFFFFFFFFFFFFF
 
 
+def residual_wanted(q: Tensor, k: Tensor, relative: bool, att_span: int, save_bias: bool) -> bool:
+    """Whether the forward writes O's rounding residual for the backward's
+    row sums dO . O (``dsa_fwd_args.out_lo``): bfloat16, the relative term
+    saved (a backward will follow) and a sequence longer than 2 att_span,
+    where the table rows aggregate several offsets each and a row sum of
+    dKr / dQr can keep the per-row offset that a bf16-rounded O puts into
+    dS.  Up to that length (the benchmarked shape included) nothing is
+    written."""
+    return q.dtype == torch.bfloat16 and relative and save_bias and max(q.shape[1], k.shape[1]) > 2 * int(att_span)
+
+
+def aux_layout(q: Tensor, k: Tensor, dropout_t: int, residual: bool) -> tuple[int, int, int]:
+    """(keep-bit bytes, byte offset of O's residual, total bytes) of the
+    forward's fourth output."""
+    nd = dropout_bytes(q, k, dropout_t)
+    if not residual:
+        return nd, nd, nd
+    off = (nd + 255) // 256 * 256
+    return nd, off, off + q.shape[0] * q.shape[1] * q.shape[2] * q.shape[3] * 2
+
+
 def _check_threshold(t: int) -> None:
     if not 0 <= int(t) <= 65535:
         raise ValueError(f"dsa: dropout threshold must be in [0, 65535] (units of 1/65536), got {t}")
@@ -179,10 +205,18 @@ def _fill_fwd_args(
     _check_threshold(dropout_t)
     a.dropout_threshold = int(dropout_t)
     a.dropout_seed = _seed_value(dropout_seed, int(dropout_t))
-    if dropout_t and dropout_bits is not None and dropout_bits.numel():
-        if dropout_bits.numel() * dropout_bits.element_size() < dropout_bytes(q, k, dropout_t):
-            raise ValueError("dsa: dropout_bits is smaller than the call's keep bits")
-        a.dropout_bits = dropout_bits.data_ptr()
+    if dropout_bits is not None and dropout_bits.numel():
+        # the forward's fourth output: keep bits, then O's residual
+        residual = residual_wanted(q, k, a.flags != 0, att_span, a.bias is not None)
+        nd, lo_off, total = aux_layout(q, k, dropout_t, residual)
+        if dropout_bits.numel() * dropout_bits.element_size() < total:
+            raise ValueError("dsa: dropout_bits is smaller than the call's keep bits and O's residual")
+        if dropout_t and nd:
+            a.dropout_bits = dropout_bits.data_ptr()
+        if residual:
+            if not (out.is_contiguous() and out.dtype == torch.bfloat16):
+                raise ValueError("dsa: O's residual needs a contiguous bfloat16 out")
+            a.out_lo = dropout_bits.data_ptr() + lo_off
     return a
 
 
@@ -266,7 +300,8 @@ def _dsa_fwd_impl(
     needs it); else ``bias`` is empty.  ``qc``: the c2p term's query rows (q
     when None).  ``dropout_t`` / ``dropout_seed``: attention dropout (lse is
     that of the probabilities before dropout); its keep bits come back in
-    ``drop_bits`` for the backward (empty without dropout)."""
+    ``drop_bits`` for the backward, followed by O's rounding residual when
+    ``residual_wanted`` (empty when there is neither)."""
     _eager.refuse_capture("deberta_amd::dsa_fwd")
     _validate(q, k, v, kr, qr, rel_table, key_keep, pair_keep, att_span, qc)
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
@@ -280,7 +315,8 @@ def _dsa_fwd_impl(
         bias = torch.empty(bias_shape(q, k), dtype=bias_dtype(q.dtype), device=q.device)
     else:
         bias = torch.empty((0,), dtype=bias_dtype(q.dtype), device=q.device)
-    drop_bits = torch.empty((dropout_bytes(q, k, dropout_t),), dtype=torch.uint8, device=q.device)
+    residual = residual_wanted(q, k, kr is not None or qr is not None, att_span, save_bias)
+    drop_bits = torch.empty((aux_layout(q, k, dropout_t, residual)[2],), dtype=torch.uint8, device=q.device)
     args = _fill_fwd_args(
         q, k, v, kr, qr, rel_table, key_keep, pair_keep, out, lse, att_span, scale, bias, qc, dropout_t, dropout_seed,
         drop_bits,
@@ -320,7 +356,8 @@ def _dsa_fwd_fake(
         bias = q.new_empty(bias_shape(q, k), dtype=bias_dtype(q.dtype))
     else:
         bias = q.new_empty((0,), dtype=bias_dtype(q.dtype))
-    return out, lse, bias, q.new_empty((dropout_bytes(q, k, dropout_t),), dtype=torch.uint8)
+    residual = residual_wanted(q, k, kr is not None or qr is not None, att_span, save_bias)
+    return out, lse, bias, q.new_empty((aux_layout(q, k, dropout_t, residual)[2],), dtype=torch.uint8)
 
 
 def bwd_workspace_bytes(args: _lib.DsaBwdArgs) -> int:

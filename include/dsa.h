@@ -165,6 +165,17 @@ typedef struct dsa_fwd_args {
      regenerates them from the seed in its own (dsa_bwd_workspace_bytes
      counts them).  (Version 10.) */
   void* dropout_bits;
+  /* Optional, bf16 only: O's rounding residual, bf16(o - bf16(o)) for
+     every output element, written by dsa_fwd with out's strides (an
+     allocation of out's extent, 16-byte aligned).  dsa_bwd, given the same
+     pointer, takes the row sums dO . O of its preparation on bf16(o) plus
+     the residual instead of bf16(o) alone.  Rounding O to bf16 otherwise
+     offsets every dS element of a row alike (dS = P (dP - dO . O)), and a
+     table gradient that sums nearly all pairs of a row onto one table row
+     (few keys against many queries, narrow log buckets) keeps that offset
+     where the other sums cancel it.  NULL: no residual; ignored for fp32.
+     (Version 11.) */
+  void* out_lo;
 } dsa_fwd_args;
 
 typedef struct dsa_bwd_args {

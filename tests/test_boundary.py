@@ -180,10 +180,17 @@ def test_fake_shapes():
         assert g[5].shape == q.shape
         b = torch.ops.deberta_amd.dsa_bias(q, k, kr, qr, table, 16, 0.1, None)
         assert b.shape == (2, 2, 64, 64) and b.dtype == q.dtype
-        # with attention dropout: the keep bits come back as a fourth output
+        # with attention dropout: the keep bits come back as a fourth output,
+        # followed (bf16, L = 64 > 2 A = 32) by O's rounding residual at the
+        # next 256-byte boundary
         seed = torch.tensor([7], dtype=torch.int64)
         *_, bits = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, 16, 0.1, True, None, 6554, seed)
-        assert bits.shape == (2 * 2 * 4 * 2 * 64 * 4,) and bits.dtype == torch.uint8
+        assert bits.shape == (2 * 2 * 4 * 2 * 64 * 4 + q.numel() * 2,) and bits.dtype == torch.uint8
+        # neither without dropout and with L <= 2 A, nor without a saved term
+        assert torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, 32, 0.1)[3].shape == (0,)
+        assert torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, 16, 0.1, False)[3].shape == (0,)
+        # the residual alone
+        assert torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, None, None, 16, 0.1)[3].shape == (q.numel() * 2,)
 
 
 def test_trace_forward_and_backward_with_fake_tensors():
