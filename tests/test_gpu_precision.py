@@ -40,19 +40,35 @@ def _say(msg: str) -> None:
 
 def _reference_bf16(c: Case, x: dict) -> dict:
     """The oracle's op chain under CPU bf16 autocast on the bf16-rounded
-    inputs: the reference's own bf16 numerics."""
+    inputs (with the case's mask and dropout keep mask, as oracle_run
+    gives them): the reference's own bf16 numerics."""
+    types = c.type_list
     r = lambda t: t.to(torch.bfloat16).to(torch.float32).detach().clone().requires_grad_(True)
     q, k, v = (r(x[n]).permute(0, 2, 1, 3) for n in ("q", "k", "v"))
-    kr, qr = r(x["kr"]), r(x["qr"])
-    rel = eager.relative_positions(c.L, c.Lk or c.L, c.buckets, c.max_pos)
+    kr = r(x["kr"]) if "c2p" in types else None
+    qr = r(x["qr"]) if "p2c" in types else None
+    use_rel = kr is not None or qr is not None
+    Lk = c.Lk or c.L
+    rel = eager.relative_positions(c.L, Lk, c.buckets, c.max_pos) if use_rel else None
+    keep, p = None, 0.0
+    if c.drop_t:
+        from oracle.dropout import keep_mask
+
+        keep = torch.from_numpy(keep_mask(c.drop_seed, c.drop_t, c.B, c.H, c.L, Lk))
+        p = c.drop_t / 65536
     with torch.autocast("cpu", dtype=torch.bfloat16):
-        ctx, _ = eager.attend(q, k, v, kr, qr, rel, None, types=c.type_list, att_span=c.A)
+        ctx, _ = eager.attend(
+            q, k, v, kr, qr, rel, x["mask"], types=types, att_span=c.A, use_relative=use_rel, dropout_keep=keep,
+            dropout_p=p,
+        )
     dout = x["dout"].to(torch.bfloat16).float().permute(0, 2, 1, 3)
-    gs = torch.autograd.grad(ctx.float(), (q, k, v, kr, qr), dout)
+    leaves = [t for t in (q, k, v, kr, qr) if t is not None]
+    names = ["dq", "dk", "dv"] + (["dkr"] if kr is not None else []) + (["dqr"] if qr is not None else [])
+    gs = torch.autograd.grad(ctx.float(), leaves, dout, allow_unused=True)
     res = {"out": ctx.float().permute(0, 2, 1, 3).detach()}
-    for n, g in zip(("dq", "dk", "dv"), gs[:3]):
-        res[n] = g.permute(0, 2, 1, 3).detach()
-    res["dkr"], res["dqr"] = gs[3].detach(), gs[4].detach()
+    for n, g, t in zip(names, gs, leaves):
+        g = torch.zeros_like(t) if g is None else g.detach()
+        res[n] = g.permute(0, 2, 1, 3) if n in ("dq", "dk", "dv") else g
     return res
 
 
