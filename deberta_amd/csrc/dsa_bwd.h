@@ -56,8 +56,8 @@ DSA_DEV void prep_delta(const BwdParams& bp, int blk) {
 #pragma unroll
       for (int e = 0; e < VEC; ++e) acc += (float)ov[e] * (float)dv[e];
       if (sizeof(T) == 2 && p.olo) {
-        // O's rounding residual (the forward's p.olo, out's strides)
-        const T* lo = (const T*)p.olo + (int64_t)b * p.os[0] + (int64_t)i * p.os[1] + (int64_t)h * p.os[2];
+        // O's rounding residual (the forward's p.olo, with out's strides)
+        const T* lo = (const T*)((uintptr_t)o + ((uintptr_t)p.olo - (uintptr_t)p.out));
         const vecT lv = *reinterpret_cast<const vecT*>(lo + part * VEC);
 #pragma unroll
         for (int e = 0; e < VEC; ++e) acc += (float)lv[e] * (float)dv[e];

@@ -435,10 +435,9 @@ __global__ __launch_bounds__(256, 2) void dsa_fwd_kernel(FwdParams p) {
     if (i < Lq) {
       T* orow = obase + (int64_t)i * p.os[1];
       // bf16 with p.olo: also the rounding residual of each element, for
-      // the backward's row sums dO . O
-      T* lrow = (sizeof(T) == 2 && p.olo)
-                    ? (T*)p.olo + (int64_t)b * p.os[0] + (int64_t)h * p.os[2] + (int64_t)i * p.os[1]
-                    : nullptr;
+      // the backward's row sums dO . O (p.olo has out's strides: the same
+      // byte offset from its base)
+      T* lrow = (sizeof(T) == 2 && p.olo) ? (T*)((uintptr_t)orow + ((uintptr_t)p.olo - (uintptr_t)p.out)) : nullptr;
 #pragma unroll
       for (int db = 0; db < ND; ++db) {
         typedef T vec4 __attribute__((ext_vector_type(4)));
