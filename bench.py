@@ -53,7 +53,7 @@ WORKLOADS = {
 
 
 # untimed op steps between the per-kernel timing and the W warm-up steps
-SETTLE_STEPS = 100
+SETTLE_STEPS = 400
 
 # HBM bytes per launch at this workload come from the committed rocprofv3
 # summary of this build's kernels (two --pmc passes over `bench.py
