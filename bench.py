@@ -419,7 +419,8 @@ def run_eager(args) -> None:
     reference computes it, in torch operations on the GPU (the package's
     torch path, deberta_amd.unfused: the reference's score chain of
     deberta_v2_native.py:592-652 with the dynamic bias of :349-432), both on
-    the same bf16 leaves (the fused op over 50 steps after 300 warm-up
+    the same bf16 leaves, or float32 ones with --fp32 (the reference's
+    train.mixed_precision=no) (the fused op over 50 steps after 300 warm-up
     ones, the eager chain over 20 after 10: each warm-up is over 0.1 s).  A
     reference figure (the eager path's speed on this GPU), not the metric."""
     import torch
@@ -431,8 +432,10 @@ def run_eager(args) -> None:
 
     dev = torch.device("cuda:0")
     B, L, H, _, desc = WORKLOADS["eager"]
+    # --fp32: both in float32, the reference's train.mixed_precision=no
+    dtype = torch.float32 if args.fp32 else torch.bfloat16
     g = torch.Generator(device="cpu").manual_seed(0)
-    mk = lambda *s: torch.randn(*s, generator=g).to(device=dev, dtype=torch.bfloat16)
+    mk = lambda *s: torch.randn(*s, generator=g).to(device=dev, dtype=dtype)
     leaves = [mk(B, L, H, D) for _ in range(3)] + [mk(H, R, D) for _ in range(2)]
     for t in leaves:
         t.requires_grad_(True)
@@ -461,7 +464,7 @@ def run_eager(args) -> None:
         return a.elapsed_time(b) / n
 
     f = 3 * flops_fwd(B, L, H, D, R)
-    res = {"workload": "eager", "description": desc}
+    res = {"workload": "eager", "description": desc, "dtype": "fp32" if args.fp32 else "bf16"}
     # warm-up long enough (over 0.1 s) for the clocks to settle under either
     for name, fn, warm, n in (("fused", fused_step, 300, 50), ("eager_torch_ops", eager_step, 10, 20)):
         ms = timed(fn, warm, n)
@@ -775,6 +778,11 @@ def main() -> None:
         "--atomics-probe",
         action="store_true",
         help="only time the fp32 atomic flush a backward without dS would make at the workload's shape, and exit",
+    )
+    ap.add_argument(
+        "--fp32",
+        action="store_true",
+        help="with --workload eager: both sides in float32 (the reference's train.mixed_precision=no)",
     )
     ap.add_argument(
         "--cpu-c4",
