@@ -99,8 +99,8 @@ def oracle_run(c: Case, x: dict, dtype: torch.dtype, grads: bool = True) -> dict
     types = c.type_list
     r = lambda t: t.to(dtype).to(torch.float32).detach().clone().requires_grad_(grads)
     q, k, v = (r(x[n]).permute(0, 2, 1, 3) for n in ("q", "k", "v"))
-    kr = r(x["kr"]) if "c2p" in types else None
-    qr = r(x["qr"]) if "p2c" in types else None
+    kr = r(x["kr"]) if ("c2p" in types or "p2p" in types) else None
+    qr = r(x["qr"]) if ("p2c" in types or "p2p" in types) else None
     use_rel = kr is not None or qr is not None
     Lk = c.Lk or c.L
     rel = eager.relative_positions(c.L, Lk, c.buckets, c.max_pos) if use_rel else None
@@ -130,6 +130,7 @@ def oracle_run(c: Case, x: dict, dtype: torch.dtype, grads: bool = True) -> dict
 def hip_run(c: Case, x: dict, dtype: torch.dtype, device, grads: bool = True) -> dict:
     """The HIP op through the custom-op boundary (autograd for the backward)."""
     from deberta_amd import ops  # noqa: F401
+    from deberta_amd.attention import relative_operands
     from deberta_amd.masks import kernel_masks
     from deberta_amd.relpos import relative_offset_table
 
@@ -137,8 +138,11 @@ def hip_run(c: Case, x: dict, dtype: torch.dtype, device, grads: bool = True) ->
     Lk = c.Lk or c.L
     dev = lambda t: t.to(device=device, dtype=dtype).detach().clone().requires_grad_(grads)
     q, k, v = dev(x["q"]), dev(x["k"]), dev(x["v"])
-    kr = dev(x["kr"]) if "c2p" in types else None
-    qr = dev(x["qr"]) if "p2c" in types else None
+    kr = dev(x["kr"]) if ("c2p" in types or "p2p" in types) else None
+    qr = dev(x["qr"]) if ("p2c" in types or "p2p" in types) else None
+    # p2p rides on the c2p term's query rows qc (autograd takes qc's
+    # gradient back to q and qr)
+    kr_op, qr_op, qc = relative_operands(types, q, kr, qr, c.A)
     table = None
     if kr is not None or qr is not None:
         table = relative_offset_table(c.L, Lk, bucket_size=c.buckets, max_position=c.max_pos, device=device)
@@ -156,7 +160,7 @@ def hip_run(c: Case, x: dict, dtype: torch.dtype, device, grads: bool = True) ->
     sf = 1 + sum(t in types for t in ("c2p", "p2c", "p2p"))
     scale = 1.0 / math.sqrt(c.D * sf)
     seed = torch.tensor([c.drop_seed], dtype=torch.int64) if c.drop_t else None
-    out, lse, _, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr, qr, table, kk, pk, c.A, scale, True, None, c.drop_t, seed)
+    out, lse, _, _ = torch.ops.deberta_amd.dsa_fwd(q, k, v, kr_op, qr_op, table, kk, pk, c.A, scale, True, qc, c.drop_t, seed)
     res = {"out": out.detach().float().cpu(), "lse": lse.detach().cpu()}
     if grads:
         dout = x["dout"].to(device=device, dtype=dtype)

@@ -50,13 +50,16 @@ def _oracle_bias(ref, q, k, rel, types, sf, relative_pos=None):
 @pytest.mark.parametrize("types", ["c2p|p2c", "c2p", "p2c", "p2p", "c2p|p2c|p2p"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
 @pytest.mark.parametrize("share", [False, True])
-def test_bias_api_matches_oracle(types, dtype, share, gpu):
+@pytest.mark.parametrize("D", [32, 64])
+def test_bias_api_matches_oracle(types, dtype, share, D, gpu):
     """disentangled_attention_bias on the GPU against the oracle's bias
-    (einsum + gather) at L = 300 (ragged tiles, log buckets in use)."""
-    cfg = eager.make_config(hidden_size=128, num_attention_heads=4, share_att_key=share, pos_att_type=types)
+    (einsum + gather) at L = 300 (ragged tiles, log buckets in use), head
+    dims 32 and 64 (hidden 128 over 4 or 2 heads)."""
+    H = 128 // D
+    cfg = eager.make_config(hidden_size=128, num_attention_heads=H, share_att_key=share, pos_att_type=types)
     ref, ours = _pair(cfg, seed=11)
     ours = ours.to(gpu)
-    B, H, L, D = 2, 4, 300, 32
+    B, L = 2, 300
     q, k, rel = _bias_inputs(B, H, L, D, 128, seed=4)
     rnd = lambda t: t.to(dtype).float()
     types_l = eager.pos_att_types(types)
@@ -73,11 +76,11 @@ def test_bias_api_matches_oracle(types, dtype, share, gpu):
     got = got.float().cpu()
     if dtype == torch.float32:
         err = max_rel(got, want)
-        _say(f"[bias {types} fp32 share={share}] rel {err:.2e}")
+        _say(f"[bias {types} fp32 D={D} share={share}] rel {err:.2e}")
         assert err <= 1e-4
     else:
         err = max_abs(got, want)
-        _say(f"[bias {types} bf16 share={share}] abs {err:.2e} (max |ref| {float(want.abs().max()):.2f})")
+        _say(f"[bias {types} bf16 D={D} share={share}] abs {err:.2e} (max |ref| {float(want.abs().max()):.2f})")
         assert err <= 2e-2
 
 

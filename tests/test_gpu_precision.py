@@ -45,8 +45,8 @@ def _reference_bf16(c: Case, x: dict) -> dict:
     types = c.type_list
     r = lambda t: t.to(torch.bfloat16).to(torch.float32).detach().clone().requires_grad_(True)
     q, k, v = (r(x[n]).permute(0, 2, 1, 3) for n in ("q", "k", "v"))
-    kr = r(x["kr"]) if "c2p" in types else None
-    qr = r(x["qr"]) if "p2c" in types else None
+    kr = r(x["kr"]) if ("c2p" in types or "p2p" in types) else None
+    qr = r(x["qr"]) if ("p2c" in types or "p2p" in types) else None
     use_rel = kr is not None or qr is not None
     Lk = c.Lk or c.L
     rel = eager.relative_positions(c.L, Lk, c.buckets, c.max_pos) if use_rel else None
