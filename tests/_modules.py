@@ -60,3 +60,37 @@ def _errors(ref: dict, got: dict) -> dict:
         else:
             errs[k] = max_rel(got[k], ref[k])
     return errs
+
+
+def bias_dtype_contract(types: str, dev, monkeypatch) -> float:
+    """The reference's dtype contract of the relative products
+    (tests/test_smoke.py:1904-1965 and :1968-2029): projected tables that
+    come back in bfloat16 (``_project_rel`` replaced) meet float32 query and
+    key layers in float32 (head dim 32, the kernels' smallest, in place of
+    the reference's 8).  Asserts a float32 bias of the right shape and
+    returns its max|err| / max|ref| against the oracle's bias on the bf16
+    tables widened to float32."""
+    cfg = eager.make_config(hidden_size=128, num_attention_heads=4, max_position_embeddings=32,
+                            position_buckets=-1, max_relative_positions=-1, pos_att_type=types)
+    attn = DisentangledSelfAttention(cfg).to(dev).eval()
+    A, H, D = int(attn.pos_ebd_size), 4, 32
+    g = torch.Generator().manual_seed(19)
+    tables = {u: torch.randn(H, 2 * A, D, generator=g).to(torch.bfloat16) for u in (False, True)}
+    calls = []
+
+    def fake_project_rel(rel, *, use_query):
+        calls.append(use_query)
+        return tables[use_query].to(dev)
+
+    monkeypatch.setattr(attn, "_project_rel", fake_project_rel)
+    B, L = 2, 40
+    q = torch.randn(B, H, L, D, generator=g)
+    k = torch.randn(B, H, L, D, generator=g)
+    rel = torch.randn(2 * A, 128, generator=g)
+    with torch.no_grad():
+        got = attn.disentangled_attention_bias(q.to(dev), k.to(dev), None, rel.to(dev), 2)
+    assert calls and got.dtype == torch.float32 and tuple(got.shape) == (B, H, L, L)
+    kr = tables[False].float() if types == "c2p" else None
+    qr = tables[True].float() if types == "p2c" else None
+    want = eager.relative_bias(q, k, kr, qr, eager.relative_positions(L, L, -1, -1), A, [types], 2, D)
+    return max_rel(got.float().cpu(), want)

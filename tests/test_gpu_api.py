@@ -409,3 +409,18 @@ def test_packed_qkv_op_equals_separate_op(types, gpu):
             assert err <= 1e-2, f"{name}: {err:.3e}"  # bf16 roundings of fp32 sums in other orders
         else:
             assert torch.equal(a, b), f"{name} differs between the packed and the separate op"
+
+
+
+@pytest.mark.parametrize("types", ["c2p", "p2c"])
+def test_bias_api_casts_tables_to_query_dtype(types, gpu, monkeypatch):
+    """The reference's dtype contract of the relative products
+    (tests/test_smoke.py:1904-1965, :1968-2029) on the kernels: bf16
+    projected tables meet float32 layers in float32 (tests/_modules.py
+    ``bias_dtype_contract``; the CPU route has the same test in
+    tests/test_module_cpu.py)."""
+    from tests._modules import bias_dtype_contract
+
+    err = bias_dtype_contract(types, gpu, monkeypatch)
+    _say(f"[bias dtype contract {types}] rel {err:.2e}")
+    assert err <= 1e-5

@@ -249,3 +249,13 @@ def test_module_on_cpu_alternating_relative_pos():
             a, _ = ref(x, None, relative_pos=rp, rel_embeddings=rel)
             b, _ = ours(x, None, relative_pos=rp, rel_embeddings=rel)
             assert max_rel(b, a) <= TOL, n
+
+
+@pytest.mark.parametrize("types", ["c2p", "p2c"])
+def test_bias_api_on_cpu_casts_tables_to_query_dtype(types, monkeypatch):
+    """The reference's dtype contract of the relative products
+    (tests/test_smoke.py:1904-1965, :1968-2029) on the CPU route: bf16
+    projected tables meet float32 layers in float32."""
+    from tests._modules import bias_dtype_contract
+
+    assert bias_dtype_contract(types, torch.device("cpu"), monkeypatch) <= TOL
