@@ -41,7 +41,8 @@ R = 2 * A
 #   name: (batch, seq_len, heads, mask kind, description)
 WORKLOADS = {
     "headline": (32, 512, 12, None, "BASELINE configs[1] shape, all-ones mask"),
-    "C2pad": (32, 512, 12, "key", "configs[1] shape, per-row valid length ~U{64..512} as a (B,1,1,L) key mask"),
+    "C2pad": (32, 512, 12, "pad", "configs[1] shape, per-row valid length ~U{64..512}, given as the encoder gives a padding mask to its layers: the (B,1,L,L) pair mask keep_i & keep_j (recognised once and run as segment ids)"),
+    "C2key": (32, 512, 12, "key", "as C2pad, the same lengths as a (B,1,1,L) key mask: every query row, padded ones included, attends to its row's valid keys"),
     "C5": (64, 512, 16, None, "B=64 L=512 H=16, no mask"),
     "C3": (16, 512, 12, None, "12-layer DeBERTa-v3-base-shaped encoder fwd+bwd under an RTD loss, bf16 autocast, fused attention and fused row kernels around it (step time with plain torch blocks beside it)"),
     "C5layer": (64, 512, 16, None, "DeBERTa-v3-large-shaped attention layer (hidden 1024, projections included) fwd+bwd, bf16, inside torch.compile"),
@@ -221,10 +222,15 @@ def workload_mask(kind, b: int, l: int, g, dev):
 
     if kind is None:
         return None, b * l * l, b * l
-    if kind == "key":
+    if kind in ("key", "pad"):
         lens = torch.randint(64, l + 1, (b,), generator=g)
         keep = torch.arange(l)[None, :] < lens[:, None]
-        return keep[:, None, None, :].to(dev), int((lens.double() ** 2).sum()), int(lens.sum())
+        if kind == "key":  # every query row attends to the row's valid keys
+            return keep[:, None, None, :].to(dev), l * int(lens.sum()), b * l
+        # the encoder's form of a padding mask (deberta_v2_native.py:1049-1068):
+        # padded query rows keep no key
+        pair = keep[:, :, None] & keep[:, None, :]
+        return pair[:, None].to(dev), int((lens.double() ** 2).sum()), int(lens.sum())
     ids = torch.zeros(b, l, dtype=torch.int64)
     for r in range(b):  # document lengths 1 + Geometric(p = 1/600) by inversion, cut at the row's end
         pos, doc = 0, 1
