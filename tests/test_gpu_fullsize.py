@@ -9,6 +9,9 @@ test_gpu_parity.py).
   get exactly zero gradient.  The upstream gradient of padded query rows is
   zero, so that they contribute nothing (they attend the valid keys, as in
   the reference, whose key-padding mask leaves them live).
+* Configuration 2 in the encoder's pair form (keep_i & keep_j): its live
+  rows and every key's gradients equal the key-mask run's with the padded
+  rows' upstream gradient zeroed; dead rows give exact zeros.
 * Configuration 4 (B=4, L=4096, H=12, D=64, bf16, packed documents given as
   segment ids; lengths as in the configuration but at least 96 tokens):
   each document of the packed run equals the document run alone as its own
@@ -95,6 +98,35 @@ def test_config2_padded_rows_equal_unpadded_runs(gpu):
         sum_qr += r[5]
     _tables("dkr", dkr, sum_kr)
     _tables("dqr", dqr, sum_qr)
+
+
+def test_config2_pair_form_equals_key_form_on_live_rows(gpu):
+    """Configuration 2's padding as the reference's encoder hands it to its
+    layers (get_attention_mask, deberta_v2_native.py:1049-1068: the pair
+    mask keep_i & keep_j, padded queries dead rows; recognised and run as
+    segment ids) against the key-mask run of the same inputs whose padded
+    query rows get no upstream gradient: live rows and every key's
+    gradients agree, dead rows' outputs and dq are exactly zero, and the
+    dead rows' upstream gradient (left nonzero here) reaches nothing."""
+    B, L = 32, 512
+    q, k, v, kr, qr, dout, g = _inputs(B, L, 62, gpu)
+    lens = torch.randint(64, L + 1, (B,), generator=g)
+    keep = torch.arange(L)[None, :] < lens[:, None]
+    pair = (keep[:, :, None] & keep[:, None, :])[:, None].to(gpu)
+    kk, pk = kernel_masks(pair, B, L, L, gpu)
+    assert pk is None and kk is not None and kk.dtype == torch.int32, "padding pair mask not run as segments"
+    _say(f"[fullsize] C2 pair form B={B} L={L}, lengths {int(lens.min())}..{int(lens.max())}")
+    got = _run(q, k, v, kr, qr, dout, pair)
+    live = keep[:, :, None, None].to(gpu)
+    ref = _run(q, k, v, kr, qr, dout * live.to(dout.dtype), keep[:, None, None, :].to(gpu))
+    for name, a, b in zip(("out", "dq"), got[:2], ref[:2]):
+        _close(f"live rows {name}", a * live, b * live)
+        assert float((a * ~live).abs().max()) == 0.0, f"dead rows: nonzero {name}"
+    for name, a, b in zip(("dk", "dv"), got[2:4], ref[2:4]):
+        _close(name, a, b)
+        assert float((a * ~live).abs().max()) == 0.0, f"padded keys got a {name}"
+    _tables("dkr", got[4], ref[4])
+    _tables("dqr", got[5], ref[5])
 
 
 def test_config4_packed_documents_equal_separate_runs(gpu):
