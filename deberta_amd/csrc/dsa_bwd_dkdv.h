@@ -405,6 +405,14 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
         }
       }
       auto probs = [&](auto plain) {
+        // segment masks: the lane's query segments, four consecutive rows
+        // of each 16-row block in one 16-byte LDS read (read per element,
+        // they cost segment-masked steps 4 to 13%)
+        int4 qv[BQ / 16];
+        if constexpr (MASK == MASK_SEG && !decltype(plain)::value) {
+#pragma unroll
+          for (int ib = 0; ib < BQ / 16; ++ib) qv[ib] = *reinterpret_cast<const int4*>(&qsg[n & 1][16 * ib + 4 * g]);
+        }
 #pragma unroll
         for (int ib = 0; ib < BQ / 16; ++ib) {
           frag dof[NS];
@@ -427,7 +435,8 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
                 // rows without probabilities (dead, padding) have lr = inf and may hold an
                 // unwritten saved term: they are never exponentiated
                 bool keep = jkeep[jb] && lr != INFINITY;
-                if (MASK == MASK_SEG && !full) keep = keep && qsg[n & 1][il] == jseg[jb];
+                if (MASK == MASK_SEG && !full)
+                  keep = keep && (e == 0 ? qv[ib].x : e == 1 ? qv[ib].y : e == 2 ? qv[ib].z : qv[ib].w) == jseg[jb];
                 if (MASK == MASK_PAIR) keep = keep && ((pmask[il][2 * w + jb] >> c16) & 1u);
                 pe = keep ? __builtin_amdgcn_exp2f(__builtin_fmaf(sc[jb][ib][e], sl2, -lr)) : 0.f;
               }
@@ -443,7 +452,10 @@ __global__ __launch_bounds__(256, 2) void dsa_bwd_dkdv_kernel(BwdParams bp) {
           }
         }
       };
-      if (!DROP && keys_in && i0 + BQ <= Lq)
+      // without masking: unmasked tiles inside the sequence, and segment
+      // tiles listed as full (every query and key of the tile active and in
+      // one segment, so every pair is kept and every row has probabilities)
+      if (!DROP && ((keys_in && i0 + BQ <= Lq) || (MASK == MASK_SEG && full)))
         probs(std::true_type{});
       else
         probs(std::false_type{});
